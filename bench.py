@@ -1,0 +1,393 @@
+#!/usr/bin/env python3
+"""Throughput of the llama3.x.c matmul hot path on one MI355X.
+
+Headline (`value`): Llama-3.1-8B Q8_0 decode, tokens/s of the decode-step matmul set at batch 1: per layer the
+activation quantization and the W8A8 GEMVs of QKV (one three-segment launch), Wo (+residual), W1/W3 (SwiGLU) and W2
+(+residual), for 32 layers, then the classifier (128256 x 4096); gs = 64. A step is one token's set, replayed from a
+HIP graph with every input already in HBM; attention, RMSNorm and RoPE are not part of the set.
+
+Alongside (`prefill`): the 8B INT8 W8A8 prefill of a 2048-token prompt: per layer quantize the 2048 rows and run the
+int8-MFMA GEMMs (QKV, Wo + residual, W1/W3 SwiGLU, W2 + residual), then the last row's classifier GEMV.
+
+Weights ~N(0, 0.02) and activations ~N(0, 1) are drawn on the device (torch, seeded) and quantized by the library's
+own k_quantize rule; the data is synthetic. `roofline` is the dominant kernel of the decode step (the SwiGLU GEMV),
+timed launch by launch with HIP events on the library stream. `cpu_baseline` runs the reference's own gemm-bench
+(oracle/_ref, built from the reference's sources) on the same shapes on this host's cores.
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "llama3.x.c_amd")
+for p in (ROOT, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+# Llama-3.1-8B
+DIM, KV_DIM, HIDDEN, VOCAB, LAYERS, GS = 4096, 1024, 14336, 128256, 32, 64
+PROMPT = 2048
+
+
+def q8_bytes(rows, k, gs=GS):
+    """Algorithmic bytes of one Q8_0 GEMV: int8 weights, their FP32 scales, the int8 input and its scales, the FP32
+    output (read too for the residual kinds is not counted)."""
+    return rows * k + rows * (k // gs) * 4 + k + (k // gs) * 4 + rows * 4
+
+
+def weight_bytes(rows, k, gs=GS):
+    return rows * k + rows * (k // gs) * 4
+
+
+class Model8B:
+    """Device-resident Q8_0 weights of the 8B matmul set, drawn and quantized on the GPU."""
+
+    def __init__(self, torch, lh, seed):
+        self.torch, self.lh = torch, lh
+        L = lh.load()
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(seed)
+        self.layers = []
+        shapes = [("wq", DIM, DIM), ("wk", KV_DIM, DIM), ("wv", KV_DIM, DIM), ("wo", DIM, DIM), ("w1", HIDDEN, DIM),
+                  ("w3", HIDDEN, DIM), ("w2", DIM, HIDDEN)]
+        total = sum(r * k for _, r, k in shapes) * LAYERS + VOCAB * DIM
+        self.q_all = torch.empty(total, dtype=torch.int8, device="cuda")
+        self.s_all = torch.empty(total // GS, dtype=torch.float32, device="cuda")
+        scratch = torch.empty(VOCAB * DIM, dtype=torch.float32, device="cuda")
+        self.cursor = 0
+
+        def make(rows, k):
+            n = rows * k
+            w = scratch[:n].view(rows, k)
+            w.normal_(0.0, 0.02, generator=gen)
+            q = self.q_all[self.cursor: self.cursor + n].view(rows, k)
+            s = self.s_all[self.cursor // GS: (self.cursor + n) // GS].view(rows, k // GS)
+            self.cursor += n
+            torch.cuda.synchronize()
+            L.k_quantize_rows(q.data_ptr(), s.data_ptr(), w.data_ptr(), k, rows, k, GS)
+            L.llhip_synchronize()
+            return q, s
+
+        for _ in range(LAYERS):
+            self.layers.append({name: make(r, k) for name, r, k in shapes})
+        self.cls = make(VOCAB, DIM)
+        del scratch
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+
+def decode_set(torch, lh, model, seed):
+    """Buffers and the call sequence of one token's matmul set."""
+    L = lh.load()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 1)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    acts = [{k: torch.randn(n, generator=gen, **f32) for k, n in (("att", DIM), ("o", DIM), ("ffn", DIM),
+                                                                    ("h", HIDDEN))} for _ in range(LAYERS)]
+    x_cls = torch.randn(DIM, generator=gen, **f32)
+    xq_d, xs_d = torch.empty(DIM, dtype=torch.int8, device="cuda"), torch.empty(DIM // GS, **f32)
+    xq_h, xs_h = torch.empty(HIDDEN, dtype=torch.int8, device="cuda"), torch.empty(HIDDEN // GS, **f32)
+    q, k, v = torch.empty(DIM, **f32), torch.empty(KV_DIM, **f32), torch.empty(KV_DIM, **f32)
+    resid, hb, logits = torch.zeros(DIM, **f32), torch.empty(HIDDEN, **f32), torch.empty(VOCAB, **f32)
+    torch.cuda.synchronize()
+    P = lh.ptr
+
+    def w8(pair):
+        return lh.K8Weight(P(pair[0]), P(pair[1]))
+
+    inputs_d, inputs_h = lh.K8Input(P(xq_d), P(xs_d), None), lh.K8Input(P(xq_h), P(xs_h), None)
+
+    def step(only=None):
+        for l, lay in enumerate(model.layers):
+            a = acts[l]
+            L.k_quantize(P(xq_d), P(xs_d), P(a["att"]), DIM, GS)
+            if only in (None, "qkv"):
+                L.k_matmul_q8_qkv(P(q), P(k), P(v), inputs_d, w8(lay["wq"]), w8(lay["wk"]), w8(lay["wv"]), DIM, DIM,
+                                  KV_DIM, GS)
+            L.k_quantize(P(xq_d), P(xs_d), P(a["o"]), DIM, GS)
+            if only in (None, "wo"):
+                L.k_matmul_q8_add(P(resid), inputs_d, w8(lay["wo"]), DIM, DIM, GS)
+            L.k_quantize(P(xq_d), P(xs_d), P(a["ffn"]), DIM, GS)
+            if only in (None, "w13"):
+                if only == "w13":
+                    yield "w13"
+                L.k_matmul_q8_swiglu(P(hb), inputs_d, w8(lay["w1"]), w8(lay["w3"]), DIM, HIDDEN, GS)
+                if only == "w13":
+                    yield "w13-end"
+            L.k_quantize(P(xq_h), P(xs_h), P(a["h"]), HIDDEN, GS)
+            if only in (None, "w2"):
+                L.k_matmul_q8_add(P(resid), inputs_h, w8(lay["w2"]), HIDDEN, DIM, GS)
+        L.k_quantize(P(xq_d), P(xs_d), P(x_cls), DIM, GS)
+        if only in (None, "cls"):
+            L.k_matmul_q8(P(logits), inputs_d, w8(model.cls), DIM, VOCAB, GS)
+
+    def run_step():
+        for _ in step():
+            pass
+
+    return run_step, step
+
+
+def time_graph(torch, L, graph, steps, warmup):
+    stream = torch.cuda.ExternalStream(L.llhip_stream())
+    for _ in range(warmup):
+        L.llhip_graph_launch(graph)
+    L.llhip_synchronize()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        L.llhip_graph_launch(graph)
+    end.record(stream)
+    end.synchronize()
+    L.llhip_synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1000.0
+
+
+def time_launches(torch, L, calls):
+    """GPU duration of each call's launch, bracketed by HIP events on the library stream. A spin kernel keeps the
+    stream busy while the host enqueues, so every event pair encloses its kernel and nothing else."""
+    stream = torch.cuda.ExternalStream(L.llhip_stream())
+    L.llhip_synchronize()
+    pairs = []
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(200_000_000)
+        for call in calls:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            call()
+            e1.record(stream)
+            pairs.append((e0, e1))
+    pairs[-1][1].synchronize()
+    L.llhip_synchronize()
+    return [a.elapsed_time(b) / 1000.0 for a, b in pairs]
+
+
+def prefill_set(torch, lh, model, seed):
+    L = lh.load()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 2)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    x_in = torch.randn(PROMPT, DIM, generator=gen, **f32)
+    h_in = torch.randn(PROMPT, HIDDEN, generator=gen, **f32)
+    xq = torch.empty(PROMPT, HIDDEN, dtype=torch.int8, device="cuda")
+    xs = torch.empty(PROMPT, HIDDEN // GS, **f32)
+    q, k, v = torch.empty(PROMPT, DIM, **f32), torch.empty(PROMPT, KV_DIM, **f32), torch.empty(PROMPT, KV_DIM, **f32)
+    resid, hb = torch.zeros(PROMPT, DIM, **f32), torch.empty(PROMPT, HIDDEN, **f32)
+    logits = torch.empty(VOCAB, **f32)
+    torch.cuda.synchronize()
+    P = lh.ptr
+
+    def w8(pair):
+        return lh.K8Weight(P(pair[0]), P(pair[1]))
+
+    def seg(c, pair, n, kind, pair3=None):
+        return lh.GemmQ8Segment(P(c), n, w8(pair), w8(pair3) if pair3 else lh.K8Weight(), None, None, n, kind)
+
+    gemms = []  # (callable, ops) of every GEMM launch, for the roofline
+    for lay in model.layers:
+        qkv = (lh.GemmQ8Segment * 3)(seg(q, lay["wq"], DIM, lh.GEMM_STORE), seg(k, lay["wk"], KV_DIM, lh.GEMM_STORE),
+                                     seg(v, lay["wv"], KV_DIM, lh.GEMM_STORE))
+        wo = seg(resid, lay["wo"], DIM, lh.GEMM_ADD)
+        w13 = seg(hb, lay["w1"], HIDDEN, lh.GEMM_SWIGLU, lay["w3"])
+        w2 = seg(resid, lay["w2"], DIM, lh.GEMM_ADD)
+        gemms.append((lambda s=qkv: L.k_gemm_q8(P(xq), P(xs), PROMPT, DIM, GS, s, 3), 2 * PROMPT * DIM * (DIM + 2 * KV_DIM)))
+        gemms.append((lambda s=wo: L.k_gemm_q8(P(xq), P(xs), PROMPT, DIM, GS, s, 1), 2 * PROMPT * DIM * DIM))
+        gemms.append((lambda s=w13: L.k_gemm_q8(P(xq), P(xs), PROMPT, DIM, GS, s, 1), 2 * PROMPT * DIM * HIDDEN * 2))
+        gemms.append((lambda s=w2: L.k_gemm_q8(P(xq), P(xs), PROMPT, HIDDEN, GS, s, 1), 2 * PROMPT * HIDDEN * DIM))
+    last = lh.K8Input(P(xq), P(xs), None)
+
+    def run():
+        for i, (call, _) in enumerate(gemms):
+            if i % 4 == 3:
+                L.k_quantize_rows(P(xq), P(xs), P(h_in), HIDDEN, PROMPT, HIDDEN, GS)
+            else:
+                L.k_quantize_rows(P(xq), P(xs), P(x_in), DIM, PROMPT, DIM, GS)
+            call()
+        # the classifier on the last row only (tp.c:610-618)
+        L.k_quantize(P(xq), P(xs), P(x_in[PROMPT - 1]), DIM, GS)
+        L.k_matmul_q8(P(logits), last, w8(model.cls), DIM, VOCAB, GS)
+
+    ops = sum(o for _, o in gemms) + 2 * VOCAB * DIM
+    return run, gemms, ops
+
+
+def cpu_baseline(threads, budget_s=30.0):
+    """The reference's own instrument, gemm-bench --gemv (tests/gemm_bench.c), on the five 8B decode shapes with cold
+    weights, scaled to one token (32 x the layer set + the classifier). Falls back to the oracle's threaded scalar GEMV
+    when the reference was not built here."""
+    exe = os.path.join(ROOT, "oracle", "_ref", "gemm-bench")
+    shapes = [(DIM, DIM), (KV_DIM, DIM), (HIDDEN, DIM), (DIM, HIDDEN), (VOCAB, DIM)]
+    per_token = {(DIM, DIM): 2 * LAYERS, (KV_DIM, DIM): 2 * LAYERS, (HIDDEN, DIM): 2 * LAYERS, (DIM, HIDDEN): LAYERS,
+                 (VOCAB, DIM): 1}
+    if os.path.exists(exe):
+        env = dict(os.environ, LLAMA_THREADS=str(threads), LLAMA_KERNELS="auto")
+        cmd = [exe, "--kernel", "q8", "--gemv", "--m", "1", "--reps", "5", "--cold-mib", "1200", "--shapes",
+               ",".join(f"{n}x{k}" for n, k in shapes)]
+        t0 = time.time()
+        r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+        if r.returncode == 0:
+            med = {}
+            isa = "?"
+            for line in r.stdout.splitlines():
+                rec = json.loads(line)
+                if rec["kernel"] == "gemv_rows_q8":
+                    med[(rec["n"], rec["k"])] = rec["median_s"]
+                    isa = rec["isa"]
+            token_s = sum(med[s] * c for s, c in per_token.items())
+            return {"value": round(1.0 / token_s, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+                    "sample": f"reference gemm-bench --kernel q8 --gemv (isa {isa}, {threads} threads, 5 reps, cold "
+                              f"copies over 1200 MiB) on the 8B shapes 4096x4096, 1024x4096, 14336x4096, 4096x14336, "
+                              f"128256x4096; per-token time = 32 x (2 wq/wo + 2 wk/wv + 2 w1/w3 + w2) + classifier "
+                              f"= {token_s * 1e3:.2f} ms; wall {time.time() - t0:.1f} s",
+                    "weight_gbs": round(7973699584 / token_s / 1e9, 1)}
+    # fallback: the oracle's scalar GEMV on one 4096x4096 matrix, threaded, scaled to a token by bytes
+    import numpy as np
+
+    from oracle import pyoracle as orc
+
+    rng = orc.Rng()
+    wq = (rng.uniform(DIM * DIM) * 120).astype(np.int8).reshape(DIM, DIM)
+    ws = np.full((DIM, DIM // GS), 0.001, np.float32)
+    xq = (rng.uniform(DIM) * 120).astype(np.int8)
+    xs = np.full(DIM // GS, 0.01, np.float32)
+    out = np.zeros(DIM, np.float32)
+    L = orc.lib()
+    reps, t0 = 0, time.time()
+    while time.time() - t0 < min(budget_s, 10.0):
+        L.orc_matmul_q8_threads(orc.ptr(out), orc.ptr(xq), orc.ptr(xs), orc.ptr(wq), orc.ptr(ws), DIM, DIM, GS, threads)
+        reps += 1
+    per_call = (time.time() - t0) / reps
+    token_s = per_call * 7973699584 / weight_bytes(DIM, DIM)
+    return {"value": round(1.0 / token_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle scalar Q8 GEMV 4096x4096 x{reps}, {threads} threads, scaled to the 8B token by bytes"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--prefill-steps", type=int, default=3)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--seed", type=int, default=88172645463325252 % (1 << 31))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import llama_hip as lh
+
+    L = lh.load()
+    if L.llhip_init() != 0:
+        raise SystemExit(f"no usable MI355X: {lh.last_error()}")
+    t_setup = time.time()
+    model = Model8B(torch, lh, args.seed)
+    run_step, step_gen = decode_set(torch, lh, model, args.seed)
+    print(f"# weights resident: {model.cursor / 1e9:.2f} GB int8 + scales, setup {time.time() - t_setup:.1f} s",
+          file=sys.stderr, flush=True)
+
+    # decode: one token's matmul set as a HIP graph
+    run_step()
+    L.llhip_synchronize()
+    assert L.llhip_graph_begin() == 0
+    run_step()
+    graph = L.llhip_graph_end()
+    if not graph:
+        raise SystemExit(f"graph capture failed: {lh.last_error()}")
+    seconds = time_graph(torch, L, graph, args.steps, args.warmup)
+    tok_s = args.steps / seconds
+    step_bytes = LAYERS * (q8_bytes(DIM + 2 * KV_DIM, DIM) + q8_bytes(DIM, DIM) + 2 * weight_bytes(HIDDEN, DIM)
+                           + DIM + DIM // GS * 4 + HIDDEN * 4 + q8_bytes(DIM, HIDDEN)) + q8_bytes(VOCAB, DIM)
+    print(f"# decode: {seconds / args.steps * 1e3:.3f} ms/token, {tok_s:.1f} tok/s, "
+          f"{step_bytes / (seconds / args.steps) / 1e9:.0f} GB/s over the step", file=sys.stderr, flush=True)
+
+    # roofline of the dominant kernel: the W1/W3 SwiGLU GEMV, one launch per layer, timed launch by launch
+    sw_calls = []
+    gen = step_gen(only="w13")
+    # collect the 32 SwiGLU launches as separate callables by re-running the generator's layer loop
+    P = lh.ptr
+    xq_probe = torch.empty(DIM, dtype=torch.int8, device="cuda")
+    xs_probe = torch.empty(DIM // GS, dtype=torch.float32, device="cuda")
+    xf = torch.randn(DIM, device="cuda")
+    hb = torch.empty(HIDDEN, device="cuda")
+    torch.cuda.synchronize()
+    L.k_quantize(P(xq_probe), P(xs_probe), P(xf), DIM, GS)
+    inp = lh.K8Input(P(xq_probe), P(xs_probe), None)
+    for lay in model.layers:
+        w1, w3 = lay["w1"], lay["w3"]
+        sw_calls.append(lambda w1=w1, w3=w3: L.k_matmul_q8_swiglu(P(hb), inp, lh.K8Weight(P(w1[0]), P(w1[1])),
+                                                                  lh.K8Weight(P(w3[0]), P(w3[1])), DIM, HIDDEN, GS))
+    del gen
+    durations = []
+    for _ in range(3):
+        durations += time_launches(torch, L, sw_calls)
+    avg = sum(durations) / len(durations)
+    sw_bytes = 2 * weight_bytes(HIDDEN, DIM) + DIM + DIM // GS * 4 + HIDDEN * 4
+    achieved = sw_bytes / avg / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "q8_gemv<2, SWIGLU> (W1/W3 14336x4096 x2, gs 64)",
+                "avg_launch_us": round(avg * 1e6, 2), "bytes_per_launch": sw_bytes}
+
+    result = {
+        "metric": "8B Q8_0 decode tok/s (%HBM peak); 2048-tok prefill tok/s (%MFMA peak)",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(seconds / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 W8A8 (int32 group dots, fp32 scales)", "data": "synthetic",
+        "config": {"workload": "Llama-3.1-8B Q8_0 decode-step matmul set, batch 1: 32 x (quantize + QKV 6144x4096, "
+                               "Wo 4096x4096 +resid, W1/W3 2x14336x4096 SwiGLU, W2 4096x14336 +resid) + classifier "
+                               "128256x4096, gs 64, HIP graph",
+                   "algorithmic_bytes_per_step": step_bytes,
+                   "step_hbm_frac": round(step_bytes / (seconds / args.steps) / 1e9 / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+    }
+
+    if not args.no_prefill:
+        run_prefill, gemms, ops = prefill_set(torch, lh, model, args.seed)
+        run_prefill()
+        L.llhip_synchronize()
+        assert L.llhip_graph_begin() == 0
+        run_prefill()
+        pgraph = L.llhip_graph_end()
+        psec = time_graph(torch, L, pgraph, args.prefill_steps, 1)
+        ptok = PROMPT * args.prefill_steps / psec
+        # the dominant prefill kernel: the W1/W3 SwiGLU GEMM (2048 x 2 x 14336 x 4096), timed launch by launch
+        w13 = [c for i, (c, _) in enumerate(gemms) if i % 4 == 2]
+        d = time_launches(torch, L, w13)
+        pavg = sum(d) / len(d)
+        w13_ops = 2 * PROMPT * DIM * HIDDEN * 2
+        ach = w13_ops / pavg / 1e12
+        result["prefill"] = {
+            "value": round(ptok, 1), "unit": "tok/s", "ms_per_prompt": round(psec / args.prefill_steps * 1e3, 3),
+            "workload": "Llama-3.1-8B INT8 W8A8 prefill, 2048 tokens, 32 layers of quantize_rows + int8-MFMA GEMMs "
+                        "(QKV, Wo +resid, W1/W3 SwiGLU, W2 +resid) + last-row classifier GEMV, gs 64",
+            "ops_per_prompt": ops, "tops": round(ops / (psec / args.prefill_steps) / 1e12, 1),
+            "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                         "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": None,
+                         "kernel": "q8_gemm_mfma (W1/W3 SwiGLU 2048x(2x14336)x4096)",
+                         "avg_launch_us": round(pavg * 1e6, 1)},
+        }
+        L.llhip_graph_destroy(pgraph)
+        print(f"# prefill: {psec / args.prefill_steps * 1e3:.2f} ms/prompt, {ptok:.0f} tok/s, "
+              f"{ach:.0f} TOP/s in the W1/W3 GEMM", file=sys.stderr, flush=True)
+    L.llhip_graph_destroy(graph)
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_threads)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

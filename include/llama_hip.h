@@ -1,0 +1,84 @@
+/* llama3.x.c matmul hot path on an MI355X (gfx950): the C ABI of libllama3x_hip.so.
+ *
+ * The reference-named entry points are declared in llama_hip_kernels.h (GEMV), llama_hip_gemm.h (batched GEMM) and
+ * llama_hip_prefill.h (prefill policy). This header adds what a GPU needs and the reference has no counterpart for:
+ * opening the device, making weights resident in HBM once, the stream the calls are ordered on, graph capture of a
+ * decode step, and the failure mode.
+ *
+ * Residency. Every pointer an entry point receives is resolved per call:
+ *   - device memory (hipMalloc, llhip_malloc, a torch CUDA tensor) is used in place; the call is a launch on the
+ *     library stream and returns before the GPU finishes (llhip_synchronize waits);
+ *   - host memory inside a range given to llhip_register_host resolves to its device copy (weights: upload once);
+ *   - any other host memory is copied to a device arena before the launch and back after it, and the call waits,
+ *     so it behaves like the reference's synchronous CPU call.
+ * The reference's calls are synchronous; with device pointers, ordering is the stream's order, and the host must call
+ * llhip_synchronize before reading results or writing inputs through another route.
+ *
+ * Failures. Preconditions fail as in the reference (fail(): message, then exit(EXIT_FAILURE)). A non-finite
+ * activation seen by a device quantizer is reported at the next host-visible point (llhip_synchronize or any staged
+ * call). */
+#ifndef LLAMA_HIP_H
+#define LLAMA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "llama_hip_gemm.h"
+#include "llama_hip_kernels.h"
+#include "llama_hip_prefill.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opens the device (LLAMA_HIP_DEVICE, default 0) and creates the library stream; 0 on success. Every entry point
+ * calls it on first use. */
+int llhip_init(void);
+const char *llhip_device_name(void);
+int llhip_device_cu_count(void);
+/* The hipStream_t every launch goes to (default priority). */
+void *llhip_stream(void);
+/* Waits for the stream; then fails if a device quantizer saw a non-finite activation since the last check. */
+void llhip_synchronize(void);
+
+/* Uploads [host, host + bytes) to HBM once; pointers inside the range then resolve to the copy. The host bytes must
+ * not change afterwards (re-register to refresh). Returns 0, or -1 after a failure. */
+int llhip_register_host(const void *host, size_t bytes);
+int llhip_unregister_host(const void *host);
+/* The device address a host address resolves to (NULL when it is not inside a registered range). */
+void *llhip_resolve(const void *host);
+
+/* Device memory owned by the caller, and stream-ordered copies (all on the library stream). */
+void *llhip_malloc(size_t bytes);
+void llhip_free(void *device);
+void llhip_memcpy_h2d(void *device, const void *host, size_t bytes);
+void llhip_memcpy_d2h(void *host, const void *device, size_t bytes);
+void llhip_memcpy_d2d(void *dst, const void *src, size_t bytes);
+
+/* Graph capture of a sequence of entry-point calls on device-resident pointers (a decode step): begin, make the
+ * calls, end. A staged (host-pointer) call inside a capture fails. The returned handle replays with
+ * llhip_graph_launch (stream-ordered) and is released with llhip_graph_destroy. */
+int llhip_graph_begin(void);
+void *llhip_graph_end(void);
+int llhip_graph_launch(void *graph);
+void llhip_graph_destroy(void *graph);
+
+/* Failure behaviour. The handler (NULL = default) receives the formatted message and is expected not to return,
+ * like the reference's fail(). LLHIP_FAIL_RECORD instead keeps the message, and the failing call returns without
+ * doing its work (for tests of the error paths). */
+typedef void (*LlhipFailFn)(const char *message);
+void llhip_set_fail_handler(LlhipFailFn handler);
+enum { LLHIP_FAIL_EXIT = 0, LLHIP_FAIL_RECORD = 1 };
+void llhip_set_fail_mode(int mode);
+const char *llhip_last_error(void); /* "" when none */
+void llhip_clear_error(void);
+
+/* The int32 probe of the decode GEMV: dots[g * d + r] = the exact int32 dot of group g of input row xq and weight
+ * row r, as the streaming GEMV kernel itself forms it before the FP32 rescale (gs % 16 == 0 takes the fast kernel). */
+void llhip_q8_gemv_group_dots(int32_t *dots, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws,
+                              size_t ld, int n, int d, int gs);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,157 @@
+// Internal to the HIP library: device state, pointer residency, failure handling and the kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "llama_hip.h"
+
+namespace llhip {
+
+// ---- failure ----------------------------------------------------------------------------------------------------
+// The reference's fail() prints the message and exits (runtime.c:49-63). Here the default does the same; a host that
+// has its own fail() installs it with llhip_set_fail_handler, and tests switch to LLHIP_FAIL_RECORD, where the
+// failing entry point returns without doing its work. raise() returns false in that mode so callers can `return`.
+bool raise(const char *format, ...) __attribute__((format(printf, 1, 2)));
+bool check_hip(hipError_t status, const char *what);
+#define LLHIP_CHECK(call) ::llhip::check_hip((call), #call)
+
+// ---- device state -----------------------------------------------------------------------------------------------
+struct Device {
+  bool ready = false;
+  int ordinal = 0;
+  hipStream_t stream = nullptr;
+  int *error_flags = nullptr; // device: [0] non-finite activation seen by a quantizer
+  int cu_count = 0;
+  bool capturing = false;
+};
+Device &device();
+bool ensure_device(); // opens the device on first use; false (after raise) when none is usable
+// Waits for the stream and turns a device-side error flag into a failure (the reference fails at once; a device
+// kernel can only report at the next host-visible point).
+bool synchronize_and_check();
+
+// ---- pointer residency ------------------------------------------------------------------------------------------
+// Every pointer an entry point receives is resolved once per call: device memory is used in place, host memory
+// inside a registered range maps to its uploaded copy, and any other host memory is staged through a device arena
+// (copied in before the launch, copied out after it, then the call synchronizes).
+// A resolved pointer: device memory in place, or an index into the call's staged copies.
+struct Ref {
+  void *direct = nullptr;
+  int staged = -1;
+};
+
+class Call {
+ public:
+  explicit Call(const char *name);
+  ~Call();
+  Ref in(const void *p, size_t bytes) { return in2d(p, bytes, bytes, 1); }
+  Ref in2d(const void *p, size_t row_bytes, size_t pitch, size_t rows);
+  Ref out(void *p, size_t bytes, bool read_too) { return out2d(p, bytes, bytes, 1, read_too); }
+  Ref out2d(void *p, size_t row_bytes, size_t pitch, size_t rows, bool read_too);
+  // Allocates the arena and performs the staging copies; false when something failed (already raised).
+  bool ready();
+  // The device address of a resolved pointer (valid after ready()).
+  template <class T> T *ptr(const Ref &r) const { return (T *)address(r); }
+  // Copies staged outputs back and, if anything was staged, synchronizes. Returns false on failure.
+  bool finish();
+  bool staged() const { return staged_; }
+  bool failed() const { return failed_; }
+  hipStream_t stream() const;
+
+ private:
+  struct Copy {
+    void *host;
+    size_t offset, row_bytes, pitch, rows;
+    bool to_device, to_host;
+  };
+  void *address(const Ref &r) const;
+  Ref stage(void *host, size_t row_bytes, size_t pitch, size_t rows, bool to_device, bool to_host);
+  const char *name_;
+  Copy copies_[16];
+  int ncopies_ = 0;
+  size_t arena_used_ = 0;
+  bool staged_ = false, failed_ = false;
+};
+
+// ---- kernel launchers (stream-ordered, no synchronization) ------------------------------------------------------
+enum Epilogue { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+
+struct QuantizeJob {
+  int8_t *q;
+  float *s;
+  const float *x;
+  size_t ldx; // floats
+  int m, n, gs;
+};
+bool launch_quantize(const QuantizeJob &job, hipStream_t stream);
+
+struct GemvSegment {
+  float *out;
+  const int8_t *wq;
+  const float *ws;
+  const int8_t *w3q; // SWIGLU
+  const float *w3s;
+  int rows;
+};
+struct GemvJob {
+  GemvSegment seg[3];
+  int nseg;
+  const int8_t *xq; // W8A8 input (xq, xs) or, with xq == nullptr, the W8A32 input xf
+  const float *xs;
+  const float *xf;
+  int n, gs;
+  size_t ld; // weight row stride in values
+  Epilogue epi;
+  int32_t *probe; // optional: exact int32 group dots of segment 0, probe[g * rows + r]
+};
+bool launch_q8_gemv(const GemvJob &job, hipStream_t stream);
+
+struct F32GemvSegment {
+  float *out;
+  const float *w, *w3;
+  int rows;
+};
+struct F32GemvJob {
+  F32GemvSegment seg[3];
+  int nseg;
+  const float *x;
+  int n;
+  size_t ld;
+  Epilogue epi;
+};
+bool launch_f32_gemv(const F32GemvJob &job, hipStream_t stream);
+
+struct GemmSegmentDev {
+  float *c;
+  int ldc;
+  const void *w, *w3;   // int8 row-major (Q8), fp32 row-major (F32) or packed bf16 (BF16)
+  const float *ws, *w3s; // Q8 weight scales
+  size_t ldw;            // F32 only: weight row stride in floats
+  int n;
+  Epilogue epi;
+};
+struct GemmQ8Job {
+  const int8_t *xq;
+  const float *xs;
+  int m, k, gs;
+  GemmSegmentDev seg[3];
+  int nseg;
+};
+bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream);
+bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream);
+bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs, const int8_t *wq, int n,
+                          hipStream_t stream);
+
+struct GemmF32Job {
+  const float *a;
+  int lda, m, k;
+  GemmSegmentDev seg[3];
+  int nseg;
+  bool bf16; // BF16 mode: seg[].w are packed bf16 (pack_bf16_vnni layout), A is rounded to bf16 on the fly
+};
+bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream);
+
+} // namespace llhip

@@ -1,0 +1,553 @@
+// Batched-prefill GEMMs for gfx950 on MFMA: W8A8 Q8_0 on int8 MFMA, FP32 on FP32 MFMA, BF16 on BF16 MFMA.
+//
+// All three compute C[m][n] (op)= A[m][k] . W[n][k]^T over up to three segments that share A. A block owns a
+// 128 x 128 output tile (64 columns of W1 plus the same 64 of W3 for SWIGLU), four waves each own 64 x 64 as a 4 x 4
+// grid of 16 x 16 MFMA tiles, and K is staged through double-buffered LDS. MFMA operand loads are symmetric (lane l
+// supplies row l % 16 of A and column l % 16 of W with the same K slice), so the dot products do not depend on how the
+// instruction orders K inside a lane; the 16 x 16 result holds C[4 (l / 16) + e][l % 16] in element e of lane l.
+#include <vector>
+
+#include "common.h"
+
+namespace llhip {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kTile = 128; // block tile rows and columns
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float silu_gate(float value, float gate) {
+  value *= (1.0f / (1.0f + expf(-value)));
+  return value * gate;
+}
+
+struct TileSeg {
+  float *c;
+  int ldc;
+  const void *w, *w3;
+  const float *ws, *w3s;
+  long long ldw;
+  int n;
+  int epi;
+  int first_tile; // first logical tile of this segment
+  int ntiles;     // its column tiles
+};
+
+struct TileGrid {
+  TileSeg seg[3];
+  int nseg;
+  int mtiles;
+  int total;
+};
+
+// Blocks go to the eight XCDs round-robin (block b on XCD b % 8). Renumbering gives every XCD a contiguous run of
+// logical tiles, and logical tiles walk M fastest, so the blocks that share a weight tile meet in one XCD's L2.
+__device__ __forceinline__ int xcd_logical(int b, int total) {
+  const int q = total / 8, r = total % 8, xcd = b % 8, pos = b / 8;
+  return xcd < r ? xcd * (q + 1) + pos : r * (q + 1) + (xcd - r) * q + pos;
+}
+
+struct TilePos {
+  int s, m0, n0;
+  bool swiglu;
+};
+
+__device__ __forceinline__ TilePos tile_of(const TileGrid &g, int logical) {
+  int s = 0;
+  while (s + 1 < g.nseg && logical >= g.seg[s + 1].first_tile)
+    s++;
+  const int local = logical - g.seg[s].first_tile;
+  TilePos t;
+  t.s = s;
+  t.swiglu = g.seg[s].epi == EPI_SWIGLU;
+  t.m0 = (local % g.mtiles) * kTile;
+  t.n0 = (local / g.mtiles) * (t.swiglu ? kTile / 2 : kTile);
+  return t;
+}
+
+__device__ __forceinline__ TileSeg seg_of(const TileGrid &g, int s) { return s == 0 ? g.seg[0] : s == 1 ? g.seg[1] : g.seg[2]; }
+
+// Row r (0..127) of the block's B tile: which weight matrix and which output column it feeds.
+__device__ __forceinline__ int b_col(const TilePos &t, int r) { return t.swiglu ? t.n0 + (r & 63) : t.n0 + r; }
+
+// The B-tile row a wave's column tile j reads: waves split columns 64/64, or 32/32 of W1 and W3 under SWIGLU.
+__device__ __forceinline__ int b_row(bool swiglu, int wn, int j) {
+  return swiglu ? (j < 2 ? 32 * wn + 16 * j : 64 + 32 * wn + 16 * (j - 2)) : 64 * wn + 16 * j;
+}
+
+__device__ __forceinline__ void store_tile(const TileSeg &seg, const TilePos &t, const v4f (&acc)[4][4], int wm, int wn,
+                                           int lane, int m) {
+  const int lc = lane & 15, lr = (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int row = t.m0 + wm * 64 + 16 * i + lr + e;
+      if (row >= m)
+        continue;
+      float *crow = seg.c + (long long)row * seg.ldc;
+      if (t.swiglu) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const int col = t.n0 + 32 * wn + 16 * j + lc;
+          if (col < seg.n)
+            crow[col] = silu_gate(acc[i][j][e], acc[i][j + 2][e]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int col = t.n0 + 64 * wn + 16 * j + lc;
+          if (col >= seg.n)
+            continue;
+          if (seg.epi == EPI_ADD)
+            crow[col] += acc[i][j][e];
+          else
+            crow[col] = acc[i][j][e];
+        }
+      }
+    }
+}
+
+// ---- W8A8 Q8_0 on int8 MFMA -----------------------------------------------------------------------------------------
+
+constexpr int kQ8Pitch = 80; // LDS row pitch in bytes for 64 int8 values: 16-byte aligned, spreads rows over banks
+
+struct Q8Params {
+  TileGrid grid;
+  const int8_t *xq;
+  const float *xs;
+  int m, k, gs;
+  int32_t *probe; // optional (one segment, no SWIGLU): probe[(g * m + r) * n + c]
+};
+
+// One K step is 64 values, one v_mfma_i32_16x16x64_i8 per 16 x 16 tile. A group of gs values is gs / 64 steps whose
+// int32 results accumulate in the MFMA itself (exact: |dot| <= 64 * 127 * 127 * steps < 2^31); at the group's last
+// step every output adds ((float)dot * ws[n][g]) * xs[m][g] to its FP32 accumulator (src/gemv.c:428's expression).
+template <bool PROBE>
+__global__ __launch_bounds__(kBlock) void q8_gemm_mfma(Q8Params p) {
+  __shared__ __align__(16) int8_t sa[2][kTile * kQ8Pitch];
+  __shared__ __align__(16) int8_t sb[2][kTile * kQ8Pitch];
+  __shared__ float sscale[2][2 * kTile]; // [0, 128): xs of the tile rows, [128, 256): ws of the B rows
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  const TilePos t = tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
+  const TileSeg seg = seg_of(p.grid, t.s);
+  const int groups = p.k / p.gs, steps_per_group = p.gs / 64, steps = p.k / 64;
+  const int8_t *w1 = (const int8_t *)seg.w, *w3 = (const int8_t *)seg.w3;
+
+  // Global -> register staging: thread t moves 16-byte chunks t and t + 256 of each 128 x 64 tile.
+  int4 ra[2], rb[2];
+  float rs;
+  auto load = [&](int step) {
+    const int k0 = step * 64;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int chunk = tid + h * kBlock, r = chunk >> 2, c16 = (chunk & 3) * 16;
+      const int row = t.m0 + r;
+      ra[h] = row < p.m ? *reinterpret_cast<const int4 *>(p.xq + (long long)row * p.k + k0 + c16) : int4{0, 0, 0, 0};
+      const int col = b_col(t, r);
+      const int8_t *wsrc = (t.swiglu && r >= 64) ? w3 : w1;
+      rb[h] = col < seg.n ? *reinterpret_cast<const int4 *>(wsrc + (long long)col * p.k + k0 + c16) : int4{0, 0, 0, 0};
+    }
+    const int g = k0 / p.gs;
+    if (tid < kTile) {
+      const int row = t.m0 + tid;
+      rs = row < p.m ? p.xs[(long long)row * groups + g] : 0.0f;
+    } else {
+      const int r = tid - kTile, col = b_col(t, r);
+      const float *src = (t.swiglu && r >= 64) ? seg.w3s : seg.ws;
+      rs = col < seg.n ? src[(long long)col * groups + g] : 0.0f;
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int chunk = tid + h * kBlock, r = chunk >> 2, c16 = (chunk & 3) * 16;
+      *reinterpret_cast<int4 *>(&sa[buf][r * kQ8Pitch + c16]) = ra[h];
+      *reinterpret_cast<int4 *>(&sb[buf][r * kQ8Pitch + c16]) = rb[h];
+    }
+    sscale[buf][tid] = rs;
+  };
+
+  v4f acc[4][4];
+  v4i dot[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      dot[i][j] = v4i{0, 0, 0, 0};
+    }
+
+  load(0);
+  store(0);
+  __syncthreads();
+  const int lrow = lane & 15, lk = (lane >> 4) * 16;
+  for (int step = 0; step < steps; step++) {
+    const int buf = step & 1;
+    if (step + 1 < steps)
+      load(step + 1);
+    v4i a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      a[i] = *reinterpret_cast<const v4i *>(&sa[buf][(wm * 64 + 16 * i + lrow) * kQ8Pitch + lk]);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      b[j] = *reinterpret_cast<const v4i *>(&sb[buf][(b_row(t.swiglu, wn, j) + lrow) * kQ8Pitch + lk]);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], dot[i][j], 0, 0, 0);
+    if ((step + 1) % steps_per_group == 0) {
+      const int g = step / steps_per_group;
+      const int lr = (lane >> 4) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const v4f xsv = *reinterpret_cast<const v4f *>(&sscale[buf][wm * 64 + 16 * i + lr]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float wsc = sscale[buf][kTile + b_row(t.swiglu, wn, j) + lrow];
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            acc[i][j][e] += ((float)dot[i][j][e] * wsc) * xsv[e];
+          if (PROBE) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const int row = t.m0 + wm * 64 + 16 * i + lr + e, col = t.n0 + 64 * wn + 16 * j + lrow;
+              if (row < p.m && col < seg.n)
+                p.probe[((long long)g * p.m + row) * seg.n + col] = dot[i][j][e];
+            }
+          }
+          dot[i][j] = v4i{0, 0, 0, 0};
+        }
+      }
+    }
+    if (step + 1 < steps)
+      store(buf ^ 1);
+    __syncthreads();
+  }
+  store_tile(seg, t, acc, wm, wn, lane, p.m);
+}
+
+// Any group size (gs % 64 != 0): one thread per output, the per-group int32 dot in plain integer arithmetic.
+__global__ __launch_bounds__(kBlock) void q8_gemm_generic(TileGrid g, const int8_t *xq, const float *xs, int m, int k,
+                                                          int gs) {
+  long long idx = (long long)blockIdx.x * kBlock + threadIdx.x;
+  int s = 0;
+  long long base = 0;
+  for (; s < g.nseg; s++) {
+    const long long count = (long long)m * g.seg[s].n;
+    if (idx < base + count)
+      break;
+    base += count;
+  }
+  if (s >= g.nseg)
+    return;
+  const TileSeg seg = seg_of(g, s);
+  const long long local = idx - base;
+  const int row = (int)(local / seg.n), col = (int)(local % seg.n);
+  const int groups = k / gs;
+  auto dots = [&](const int8_t *w, const float *ws) {
+    const int8_t *x = xq + (long long)row * k, *wr = w + (long long)col * k;
+    float total = 0.0f;
+    for (int grp = 0; grp < groups; grp++) {
+      int d = 0;
+      for (int t = 0; t < gs; t++)
+        d += (int)x[grp * gs + t] * (int)wr[grp * gs + t];
+      total += ((float)d * ws[(long long)col * groups + grp]) * xs[(long long)row * groups + grp];
+    }
+    return total;
+  };
+  const float sum = dots((const int8_t *)seg.w, seg.ws);
+  float *o = seg.c + (long long)row * seg.ldc + col;
+  if (seg.epi == EPI_SWIGLU)
+    *o = silu_gate(sum, dots((const int8_t *)seg.w3, seg.w3s));
+  else if (seg.epi == EPI_ADD)
+    *o += sum;
+  else
+    *o = sum;
+}
+
+// ---- FP32 and BF16 on MFMA -----------------------------------------------------------------------------------------
+
+constexpr int kF32Slice = 16; // K values staged per step
+constexpr int kF32Pitch = 17; // floats per LDS row of a K slice, padded against bank conflicts
+constexpr int kBf16Pitch = 40; // bf16 values per LDS row of a 32-wide K slice (80 bytes)
+
+struct F32Params {
+  TileGrid grid;
+  const float *a;
+  long long lda;
+  int m, k;
+};
+
+// FP32: v_mfma_f32_16x16x4_f32, K staged 16 at a time; lane l supplies A[l % 16][k0 + l / 16] and the matching W value.
+__global__ __launch_bounds__(kBlock) void f32_gemm_mfma(F32Params p) {
+  __shared__ float sa[2][kTile * kF32Pitch];
+  __shared__ float sb[2][kTile * kF32Pitch];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  const TilePos t = tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
+  const TileSeg seg = seg_of(p.grid, t.s);
+  const float *w1 = (const float *)seg.w, *w3 = (const float *)seg.w3;
+  const int steps = (p.k + kF32Slice - 1) / kF32Slice;
+  float ra[8], rb[8];
+  // thread t moves rows (t / 16) + 16 h (h = 0..7) at column t % 16 of each 128 x 16 slice
+  auto load = [&](int step) {
+    const int kk = step * kF32Slice + (tid & 15);
+#pragma unroll
+    for (int h = 0; h < 8; h++) {
+      const int r = (tid >> 4) + 16 * h;
+      const int row = t.m0 + r;
+      ra[h] = (row < p.m && kk < p.k) ? p.a[(long long)row * p.lda + kk] : 0.0f;
+      const int wc = b_col(t, r);
+      const float *src = (t.swiglu && r >= 64) ? w3 : w1;
+      rb[h] = (wc < seg.n && kk < p.k) ? src[(long long)wc * seg.ldw + kk] : 0.0f;
+    }
+  };
+  auto store = [&](int buf) {
+    const int col = tid & 15;
+#pragma unroll
+    for (int h = 0; h < 8; h++) {
+      const int r = (tid >> 4) + 16 * h;
+      sa[buf][r * kF32Pitch + col] = ra[h];
+      sb[buf][r * kF32Pitch + col] = rb[h];
+    }
+  };
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  load(0);
+  store(0);
+  __syncthreads();
+  const int lrow = lane & 15, lk = lane >> 4;
+  for (int step = 0; step < steps; step++) {
+    const int buf = step & 1;
+    if (step + 1 < steps)
+      load(step + 1);
+#pragma unroll
+    for (int kk = 0; kk < kF32Slice; kk += 4) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        a[i] = sa[buf][(wm * 64 + 16 * i + lrow) * kF32Pitch + kk + lk];
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        b[j] = sb[buf][(b_row(t.swiglu, wn, j) + lrow) * kF32Pitch + kk + lk];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (step + 1 < steps)
+      store(buf ^ 1);
+    __syncthreads();
+  }
+  store_tile(seg, t, acc, wm, wn, lane, p.m);
+}
+
+// Round to nearest even on the 16 dropped bits, NaN quieted with its sign and top payload bits, denormals kept,
+// overflow to infinity: the conversion of the reference's bf16_from_f32 (src/gemm.c:335-342), as an integer formula.
+__device__ __forceinline__ unsigned short to_bf16(float x) {
+  unsigned u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u)
+    return (unsigned short)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (unsigned short)(u >> 16);
+}
+
+// BF16: activations rounded to BF16 while staged, weights read from the pack_bf16_vnni layout (16-row tiles, K pairs:
+// element ((tile * kp / 2 + pair) * 16 + row) * 2 + e), v_mfma_f32_16x16x32_bf16 per 16 x 16 tile and 32 values of K.
+__global__ __launch_bounds__(kBlock) void bf16_gemm_mfma(F32Params p) {
+  __shared__ __align__(16) unsigned short sa[2][kTile * kBf16Pitch];
+  __shared__ __align__(16) unsigned short sb[2][kTile * kBf16Pitch];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  const TilePos t = tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
+  const TileSeg seg = seg_of(p.grid, t.s);
+  const unsigned short *w1 = (const unsigned short *)seg.w, *w3 = (const unsigned short *)seg.w3;
+  const long long kp = (p.k + 31) / 32 * 32;
+  const int steps = (int)(kp / 32);
+  // Thread t stages row t / 2 of both tiles, K values (t % 2) * 16 .. + 15 of the slice: 16 activations rounded to
+  // BF16, and the weight row's 8 K pairs gathered from the packed layout.
+  float ra[16];
+  unsigned rbp[8]; // 8 pairs of bf16 for one weight row
+  auto load = [&](int step) {
+    const int k0 = step * 32;
+    const int r = tid >> 1, half = (tid & 1) * 16;
+    const int row = t.m0 + r;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const int kk = k0 + half + e;
+      ra[e] = (row < p.m && kk < p.k) ? p.a[(long long)row * p.lda + kk] : 0.0f;
+    }
+    const int wc = b_col(t, r);
+    const unsigned short *src = (t.swiglu && r >= 64) ? w3 : w1;
+    if (wc < seg.n) {
+      const long long tile = wc / 16, c = wc % 16;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const long long pair = (k0 + half) / 2 + q;
+        rbp[q] = *reinterpret_cast<const unsigned *>(src + ((tile * (kp / 2) + pair) * 16 + c) * 2);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        rbp[q] = 0u;
+    }
+  };
+  auto store = [&](int buf) {
+    const int r = tid >> 1, half = (tid & 1) * 16;
+    unsigned short *arow = &sa[buf][r * kBf16Pitch + half];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2)
+      *reinterpret_cast<unsigned *>(arow + e) = (unsigned)to_bf16(ra[e]) | ((unsigned)to_bf16(ra[e + 1]) << 16);
+    unsigned *brow = reinterpret_cast<unsigned *>(&sb[buf][r * kBf16Pitch + half]);
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+      brow[q] = rbp[q];
+  };
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  load(0);
+  store(0);
+  __syncthreads();
+  const int lrow = lane & 15, lk = (lane >> 4) * 8;
+  for (int step = 0; step < steps; step++) {
+    const int buf = step & 1;
+    if (step + 1 < steps)
+      load(step + 1);
+    v8bf a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      a[i] = *reinterpret_cast<const v8bf *>(&sa[buf][(wm * 64 + 16 * i + lrow) * kBf16Pitch + lk]);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      b[j] = *reinterpret_cast<const v8bf *>(&sb[buf][(b_row(t.swiglu, wn, j) + lrow) * kBf16Pitch + lk]);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    if (step + 1 < steps)
+      store(buf ^ 1);
+    __syncthreads();
+  }
+  store_tile(seg, t, acc, wm, wn, lane, p.m);
+}
+
+bool launch_ok(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess)
+    return true;
+  return raise("launching %s failed: %s", what, hipGetErrorString(e));
+}
+
+TileGrid make_grid(const GemmSegmentDev *segs, int nseg, int m) {
+  TileGrid g{};
+  g.nseg = nseg;
+  g.mtiles = (m + kTile - 1) / kTile;
+  int tiles = 0;
+  for (int s = 0; s < nseg; s++) {
+    const GemmSegmentDev &d = segs[s];
+    const int width = d.epi == EPI_SWIGLU ? kTile / 2 : kTile;
+    g.seg[s] = TileSeg{d.c, d.ldc, d.w, d.w3, d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width};
+    tiles += g.seg[s].ntiles * g.mtiles;
+  }
+  g.total = tiles;
+  return g;
+}
+
+} // namespace
+
+bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream) {
+  if (job.m <= 0 || job.k <= 0)
+    return true;
+  Q8Params p{};
+  p.grid = make_grid(job.seg, job.nseg, job.m);
+  p.xq = job.xq;
+  p.xs = job.xs;
+  p.m = job.m;
+  p.k = job.k;
+  p.gs = job.gs;
+  if (p.grid.total <= 0)
+    return true;
+  hipLaunchKernelGGL(q8_gemm_mfma<false>, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
+  return launch_ok("q8_gemm_mfma");
+}
+
+bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream) {
+  if (job.m <= 0 || job.k <= 0)
+    return true;
+  TileGrid g = make_grid(job.seg, job.nseg, job.m);
+  long long outputs = 0;
+  for (int s = 0; s < job.nseg; s++)
+    outputs += (long long)job.m * job.seg[s].n;
+  if (!outputs)
+    return true;
+  hipLaunchKernelGGL(q8_gemm_generic, dim3((unsigned)((outputs + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream, g,
+                     job.xq, job.xs, job.m, job.k, job.gs);
+  return launch_ok("q8_gemm_generic");
+}
+
+bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs, const int8_t *wq, int n,
+                          hipStream_t stream) {
+  if (m <= 0 || n <= 0 || k <= 0)
+    return true;
+  // The same kernel as k_gemm_q8 with unit scales, a scratch output and the probe on.
+  float *scratch = nullptr, *ones = nullptr;
+  const int groups = k / gs;
+  const size_t ones_count = (size_t)(m > n ? m : n) * groups;
+  if (!LLHIP_CHECK(hipMallocAsync((void **)&scratch, (size_t)m * n * sizeof(float), stream)) ||
+      !LLHIP_CHECK(hipMallocAsync((void **)&ones, ones_count * sizeof(float), stream)))
+    return false;
+  std::vector<float> host_ones(ones_count, 1.0f);
+  if (!LLHIP_CHECK(hipMemcpyAsync(ones, host_ones.data(), ones_count * sizeof(float), hipMemcpyHostToDevice, stream)) ||
+      !LLHIP_CHECK(hipStreamSynchronize(stream)))
+    return false;
+  GemmSegmentDev seg{scratch, n, wq, nullptr, ones, nullptr, (size_t)k, n, EPI_STORE};
+  Q8Params p{};
+  p.grid = make_grid(&seg, 1, m);
+  p.xq = xq;
+  p.xs = ones;
+  p.m = m;
+  p.k = k;
+  p.gs = gs;
+  p.probe = dots;
+  hipLaunchKernelGGL(q8_gemm_mfma<true>, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
+  bool ok = launch_ok("q8_gemm_mfma (probe)");
+  (void)hipFreeAsync(scratch, stream);
+  (void)hipFreeAsync(ones, stream);
+  return ok;
+}
+
+bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream) {
+  if (job.m <= 0 || job.k <= 0)
+    return true;
+  F32Params p{};
+  p.grid = make_grid(job.seg, job.nseg, job.m);
+  p.a = job.a;
+  p.lda = job.lda;
+  p.m = job.m;
+  p.k = job.k;
+  if (p.grid.total <= 0)
+    return true;
+  if (job.bf16) {
+    hipLaunchKernelGGL(bf16_gemm_mfma, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
+    return launch_ok("bf16_gemm_mfma");
+  }
+  hipLaunchKernelGGL(f32_gemm_mfma, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
+  return launch_ok("f32_gemm_mfma");
+}
+
+} // namespace llhip

@@ -1,0 +1,451 @@
+// Device state, failure handling, the host-range registry, host staging, copies and graph capture.
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+
+#include "common.h"
+
+namespace llhip {
+
+// ---- failure ----------------------------------------------------------------------------------------------------
+
+namespace {
+std::mutex fail_mutex;
+LlhipFailFn fail_handler = nullptr;
+int fail_mode = LLHIP_FAIL_EXIT;
+char last_error[512] = "";
+} // namespace
+
+bool raise(const char *format, ...) {
+  char message[512];
+  va_list args;
+  va_start(args, format);
+  vsnprintf(message, sizeof(message), format, args);
+  va_end(args);
+  std::lock_guard<std::mutex> lock(fail_mutex);
+  snprintf(last_error, sizeof(last_error), "%s", message);
+  if (fail_mode == LLHIP_FAIL_RECORD)
+    return false;
+  if (fail_handler)
+    fail_handler(message);
+  fprintf(stderr, "error: %s\n", message);
+  fflush(stderr);
+  exit(EXIT_FAILURE);
+}
+
+bool check_hip(hipError_t status, const char *what) {
+  if (status == hipSuccess)
+    return true;
+  return raise("HIP call %s failed: %s", what, hipGetErrorString(status));
+}
+
+// ---- device -------------------------------------------------------------------------------------------------------
+
+namespace {
+std::mutex device_mutex;
+Device the_device;
+char device_name[256] = "";
+} // namespace
+
+Device &device() { return the_device; }
+
+bool ensure_device() {
+  if (the_device.ready)
+    return true;
+  std::lock_guard<std::mutex> lock(device_mutex);
+  if (the_device.ready)
+    return true;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count < 1) {
+    (void)hipGetLastError();
+    return raise("no HIP device is available (this library runs the matmul hot path on an MI355X)");
+  }
+  int ordinal = 0;
+  if (const char *env = getenv("LLAMA_HIP_DEVICE"); env && *env) {
+    char *end;
+    long value = strtol(env, &end, 10);
+    if (*end || value < 0 || value >= count)
+      return raise("LLAMA_HIP_DEVICE must be an integer in 0..%d", count - 1);
+    ordinal = (int)value;
+  }
+  if (!LLHIP_CHECK(hipSetDevice(ordinal)))
+    return false;
+  hipDeviceProp_t props;
+  if (!LLHIP_CHECK(hipGetDeviceProperties(&props, ordinal)))
+    return false;
+  if (strncmp(props.gcnArchName, "gfx950", 6) != 0)
+    return raise("device %d is %s; this library is built for gfx950 (MI355X)", ordinal, props.gcnArchName);
+  snprintf(device_name, sizeof(device_name), "%s%s%s, %d CUs", props.name, props.name[0] ? " " : "",
+           props.gcnArchName, props.multiProcessorCount);
+  hipStream_t stream;
+  if (!LLHIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking)))
+    return false;
+  int *flags;
+  if (!LLHIP_CHECK(hipMalloc(&flags, 64)))
+    return false;
+  int zero[16] = {0};
+  if (!LLHIP_CHECK(hipMemcpy(flags, zero, sizeof(zero), hipMemcpyHostToDevice)))
+    return false;
+  the_device.ordinal = ordinal;
+  the_device.stream = stream;
+  the_device.error_flags = flags;
+  the_device.cu_count = props.multiProcessorCount;
+  the_device.ready = true;
+  return true;
+}
+
+bool synchronize_and_check() {
+  if (!ensure_device())
+    return false;
+  Device &dev = the_device;
+  if (dev.capturing)
+    return raise("a host-visible wait was requested during graph capture");
+  if (!LLHIP_CHECK(hipStreamSynchronize(dev.stream)))
+    return false;
+  int flags[16];
+  if (!LLHIP_CHECK(hipMemcpy(flags, dev.error_flags, sizeof(flags), hipMemcpyDeviceToHost)))
+    return false;
+  if (flags[0]) {
+    int zero[16] = {0};
+    (void)hipMemcpy(dev.error_flags, zero, sizeof(zero), hipMemcpyHostToDevice);
+    return raise("nonfinite activation during INT8 quantization");
+  }
+  return true;
+}
+
+// ---- registry of uploaded host ranges ----------------------------------------------------------------------------
+
+namespace {
+struct Region {
+  size_t bytes;
+  void *device;
+};
+std::mutex registry_mutex;
+std::map<uintptr_t, Region> registry;
+
+// The device copy of p when p lies inside a registered range, else nullptr; *room receives the bytes of the range
+// from p to its end.
+void *lookup(const void *p, size_t *room = nullptr) {
+  std::lock_guard<std::mutex> lock(registry_mutex);
+  if (registry.empty())
+    return nullptr;
+  uintptr_t addr = (uintptr_t)p;
+  auto it = registry.upper_bound(addr);
+  if (it == registry.begin())
+    return nullptr;
+  --it;
+  if (addr >= it->first + it->second.bytes)
+    return nullptr;
+  if (room)
+    *room = it->first + it->second.bytes - addr;
+  return (char *)it->second.device + (addr - it->first);
+}
+
+// 1: device memory with at least `bytes` from p to the end of its allocation; -1: device memory that is shorter
+// (the launch would read or write past it); 0: not device memory.
+int device_extent(const void *p, size_t bytes) {
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (attr.type != hipMemoryTypeDevice)
+    return 0;
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
+    (void)hipGetLastError();
+    return 1; // device memory whose extent the runtime cannot tell: trusted, like any C caller's buffer
+  }
+  return (uintptr_t)p + bytes <= (uintptr_t)base + size ? 1 : -1;
+}
+
+// The staging arena for host buffers: grown on demand, reused by every staged call.
+void *arena = nullptr;
+size_t arena_bytes = 0;
+std::mutex arena_mutex;
+} // namespace
+
+// ---- Call ---------------------------------------------------------------------------------------------------------
+
+Call::Call(const char *name) : name_(name) {
+  if (!ensure_device())
+    failed_ = true;
+}
+
+Call::~Call() {
+  if (staged_)
+    arena_mutex.unlock();
+}
+
+hipStream_t Call::stream() const { return the_device.stream; }
+
+Ref Call::stage(void *host, size_t row_bytes, size_t pitch, size_t rows, bool to_device, bool to_host) {
+  if (ncopies_ == (int)(sizeof(copies_) / sizeof(copies_[0]))) {
+    failed_ = true;
+    raise("%s: too many host buffers in one call", name_);
+    return Ref{};
+  }
+  if (the_device.capturing) {
+    failed_ = true;
+    raise("%s: host memory cannot be staged during graph capture (register it or pass device memory)", name_);
+    return Ref{};
+  }
+  if (!staged_) {
+    arena_mutex.lock(); // one staged call at a time: they share the arena
+    staged_ = true;
+  }
+  size_t bytes = rows ? (rows - 1) * pitch + row_bytes : 0;
+  size_t offset = (arena_used_ + 255) & ~(size_t)255;
+  arena_used_ = offset + bytes;
+  copies_[ncopies_] = Copy{host, offset, row_bytes, pitch, rows, to_device, to_host};
+  return Ref{nullptr, ncopies_++};
+}
+
+void *Call::address(const Ref &r) const {
+  return r.staged < 0 ? r.direct : (void *)((char *)arena + copies_[r.staged].offset);
+}
+
+Ref Call::in2d(const void *p, size_t row_bytes, size_t pitch, size_t rows) {
+  if (!p || failed_ || !rows)
+    return Ref{const_cast<void *>(p), -1};
+  const size_t extent = (rows - 1) * pitch + row_bytes;
+  size_t room = 0;
+  if (void *dev = lookup(p, &room)) {
+    if (room < extent) {
+      failed_ = true;
+      raise("%s: %zu bytes at %p run past the end of their registered range", name_, extent, p);
+      return Ref{};
+    }
+    return Ref{dev, -1};
+  }
+  const int where = device_extent(p, extent);
+  if (where < 0) {
+    failed_ = true;
+    raise("%s: %zu bytes at device address %p run past the end of its allocation", name_, extent, p);
+    return Ref{};
+  }
+  if (where > 0)
+    return Ref{const_cast<void *>(p), -1};
+  return stage(const_cast<void *>(p), row_bytes, pitch, rows, true, false);
+}
+
+Ref Call::out2d(void *p, size_t row_bytes, size_t pitch, size_t rows, bool read_too) {
+  if (!p || failed_ || !rows)
+    return Ref{p, -1};
+  if (lookup(p)) {
+    failed_ = true;
+    raise("%s: an output lies inside a registered (read-only) weight range", name_);
+    return Ref{};
+  }
+  const size_t extent = (rows - 1) * pitch + row_bytes;
+  const int where = device_extent(p, extent);
+  if (where < 0) {
+    failed_ = true;
+    raise("%s: %zu bytes at device address %p run past the end of its allocation", name_, extent, p);
+    return Ref{};
+  }
+  if (where > 0)
+    return Ref{p, -1};
+  return stage(p, row_bytes, pitch, rows, read_too, true);
+}
+
+bool Call::ready() {
+  if (failed_)
+    return false;
+  if (!staged_)
+    return true;
+  if (arena_used_ > arena_bytes) {
+    if (arena) {
+      (void)hipStreamSynchronize(the_device.stream);
+      (void)hipFree(arena);
+    }
+    arena = nullptr;
+    arena_bytes = 0;
+    size_t want = arena_used_ + (arena_used_ >> 2) + 4096;
+    if (!LLHIP_CHECK(hipMalloc(&arena, want))) {
+      arena = nullptr;
+      failed_ = true;
+      return false;
+    }
+    arena_bytes = want;
+  }
+  for (int i = 0; i < ncopies_; i++) {
+    Copy &c = copies_[i];
+    if (!c.to_device || !c.rows)
+      continue;
+    if (!LLHIP_CHECK(hipMemcpy2DAsync((char *)arena + c.offset, c.pitch, c.host, c.pitch, c.row_bytes, c.rows,
+                                      hipMemcpyHostToDevice, the_device.stream))) {
+      failed_ = true;
+      return false;
+    }
+  }
+  return true;
+}
+
+bool Call::finish() {
+  if (failed_)
+    return false;
+  if (!staged_)
+    return true;
+  for (int i = 0; i < ncopies_; i++) {
+    Copy &c = copies_[i];
+    if (!c.to_host || !c.rows)
+      continue;
+    if (!LLHIP_CHECK(hipMemcpy2DAsync(c.host, c.pitch, (char *)arena + c.offset, c.pitch, c.row_bytes, c.rows,
+                                      hipMemcpyDeviceToHost, the_device.stream)))
+      return false;
+  }
+  return synchronize_and_check();
+}
+
+} // namespace llhip
+
+// ---- C ABI: device and residency ----------------------------------------------------------------------------------
+
+using namespace llhip;
+
+extern "C" {
+
+int llhip_init(void) { return ensure_device() ? 0 : -1; }
+
+const char *llhip_device_name(void) { return ensure_device() ? device_name : ""; }
+
+int llhip_device_cu_count(void) { return ensure_device() ? the_device.cu_count : 0; }
+
+void *llhip_stream(void) { return ensure_device() ? (void *)the_device.stream : nullptr; }
+
+void llhip_synchronize(void) { (void)synchronize_and_check(); }
+
+int llhip_register_host(const void *host, size_t bytes) {
+  if (!ensure_device())
+    return -1;
+  if (!host || !bytes)
+    return raise("llhip_register_host: empty range"), -1;
+  {
+    std::lock_guard<std::mutex> lock(registry_mutex);
+    uintptr_t a = (uintptr_t)host;
+    for (auto &kv : registry)
+      if (a < kv.first + kv.second.bytes && kv.first < a + bytes)
+        return raise("llhip_register_host: range overlaps a registered range"), -1;
+  }
+  void *dev;
+  if (!LLHIP_CHECK(hipMalloc(&dev, bytes)))
+    return -1;
+  if (!LLHIP_CHECK(hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice))) {
+    (void)hipFree(dev);
+    return -1;
+  }
+  std::lock_guard<std::mutex> lock(registry_mutex);
+  registry[(uintptr_t)host] = Region{bytes, dev};
+  return 0;
+}
+
+int llhip_unregister_host(const void *host) {
+  if (!ensure_device())
+    return -1;
+  void *dev = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(registry_mutex);
+    auto it = registry.find((uintptr_t)host);
+    if (it == registry.end())
+      return raise("llhip_unregister_host: %p is not the start of a registered range", host), -1;
+    dev = it->second.device;
+    registry.erase(it);
+  }
+  if (!LLHIP_CHECK(hipStreamSynchronize(the_device.stream)))
+    return -1;
+  return LLHIP_CHECK(hipFree(dev)) ? 0 : -1;
+}
+
+void *llhip_resolve(const void *host) { return lookup(host); }
+
+void *llhip_malloc(size_t bytes) {
+  if (!ensure_device())
+    return nullptr;
+  void *p = nullptr;
+  if (!LLHIP_CHECK(hipMalloc(&p, bytes ? bytes : 1)))
+    return nullptr;
+  return p;
+}
+
+void llhip_free(void *p) {
+  if (!p || !ensure_device())
+    return;
+  if (LLHIP_CHECK(hipStreamSynchronize(the_device.stream)))
+    (void)LLHIP_CHECK(hipFree(p));
+}
+
+void llhip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+  if (ensure_device() && bytes && LLHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, the_device.stream)))
+    (void)LLHIP_CHECK(hipStreamSynchronize(the_device.stream));
+}
+
+void llhip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+  if (ensure_device() && bytes && LLHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, the_device.stream)))
+    (void)LLHIP_CHECK(hipStreamSynchronize(the_device.stream));
+}
+
+void llhip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+  if (ensure_device() && bytes)
+    (void)LLHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, the_device.stream));
+}
+
+int llhip_graph_begin(void) {
+  if (!ensure_device())
+    return -1;
+  if (the_device.capturing)
+    return raise("llhip_graph_begin: a capture is already open"), -1;
+  if (!LLHIP_CHECK(hipStreamBeginCapture(the_device.stream, hipStreamCaptureModeThreadLocal)))
+    return -1;
+  the_device.capturing = true;
+  return 0;
+}
+
+void *llhip_graph_end(void) {
+  if (!ensure_device() || !the_device.capturing) {
+    raise("llhip_graph_end: no capture is open");
+    return nullptr;
+  }
+  the_device.capturing = false;
+  hipGraph_t graph;
+  if (!LLHIP_CHECK(hipStreamEndCapture(the_device.stream, &graph)))
+    return nullptr;
+  hipGraphExec_t exec;
+  bool ok = LLHIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+  (void)hipGraphDestroy(graph);
+  return ok ? (void *)exec : nullptr;
+}
+
+int llhip_graph_launch(void *graph) {
+  if (!ensure_device() || !graph)
+    return -1;
+  return LLHIP_CHECK(hipGraphLaunch((hipGraphExec_t)graph, the_device.stream)) ? 0 : -1;
+}
+
+void llhip_graph_destroy(void *graph) {
+  if (graph && ensure_device() && LLHIP_CHECK(hipStreamSynchronize(the_device.stream)))
+    (void)hipGraphExecDestroy((hipGraphExec_t)graph);
+}
+
+void llhip_set_fail_handler(LlhipFailFn handler) {
+  std::lock_guard<std::mutex> lock(fail_mutex);
+  fail_handler = handler;
+}
+
+void llhip_set_fail_mode(int mode) {
+  std::lock_guard<std::mutex> lock(fail_mutex);
+  fail_mode = mode == LLHIP_FAIL_RECORD ? LLHIP_FAIL_RECORD : LLHIP_FAIL_EXIT;
+}
+
+const char *llhip_last_error(void) { return last_error; }
+
+void llhip_clear_error(void) {
+  std::lock_guard<std::mutex> lock(fail_mutex);
+  last_error[0] = '\0';
+}
+
+} // extern "C"

@@ -1,0 +1,385 @@
+"""GPU parity of the Q8_0 hot path through the C ABI: quantizer, decode GEMV, batched GEMM, int32 probes.
+
+The oracle (oracle/, pinned to the reference by tests/test_oracle.py) is the checker. The bar: int8 activations, their
+scales and the int32 group dots are bitwise the oracle's; FP32 outputs lie within the reference's budget
+2e-5 * sum|w x| + 1e-6 of the float64 dequantized reference (tests/q8.c:128-133), which also bounds the difference to
+the reference's own scalar results; the floored relative error d / (|ref| + 1e-3) (tests/q8_engine.c:71) is checked
+against the north-star tolerance 1e-4.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import llama_hip as lh
+from oracle import pyoracle as orc
+from tests import hip_util as hu
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    L = hu.lib()
+    assert L.llhip_init() == 0, hu.lh.last_error()
+    print("device:", L.llhip_device_name().decode(), flush=True)
+    yield L
+
+
+def synth_weights(rng, d, n, gs, std=0.02):
+    return orc.quantize_weights(rng.normal(d * n, 0.0, std).reshape(d, n), gs)
+
+
+# ---- quantizer -----------------------------------------------------------------------------------------------------
+
+
+def test_quantize_golden_bitwise_device_and_host():
+    g = np.load(os.path.join(GOLDEN, "quantize.npz"))
+    L = hu.lib()
+    names = sorted({k.split("/")[0] for k in g.files})
+    for name in names:
+        x, gs = g[f"{name}/x"], int(g[f"{name}/gs"])
+        n = x.shape[0]
+        want_q, want_s = g[f"{name}/q"], g[f"{name}/s"]
+        # device-resident buffers
+        xd, qd, sd = hu.dev(x), hu.empty(n, hu.torch().int8), hu.empty(n // gs, hu.torch().float32)
+        L.k_quantize(lh.ptr(qd), lh.ptr(sd), lh.ptr(xd), n, gs)
+        assert np.array_equal(hu.host(qd), want_q), name
+        assert np.array_equal(hu.bits(hu.host(sd)), hu.bits(want_s)), name
+        # host buffers (staged through the device)
+        q, s = np.zeros(n, np.int8), np.zeros(n // gs, np.float32)
+        L.k_quantize(lh.ptr(q), lh.ptr(s), lh.ptr(x), n, gs)
+        assert np.array_equal(q, want_q) and np.array_equal(hu.bits(s), hu.bits(want_s)), name
+
+
+@pytest.mark.parametrize("m,n,gs,ldx", [(1, 4096, 64, 4096), (7, 14336, 64, 14400), (33, 2048, 128, 2048),
+                                        (5, 768, 32, 800), (3, 96, 2, 96), (4, 200, 8, 203), (2, 1024, 1024, 1024)])
+def test_quantize_rows_bitwise(m, n, gs, ldx):
+    rng = orc.Rng(orc.SEED + 11 * m + n)
+    x = rng.normal(m * ldx, 0.0, 1.5).reshape(m, ldx)
+    x[0, :gs] = 0.0  # an all-zero group
+    want_q, want_s = orc.quantize(np.ascontiguousarray(x[:, :n]), gs)
+    L = hu.lib()
+    xd = hu.dev(x)
+    qd, sd = hu.empty((m, n), hu.torch().int8), hu.empty((m, n // gs), hu.torch().float32)
+    L.k_quantize_rows(lh.ptr(qd), lh.ptr(sd), lh.ptr(xd), ldx, m, n, gs)
+    assert np.array_equal(hu.host(qd), want_q)
+    assert np.array_equal(hu.bits(hu.host(sd)), hu.bits(want_s))
+
+
+def test_quantize_nonfinite_fails_at_the_next_host_visible_point():
+    L = hu.lib()
+    lh.record_failures()
+    try:
+        x = np.ones(256, np.float32)
+        x[100] = np.nan
+        q, s = np.zeros(256, np.int8), np.zeros(4, np.float32)
+        L.k_quantize(lh.ptr(q), lh.ptr(s), lh.ptr(x), 256, 64)  # host buffers: the call itself waits and fails
+        assert "nonfinite activation during INT8 quantization" in lh.last_error()
+        L.llhip_clear_error()
+        x[100] = np.inf
+        xd, qd, sd = hu.dev(x), hu.empty(256, hu.torch().int8), hu.empty(4, hu.torch().float32)
+        L.k_quantize(lh.ptr(qd), lh.ptr(sd), lh.ptr(xd), 256, 64)  # device buffers: reported by the next wait
+        L.llhip_synchronize()
+        assert "nonfinite activation during INT8 quantization" in lh.last_error()
+        L.llhip_clear_error()
+        L.llhip_synchronize()  # the flag was consumed
+        assert lh.last_error() == ""
+    finally:
+        L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+        L.llhip_clear_error()
+
+
+# ---- decode GEMV ---------------------------------------------------------------------------------------------------
+
+
+def c1_inputs():
+    rng = orc.Rng()
+    wq, ws = synth_weights(rng, 2048, 2048, 64)
+    x = rng.normal(2048, 0.0, 1.0)
+    xq, xs = orc.quantize(x, 64)
+    return wq, ws, x, xq, xs
+
+
+def test_c1_gemv_parity_and_probe():
+    """C1: the 1B wq GEMV (2048 x 2048, gs 64): outputs within budget of the float64 reference and of the reference's
+    own scalar output (golden), int32 group dots bitwise."""
+    L = hu.lib()
+    wq, ws, x, xq, xs = c1_inputs()
+    golden = np.load(os.path.join(GOLDEN, "gemv_q8.npz"))["c1/y"]
+    want = orc.matmul_q8(xq, xs, wq, ws, 64)
+    assert np.array_equal(hu.bits(want), hu.bits(golden))  # the oracle is the reference here, bit for bit
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, 64)
+    wqd, wsd, xqd, xsd = hu.dev(wq), hu.dev(ws), hu.dev(xq), hu.dev(xs)
+    out = hu.empty(2048, hu.torch().float32)
+    L.k_matmul_q8(lh.ptr(out), lh.k8(xqd, xsd, None), lh.w8(wqd, wsd), 2048, 2048, 64)
+    got = hu.host(out)
+    hu.assert_within_budget(got, ref, mag, what="C1 vs float64")
+    hu.assert_within_budget(got, golden, mag, rel=4e-5, what="C1 vs reference scalar")
+    assert hu.max_rel_error(got, ref) < 1e-4
+    dots = np.zeros((32, 2048), np.int32)
+    L.llhip_q8_gemv_group_dots(lh.ptr(dots), lh.ptr(xqd), lh.ptr(xsd), lh.ptr(wqd), lh.ptr(wsd), 0, 2048, 2048, 64)
+    want_dots = orc.group_dots(xq.reshape(1, -1), wq, 64)[:, 0, :]
+    assert np.array_equal(dots, want_dots)
+
+
+@pytest.mark.parametrize("d,n,gs", [(4096, 4096, 64), (1024, 14336, 64), (333, 4096, 128), (77, 2048, 32),
+                                    (64, 1088, 64), (5, 256, 16), (9, 64, 4), (3, 12, 2), (17, 320, 64)])
+def test_gemv_shapes_budget_and_probe(d, n, gs):
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + d * 7 + n)
+    wq, ws = synth_weights(rng, d, n, gs)
+    x = rng.normal(n, 0.0, 1.0)
+    xq, xs = orc.quantize(x, gs)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    out = hu.empty(d, hu.torch().float32)
+    dxq, dxs, dwq, dws = hu.dev(xq), hu.dev(xs), hu.dev(wq), hu.dev(ws)  # held: the call only sees their addresses
+    L.k_matmul_q8(lh.ptr(out), lh.k8(dxq, dxs), lh.w8(dwq, dws), n, d, gs)
+    hu.assert_within_budget(hu.host(out), ref, mag, what=f"gemv {d}x{n} gs {gs}")
+    dots = np.zeros((n // gs, d), np.int32)
+    L.llhip_q8_gemv_group_dots(lh.ptr(dots), lh.ptr(xq), lh.ptr(xs), lh.ptr(wq), lh.ptr(ws), 0, n, d, gs)
+    assert np.array_equal(dots, orc.group_dots(xq.reshape(1, -1), wq, gs)[:, 0, :])
+
+
+def test_gemv_entry_points_against_reference_golden():
+    """Every GEMV entry point, W8A8 and W8A32, on the reference's own golden small cases (host buffers)."""
+    g = np.load(os.path.join(GOLDEN, "gemv_q8.npz"))
+    L = hu.lib()
+    keys = sorted({k.split("/")[0] for k in g.files if k.endswith("/gs")})
+    for key in keys:
+        gs, x, base = int(g[f"{key}/gs"]), g[f"{key}/x"], g[f"{key}/base"]
+        n, d = x.shape[0], base.shape[0]
+        w = [(g[f"{key}/wq{j}"], g[f"{key}/ws{j}"]) for j in range(3)]
+        xq, xs = orc.quantize(x, gs)
+        for mode in ("w8a8", "w8a32"):
+            inp = lh.k8(xq, xs, x) if mode == "w8a8" else lh.k8(None, None, x)
+            aq, as_ = (xq, xs) if mode == "w8a8" else (None, None)
+            ref = [hu.dequant_reference(xq, xs, q, s, gs) for q, s in w] if mode == "w8a8" else None
+            for kname in ("store", "add", "swiglu", "qkv"):
+                want = g[f"{key}/{mode}/{kname}"]
+                if kname == "qkv":
+                    y = [base.copy(), np.zeros(d, np.float32), np.zeros(d, np.float32)]
+                    L.k_matmul_q8_qkv(lh.ptr(y[0]), lh.ptr(y[1]), lh.ptr(y[2]), inp, lh.w8(*w[0]), lh.w8(*w[1]),
+                                      lh.w8(*w[2]), n, d, d, gs)
+                    got = np.concatenate(y)
+                else:
+                    got = base.copy()
+                    if kname == "store":
+                        L.k_matmul_q8(lh.ptr(got), inp, lh.w8(*w[0]), n, d, gs)
+                    elif kname == "add":
+                        L.k_matmul_q8_add(lh.ptr(got), inp, lh.w8(*w[0]), n, d, gs)
+                    else:
+                        L.k_matmul_q8_swiglu(lh.ptr(got), inp, lh.w8(*w[0]), lh.w8(*w[1]), n, d, gs)
+                oracle = _oracle_gemv(kname, aq, as_, x, w, gs, base)
+                np.testing.assert_allclose(oracle, want, rtol=0, atol=0)  # the oracle is bitwise the reference
+                if ref is not None and kname in ("store", "add"):
+                    r, mag = ref[0]
+                    r = r + (base if kname == "add" else 0)
+                    hu.assert_within_budget(got, r, mag + (np.abs(base) if kname == "add" else 0),
+                                            what=f"{key} {mode} {kname}")
+                else:
+                    scale = np.maximum(np.abs(want), 1.0)
+                    assert np.all(np.abs(got - want) <= 1e-4 * scale), (key, mode, kname, got, want)
+
+
+def _oracle_gemv(kname, aq, as_, x, w, gs, base):
+    if kname == "qkv":
+        return np.concatenate([orc.matmul_q8(aq, as_, w[0][0], w[0][1], gs, xf=x, out=base.copy()),
+                               orc.matmul_q8(aq, as_, w[1][0], w[1][1], gs, xf=x),
+                               orc.matmul_q8(aq, as_, w[2][0], w[2][1], gs, xf=x)])
+    kind = {"store": orc.K_STORE, "add": orc.K_ADD, "swiglu": orc.K_SWIGLU}[kname]
+    return orc.matmul_q8(aq, as_, w[0][0], w[0][1], gs, kind, out=base.copy(), w3q=w[1][0], w3s=w[1][1], xf=x)
+
+
+def test_gemv_ld_and_worker_forms():
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 404)
+    d, n, ld, gs = 50, 512, 640, 64
+    wq, ws = synth_weights(rng, d, ld, gs)
+    xq, xs = orc.quantize(rng.normal(n, 0.0, 1.0), gs)
+    ref, mag = hu.dequant_reference(xq, xs, wq[:, :n], ws[:, : n // gs], gs)
+    base = rng.uniform(d, 2.0)
+    for kind in (lh.K_STORE, lh.K_PARTIAL, lh.K_ADD):
+        out = base.copy()
+        wv = lh.w8(wq, ws)
+        L.k_matmul_q8_ld(lh.ptr(out), lh.k8(xq, xs), wv, ld, n, d, gs, kind)
+        want = ref + (base if kind == lh.K_ADD else 0)
+        hu.assert_within_budget(out, want, mag + np.abs(base), what=f"_ld kind {kind}")
+    # the worker form: the union of the members' static shares is the whole result; done() sees each share
+    seen = []
+    cb = lh.RowsDoneFn(lambda ctx, r0, r1: seen.append((r0, r1)))
+    out = np.zeros(d, np.float32)
+    for worker in range(3):
+        L.k_matmul_q8_ld_worker(lh.ptr(out), lh.k8(xq, xs), lh.w8(wq, ws), ld, n, d, gs, lh.K_STORE, worker, 3, None,
+                                cb, None)
+    hu.assert_within_budget(out, ref, mag, what="_ld_worker union")
+    assert seen == [(0, 16), (16, 33), (33, 50)]
+    # the SwiGLU shard form
+    w3q, w3s = synth_weights(rng, d, ld, gs)
+    r3, _ = hu.dequant_reference(xq, xs, w3q[:, :n], w3s[:, : n // gs], gs)
+    out = np.zeros(d, np.float32)
+    L.k_matmul_q8_swiglu_ld(lh.ptr(out), lh.k8(xq, xs), lh.w8(wq, ws), lh.w8(w3q, w3s), ld, n, d, gs)
+    want = ref / (1 + np.exp(-ref)) * r3
+    np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-5)
+
+
+def test_gemv_qkv_device_resident_and_graph_replay():
+    """The three-segment QKV launch on device buffers, captured into a graph and replayed with eager work between
+    the replays; every replay equals the eager result bitwise."""
+    L = hu.lib()
+    T = hu.torch()
+    rng = orc.Rng(orc.SEED + 505)
+    n, dq, dkv, gs = 2048, 2048, 512, 64
+    ws_ = [synth_weights(rng, d, n, gs) for d in (dq, dkv, dkv)]
+    x = rng.normal(n, 0.0, 1.0)
+    xd = hu.dev(x)
+    xqd, xsd = hu.empty(n, T.int8), hu.empty(n // gs, T.float32)
+    wdev = [(hu.dev(q), hu.dev(s)) for q, s in ws_]
+    outs = [hu.empty(d, T.float32) for d in (dq, dkv, dkv)]
+
+    def step():
+        L.k_quantize(lh.ptr(xqd), lh.ptr(xsd), lh.ptr(xd), n, gs)
+        L.k_matmul_q8_qkv(lh.ptr(outs[0]), outs[1].data_ptr(), outs[2].data_ptr(), lh.k8(xqd, xsd, xd),
+                          lh.w8(*wdev[0]), lh.w8(*wdev[1]), lh.w8(*wdev[2]), n, dq, dkv, gs)
+
+    step()
+    eager = [hu.host(o) for o in outs]
+    xq, xs = orc.quantize(x, gs)
+    for (q, s), got in zip(ws_, eager):
+        ref, mag = hu.dequant_reference(xq, xs, q, s, gs)
+        hu.assert_within_budget(got, ref, mag, what="qkv")
+    assert L.llhip_graph_begin() == 0
+    step()
+    graph = L.llhip_graph_end()
+    assert graph, lh.last_error()
+    try:
+        for replay in range(4):
+            for o in outs:
+                o.fill_(-1.0)
+            T.cuda.synchronize()
+            assert L.llhip_graph_launch(graph) == 0
+            got = [hu.host(o) for o in outs]
+            for a, b in zip(got, eager):
+                assert np.array_equal(hu.bits(a), hu.bits(b)), replay
+    finally:
+        L.llhip_graph_destroy(graph)
+
+
+def test_registered_host_weights_resolve_to_hbm():
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 606)
+    d, n, gs = 300, 1024, 64
+    wq, ws = synth_weights(rng, d, n, gs)
+    xq, xs = orc.quantize(rng.normal(n, 0.0, 1.0), gs)
+    assert L.llhip_register_host(lh.ptr(wq), wq.nbytes) == 0
+    assert L.llhip_register_host(lh.ptr(ws), ws.nbytes) == 0
+    try:
+        assert L.llhip_resolve(lh.ptr(wq) + 64) is not None
+        out = np.zeros(d, np.float32)
+        L.k_matmul_q8(lh.ptr(out), lh.k8(xq, xs), lh.w8(wq, ws), n, d, gs)
+        ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+        hu.assert_within_budget(out, ref, mag, what="registered weights")
+    finally:
+        L.llhip_unregister_host(lh.ptr(wq))
+        L.llhip_unregister_host(lh.ptr(ws))
+
+
+# ---- batched GEMM ---------------------------------------------------------------------------------------------------
+
+
+def gemm_case(m, n, k, gs, seed):
+    rng = orc.Rng(orc.SEED + seed)
+    x = rng.normal(m * k, 0.0, 1.0).reshape(m, k)
+    xq, xs = orc.quantize(x, gs)
+    (wq, ws), (w3q, w3s) = synth_weights(rng, n, k, gs), synth_weights(rng, n, k, gs)
+    return xq, xs, wq, ws, w3q, w3s, rng
+
+
+@pytest.mark.parametrize("m,n,k,gs", [(1, 64, 64, 64), (33, 20, 128, 64), (40, 33, 192, 64), (130, 257, 1024, 64),
+                                      (256, 384, 4096, 64), (77, 200, 2048, 128), (64, 96, 512, 32), (5, 7, 16, 4),
+                                      (129, 129, 640, 64)])
+def test_gemm_q8_all_kinds_within_budget(m, n, k, gs):
+    L = hu.lib()
+    T = hu.torch()
+    xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, m * 31 + n)
+    ldc = n + 5
+    base = rng.uniform(m * ldc, 3.0).reshape(m, ldc)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    r3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
+    dx = [hu.dev(a) for a in (xq, xs, wq, ws, w3q, w3s)]
+    for kind in (lh.GEMM_STORE, lh.GEMM_ADD, lh.GEMM_SWIGLU, lh.GEMM_PARTIAL):
+        c = hu.dev(base)
+        seg = lh.GemmQ8Segment(lh.ptr(c), ldc, lh.w8(dx[2], dx[3]), lh.w8(dx[4], dx[5]), None, None, n, kind)
+        L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+        got = hu.host(c)
+        assert np.array_equal(hu.bits(got[:, n:]), hu.bits(base[:, n:])), "row padding was written"
+        got = got[:, :n]
+        if kind == lh.GEMM_ADD:
+            hu.assert_within_budget(got, base[:, :n] + ref, mag + np.abs(base[:, :n]), what=f"add {m}x{n}x{k}")
+        elif kind == lh.GEMM_SWIGLU:
+            want = ref / (1 + np.exp(-ref)) * r3
+            tol = 2e-5 * (mag * (np.abs(r3) + 1) + mag3 * (np.abs(ref) + 1)) + 1e-6  # tests/q8.c:130
+            assert np.all(np.abs(got - want) <= tol), f"swiglu {m}x{n}x{k}"
+        else:
+            hu.assert_within_budget(got, ref, mag, what=f"store {m}x{n}x{k}")
+    del T
+
+
+def test_gemm_q8_qkv_segments_and_gemv_agreement():
+    """Three segments sharing the activations (QKV), and each GEMM row against the GEMV of that row."""
+    L = hu.lib()
+    m, k, gs = 70, 1024, 64
+    xq, xs, wq, ws, _, _, rng = gemm_case(m, 96, k, gs, 707)
+    mats = [synth_weights(rng, n, k, gs) for n in (96, 32, 32)]
+    dxq, dxs = hu.dev(xq), hu.dev(xs)
+    outs = [hu.empty((m, n), hu.torch().float32) for n in (96, 32, 32)]
+    dw = [(hu.dev(q), hu.dev(s)) for q, s in mats]
+    segs = (lh.GemmQ8Segment * 3)(*[lh.GemmQ8Segment(lh.ptr(o), o.shape[1], lh.w8(*w), lh.K8Weight(), None, None,
+                                                     o.shape[1], lh.GEMM_STORE) for o, w in zip(outs, dw)])
+    L.k_gemm_q8(lh.ptr(dxq), lh.ptr(dxs), m, k, gs, segs, 3)
+    for o, (q, s), w in zip(outs, mats, dw):
+        got = hu.host(o)
+        ref, mag = hu.dequant_reference(xq, xs, q, s, gs)
+        hu.assert_within_budget(got, ref, mag, what="qkv segment")
+        for i in (0, m // 2, m - 1):
+            row = hu.empty(q.shape[0], hu.torch().float32)
+            L.k_matmul_q8(lh.ptr(row), lh.k8(dxq[i], dxs[i]), lh.w8(*w), k, q.shape[0], gs)
+            hu.assert_within_budget(hu.host(row), got[i], mag[i] * 2, what="gemm row vs gemv")
+
+
+@pytest.mark.parametrize("m,n,k,gs", [(33, 20, 128, 64), (130, 200, 1024, 64), (64, 64, 512, 128)])
+def test_gemm_q8_int32_probe_bitwise(m, n, k, gs):
+    L = hu.lib()
+    xq, _, wq, _, _, _, _ = gemm_case(m, n, k, gs, 808 + m)
+    dots = np.zeros((k // gs, m, n), np.int32)
+    L.llhip_q8_group_dots(lh.ptr(dots), lh.ptr(xq), m, k, gs, lh.ptr(wq), n)
+    assert lh.last_error() == ""
+    assert np.array_equal(dots, orc.group_dots(xq, wq, gs))
+
+
+def test_gemm_q8_reference_golden_and_backends():
+    """The reference's golden portable-GEMM cases: the MFMA backend (gs % 64 == 0) and the generic one, each within
+    budget of the reference's outputs; the probe equals the reference's AMX int32 dots where the fixture has them."""
+    g = np.load(os.path.join(GOLDEN, "gemm_q8.npz"))
+    L = hu.lib()
+    for key in sorted({k.split("/")[0] for k in g.files if k.endswith("/shape")}):
+        m, n, k, gs = (int(v) for v in g[f"{key}/shape"])
+        xq, xs, base = g[f"{key}/xq"], g[f"{key}/xs"], g[f"{key}/base"]
+        wq, ws, w3q, w3s = (g[f"{key}/{a}"] for a in ("wq", "ws", "w3q", "w3s"))
+        ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+        backends = [lh.Q8_GEMM_PORTABLE] + ([lh.Q8_GEMM_HIP_MFMA] if gs % 64 == 0 else [])
+        assert L.k_gemm_q8_pick(gs, None, 1) == (lh.Q8_GEMM_HIP_MFMA if gs % 64 == 0 else lh.Q8_GEMM_PORTABLE)
+        for backend in backends:
+            c = base.copy()
+            seg = lh.GemmQ8Segment(lh.ptr(c), c.shape[1], lh.w8(wq, ws), lh.w8(w3q, w3s), None, None, n,
+                                   lh.GEMM_STORE)
+            assert L.k_gemm_q8_backend_test(backend, lh.ptr(xq), lh.ptr(xs), m, k, gs, seg, 1) == 1
+            hu.assert_within_budget(c[:, :n], g[f"{key}/store"][:, :n], mag, rel=4e-5, what=f"{key} backend {backend}")
+            hu.assert_within_budget(c[:, :n], ref, mag, what=f"{key} backend {backend} vs float64")
+            assert np.array_equal(hu.bits(c[:, n:]), hu.bits(base[:, n:]))
+        assert L.k_gemm_q8_backend_test(lh.Q8_GEMM_AMX, lh.ptr(xq), lh.ptr(xs), m, k, gs, None, 1) == 0
+        if f"{key}/amx_dots" in g.files:
+            dots = np.zeros((k // gs, m, n), np.int32)
+            L.llhip_q8_group_dots(lh.ptr(dots), lh.ptr(xq), m, k, gs, lh.ptr(wq), n)
+            assert np.array_equal(dots, g[f"{key}/amx_dots"]), key
