@@ -29,6 +29,11 @@ void quantize_rows(const char *name, int8_t *q, float *s, const float *x, size_t
   Ref S = call.out(s, (size_t)m * groups * sizeof(float), false);
   if (!call.ready())
     return;
+  if (m == 1 && !call.staged() && quantize_fusion_enabled() && n % gs == 0) {
+    // one device-resident row: the next GEMV reading (q, s) quantizes it in its prologue
+    defer_quantize(PendingQuantize{call.ptr<int8_t>(Q), call.ptr<float>(S), call.ptr<const float>(X), n, gs});
+    return;
+  }
   QuantizeJob job{call.ptr<int8_t>(Q), call.ptr<float>(S), call.ptr<const float>(X), ldx, m, n, gs};
   if (launch_quantize(job, call.stream()))
     call.finish();
@@ -65,7 +70,7 @@ void q8_gemv(const char *name, const Q8Member *members, int count, const K8Input
   const int groups = n / gs;
   if (total <= 0)
     return;
-  Call call(name);
+  Call call(name, true);
   const size_t used = (size_t)(groups > 0 ? groups : 0) * gs;
   const size_t sld = ld / (size_t)gs;
   Ref XQ, XS, XF;
@@ -108,6 +113,26 @@ void q8_gemv(const char *name, const Q8Member *members, int count, const K8Input
   job.ld = ld;
   job.epi = epi;
   job.probe = probe;
+  PendingQuantize pq;
+  if (w8a8 && take_pending_quantize(x->q, x->s, job.n, gs, &pq)) {
+    GemvJob fused = job;
+    fused.xf_quantize = true;
+    fused.xf = pq.x;
+    fused.xq_out = pq.q;
+    fused.xs_out = pq.s;
+    fused.xq = nullptr;
+    fused.xs = nullptr;
+    if (gemv_fast_path(fused)) {
+      if (launch_q8_gemv(fused, call.stream()))
+        call.finish();
+      return;
+    }
+    // not a shape the fused kernel takes: quantize first, as recorded
+    if (!launch_quantize(QuantizeJob{pq.q, pq.s, pq.x, (size_t)pq.n, 1, pq.n, pq.gs}, call.stream()))
+      return;
+  } else if (!flush_pending_quantize()) {
+    return;
+  }
   if (launch_q8_gemv(job, call.stream()))
     call.finish();
 }

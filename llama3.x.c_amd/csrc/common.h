@@ -43,9 +43,26 @@ struct Ref {
   int staged = -1;
 };
 
+// A k_quantize on device buffers is not launched at once: it is recorded, and the next k_matmul_q8* whose input is
+// exactly those buffers quantizes in its own prologue (one launch instead of two; block 0 still stores q and s). Any
+// other entry point, llhip_synchronize and the end of a graph capture launch a recorded quantization first, so every
+// observer sees the reference's order. LLAMA_HIP_FUSE_QUANT=0 turns the deferral off.
+struct PendingQuantize {
+  int8_t *q;
+  float *s;
+  const float *x;
+  int n, gs;
+};
+bool quantize_fusion_enabled();
+void defer_quantize(const PendingQuantize &job);
+bool take_pending_quantize(const int8_t *q, const float *s, int n, int gs, PendingQuantize *out);
+bool flush_pending_quantize(); // launches a recorded quantization, if any
+
 class Call {
  public:
-  explicit Call(const char *name);
+  // keep_pending: the caller may consume a recorded quantization (the Q8 GEMV entry points); every other call
+  // launches it first.
+  explicit Call(const char *name, bool keep_pending = false);
   ~Call();
   Ref in(const void *p, size_t bytes) { return in2d(p, bytes, bytes, 1); }
   Ref in2d(const void *p, size_t row_bytes, size_t pitch, size_t rows);
@@ -106,7 +123,12 @@ struct GemvJob {
   size_t ld; // weight row stride in values
   Epilogue epi;
   int32_t *probe; // optional: exact int32 group dots of segment 0, probe[g * rows + r]
+  // Fused quantization: quantize xf in the prologue (the k_quantize rule) and store it to (xq_out, xs_out).
+  bool xf_quantize;
+  int8_t *xq_out;
+  float *xs_out;
 };
+bool gemv_fast_path(const GemvJob &job);
 bool launch_q8_gemv(const GemvJob &job, hipStream_t stream);
 
 struct F32GemvSegment {

@@ -3,6 +3,8 @@
 // Lane layout shared by the quantizer and the GEMV: a wave covers 1024 consecutive values of a row per step, lane l
 // holding values [16 l, 16 l + 16). With gs % 16 == 0 a group is gs / 16 consecutive lanes (a quad for gs = 64), so
 // group maxima and int32 group dots are lane reductions inside the wave (DPP / swizzle shuffles), with no LDS.
+#include <cstdlib>
+
 #include "common.h"
 
 namespace llhip {
@@ -17,23 +19,58 @@ __device__ __forceinline__ float silu_gate(float value, float gate) {
   return value * gate;
 }
 
+// Lane exchanges inside a row of 16 lanes use DPP (a VALU operand modifier, no LDS round trip): quad_perm [1,0,3,2]
+// and [2,3,0,1] pair lanes at distance 1 and 2, row_half_mirror pairs each lane with one in the other half of its
+// 8-lane group and row_mirror with one in the other half of its row. After the quad steps every lane of a quad holds
+// the same value, so the mirror steps complete the reduction over 8 and 16 lanes. Distances 16 and 32 use a swizzle.
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
+
+template <int CTRL> __device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+struct AddOp {
+  template <class T> __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// Reduction over aligned groups of `lanes` lanes (a power of two <= 64, wave-uniform); every lane gets its group's
+// result.
+template <class T, class Op> __device__ __forceinline__ T group_reduce(T v, int lanes, Op op) {
+  if (lanes > 1)
+    v = op(v, dpp<kDppQuadXor1>(v));
+  if (lanes > 2)
+    v = op(v, dpp<kDppQuadXor2>(v));
+  if (lanes > 4)
+    v = op(v, dpp<kDppRowHalfMirror>(v));
+  if (lanes > 8)
+    v = op(v, dpp<kDppRowMirror>(v));
+  if (lanes > 16)
+    v = op(v, __shfl_xor(v, 16));
+  if (lanes > 32)
+    v = op(v, __shfl_xor(v, 32));
+  return v;
+}
+
+template <class T> __device__ __forceinline__ T group_reduce_add(T v, int lanes) { return group_reduce(v, lanes, AddOp{}); }
+
+__device__ __forceinline__ float group_reduce_max(float v, int lanes) { return group_reduce(v, lanes, MaxOp{}); }
+
+// Sum over the wave: each 16-lane row reduces with DPP, then the four row sums are read out of lanes 0, 16, 32, 48.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1)
-    v += __shfl_xor(v, m);
-  return v;
-}
-
-template <class T> __device__ __forceinline__ T group_reduce_add(T v, int lpg) {
-  for (int m = 1; m < lpg; m <<= 1)
-    v += __shfl_xor(v, m);
-  return v;
-}
-
-__device__ __forceinline__ float group_reduce_max(float v, int lpg) {
-  for (int m = 1; m < lpg; m <<= 1)
-    v = fmaxf(v, __shfl_xor(v, m));
-  return v;
+  v += dpp<kDppQuadXor1>(v);
+  v += dpp<kDppQuadXor2>(v);
+  v += dpp<kDppRowHalfMirror>(v);
+  v += dpp<kDppRowMirror>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
 }
 
 // One value of k_quantize (src/gemv.c:618-620): the IEEE quotient (hipcc emits a correctly rounded fp32 division by
@@ -41,6 +78,28 @@ __device__ __forceinline__ float group_reduce_max(float v, int lpg) {
 __device__ __forceinline__ int quantize_one(float x, float scale) {
   float ratio = scale == 0.0f ? 0.0f : x / scale;
   return (int)roundf(fmaxf(-127.0f, fminf(127.0f, ratio)));
+}
+
+// The same value through the reciprocal, for normal scales: r = x * rcp(scale) lies within 127 * 3 * 2^-24 < 2.3e-5 of
+// the correctly rounded quotient fl(x / scale) (v_rcp_f32 is within 1 ulp, the product rounds once, |x / scale| <=
+// 127 (1 + 2^-23)). roundf changes value only at k + 0.5 and the clamp only binds above 127, so wherever
+// |frac(|r|) - 0.5| >= 2^-12 both give the same integer. Inside that margin, for subnormal x (a flushing multiply would
+// lose it) and for a scale that is 0 or not normal, the exact quotient decides.
+__device__ __forceinline__ int quantize_fast(float x, float scale, float inv, bool inv_ok) {
+  const float r = x * inv;
+  const float a = fabsf(r);
+  const float t = truncf(a);
+  const float f = a - t;
+  const bool tiny = x != 0.0f && fabsf(x) < 1.17549435e-38f;
+  if (!inv_ok || tiny || fabsf(f - 0.5f) < 0x1p-12f)
+    return quantize_one(x, scale);
+  const int m = (int)fminf(t + (f > 0.5f ? 1.0f : 0.0f), 127.0f);
+  return r < 0.0f ? -m : m;
+}
+
+__device__ __forceinline__ float group_reciprocal(float scale, bool &ok) {
+  ok = scale >= 1.17549435e-38f; // normal (finite: |x| is finite, so scale <= FLT_MAX / 127)
+  return ok ? __builtin_amdgcn_rcpf(scale) : 0.0f;
 }
 
 __device__ __forceinline__ int pack_bytes(int a, int b, int c, int d) {
@@ -62,16 +121,26 @@ __device__ __forceinline__ int4 quantize_slice(const float4 (&v)[4], int lpg, fl
   }
   peak = group_reduce_max(peak, lpg);
   scale = peak / 127.0f;
-  int4 q;
-  q.x = pack_bytes(quantize_one(v[0].x, scale), quantize_one(v[0].y, scale), quantize_one(v[0].z, scale),
-                   quantize_one(v[0].w, scale));
-  q.y = pack_bytes(quantize_one(v[1].x, scale), quantize_one(v[1].y, scale), quantize_one(v[1].z, scale),
-                   quantize_one(v[1].w, scale));
-  q.z = pack_bytes(quantize_one(v[2].x, scale), quantize_one(v[2].y, scale), quantize_one(v[2].z, scale),
-                   quantize_one(v[2].w, scale));
-  q.w = pack_bytes(quantize_one(v[3].x, scale), quantize_one(v[3].y, scale), quantize_one(v[3].z, scale),
-                   quantize_one(v[3].w, scale));
-  return q;
+  bool ok;
+  const float inv = group_reciprocal(scale, ok);
+  int w[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    w[i] = pack_bytes(quantize_fast(v[i].x, scale, inv, ok), quantize_fast(v[i].y, scale, inv, ok),
+                      quantize_fast(v[i].z, scale, inv, ok), quantize_fast(v[i].w, scale, inv, ok));
+  return int4{w[0], w[1], w[2], w[3]};
+}
+
+// Four values per lane (one float4): the group spans gs / 4 lanes (lpg4, a power of two <= 64).
+__device__ __forceinline__ int quantize_quad(float4 v, int lpg4, float &scale, bool &bad) {
+  bad |= !isfinite(v.x) || !isfinite(v.y) || !isfinite(v.z) || !isfinite(v.w);
+  float peak = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  peak = group_reduce_max(peak, lpg4);
+  scale = peak / 127.0f;
+  bool ok;
+  const float inv = group_reciprocal(scale, ok);
+  return pack_bytes(quantize_fast(v.x, scale, inv, ok), quantize_fast(v.y, scale, inv, ok),
+                    quantize_fast(v.z, scale, inv, ok), quantize_fast(v.w, scale, inv, ok));
 }
 
 // k_quantize / k_quantize_rows, fast form: gs = 16 * lpg with lpg a power of two <= 64, n % 16 == 0, 16-byte aligned
@@ -141,20 +210,47 @@ struct GemvSeg {
 struct GemvParams {
   GemvSeg seg[3];
   int nseg;
-  const int8_t *xq;
+  const int8_t *xq; // the quantized input (xq, xs), or with FUSED the FP32 input xf, quantized in the prologue
   const float *xs;
-  int n, gs, lpg;
+  const float *xf;
+  int8_t *xq_out;   // FUSED: where block 0 stores the quantization it made (the caller's k_quantize outputs)
+  float *xs_out;
+  int n, gs, lpg, nchunks;
   long long ld;     // weight row stride in values
   long long sld;    // weight scale row stride (ld / gs)
   int epi;
   int total_waves;
   int32_t *probe;   // optional, segment 0 only: probe[g * seg[0].rows + r]
+  int *flags;
 };
 
 // A wave-uniform segment from a kernel-argument array, by selects rather than a dynamic index (which would copy the
 // arguments to scratch memory).
 template <class T> __device__ __forceinline__ T pick(const T (&segs)[3], int s) {
   return s == 0 ? segs[0] : s == 1 ? segs[1] : segs[2];
+}
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Buffer resources (V#): a base address and a byte bound. A buffer load past the bound returns zero and touches no
+// memory, so a row's resource bounded to its n valid bytes (0 for a row the wave does not own) needs no clamping or
+// masking, and the loads take a 32-bit offset plus an immediate instead of a 64-bit address each.
+constexpr int kBufferWord3 = 0x00020000; // raw buffer, 32-bit data format
+constexpr int kStream = 2;               // cache policy nt: weights are read once, stream them past the caches
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void *base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kBufferWord3);
+}
+
+__device__ __forceinline__ int4 load16(__amdgpu_buffer_rsrc_t r, int offset, int policy) {
+  const v4i v = policy ? __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kStream)
+                       : __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+  return int4{v.x, v.y, v.z, v.w};
+}
+
+// One FP32 value: the builtin returns the 32 bits as an integer, reinterpreted here (not converted).
+__device__ __forceinline__ float load4(__amdgpu_buffer_rsrc_t r, int offset) {
+  return __uint_as_float((unsigned)__builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
 }
 
 __device__ __forceinline__ int dot16(int4 w, int4 x) {
@@ -164,90 +260,209 @@ __device__ __forceinline__ int dot16(int4 w, int4 x) {
   return __builtin_amdgcn_sdot4(w.w, x.w, d, false);
 }
 
-// Streaming W8A8 GEMV: each wave owns ROWS consecutive output rows of one segment and walks K in 1024-value steps.
-// The block stages the int8 activations and their scales in LDS once; per row and step a lane reads 16 weight bytes
-// (one 128-bit load), forms its partial int32 dot with four dot4 instructions, the group's lanes add their partials
-// into the exact int32 group dot, and the group's first lane adds ((float)dot * ws) * xs to its FP32 accumulator (the
-// reference's per-group expression, src/gemv.c:428). A wave reduction and the epilogue finish each row.
-template <int ROWS, bool SWIGLU>
-__global__ __launch_bounds__(kBlock) void q8_gemv(GemvParams p) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  int8_t *sxq = reinterpret_cast<int8_t *>(smem);
-  float *sxs = reinterpret_cast<float *>(smem + ((p.n + 15) & ~15));
-  const int tid = threadIdx.x, lane = tid & (kWave - 1);
-  for (int off = tid * 16; off < p.n; off += kBlock * 16)
-    *reinterpret_cast<int4 *>(sxq + off) = *reinterpret_cast<const int4 *>(p.xq + off);
-  for (int g = tid; g < p.n / p.gs; g += kBlock)
-    sxs[g] = p.xs[g];
-  __syncthreads();
+// The block's copy of the input in LDS: the int8 activations and their scales, copied from (xq, xs), or (FUSED) made
+// here from the FP32 input with the k_quantize rule, block 0 also storing them for the caller. load() only issues the
+// global loads into registers; the kernel issues it before the weight loads, so waiting for the input does not wait
+// for the weights (loads complete in issue order for the counter the waits use).
+template <bool FUSED, int BLOCK, int MAXC> struct Input {
+  static constexpr int kFusedPasses = (MAXC * 1024 + BLOCK * 4 - 1) / (BLOCK * 4); // 4 values per thread and pass
+  static constexpr int kCopyPasses = (MAXC * 1024 + BLOCK * 16 - 1) / (BLOCK * 16);
+  static constexpr int kScalePasses = (MAXC * 64 + BLOCK - 1) / BLOCK; // gs >= 16: at most n / 16 scales
+  float4 xf[FUSED ? kFusedPasses : 1];
+  int4 xq[FUSED ? 1 : kCopyPasses];
+  float xs[FUSED ? 1 : kScalePasses];
 
-  const int gw = blockIdx.x * (kBlock / kWave) + (tid >> 6);
-  if (gw >= p.total_waves)
-    return;
-  int s = 0;
-  while (s + 1 < p.nseg && gw >= p.seg[s + 1].first_wave)
-    s++;
-  const GemvSeg seg = pick(p.seg, s);
-  const int r0 = (gw - seg.first_wave) * ROWS;
-  const int nrows = min(ROWS, seg.rows - r0);
-  const bool leader = (lane & (p.lpg - 1)) == 0;
-  int32_t *probe = (s == 0) ? p.probe : nullptr;
-
-  float acc[ROWS], gacc[ROWS];
+  // Unconditional buffer loads bounded to the input (see RowSet::load): values past n read zero.
+  __device__ __forceinline__ void load(const GemvParams &p) {
+    const int tid = threadIdx.x;
+    if (FUSED) {
+      const __amdgpu_buffer_rsrc_t r = buffer(p.xf, (unsigned)p.n * 4u);
 #pragma unroll
-  for (int i = 0; i < ROWS; i++)
-    acc[i] = gacc[i] = 0.0f;
+      for (int i = 0; i < kFusedPasses; i++) {
+        const int4 v = load16(r, (i * BLOCK * 4 + tid * 4) * 4, 0);
+        xf[i] = float4{__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w)};
+      }
+    } else {
+      const __amdgpu_buffer_rsrc_t rq = buffer(p.xq, (unsigned)p.n), rs = buffer(p.xs, (unsigned)(p.n / p.gs) * 4u);
+#pragma unroll
+      for (int i = 0; i < kCopyPasses; i++)
+        xq[i] = load16(rq, i * BLOCK * 16 + tid * 16, 0);
+#pragma unroll
+      for (int i = 0; i < kScalePasses; i++)
+        xs[i] = load4(rs, (i * BLOCK + tid) * 4);
+    }
+  }
 
-  const int steps = (p.n + 1023) >> 10;
-  for (int c = 0; c < steps; c++) {
-    const int off = (c << 10) + lane * 16;
-    const bool active = off < p.n;
-    const int4 xv = active ? *reinterpret_cast<const int4 *>(sxq + off) : int4{0, 0, 0, 0};
-    const int g = off / p.gs;
-    const float xsg = active ? sxs[g] : 0.0f;
-    int4 wv[ROWS], w3v[ROWS];
+  __device__ __forceinline__ void stage(const GemvParams &p, int8_t *sxq, float *sxs) const {
+    const int tid = threadIdx.x;
+    if (!FUSED) {
+#pragma unroll
+      for (int i = 0; i < kCopyPasses; i++) {
+        const int off = i * BLOCK * 16 + tid * 16;
+        if (off < p.n)
+          *reinterpret_cast<int4 *>(sxq + off) = xq[i];
+      }
+#pragma unroll
+      for (int i = 0; i < kScalePasses; i++) {
+        const int g = i * BLOCK + tid;
+        if (g < p.n / p.gs)
+          sxs[g] = xs[i];
+      }
+      return;
+    }
+    const bool keep = blockIdx.x == 0;
+    const int lpg4 = p.gs >> 2;
+    bool bad = false;
+    // every lane takes part in every pass (the group max is a lane reduction); lanes past n hold zeros
+#pragma unroll
+    for (int i = 0; i < kFusedPasses; i++) {
+      const int off = i * BLOCK * 4 + tid * 4;
+      float scale;
+      const int q = quantize_quad(xf[i], lpg4, scale, bad);
+      if (off < p.n) {
+        *reinterpret_cast<int *>(sxq + off) = q;
+        const bool first = (tid & (lpg4 - 1)) == 0;
+        if (first)
+          sxs[off / p.gs] = scale;
+        if (keep) {
+          *reinterpret_cast<int *>(p.xq_out + off) = q;
+          if (first)
+            p.xs_out[off / p.gs] = scale;
+        }
+      }
+    }
+    if (bad)
+      p.flags[0] = 1;
+  }
+};
+
+// Streaming W8A8 GEMV on a persistent grid: about two blocks per CU, each wave walking row sets gw, gw + stride, ...
+// (a row set is ROWS consecutive output rows of one segment). For its first row set a wave issues every weight and
+// weight-scale load (ROWS x nchunks 128-bit loads per lane, nchunks = ceil(n / 1024) <= MAXC) before the block stages
+// its input, so the HBM latency overlaps that staging; the block stages (or, FUSED, quantizes) the input only once,
+// however many row sets its waves take. Per 1024-value step a lane forms its partial int32 dot of 16 values with four
+// dot4 instructions, the group's lanes add theirs into the exact int32 group dot, and the group's first lane adds
+// ((float)dot * ws) * xs to its FP32 accumulator (the reference's per-group expression, src/gemv.c:428). A wave
+// reduction and the epilogue finish each row.
+template <int MAXC, int ROWS, bool SWIGLU>
+struct RowSet {
+  int4 w[ROWS][MAXC], w3[ROWS][MAXC];
+  float ws[ROWS][MAXC], w3s[ROWS][MAXC];
+  GemvSeg seg;
+  int s, r0, nrows;
+
+  // Every load is issued unconditionally through per-row buffer resources: a row past nrows has a zero bound, and
+  // lanes or chunk slots past n fall outside the row's bound, so all of them read zero with no memory access. With no
+  // branch around any load the compiler can count them and wait for each only when it is used.
+  __device__ __forceinline__ void load(const GemvParams &p, int gw, int lane) {
+    const int gl = gw < p.total_waves ? gw : p.total_waves - 1;
+    s = 0;
+    while (s + 1 < p.nseg && gl >= p.seg[s + 1].first_wave)
+      s++;
+    seg = pick(p.seg, s);
+    r0 = (gl - seg.first_wave) * ROWS;
+    nrows = gw < p.total_waves ? min(ROWS, seg.rows - r0) : 0;
+    const unsigned wbytes = (unsigned)p.n, sbytes = (unsigned)(p.n / p.gs) * 4u;
+    __amdgpu_buffer_rsrc_t rw[ROWS], rs[ROWS], rw3[ROWS], rs3[ROWS];
 #pragma unroll
     for (int i = 0; i < ROWS; i++) {
-      wv[i] = w3v[i] = int4{0, 0, 0, 0};
-      if (i < nrows && active) {
-        const long long row = r0 + i;
-        wv[i] = *reinterpret_cast<const int4 *>(seg.wq + row * p.ld + off);
-        if (SWIGLU)
-          w3v[i] = *reinterpret_cast<const int4 *>(seg.w3q + row * p.ld + off);
+      const long long row = r0 + i;
+      const bool own = i < nrows;
+      rw[i] = buffer(seg.wq + row * p.ld, own ? wbytes : 0u);
+      rs[i] = buffer(seg.ws + row * p.sld, own ? sbytes : 0u);
+      if (SWIGLU) {
+        rw3[i] = buffer(seg.w3q + row * p.ld, own ? wbytes : 0u);
+        rs3[i] = buffer(seg.w3s + row * p.sld, own ? sbytes : 0u);
+      }
+    }
+    // chunk-major, the order finish() consumes them in
+#pragma unroll
+    for (int c = 0; c < MAXC; c++)
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        const int off = (c << 10) + lane * 16;
+        const int soff = (off / p.gs) * 4;
+        w[i][c] = load16(rw[i], off, 1);
+        ws[i][c] = load4(rs[i], soff);
+        if (SWIGLU) {
+          w3[i][c] = load16(rw3[i], off, 1);
+          w3s[i][c] = load4(rs3[i], soff);
+        } else {
+          w3[i][c] = int4{0, 0, 0, 0};
+          w3s[i][c] = 0.0f;
+        }
+      }
+  }
+
+  // Fully unrolled over compile-time indices (guards, not early exits), so the arrays stay in registers. Rows past
+  // nrows and steps past nchunks hold zeros from load() and add nothing.
+  __device__ __forceinline__ void finish(const GemvParams &p, const int8_t *sxq, const float *sxs, int lane) {
+    const bool leader = (lane & (p.lpg - 1)) == 0;
+    int32_t *probe = (s == 0) ? p.probe : nullptr;
+    float acc[ROWS], gacc[ROWS];
+#pragma unroll
+    for (int i = 0; i < ROWS; i++)
+      acc[i] = gacc[i] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+      if (c < p.nchunks) {
+        const int off = (c << 10) + lane * 16;
+        const bool active = off < p.n;
+        const int4 xv = active ? *reinterpret_cast<const int4 *>(sxq + off) : int4{0, 0, 0, 0};
+        const int g = off / p.gs;
+        const float xsg = active ? sxs[g] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) {
+          const int d = group_reduce_add(dot16(w[i][c], xv), p.lpg);
+          if (probe && active && leader && i < nrows)
+            probe[(long long)g * seg.rows + r0 + i] = d;
+          acc[i] += leader ? ((float)d * ws[i][c]) * xsg : 0.0f;
+          if (SWIGLU) {
+            const int d3 = group_reduce_add(dot16(w3[i][c], xv), p.lpg);
+            gacc[i] += leader ? ((float)d3 * w3s[i][c]) * xsg : 0.0f;
+          }
+        }
       }
     }
 #pragma unroll
     for (int i = 0; i < ROWS; i++) {
-      if (i >= nrows)
-        break;
-      const long long row = r0 + i;
-      int d = group_reduce_add(dot16(wv[i], xv), p.lpg);
-      if (probe && active && leader)
-        probe[(long long)g * seg.rows + row] = d;
-      if (active && leader)
-        acc[i] += ((float)d * seg.ws[row * p.sld + g]) * xsg;
-      if (SWIGLU) {
-        int d3 = group_reduce_add(dot16(w3v[i], xv), p.lpg);
-        if (active && leader)
-          gacc[i] += ((float)d3 * seg.w3s[row * p.sld + g]) * xsg;
+      const float total = wave_sum(acc[i]);
+      const float gate = SWIGLU ? wave_sum(gacc[i]) : 0.0f;
+      if (lane == 0 && i < nrows) {
+        float *o = seg.out + r0 + i;
+        if (SWIGLU)
+          *o = silu_gate(total, gate);
+        else if (p.epi == EPI_ADD)
+          *o += total;
+        else
+          *o = total;
       }
     }
   }
-#pragma unroll
-  for (int i = 0; i < ROWS; i++) {
-    if (i >= nrows)
-      break;
-    const float total = wave_sum(acc[i]);
-    const float gate = SWIGLU ? wave_sum(gacc[i]) : 0.0f;
-    if (lane == 0) {
-      float *o = seg.out + r0 + i;
-      if (SWIGLU)
-        *o = silu_gate(total, gate);
-      else if (p.epi == EPI_ADD)
-        *o += total;
-      else
-        *o = total;
-    }
+};
+
+template <int MAXC, int ROWS, bool SWIGLU, bool FUSED, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void q8_gemv(GemvParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  int8_t *sxq = reinterpret_cast<int8_t *>(smem);
+  float *sxs = reinterpret_cast<float *>(smem + ((p.n + 15) & ~15));
+  const int lane = threadIdx.x & (kWave - 1);
+  const int stride = gridDim.x * WAVES;
+  // wave-uniform by construction; readfirstlane lets the compiler keep row indices and pointers in scalar registers
+  int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * WAVES + (threadIdx.x >> 6));
+  Input<FUSED, WAVES * 64, MAXC> in;
+  in.load(p);
+  __builtin_amdgcn_sched_barrier(0);
+  RowSet<MAXC, ROWS, SWIGLU> set;
+  set.load(p, gw, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  in.stage(p, sxq, sxs);
+  __syncthreads();
+  while (gw < p.total_waves) {
+    set.finish(p, sxq, sxs, lane);
+    gw += stride;
+    if (gw < p.total_waves)
+      set.load(p, gw, lane);
   }
 }
 
@@ -444,10 +659,56 @@ bool launch_quantize(const QuantizeJob &job, hipStream_t stream) {
   return true;
 }
 
-template <int ROWS, bool SWIGLU> static void launch_fast(const GemvParams &p, hipStream_t stream) {
-  const int blocks = (p.total_waves + 3) / 4;
+// Blocks per CU of the persistent GEMV grid (LLAMA_HIP_GEMV_BLOCKS_PER_CU overrides, for sweeps).
+static int gemv_blocks_per_cu() {
+  static const int value = [] {
+    const char *env = getenv("LLAMA_HIP_GEMV_BLOCKS_PER_CU");
+    const int v = env && *env ? atoi(env) : 0;
+    return v >= 1 && v <= 64 ? v : 2;
+  }();
+  return value;
+}
+
+// 8-wave blocks on a grid of a few blocks per CU: every block stages (or quantizes) the input once, however many row
+// sets its waves stream.
+template <int MAXC, int ROWS, bool SWIGLU>
+static void launch_fast(const GemvParams &p, bool fused, hipStream_t stream) {
   const size_t lds = ((size_t)(p.n + 15) & ~(size_t)15) + (size_t)(p.n / p.gs) * sizeof(float);
-  hipLaunchKernelGGL((q8_gemv<ROWS, SWIGLU>), dim3(blocks), dim3(kBlock), lds, stream, p);
+  const int want = (p.total_waves + 7) / 8;
+  const int cap = device().cu_count * gemv_blocks_per_cu();
+  const int blocks = want < cap ? want : cap;
+  if (fused)
+    hipLaunchKernelGGL((q8_gemv<MAXC, ROWS, SWIGLU, true, 8>), dim3(blocks), dim3(512), lds, stream, p);
+  else
+    hipLaunchKernelGGL((q8_gemv<MAXC, ROWS, SWIGLU, false, 8>), dim3(blocks), dim3(512), lds, stream, p);
+}
+
+// Rows per wave: one. More rows per wave carry more bytes per wave, but measured on MI355X the 8B shapes stream best
+// with one row per wave and more waves (W1/W3 5.5 vs 4.8 TB/s, the classifier 6.5 vs 6.3). LLAMA_HIP_GEMV_ROWS=2 or 4
+// selects the multi-row kernels (for sweeps); the register budget caps ROWS * MAXC.
+static int rows_per_wave(int total_rows, int maxc, bool swiglu) {
+  (void)total_rows;
+  static const int forced = [] {
+    const char *env = getenv("LLAMA_HIP_GEMV_ROWS");
+    return env && *env ? atoi(env) : 0;
+  }();
+  if ((forced == 2 && maxc <= 8 && !(swiglu && maxc > 4)) || (forced == 4 && maxc <= 4 && !swiglu))
+    return forced;
+  return 1;
+}
+
+bool gemv_fast_path(const GemvJob &job) {
+  const int lpg = lanes_per_group(job.gs);
+  const size_t lds = job.gs > 0 ? ((size_t)(job.n + 15) & ~(size_t)15) + (size_t)(job.n / job.gs) * sizeof(float) : 0;
+  bool fast = (job.xq || job.xf_quantize) && lpg && job.n > 0 && job.n % job.gs == 0 && job.ld % 16 == 0 &&
+              lds <= 65536 && (job.n + 1023) / 1024 <= 16;
+  // The fused prologue keeps the whole FP32 input in registers while the weights stream: up to 8192 values (K of
+  // the 8B model's QKV, Wo and W1/W3); a longer input (W2's 14336) is quantized by its own launch.
+  fast = fast && (job.xf_quantize ? aligned16(job.xf) && aligned16(job.xq_out) && job.gs <= 256 && job.n <= 8192
+                                  : aligned16(job.xq));
+  for (int s = 0; s < job.nseg && fast; s++)
+    fast = aligned16(job.seg[s].wq) && (job.epi != EPI_SWIGLU || aligned16(job.seg[s].w3q));
+  return fast;
 }
 
 bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
@@ -456,15 +717,12 @@ bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
     total_rows += job.seg[s].rows;
   if (total_rows <= 0)
     return true;
-  const int lpg = lanes_per_group(job.gs);
-  const size_t lds = job.gs > 0 ? ((size_t)(job.n + 15) & ~(size_t)15) + (size_t)(job.n / job.gs) * sizeof(float) : 0;
-  bool fast = job.xq && lpg && job.n % job.gs == 0 && job.ld % 16 == 0 && aligned16(job.xq) && lds <= 65536;
-  for (int s = 0; s < job.nseg && fast; s++)
-    fast = aligned16(job.seg[s].wq) && (job.epi != EPI_SWIGLU || aligned16(job.seg[s].w3q));
-  if (fast) {
+  if (gemv_fast_path(job)) {
     GemvParams p{};
-    // Rows per wave: four when there are enough rows to fill the chip with several waves per SIMD, fewer otherwise.
-    const int rows = job.epi == EPI_SWIGLU ? (total_rows >= 8192 ? 2 : 1) : (total_rows >= 16384 ? 4 : total_rows >= 8192 ? 2 : 1);
+    const int nchunks = (job.n + 1023) / 1024;
+    const int maxc = nchunks <= 4 ? 4 : nchunks <= 8 ? 8 : 16;
+    const bool swiglu = job.epi == EPI_SWIGLU;
+    const int rows = rows_per_wave(total_rows, maxc, swiglu);
     int waves = 0;
     for (int s = 0; s < job.nseg; s++) {
       const GemvSegment &g = job.seg[s];
@@ -474,28 +732,48 @@ bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
     p.nseg = job.nseg;
     p.xq = job.xq;
     p.xs = job.xs;
+    p.xf = job.xf;
+    p.xq_out = job.xq_out;
+    p.xs_out = job.xs_out;
     p.n = job.n;
     p.gs = job.gs;
-    p.lpg = lpg;
+    p.lpg = lanes_per_group(job.gs);
+    p.nchunks = nchunks;
     p.ld = (long long)job.ld;
     p.sld = (long long)(job.ld / job.gs);
     p.epi = job.epi;
     p.total_waves = waves;
     p.probe = job.probe;
-    if (job.epi == EPI_SWIGLU) {
-      if (rows == 2)
-        launch_fast<2, true>(p, stream);
+    p.flags = device().error_flags;
+    const bool fused = job.xf_quantize;
+    if (swiglu) {
+      if (maxc == 4 && rows == 2)
+        launch_fast<4, 2, true>(p, fused, stream);
+      else if (maxc == 4)
+        launch_fast<4, 1, true>(p, fused, stream);
+      else if (maxc == 8)
+        launch_fast<8, 1, true>(p, fused, stream);
       else
-        launch_fast<1, true>(p, stream);
-    } else if (rows == 4) {
-      launch_fast<4, false>(p, stream);
-    } else if (rows == 2) {
-      launch_fast<2, false>(p, stream);
+        launch_fast<16, 1, true>(p, fused, stream);
+    } else if (maxc == 4) {
+      if (rows == 4)
+        launch_fast<4, 4, false>(p, fused, stream);
+      else if (rows == 2)
+        launch_fast<4, 2, false>(p, fused, stream);
+      else
+        launch_fast<4, 1, false>(p, fused, stream);
+    } else if (maxc == 8) {
+      if (rows == 2)
+        launch_fast<8, 2, false>(p, fused, stream);
+      else
+        launch_fast<8, 1, false>(p, fused, stream);
     } else {
-      launch_fast<1, false>(p, stream);
+      launch_fast<16, 1, false>(p, fused, stream);
     }
     return launch_ok("q8_gemv");
   }
+  if (job.xf_quantize)
+    return raise("internal: a fused quantization was routed to the generic GEMV");
   GemvGenericParams p{};
   int rows = 0;
   for (int s = 0; s < job.nseg; s++) {

@@ -103,6 +103,8 @@ bool synchronize_and_check() {
   Device &dev = the_device;
   if (dev.capturing)
     return raise("a host-visible wait was requested during graph capture");
+  if (!flush_pending_quantize())
+    return false;
   if (!LLHIP_CHECK(hipStreamSynchronize(dev.stream)))
     return false;
   int flags[16];
@@ -171,8 +173,54 @@ std::mutex arena_mutex;
 
 // ---- Call ---------------------------------------------------------------------------------------------------------
 
-Call::Call(const char *name) : name_(name) {
+// ---- deferred quantization ---------------------------------------------------------------------------------------
+
+namespace {
+std::mutex pending_mutex;
+bool pending_active = false;
+PendingQuantize pending_job;
+} // namespace
+
+bool quantize_fusion_enabled() {
+  static const bool on = [] {
+    const char *env = getenv("LLAMA_HIP_FUSE_QUANT");
+    return !(env && !strcmp(env, "0"));
+  }();
+  return on;
+}
+
+void defer_quantize(const PendingQuantize &job) {
+  flush_pending_quantize();
+  std::lock_guard<std::mutex> lock(pending_mutex);
+  pending_job = job;
+  pending_active = true;
+}
+
+bool take_pending_quantize(const int8_t *q, const float *s, int n, int gs, PendingQuantize *out) {
+  std::lock_guard<std::mutex> lock(pending_mutex);
+  if (!pending_active || pending_job.q != q || pending_job.s != s || pending_job.n != n || pending_job.gs != gs)
+    return false;
+  *out = pending_job;
+  pending_active = false;
+  return true;
+}
+
+bool flush_pending_quantize() {
+  PendingQuantize job;
+  {
+    std::lock_guard<std::mutex> lock(pending_mutex);
+    if (!pending_active)
+      return true;
+    job = pending_job;
+    pending_active = false;
+  }
+  return launch_quantize(QuantizeJob{job.q, job.s, job.x, (size_t)job.n, 1, job.n, job.gs}, the_device.stream);
+}
+
+Call::Call(const char *name, bool keep_pending) : name_(name) {
   if (!ensure_device())
+    failed_ = true;
+  else if (!keep_pending && !flush_pending_quantize())
     failed_ = true;
 }
 
@@ -373,24 +421,24 @@ void *llhip_malloc(size_t bytes) {
 }
 
 void llhip_free(void *p) {
-  if (!p || !ensure_device())
+  if (!p || !ensure_device() || !flush_pending_quantize())
     return;
   if (LLHIP_CHECK(hipStreamSynchronize(the_device.stream)))
     (void)LLHIP_CHECK(hipFree(p));
 }
 
 void llhip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
-  if (ensure_device() && bytes && LLHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, the_device.stream)))
+  if (ensure_device() && flush_pending_quantize() && bytes && LLHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, the_device.stream)))
     (void)LLHIP_CHECK(hipStreamSynchronize(the_device.stream));
 }
 
 void llhip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
-  if (ensure_device() && bytes && LLHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, the_device.stream)))
+  if (ensure_device() && flush_pending_quantize() && bytes && LLHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, the_device.stream)))
     (void)LLHIP_CHECK(hipStreamSynchronize(the_device.stream));
 }
 
 void llhip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
-  if (ensure_device() && bytes)
+  if (ensure_device() && flush_pending_quantize() && bytes)
     (void)LLHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, the_device.stream));
 }
 
@@ -410,12 +458,13 @@ void *llhip_graph_end(void) {
     raise("llhip_graph_end: no capture is open");
     return nullptr;
   }
+  const bool flushed = flush_pending_quantize(); // a recorded quantization belongs to the captured sequence
   the_device.capturing = false;
   hipGraph_t graph;
   if (!LLHIP_CHECK(hipStreamEndCapture(the_device.stream, &graph)))
     return nullptr;
   hipGraphExec_t exec;
-  bool ok = LLHIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+  bool ok = flushed && LLHIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
   (void)hipGraphDestroy(graph);
   return ok ? (void *)exec : nullptr;
 }

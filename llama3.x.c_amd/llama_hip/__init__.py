@@ -188,11 +188,13 @@ def declared_functions():
     return names
 
 
-def load(path=LIB_PATH):
-    """The library with every entry point's argument types declared. Raises if it is not built."""
+def load(path=None):
+    """The library with every entry point's argument types declared. Raises if it is not built. LLAMA_HIP_LIB names
+    another build of it (a variant under test) instead of the in-tree one."""
     global _lib
     if _lib is not None:
         return _lib
+    path = path or os.environ.get("LLAMA_HIP_LIB") or LIB_PATH
     if not os.path.exists(path):
         raise FileNotFoundError(f"{path} is not built: run make -C llama3.x.c_amd (or __graft_entry__.build())")
     # One HIP runtime per process: torch's libtorch_hip links its bundled libamdhip64.so by file name, while this

@@ -383,3 +383,72 @@ def test_gemm_q8_reference_golden_and_backends():
             dots = np.zeros((k // gs, m, n), np.int32)
             L.llhip_q8_group_dots(lh.ptr(dots), lh.ptr(xq), m, k, gs, lh.ptr(wq), n)
             assert np.array_equal(dots, g[f"{key}/amx_dots"]), key
+
+
+# ---- the deferred (fused) quantization ------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("d,n", [(4096, 4096), (512, 14336), (300, 2048), (17, 1088)])
+def test_fused_quantize_gemv(d, n):
+    """k_quantize on device buffers is consumed by the next GEMV reading them: the output is within budget, q and s
+    hold the quantization bitwise afterwards, and a second consumer reads them from memory."""
+    L = hu.lib()
+    T = hu.torch()
+    gs = 64
+    rng = orc.Rng(orc.SEED + 909 + d)
+    wq, ws = synth_weights(rng, d, n, gs)
+    x = rng.normal(n, 0.0, 1.0)
+    xq, xs = orc.quantize(x, gs)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    xd, dwq, dws = hu.dev(x), hu.dev(wq), hu.dev(ws)
+    qd, sd = T.zeros(n, dtype=T.int8, device="cuda"), T.zeros(n // gs, dtype=T.float32, device="cuda")
+    out, out2 = hu.empty(d, T.float32), hu.dev(np.ones(d, np.float32))
+    T.cuda.synchronize()
+    L.k_quantize(lh.ptr(qd), lh.ptr(sd), lh.ptr(xd), n, gs)
+    L.k_matmul_q8(lh.ptr(out), lh.k8(qd, sd, xd), lh.w8(dwq, dws), n, d, gs)
+    L.k_matmul_q8_add(lh.ptr(out2), lh.k8(qd, sd, xd), lh.w8(dwq, dws), n, d, gs)
+    hu.assert_within_budget(hu.host(out), ref, mag, what="fused")
+    hu.assert_within_budget(hu.host(out2), ref + 1.0, mag + 1.0, what="second consumer")
+    assert np.array_equal(hu.host(qd), xq) and np.array_equal(hu.bits(hu.host(sd)), hu.bits(xs))
+
+
+def test_recorded_quantization_is_launched_by_other_calls():
+    L = hu.lib()
+    T = hu.torch()
+    n, gs = 2048, 64
+    rng = orc.Rng(orc.SEED + 910)
+    x = rng.normal(n, 0.0, 1.0)
+    xq, xs = orc.quantize(x, gs)
+    xd = hu.dev(x)
+    for trigger in ("synchronize", "other_call"):
+        qd, sd = T.zeros(n, dtype=T.int8, device="cuda"), T.zeros(n // gs, dtype=T.float32, device="cuda")
+        T.cuda.synchronize()
+        L.k_quantize(lh.ptr(qd), lh.ptr(sd), lh.ptr(xd), n, gs)
+        if trigger == "other_call":
+            other = hu.empty(64, T.float32)
+            y = hu.dev(np.ones(64, np.float32))
+            w = hu.dev(np.ones((64, 64), np.float32))
+            L.k_matmul(lh.ptr(other), lh.ptr(y), lh.ptr(w), 64, 64)
+        L.llhip_synchronize()
+        assert np.array_equal(hu.host(qd), xq) and np.array_equal(hu.bits(hu.host(sd)), hu.bits(xs)), trigger
+
+
+def test_fused_quantization_flags_nonfinite():
+    L = hu.lib()
+    T = hu.torch()
+    lh.record_failures()
+    try:
+        n, d, gs = 1024, 64, 64
+        x = np.ones(n, np.float32)
+        x[7] = np.nan
+        wq = np.ones((d, n), np.int8)
+        ws = np.full((d, n // gs), 0.01, np.float32)
+        xd, dwq, dws = hu.dev(x), hu.dev(wq), hu.dev(ws)
+        qd, sd, out = hu.empty(n, T.int8), hu.empty(n // gs, T.float32), hu.empty(d, T.float32)
+        L.k_quantize(lh.ptr(qd), lh.ptr(sd), lh.ptr(xd), n, gs)
+        L.k_matmul_q8(lh.ptr(out), lh.k8(qd, sd, xd), lh.w8(dwq, dws), n, d, gs)
+        L.llhip_synchronize()
+        assert "nonfinite activation during INT8 quantization" in lh.last_error()
+    finally:
+        L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+        L.llhip_clear_error()

@@ -1,0 +1,90 @@
+"""The device quantizer's reciprocal shortcut, checked on the CPU against the oracle. CPU only.
+
+The HIP quantizer (llama3.x.c_amd/csrc/gemv.hip, quantize_fast) rounds r = x * rcp(scale) instead of the exact
+quotient x / scale whenever |frac(|r|) - 0.5| >= 2^-12, and falls back to the exact quotient otherwise (and for
+subnormal x, zero or subnormal scales). The argument: |r - fl(x / scale)| < 2.3e-5 when rcp is within 1 ulp, so both
+round to the same integer outside the margin. Here the same steps run in float32 numpy with the reciprocal perturbed by
+-1, 0 and +1 ulp, on random groups and on inputs built to sit next to every rounding tie, and must reproduce the
+oracle's k_quantize bit for bit.
+"""
+import numpy as np
+
+from oracle import pyoracle as orc
+
+F32_MIN = np.float32(1.17549435e-38)
+
+
+def fast_quantize(x, gs, ulp_shift):
+    x = np.asarray(x, np.float32).reshape(-1, gs)
+    peak = np.max(np.abs(x), axis=1)
+    scale = (peak / np.float32(127.0)).astype(np.float32)
+    ok = scale >= F32_MIN
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        inv = np.where(ok, (np.float32(1.0) / np.where(ok, scale, 1)).astype(np.float32), np.float32(0))
+        for _ in range(abs(ulp_shift)):
+            inv = np.nextafter(inv, np.float32(np.inf if ulp_shift > 0 else 0)).astype(np.float32)
+        r = (x * inv[:, None]).astype(np.float32)
+        a = np.abs(r)
+        t = np.trunc(a).astype(np.float32)
+        f = (a - t).astype(np.float32)
+        near = np.abs(f - np.float32(0.5)) < np.float32(2.0 ** -12)
+        tiny = (x != 0) & (np.abs(x) < F32_MIN)
+        exact = ~ok[:, None] | tiny | near
+        m = np.minimum(t + (f > 0.5).astype(np.float32), np.float32(127)).astype(np.int32)
+        fast = np.where(r < 0, -m, m)
+    q_ref, s_ref = orc.quantize(x, gs)
+    q = np.where(exact, q_ref.astype(np.int32), fast)
+    return q.astype(np.int8), scale, exact.mean()
+
+
+def adversarial(rng, gs, groups):
+    """Groups whose max is 127 * scale exactly, with members at k + 0.5 +- a few ulps of the scaled value."""
+    out = []
+    for g in range(groups):
+        scale = np.float32(abs(rng.normal(1, 0.0, 1.0)[0]) * 10.0 ** rng.uniform(1, 6.0)[0] + 1e-6)
+        ks = np.floor(rng.uniform(gs - 1, 126.0)).astype(np.float32)
+        jitter = np.round(rng.uniform(gs - 1, 4.0)).astype(np.int32)
+        vals = []
+        for k, j in zip(ks, jitter):
+            v = np.float32((k + np.float32(0.5)) * scale)
+            for _ in range(abs(int(j))):
+                v = np.nextafter(v, np.float32(np.inf) if j > 0 else np.float32(-np.inf))
+            vals.append(v)
+        vals = np.array(vals, np.float32) * np.where(rng.uniform(gs - 1) < 0, -1, 1).astype(np.float32)
+        out.append(np.concatenate([[np.float32(127) * scale], vals]))
+    return np.concatenate(out).astype(np.float32)
+
+
+def test_fast_path_reproduces_k_quantize_bitwise():
+    rng = orc.Rng(orc.SEED + 31)
+    cases = [rng.normal(64 * 4096, 0.0, 1.0), rng.normal(64 * 1024, 0.0, 1e-3), rng.normal(64 * 1024, 0.0, 1e4),
+             adversarial(rng, 64, 2000)]
+    tiny = rng.normal(64 * 64, 0.0, 1.0) * np.float32(1e-38)
+    cases.append(tiny.astype(np.float32))
+    for x in cases:
+        want_q, want_s = orc.quantize(x.reshape(-1, 64), 64)
+        for shift in (-1, 0, 1):
+            q, s, exact_share = fast_quantize(x, 64, shift)
+            assert np.array_equal(s.view(np.uint32), want_s.ravel().view(np.uint32))
+            assert np.array_equal(q.ravel(), want_q.ravel()), shift
+
+
+def test_margin_catches_a_plausible_slip():
+    """Without the margin (always rounding r), the adversarial inputs disagree with k_quantize for some reciprocal
+    error: the fallback is what makes the shortcut exact."""
+    rng = orc.Rng(orc.SEED + 32)
+    x = adversarial(rng, 64, 3000).reshape(-1, 64)
+    want_q, _ = orc.quantize(x, 64)
+    peak = np.max(np.abs(x), axis=1)
+    scale = (peak / np.float32(127.0)).astype(np.float32)
+    mismatches = 0
+    for shift in (-1, 1):
+        inv = (np.float32(1.0) / scale).astype(np.float32)
+        inv = np.nextafter(inv, np.float32(np.inf if shift > 0 else 0)).astype(np.float32)
+        r = (x * inv[:, None]).astype(np.float32)
+        a = np.abs(r)
+        t = np.trunc(a)
+        m = np.minimum(t + ((a - t) >= 0.5), 127).astype(np.int32)
+        naive = np.where(r < 0, -m, m).astype(np.int8)
+        mismatches += int(np.sum(naive != want_q))
+    assert mismatches > 0
