@@ -11,7 +11,7 @@ int8-MFMA GEMMs (QKV, Wo + residual, W1/W3 SwiGLU, W2 + residual), then the last
 
 Weights ~N(0, 0.02) and activations ~N(0, 1) are drawn on the device (torch, seeded) and quantized by the library's
 own k_quantize rule; the data is synthetic. `roofline` is the dominant kernel of the decode step (the SwiGLU GEMV),
-timed launch by launch with HIP events on the library stream. `cpu_baseline` runs the reference's own gemm-bench
+its 32 launches captured into one graph and timed with HIP events on the library stream. `cpu_baseline` runs the reference's own gemm-bench
 (oracle/_ref, built from the reference's sources) on the same shapes on this host's cores.
 """
 import argparse
@@ -138,23 +138,54 @@ def time_graph(torch, L, graph, steps, warmup):
     return start.elapsed_time(end) / 1000.0
 
 
-def time_launches(torch, L, calls):
-    """GPU duration of each call's launch, bracketed by HIP events on the library stream. A spin kernel keeps the
-    stream busy while the host enqueues, so every event pair encloses its kernel and nothing else."""
+def time_per_launch(torch, L, calls, reps=5):
+    """Average GPU duration of one launch among `calls`: the calls are captured back to back into one HIP graph, the
+    graph is replayed `reps` times between HIP events on the library stream, and the median replay is divided by the
+    number of launches (the small gaps between graph nodes are included, so this never flatters the kernel)."""
+    L.llhip_synchronize()
+    assert L.llhip_graph_begin() == 0
+    for call in calls:
+        call()
+    graph = L.llhip_graph_end()
+    if not graph:
+        raise SystemExit("graph capture of the roofline launches failed")
     stream = torch.cuda.ExternalStream(L.llhip_stream())
+    L.llhip_graph_launch(graph)
     L.llhip_synchronize()
-    pairs = []
-    with torch.cuda.stream(stream):
-        torch.cuda._sleep(200_000_000)
-        for call in calls:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            call()
-            e1.record(stream)
-            pairs.append((e0, e1))
-    pairs[-1][1].synchronize()
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        L.llhip_graph_launch(graph)
+        e1.record(stream)
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) / 1000.0)
     L.llhip_synchronize()
-    return [a.elapsed_time(b) / 1000.0 for a, b in pairs]
+    L.llhip_graph_destroy(graph)
+    return sorted(times)[len(times) // 2] / len(calls)
+
+
+def copy_probe(torch, mib, reps=5):
+    """A plain copy kernel of known size (torch's elementwise multiply by 1 of `mib` MiB of FP32 into another buffer),
+    launched `reps` times: the calibration of the FETCH_SIZE / WRITE_SIZE counters in a --pmc run."""
+    n = mib * (1 << 20) // 4
+    src, dst = torch.ones(n, device="cuda"), torch.empty(n, device="cuda")
+    for _ in range(reps):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(f"# copy probe: {reps} x {mib} MiB read + {mib} MiB written", file=sys.stderr, flush=True)
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary (profiles/traffic.json, written from two
+    rocprofv3 --pmc runs of this script, FETCH_SIZE and WRITE_SIZE, scaled by the copy probe); None when absent."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)[kernel]
+        return int(rec["fetch_bytes"] + rec["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def prefill_set(torch, lh, model, seed):
@@ -267,6 +298,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--seed", type=int, default=88172645463325252 % (1 << 31))
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also launch a plain copy kernel of this many MiB (counter calibration for --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -300,7 +333,8 @@ def main():
     print(f"# decode: {seconds / args.steps * 1e3:.3f} ms/token, {tok_s:.1f} tok/s, "
           f"{step_bytes / (seconds / args.steps) / 1e9:.0f} GB/s over the step", file=sys.stderr, flush=True)
 
-    # roofline of the dominant kernel: the W1/W3 SwiGLU GEMV, one launch per layer, timed launch by launch
+    # roofline of the dominant kernel: the W1/W3 SwiGLU GEMV with the activation quantization fused in (the launch
+    # the step makes: k_quantize followed by k_matmul_q8_swiglu), one launch per layer
     sw_calls = []
     P = lh.ptr
     xq_probe = torch.empty(DIM, dtype=torch.int8, device="cuda")
@@ -308,22 +342,25 @@ def main():
     xf = torch.randn(DIM, device="cuda")
     hb = torch.empty(HIDDEN, device="cuda")
     torch.cuda.synchronize()
-    L.k_quantize(P(xq_probe), P(xs_probe), P(xf), DIM, GS)
     inp = lh.K8Input(P(xq_probe), P(xs_probe), None)
+
+    def swiglu(w1, w3):
+        L.k_quantize(P(xq_probe), P(xs_probe), P(xf), DIM, GS)
+        L.k_matmul_q8_swiglu(P(hb), inp, lh.K8Weight(P(w1[0]), P(w1[1])), lh.K8Weight(P(w3[0]), P(w3[1])), DIM,
+                             HIDDEN, GS)
+
     for lay in model.layers:
-        w1, w3 = lay["w1"], lay["w3"]
-        sw_calls.append(lambda w1=w1, w3=w3: L.k_matmul_q8_swiglu(P(hb), inp, lh.K8Weight(P(w1[0]), P(w1[1])),
-                                                                  lh.K8Weight(P(w3[0]), P(w3[1])), DIM, HIDDEN, GS))
-    durations = []
-    for _ in range(3):
-        durations += time_launches(torch, L, sw_calls)
-    avg = sum(durations) / len(durations)
-    sw_bytes = 2 * weight_bytes(HIDDEN, DIM) + DIM + DIM // GS * 4 + HIDDEN * 4
+        sw_calls.append(lambda w1=lay["w1"], w3=lay["w3"]: swiglu(w1, w3))
+    avg = time_per_launch(torch, L, sw_calls)
+    # weights and scales of W1 and W3, the FP32 input, the quantized input written back once, the FP32 output
+    sw_bytes = 2 * weight_bytes(HIDDEN, DIM) + DIM * 4 + DIM + DIM // GS * 4 + HIDDEN * 4
     achieved = sw_bytes / avg / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "q8_gemv<2, SWIGLU> (W1/W3 14336x4096 x2, gs 64)",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("q8_gemv_swiglu_fused"),
+                "kernel": "q8_gemv SwiGLU with fused quantization (W1/W3 2 x 14336x4096, gs 64)",
                 "avg_launch_us": round(avg * 1e6, 2), "bytes_per_launch": sw_bytes}
+    if args.copy_probe_mib:
+        copy_probe(torch, args.copy_probe_mib)
 
     result = {
         "metric": "8B Q8_0 decode tok/s (%HBM peak); 2048-tok prefill tok/s (%MFMA peak)",
@@ -347,10 +384,9 @@ def main():
         pgraph = L.llhip_graph_end()
         psec = time_graph(torch, L, pgraph, args.prefill_steps, 1)
         ptok = PROMPT * args.prefill_steps / psec
-        # the dominant prefill kernel: the W1/W3 SwiGLU GEMM (2048 x 2 x 14336 x 4096), timed launch by launch
+        # the dominant prefill kernel: the W1/W3 SwiGLU GEMM (2048 x 2 x 14336 x 4096), one launch per layer
         w13 = [c for i, (c, _) in enumerate(gemms) if i % 4 == 2]
-        d = time_launches(torch, L, w13)
-        pavg = sum(d) / len(d)
+        pavg = time_per_launch(torch, L, w13, reps=2)
         w13_ops = 2 * PROMPT * DIM * HIDDEN * 2
         ach = w13_ops / pavg / 1e12
         result["prefill"] = {
@@ -359,7 +395,7 @@ def main():
                         "(QKV, Wo +resid, W1/W3 SwiGLU, W2 +resid) + last-row classifier GEMV, gs 64",
             "ops_per_prompt": ops, "tops": round(ops / (psec / args.prefill_steps) / 1e12, 1),
             "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                         "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": None,
+                         "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": measured_traffic("q8_gemm_swiglu"),
                          "kernel": "q8_gemm_mfma (W1/W3 SwiGLU 2048x(2x14336)x4096)",
                          "avg_launch_us": round(pavg * 1e6, 1)},
         }
