@@ -137,6 +137,37 @@ typedef struct {
 } PackS8;
 void pack_s8_vnni_many(const PackS8 *jobs, int count);
 
+/* shards.h:10, 28-38, 66-78: the loaded weight shard the packing jobs of gemm.h:146-153 read, in the reference's
+ * layout (role is a TensorRole). */
+typedef enum { DT_F32, DT_Q8 } TensorDtype;
+typedef enum { SHARD_ROWS, SHARD_COLS, SHARD_COPY, SHARD_GLOBAL } ShardKind;
+typedef struct {
+  int role;
+  int layer;
+  int rows, cols;
+  TensorDtype dtype;
+  int group_size;
+  size_t offset;
+  size_t scale_offset;
+  size_t bytes;
+  int alias_of;
+} TensorDesc;
+typedef struct {
+  const TensorDesc *src;
+  ShardKind kind;
+  int socket;
+  int row0, rows, col0, cols;
+  int alias;
+  size_t q_offset, s_offset;
+  void *q;
+  float *s;
+  size_t ld;
+} Shard;
+/* gemm.h:152-153: the packing job of a bound ROWS or COLS shard of the right dtype (FP32 for BF16, Q8 for int8) at its
+ * own stride; anything else fails with the reference's message. */
+PackBf16 pack_bf16_job_from_shard(uint16_t *dst, const Shard *shard);
+PackS8 pack_s8_job_from_shard(int8_t *dst, const Shard *shard);
+
 /* testing.h:27, 61-69 analogues. k_gemm_f32_portable runs the device FP32 GEMM (kc is ignored: no K blocking);
  * k_gemm_f32_simd_test returns 0 (no CPU SIMD kernel here); k_gemv_force_hybrid is accepted (one device schedule).
  * k_gemm_q8_backend_test runs one named backend (Q8_GEMM_HIP_MFMA or Q8_GEMM_PORTABLE; returns 0 for the CPU ones). llhip_q8_group_dots is the int32 probe: the exact group dots the MFMA kernel forms,

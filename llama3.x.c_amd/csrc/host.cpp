@@ -142,14 +142,49 @@ void pack_s8_vnni(int8_t *dst, const int8_t *w, int rows, int cols, size_t ld) {
   pack_s8_vnni_tiles(dst, w, rows, cols, ld, 0, (rows + 15) / 16);
 }
 
+// gemm.c:1094-1100: the tile count of a job list must fit an int.
+static bool tiles_fit(long long tiles) {
+  return tiles <= INT32_MAX || raise("too many weight tiles to pack: %lld", tiles);
+}
+
 void pack_bf16_vnni_many(const PackBf16 *jobs, int count) {
+  long long tiles = 0;
+  for (int i = 0; i < count; i++)
+    tiles += (jobs[i].rows + 15) / 16;
+  if (!tiles_fit(tiles))
+    return;
   for (int i = 0; i < count; i++)
     pack_bf16_vnni(jobs[i].dst, jobs[i].w, jobs[i].rows, jobs[i].cols, jobs[i].ld);
 }
 
 void pack_s8_vnni_many(const PackS8 *jobs, int count) {
+  long long tiles = 0;
+  for (int i = 0; i < count; i++)
+    tiles += (jobs[i].rows + 15) / 16;
+  if (!tiles_fit(tiles))
+    return;
   for (int i = 0; i < count; i++)
     pack_s8_vnni(jobs[i].dst, jobs[i].w, jobs[i].rows, jobs[i].cols, jobs[i].ld);
+}
+
+// gemm.c:1103-1115: a job packs a bound ROWS / COLS shard of the matching dtype where it lives.
+static bool packable(const Shard *shard, TensorDtype dtype, const char *what) {
+  if (!shard || !shard->q || !shard->src || (shard->kind != SHARD_ROWS && shard->kind != SHARD_COLS) ||
+      shard->src->dtype != dtype || shard->rows <= 0 || shard->cols <= 0 || shard->ld < (size_t)shard->cols)
+    return raise("%s needs a bound ROWS or COLS %s shard", what, dtype == DT_F32 ? "FP32" : "Q8_0");
+  return true;
+}
+
+PackBf16 pack_bf16_job_from_shard(uint16_t *dst, const Shard *shard) {
+  if (!packable(shard, DT_F32, "pack_bf16_job_from_shard"))
+    return PackBf16{};
+  return PackBf16{dst, (const float *)shard->q, shard->rows, shard->cols, shard->ld};
+}
+
+PackS8 pack_s8_job_from_shard(int8_t *dst, const Shard *shard) {
+  if (!packable(shard, DT_Q8, "pack_s8_job_from_shard"))
+    return PackS8{};
+  return PackS8{dst, (const int8_t *)shard->q, shard->rows, shard->cols, shard->ld};
 }
 
 // ---- aligned workspace (gemm.c:400-411) ----------------------------------------------------------------------------

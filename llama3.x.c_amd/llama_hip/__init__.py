@@ -59,6 +59,29 @@ class AlignedBuffer(ctypes.Structure):
     _fields_ = [("base", P), ("data", P), ("bytes", SZ)]
 
 
+class PackBf16(ctypes.Structure):
+    _fields_ = [("dst", P), ("w", P), ("rows", I32), ("cols", I32), ("ld", SZ)]
+
+
+class PackS8(ctypes.Structure):
+    _fields_ = [("dst", P), ("w", P), ("rows", I32), ("cols", I32), ("ld", SZ)]
+
+
+DT_F32, DT_Q8 = 0, 1
+SHARD_ROWS, SHARD_COLS, SHARD_COPY, SHARD_GLOBAL = 0, 1, 2, 3
+
+
+class TensorDesc(ctypes.Structure):
+    _fields_ = [("role", I32), ("layer", I32), ("rows", I32), ("cols", I32), ("dtype", I32), ("group_size", I32),
+                ("offset", SZ), ("scale_offset", SZ), ("bytes", SZ), ("alias_of", I32)]
+
+
+class Shard(ctypes.Structure):
+    _fields_ = [("src", ctypes.POINTER(TensorDesc)), ("kind", I32), ("socket", I32), ("row0", I32), ("rows", I32),
+                ("col0", I32), ("cols", I32), ("alias", I32), ("q_offset", SZ), ("s_offset", SZ), ("q", P),
+                ("s", P), ("ld", SZ)]
+
+
 class Config(ctypes.Structure):
     _fields_ = [(f, I32) for f in ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size", "seq_len",
                                    "format", "max_seq_len", "shared", "head_dim")] + \
@@ -130,6 +153,8 @@ _SIGNATURES = {
     "pack_s8_vnni_tiles": (None, [P, P, I32, I32, SZ, I32, I32]),
     "pack_bf16_vnni_many": (None, [P, I32]),
     "pack_s8_vnni_many": (None, [P, I32]),
+    "pack_bf16_job_from_shard": (PackBf16, [P, ctypes.POINTER(Shard)]),
+    "pack_s8_job_from_shard": (PackS8, [P, ctypes.POINTER(Shard)]),
     "amx_bf16_tile_gemm": (None, [P, SZ, P, SZ, P, I32, I32, I32]),
     "amx_s8_tile_gemm": (None, [P, SZ, P, SZ, P, I32, I32, I32]),
     "aligned_buffer_alloc": (None, [ctypes.POINTER(AlignedBuffer), SZ, I32]),

@@ -46,6 +46,8 @@ def test_struct_layouts_match_the_reference():
     assert ctypes.sizeof(lh.GemmBf16Segment) == 40 and lh.GemmBf16Segment.kind.offset == 36
     assert ctypes.sizeof(lh.GemmQ8Segment) == 72 and lh.GemmQ8Segment.pw.offset == 48 and lh.GemmQ8Segment.n.offset == 64
     assert ctypes.sizeof(lh.AlignedBuffer) == 24
+    assert ctypes.sizeof(lh.PackBf16) == 32 and ctypes.sizeof(lh.PackS8) == 32
+    assert ctypes.sizeof(lh.TensorDesc) == 56 and ctypes.sizeof(lh.Shard) == 80 and lh.Shard.q.offset == 56
     assert ctypes.sizeof(lh.Config) == 44 + 20 + 24 + 128
     assert lh.Model.max_batch.offset == ctypes.sizeof(lh.Config) + 4 + 8 + 8 + 8 - 4 or lh.Model.max_batch.offset > 0
 
@@ -60,9 +62,11 @@ def test_reference_headers_agree_on_layouts():
 #include <stdio.h>
 #include "gemm.h"
 #include "prefill.h"
+#include "shards.h"
 int main(void) {
-  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(K8Weight), sizeof(K8Input), sizeof(GemmSegment),
-         sizeof(GemmBf16Segment), sizeof(GemmQ8Segment), sizeof(AlignedBuffer), sizeof(Config), sizeof(Model),
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(K8Weight), sizeof(K8Input),
+         sizeof(GemmSegment), sizeof(GemmBf16Segment), sizeof(GemmQ8Segment), sizeof(AlignedBuffer), sizeof(Config),
+         sizeof(Model), sizeof(TensorDesc), sizeof(Shard), sizeof(PackS8), offsetof(Shard, ld),
          offsetof(Model, max_batch), offsetof(Model, prefill_bf16));
   return 0;
 }
@@ -76,8 +80,8 @@ int main(void) {
                    check=True)
     sizes = [int(v) for v in subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()]
     mine = [ctypes.sizeof(c) for c in (lh.K8Weight, lh.K8Input, lh.GemmSegment, lh.GemmBf16Segment, lh.GemmQ8Segment,
-                                       lh.AlignedBuffer, lh.Config, lh.Model)]
-    mine += [lh.Model.max_batch.offset, lh.Model.prefill_bf16.offset]
+                                       lh.AlignedBuffer, lh.Config, lh.Model, lh.TensorDesc, lh.Shard, lh.PackS8)]
+    mine += [lh.Shard.ld.offset, lh.Model.max_batch.offset, lh.Model.prefill_bf16.offset]
     assert sizes == mine
 
 
@@ -95,6 +99,35 @@ def test_status_functions(L):
     chunks = (ctypes.c_int * 3)(4, 0, 2)
     L.kernels_parallel_segments(3, chunks, fn, None)
     assert calls == [(0, 0, 4), (2, 0, 2)]
+
+
+def test_pack_jobs_from_shards(record):
+    """gemm.c:1103-1115: a bound ROWS / COLS shard of the right dtype gives a job at its own stride; anything else fails
+    with the reference's message."""
+    L = record
+    desc_f, desc_q = lh.TensorDesc(dtype=lh.DT_F32, rows=40, cols=96), lh.TensorDesc(dtype=lh.DT_Q8, rows=40, cols=96)
+    w = np.zeros((33, 100), np.float32)
+    shard = lh.Shard(src=ctypes.pointer(desc_f), kind=lh.SHARD_COLS, rows=33, cols=96, q=w.ctypes.data, ld=100)
+    dst = np.zeros(L.bf16_vnni_elements(33, 96), np.uint16)
+    job = L.pack_bf16_job_from_shard(dst.ctypes.data, shard)
+    assert (job.dst, job.w, job.rows, job.cols, job.ld) == (dst.ctypes.data, w.ctypes.data, 33, 96, 100)
+    assert L.llhip_last_error() == b""
+    L.pack_s8_job_from_shard(None, shard)  # FP32 shard for an int8 job
+    assert L.llhip_last_error() == b"pack_s8_job_from_shard needs a bound ROWS or COLS Q8_0 shard"
+    L.llhip_clear_error()
+    qshard = lh.Shard(src=ctypes.pointer(desc_q), kind=lh.SHARD_COPY, rows=33, cols=96, q=w.ctypes.data, ld=100)
+    L.pack_s8_job_from_shard(None, qshard)  # COPY shards are not packable
+    assert L.llhip_last_error() == b"pack_s8_job_from_shard needs a bound ROWS or COLS Q8_0 shard"
+    L.llhip_clear_error()
+    qshard.kind, qshard.ld = lh.SHARD_ROWS, 95  # stride shorter than a row
+    L.pack_s8_job_from_shard(None, qshard)
+    assert L.llhip_last_error() == b"pack_s8_job_from_shard needs a bound ROWS or COLS Q8_0 shard"
+    L.llhip_clear_error()
+    qshard.ld = 96
+    job = L.pack_s8_job_from_shard(None, qshard)
+    assert (job.rows, job.cols, job.ld) == (33, 96, 96) and L.llhip_last_error() == b""
+    L.pack_bf16_job_from_shard(None, None)
+    assert L.llhip_last_error() == b"pack_bf16_job_from_shard needs a bound ROWS or COLS FP32 shard"
 
 
 def test_host_packers_and_bf16_match_the_oracle(L):
