@@ -73,6 +73,13 @@ void llhip_set_fail_mode(int mode);
 const char *llhip_last_error(void); /* "" when none */
 void llhip_clear_error(void);
 
+/* Launch shape of the streaming Q8 GEMV: waves per weight row (1, 2, 4 or 8; 0 = by K), resident 8-wave block
+ * equivalents per CU of its persistent grid (1..64; 0 = 2) and waves per block (8 or 16; 0 = 16; 16-wave blocks need
+ * an even block count per CU, else 8 is used). Results do not depend on it beyond FP32 summation order. For tuning
+ * and tests; LLAMA_HIP_GEMV_KSPLIT, LLAMA_HIP_GEMV_BLOCKS_PER_CU and LLAMA_HIP_GEMV_BLOCK_WAVES set the same at
+ * start-up. */
+void llhip_set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves);
+
 /* The int32 probe of the decode GEMV: dots[g * d + r] = the exact int32 dot of group g of input row xq and weight
  * row r, as the streaming GEMV kernel itself forms it before the FP32 rescale (gs % 16 == 0 takes the fast kernel). */
 void llhip_q8_gemv_group_dots(int32_t *dots, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws,

@@ -268,8 +268,8 @@ void gemm_q8(const char *name, bool mfma, const int8_t *xq, const float *xs, int
   bool aligned = ((uintptr_t)job.xq & 15) == 0;
   for (int s = 0; s < nseg; s++)
     aligned = aligned && ((uintptr_t)job.seg[s].w & 15) == 0 && ((uintptr_t)job.seg[s].w3 & 15) == 0;
-  const bool ok = mfma && gs % 64 == 0 && aligned ? launch_q8_gemm(job, call.stream())
-                                                  : launch_q8_gemm_generic(job, call.stream());
+  const bool ok = mfma && aligned && q8_gemm_fast_path(job.xq, m, k, gs) ? launch_q8_gemm(job, call.stream())
+                                                                          : launch_q8_gemm_generic(job, call.stream());
   if (ok)
     call.finish();
 }
@@ -498,9 +498,17 @@ void llhip_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs, 
   Ref D = call.out(dots, (size_t)(k / gs) * m * n * sizeof(int32_t), false);
   if (!call.ready())
     return;
+  if (!q8_gemm_fast_path(call.ptr<const int8_t>(XQ), m, k, gs))
+    return (void)raise("llhip_q8_group_dots: the shape (m %d, K %d) is outside the MFMA kernel's range", m, k);
   if (launch_q8_group_dots(call.ptr<int32_t>(D), call.ptr<const int8_t>(XQ), m, k, gs, call.ptr<const int8_t>(WQ), n,
                            call.stream()))
     call.finish();
+}
+
+void llhip_set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves) {
+  // the next launches use it: launch any recorded quantization under the shape it was recorded with
+  if (ensure_device() && flush_pending_quantize())
+    (void)set_gemv_shape(waves_per_row, blocks_per_cu, block_waves);
 }
 
 void llhip_q8_gemv_group_dots(int32_t *dots, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws,

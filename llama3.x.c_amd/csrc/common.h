@@ -128,6 +128,7 @@ struct GemvJob {
   int8_t *xq_out;
   float *xs_out;
 };
+bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves);
 bool gemv_fast_path(const GemvJob &job);
 bool launch_q8_gemv(const GemvJob &job, hipStream_t stream);
 
@@ -162,6 +163,7 @@ struct GemmQ8Job {
   GemmSegmentDev seg[3];
   int nseg;
 };
+bool q8_gemm_fast_path(const int8_t *xq, int m, int k, int gs); // the pipelined int8-MFMA kernel takes the shape
 bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream);
 bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream);
 bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs, const int8_t *wq, int n,

@@ -111,65 +111,121 @@ __device__ __forceinline__ void store_tile(const TileSeg &seg, const TilePos &t,
     }
 }
 
-// ---- W8A8 Q8_0 on int8 MFMA -----------------------------------------------------------------------------------------
+// ---- W8A8 Q8_0: the pipelined int8-MFMA kernel ------------------------------------------------------------------------
+//
+// 512 threads own a 256 x 128 output tile (a 128-column tile holds 64 columns of W1 and the same 64 of W3 under
+// SWIGLU); eight waves in 4 x 2 each own 64 x 64 as 4 x 4 v_mfma_i32_16x16x64_i8 tiles. A K step is 64 values. Its A
+// and B tiles (256 x 64 and 128 x 64 int8) and their group scales travel from global memory straight into LDS with
+// buffer loads (no register staging), four steps deep: at step s the block waits for step s's loads, then issues step
+// s + 3's into the stage step s - 1 used. In LDS a tile row is 64 bytes whose four 16-byte chunks are XOR-swizzled by
+// (row / 2) % 4, so the MFMA operand reads (16 rows, one chunk each) fall on distinct banks. At a group's last step
+// every output adds ((float)dot * ws) * xs to its FP32 accumulator; two waves per SIMD let one wave's rescale run while
+// the other's MFMAs do.
+constexpr int kQ8Waves = 8, kQ8Threads = kQ8Waves * 64;
+constexpr int kQ8TileM = 256, kQ8TileN = 128, kQ8Stages = 4;
+constexpr int kQ8LoadsPerStep = 4; // per wave: two A, one B and one scale load
 
-constexpr int kQ8Pitch = 80; // LDS row pitch in bytes for 64 int8 values: 16-byte aligned, spreads rows over banks
+struct Q8Stage {
+  int8_t a[kQ8TileM * 64];
+  int8_t b[kQ8TileN * 64];
+  float xs[kQ8TileM];
+  float ws[kQ8TileN];
+  float spare[64]; // where the two waves without a scale share load theirs (zero-length loads)
+};
+constexpr size_t kQ8Lds = kQ8Stages * sizeof(Q8Stage);
+
+__device__ __forceinline__ int q8_swizzle(int row) { return (row >> 1) & 3; }
+
+struct Q8Grid {
+  TileSeg seg[3];
+  int nseg;
+  int mtiles;
+  int total;
+};
 
 struct Q8Params {
-  TileGrid grid;
+  Q8Grid grid;
   const int8_t *xq;
   const float *xs;
   int m, k, gs;
   int32_t *probe; // optional (one segment, no SWIGLU): probe[(g * m + r) * n + c]
 };
 
-// One K step is 64 values, one v_mfma_i32_16x16x64_i8 per 16 x 16 tile. A group of gs values is gs / 64 steps whose
-// int32 results accumulate in the MFMA itself (exact: |dot| <= 64 * 127 * 127 * steps < 2^31); at the group's last
-// step every output adds ((float)dot * ws[n][g]) * xs[m][g] to its FP32 accumulator (src/gemv.c:428's expression).
+__device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical) {
+  int s = 0;
+  while (s + 1 < g.nseg && logical >= g.seg[s + 1].first_tile)
+    s++;
+  const int local = logical - g.seg[s].first_tile;
+  TilePos t;
+  t.s = s;
+  t.swiglu = g.seg[s].epi == EPI_SWIGLU;
+  t.m0 = (local % g.mtiles) * kQ8TileM;
+  t.n0 = (local / g.mtiles) * (t.swiglu ? kQ8TileN / 2 : kQ8TileN);
+  return t;
+}
+
+__device__ __forceinline__ TileSeg q8_seg_of(const Q8Grid &g, int s) {
+  return s == 0 ? g.seg[0] : s == 1 ? g.seg[1] : g.seg[2];
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t q8_buffer(const void *base, long long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)(bytes > 0 ? bytes : 0),
+                                           0x00020000);
+}
+
 template <bool PROBE>
-__global__ __launch_bounds__(kBlock) void q8_gemm_mfma(Q8Params p) {
-  __shared__ __align__(16) int8_t sa[2][kTile * kQ8Pitch];
-  __shared__ __align__(16) int8_t sb[2][kTile * kQ8Pitch];
-  __shared__ float sscale[2][2 * kTile]; // [0, 128): xs of the tile rows, [128, 256): ws of the B rows
+__global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
+  extern __shared__ __align__(16) unsigned char q8_smem[];
+  Q8Stage *stage = reinterpret_cast<Q8Stage *>(q8_smem);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const TilePos t = q8_tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
+  const TileSeg seg = q8_seg_of(p.grid, t.s);
+  const int groups = p.k / p.gs, spg = p.gs / 64, steps = p.k / 64;
+  const long long k = p.k;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-  const TilePos t = tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
-  const TileSeg seg = seg_of(p.grid, t.s);
-  const int groups = p.k / p.gs, steps_per_group = p.gs / 64, steps = p.k / 64;
-  const int8_t *w1 = (const int8_t *)seg.w, *w3 = (const int8_t *)seg.w3;
+  // This wave's share of every step's loads, as buffer resources bounded to the rows that exist (rows past m or n
+  // read zeros) and per-lane offsets that place lane l's 16 bytes at l * 16 of the wave's 1 KB of LDS.
+  const int ra = 32 * wave + (lane >> 2); // A rows ra and ra + 16
+  const __amdgpu_buffer_rsrc_t rA = q8_buffer(p.xq + (long long)t.m0 * k, (long long)min(kQ8TileM, p.m - t.m0) * k);
+  const int offA0 = (int)(ra * k) + (((lane & 3) ^ q8_swizzle(ra)) << 4);
+  const int offA1 = (int)((ra + 16) * k) + (((lane & 3) ^ q8_swizzle(ra + 16)) << 4);
+  const int rb = 16 * wave + (lane >> 2); // B tile row
+  const bool second = t.swiglu && wave >= 4;
+  const int col0 = t.swiglu ? t.n0 + ((16 * wave) & 63) : t.n0 + 16 * wave;
+  const int8_t *wmat = (const int8_t *)(second ? seg.w3 : seg.w);
+  const __amdgpu_buffer_rsrc_t rB = q8_buffer(wmat + (long long)col0 * k, (long long)min(16, seg.n - col0) * k);
+  const int offB = (int)((lane >> 2) * k) + (((lane & 3) ^ q8_swizzle(rb)) << 4);
+  // scale loads: waves 0-3 the 256 xs rows, waves 4-5 the 128 ws rows, waves 6-7 nothing
+  __amdgpu_buffer_rsrc_t rS;
+  int scale_dst; // float index in the stage: xs at 0, ws at kQ8TileM, spare after
+  if (wave < 4) {
+    const int r0 = t.m0 + 64 * wave;
+    rS = q8_buffer(p.xs + (long long)r0 * groups, (long long)min(64, p.m - r0) * groups * 4);
+    scale_dst = 64 * wave;
+  } else if (wave < 6) {
+    const int h = wave - 4;
+    const float *src = t.swiglu ? (h ? seg.w3s : seg.ws) : seg.ws;
+    const int c0 = t.swiglu ? t.n0 : t.n0 + 64 * h;
+    rS = q8_buffer(src + (long long)c0 * groups, (long long)min(64, seg.n - c0) * groups * 4);
+    scale_dst = kQ8TileM + 64 * h;
+  } else {
+    rS = q8_buffer(p.xs, 0);
+    scale_dst = kQ8TileM + kQ8TileN;
+  }
+  const int offS = lane * groups * 4;
+  const __amdgpu_buffer_rsrc_t none = q8_buffer(p.xq, 0);
 
-  // Global -> register staging: thread t moves 16-byte chunks t and t + 256 of each 128 x 64 tile.
-  int4 ra[2], rb[2];
-  float rs;
-  auto load = [&](int step) {
-    const int k0 = step * 64;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const int chunk = tid + h * kBlock, r = chunk >> 2, c16 = (chunk & 3) * 16;
-      const int row = t.m0 + r;
-      ra[h] = row < p.m ? *reinterpret_cast<const int4 *>(p.xq + (long long)row * p.k + k0 + c16) : int4{0, 0, 0, 0};
-      const int col = b_col(t, r);
-      const int8_t *wsrc = (t.swiglu && r >= 64) ? w3 : w1;
-      rb[h] = col < seg.n ? *reinterpret_cast<const int4 *>(wsrc + (long long)col * p.k + k0 + c16) : int4{0, 0, 0, 0};
-    }
-    const int g = k0 / p.gs;
-    if (tid < kTile) {
-      const int row = t.m0 + tid;
-      rs = row < p.m ? p.xs[(long long)row * groups + g] : 0.0f;
-    } else {
-      const int r = tid - kTile, col = b_col(t, r);
-      const float *src = (t.swiglu && r >= 64) ? seg.w3s : seg.ws;
-      rs = col < seg.n ? src[(long long)col * groups + g] : 0.0f;
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const int chunk = tid + h * kBlock, r = chunk >> 2, c16 = (chunk & 3) * 16;
-      *reinterpret_cast<int4 *>(&sa[buf][r * kQ8Pitch + c16]) = ra[h];
-      *reinterpret_cast<int4 *>(&sb[buf][r * kQ8Pitch + c16]) = rb[h];
-    }
-    sscale[buf][tid] = rs;
+  // Issue the loads of K step `step` into stage `st`; a step past the end loads nothing (zero-length resources).
+  auto issue = [&](int step, int st) {
+    const bool live = step < steps;
+    const int k0 = step * 64, g = step / spg;
+    Q8Stage &S = stage[st];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, &S.a[(32 * wave) * 64], 16, offA0 + k0, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, &S.a[(32 * wave + 16) * 64], 16, offA1 + k0, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB : none, &S.b[(16 * wave) * 64], 16, offB + k0, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rS : none, &S.xs[scale_dst], 4, offS + g * 4, 0, 0, 0);
   };
 
   v4f acc[4][4];
@@ -182,54 +238,60 @@ __global__ __launch_bounds__(kBlock) void q8_gemm_mfma(Q8Params p) {
       dot[i][j] = v4i{0, 0, 0, 0};
     }
 
-  load(0);
-  store(0);
-  __syncthreads();
-  const int lrow = lane & 15, lk = (lane >> 4) * 16;
+#pragma unroll
+  for (int s = 0; s < kQ8Stages - 1; s++)
+    issue(s, s);
+  const int lrow = lane & 15, lq = lane >> 4, lr4 = (lane >> 4) * 4;
   for (int step = 0; step < steps; step++) {
-    const int buf = step & 1;
-    if (step + 1 < steps)
-      load(step + 1);
+    // this wave's loads of `step` have landed once no more than those of the (kQ8Stages - 2) later steps are
+    // outstanding; the barrier then makes every wave's landed
+    __builtin_amdgcn_s_waitcnt((((kQ8Stages - 2) * kQ8LoadsPerStep) & 15) | (0x7 << 4) | (0xF << 8) |
+                               ((((kQ8Stages - 2) * kQ8LoadsPerStep) >> 4) << 14));
+    __builtin_amdgcn_s_barrier();
+    issue(step + kQ8Stages - 1, (step + kQ8Stages - 1) % kQ8Stages);
+    const Q8Stage &S = stage[step % kQ8Stages];
     v4i a[4], b[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      a[i] = *reinterpret_cast<const v4i *>(&sa[buf][(wm * 64 + 16 * i + lrow) * kQ8Pitch + lk]);
+    for (int i = 0; i < 4; i++) {
+      const int row = wm * 64 + 16 * i + lrow;
+      a[i] = *reinterpret_cast<const v4i *>(&S.a[row * 64 + ((lq ^ q8_swizzle(row)) << 4)]);
+    }
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-      b[j] = *reinterpret_cast<const v4i *>(&sb[buf][(b_row(t.swiglu, wn, j) + lrow) * kQ8Pitch + lk]);
+    for (int j = 0; j < 4; j++) {
+      const int row = b_row(t.swiglu, wn, j) + lrow;
+      b[j] = *reinterpret_cast<const v4i *>(&S.b[row * 64 + ((lq ^ q8_swizzle(row)) << 4)]);
+    }
+    const bool first = step % spg == 0;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], dot[i][j], 0, 0, 0);
-    if ((step + 1) % steps_per_group == 0) {
-      const int g = step / steps_per_group;
-      const int lr = (lane >> 4) * 4;
+        dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], first ? v4i{0, 0, 0, 0} : dot[i][j], 0, 0, 0);
+    if (step % spg == spg - 1) {
+      const int g = step / spg;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const v4f xsv = *reinterpret_cast<const v4f *>(&sscale[buf][wm * 64 + 16 * i + lr]);
+        const v4f xsv = *reinterpret_cast<const v4f *>(&S.xs[wm * 64 + 16 * i + lr4]);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const float wsc = sscale[buf][kTile + b_row(t.swiglu, wn, j) + lrow];
+          const float wsc = S.ws[b_row(t.swiglu, wn, j) + lrow];
 #pragma unroll
           for (int e = 0; e < 4; e++)
-            acc[i][j][e] += ((float)dot[i][j][e] * wsc) * xsv[e];
+            acc[i][j][e] = fmaf((float)dot[i][j][e] * wsc, xsv[e], acc[i][j][e]);
           if (PROBE) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-              const int row = t.m0 + wm * 64 + 16 * i + lr + e, col = t.n0 + 64 * wn + 16 * j + lrow;
+              const int row = t.m0 + wm * 64 + 16 * i + lr4 + e, col = t.n0 + 64 * wn + 16 * j + lrow;
               if (row < p.m && col < seg.n)
                 p.probe[((long long)g * p.m + row) * seg.n + col] = dot[i][j][e];
             }
           }
-          dot[i][j] = v4i{0, 0, 0, 0};
         }
       }
     }
-    if (step + 1 < steps)
-      store(buf ^ 1);
-    __syncthreads();
   }
+  // the loads issued for steps past the end still target this block's LDS: let them land before the block exits
+  __builtin_amdgcn_s_waitcnt(0);
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
@@ -468,13 +530,48 @@ TileGrid make_grid(const GemmSegmentDev *segs, int nseg, int m) {
   return g;
 }
 
+Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m) {
+  Q8Grid g{};
+  g.nseg = nseg;
+  g.mtiles = (m + kQ8TileM - 1) / kQ8TileM;
+  int tiles = 0;
+  for (int s = 0; s < nseg; s++) {
+    const GemmSegmentDev &d = segs[s];
+    const int width = d.epi == EPI_SWIGLU ? kQ8TileN / 2 : kQ8TileN;
+    g.seg[s] = TileSeg{d.c, d.ldc, d.w, d.w3, d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width};
+    tiles += g.seg[s].ntiles * g.mtiles;
+  }
+  g.total = tiles;
+  return g;
+}
+
+// The pipelined kernel takes more than the default 64 KB of dynamic LDS: raised once per instantiation.
+template <bool PROBE> bool q8_lds_ready() {
+  static const hipError_t status =
+      hipFuncSetAttribute((const void *)q8_gemm_lds<PROBE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ8Lds);
+  return check_hip(status, "allowing the Q8 GEMM its LDS");
+}
+
+template <bool PROBE> bool launch_q8_lds(const Q8Params &p, hipStream_t stream) {
+  if (!q8_lds_ready<PROBE>())
+    return false;
+  hipLaunchKernelGGL(q8_gemm_lds<PROBE>, dim3(p.grid.total), dim3(kQ8Threads), kQ8Lds, stream, p);
+  return launch_ok("q8_gemm_lds");
+}
+
 } // namespace
+
+// Shapes the pipelined kernel takes: gs a multiple of 64, 16-byte aligned operands whose 32-bit buffer offsets fit.
+bool q8_gemm_fast_path(const int8_t *xq, int m, int k, int gs) {
+  return gs > 0 && gs % 64 == 0 && k % gs == 0 && ((uintptr_t)xq & 15) == 0 &&
+         (long long)kQ8TileM * k < (1LL << 31) && (long long)m * (k / gs) * 4 < (1LL << 31);
+}
 
 bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream) {
   if (job.m <= 0 || job.k <= 0)
     return true;
   Q8Params p{};
-  p.grid = make_grid(job.seg, job.nseg, job.m);
+  p.grid = make_q8_grid(job.seg, job.nseg, job.m);
   p.xq = job.xq;
   p.xs = job.xs;
   p.m = job.m;
@@ -482,8 +579,7 @@ bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream) {
   p.gs = job.gs;
   if (p.grid.total <= 0)
     return true;
-  hipLaunchKernelGGL(q8_gemm_mfma<false>, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
-  return launch_ok("q8_gemm_mfma");
+  return launch_q8_lds<false>(p, stream);
 }
 
 bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream) {
@@ -517,15 +613,14 @@ bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs,
     return false;
   GemmSegmentDev seg{scratch, n, wq, nullptr, ones, nullptr, (size_t)k, n, EPI_STORE};
   Q8Params p{};
-  p.grid = make_grid(&seg, 1, m);
+  p.grid = make_q8_grid(&seg, 1, m);
   p.xq = xq;
   p.xs = ones;
   p.m = m;
   p.k = k;
   p.gs = gs;
   p.probe = dots;
-  hipLaunchKernelGGL(q8_gemm_mfma<true>, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
-  bool ok = launch_ok("q8_gemm_mfma (probe)");
+  bool ok = launch_q8_lds<true>(p, stream);
   (void)hipFreeAsync(scratch, stream);
   (void)hipFreeAsync(ones, stream);
   return ok;

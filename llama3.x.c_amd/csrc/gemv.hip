@@ -3,6 +3,7 @@
 // Lane layout shared by the quantizer and the GEMV: a wave covers 1024 consecutive values of a row per step, lane l
 // holding values [16 l, 16 l + 16). With gs % 16 == 0 a group is gs / 16 consecutive lanes (a quad for gs = 64), so
 // group maxima and int32 group dots are lane reductions inside the wave (DPP / swizzle shuffles), with no LDS.
+#include <atomic>
 #include <cstdlib>
 
 #include "common.h"
@@ -80,21 +81,31 @@ __device__ __forceinline__ int quantize_one(float x, float scale) {
   return (int)roundf(fmaxf(-127.0f, fminf(127.0f, ratio)));
 }
 
-// The same value through the reciprocal, for normal scales: r = x * rcp(scale) lies within 127 * 3 * 2^-24 < 2.3e-5 of
-// the correctly rounded quotient fl(x / scale) (v_rcp_f32 is within 1 ulp, the product rounds once, |x / scale| <=
-// 127 (1 + 2^-23)). roundf changes value only at k + 0.5 and the clamp only binds above 127, so wherever
-// |frac(|r|) - 0.5| >= 2^-12 both give the same integer. Inside that margin, for subnormal x (a flushing multiply would
-// lose it) and for a scale that is 0 or not normal, the exact quotient decides.
-__device__ __forceinline__ int quantize_fast(float x, float scale, float inv, bool inv_ok) {
-  const float r = x * inv;
-  const float a = fabsf(r);
-  const float t = truncf(a);
-  const float f = a - t;
-  const bool tiny = x != 0.0f && fabsf(x) < 1.17549435e-38f;
-  if (!inv_ok || tiny || fabsf(f - 0.5f) < 0x1p-12f)
-    return quantize_one(x, scale);
-  const int m = (int)fminf(t + (f > 0.5f ? 1.0f : 0.0f), 127.0f);
-  return r < 0.0f ? -m : m;
+// Values through the reciprocal, for normal scales: r = x * rcp(scale) lies within 127 * 3 * 2^-24 < 2.3e-5 of the
+// correctly rounded quotient fl(x / scale) (v_rcp_f32 is within 1 ulp, the product rounds once, |x / scale| <=
+// 127 (1 + 2^-23)). roundf changes value only at k + 0.5 and the clamp only binds above 127, so wherever r is at least
+// 2^-12 from every k + 0.5, i.e. |r - rint(r)| <= 0.5 - 2^-12 (an exact subtraction), both give clamp(rint(r)). If any
+// value of the call is inside that margin, is subnormal (a flushing multiply would lose it) or the scale is 0 or not
+// normal, the exact quotient decides for all of them: one branch per call, rarely taken.
+constexpr float kTieGuard = 0.5f - 0x1p-12f;
+constexpr int kSubnormal = 0x090; // v_cmp_class mask: negative and positive denormals
+
+template <int N>
+__device__ __forceinline__ void quantize_fast(const float (&x)[N], float scale, float inv, bool inv_ok, int (&q)[N]) {
+#pragma clang fp contract(off) // r is the rounded product: the margin test must see the value rint() rounded
+  bool slow = !inv_ok;
+#pragma unroll
+  for (int j = 0; j < N; j++) {
+    const float r = x[j] * inv;
+    const float t = __builtin_rintf(r);
+    slow |= fabsf(r - t) > kTieGuard || __builtin_amdgcn_class(x[j], kSubnormal);
+    q[j] = (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
+  }
+  if (slow) {
+#pragma unroll
+    for (int j = 0; j < N; j++)
+      q[j] = quantize_one(x[j], scale);
+  }
 }
 
 __device__ __forceinline__ float group_reciprocal(float scale, bool &ok) {
@@ -123,12 +134,12 @@ __device__ __forceinline__ int4 quantize_slice(const float4 (&v)[4], int lpg, fl
   scale = peak / 127.0f;
   bool ok;
   const float inv = group_reciprocal(scale, ok);
-  int w[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-    w[i] = pack_bytes(quantize_fast(v[i].x, scale, inv, ok), quantize_fast(v[i].y, scale, inv, ok),
-                      quantize_fast(v[i].z, scale, inv, ok), quantize_fast(v[i].w, scale, inv, ok));
-  return int4{w[0], w[1], w[2], w[3]};
+  const float e[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
+                       v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};
+  int q[16];
+  quantize_fast(e, scale, inv, ok, q);
+  return int4{pack_bytes(q[0], q[1], q[2], q[3]), pack_bytes(q[4], q[5], q[6], q[7]),
+              pack_bytes(q[8], q[9], q[10], q[11]), pack_bytes(q[12], q[13], q[14], q[15])};
 }
 
 // Four values per lane (one float4): the group spans gs / 4 lanes (lpg4, a power of two <= 64).
@@ -139,8 +150,10 @@ __device__ __forceinline__ int quantize_quad(float4 v, int lpg4, float &scale, b
   scale = peak / 127.0f;
   bool ok;
   const float inv = group_reciprocal(scale, ok);
-  return pack_bytes(quantize_fast(v.x, scale, inv, ok), quantize_fast(v.y, scale, inv, ok),
-                    quantize_fast(v.z, scale, inv, ok), quantize_fast(v.w, scale, inv, ok));
+  const float e[4] = {v.x, v.y, v.z, v.w};
+  int q[4];
+  quantize_fast(e, scale, inv, ok, q);
+  return pack_bytes(q[0], q[1], q[2], q[3]);
 }
 
 // k_quantize / k_quantize_rows, fast form: gs = 16 * lpg with lpg a power of two <= 64, n % 16 == 0, 16-byte aligned
@@ -204,7 +217,7 @@ struct GemvSeg {
   const int8_t *w3q;
   const float *w3s;
   int rows;
-  int first_wave;
+  int first_row; // index of the segment's first row among all segments' rows
 };
 
 struct GemvParams {
@@ -219,7 +232,7 @@ struct GemvParams {
   long long ld;     // weight row stride in values
   long long sld;    // weight scale row stride (ld / gs)
   int epi;
-  int total_waves;
+  int total_rows;   // rows of all segments
   int32_t *probe;   // optional, segment 0 only: probe[g * seg[0].rows + r]
   int *flags;
 };
@@ -336,133 +349,173 @@ template <bool FUSED, int BLOCK, int MAXC> struct Input {
   }
 };
 
-// Streaming W8A8 GEMV on a persistent grid: about two blocks per CU, each wave walking row sets gw, gw + stride, ...
-// (a row set is ROWS consecutive output rows of one segment). For its first row set a wave issues every weight and
-// weight-scale load (ROWS x nchunks 128-bit loads per lane, nchunks = ceil(n / 1024) <= MAXC) before the block stages
-// its input, so the HBM latency overlaps that staging; the block stages (or, FUSED, quantizes) the input only once,
-// however many row sets its waves take. Per 1024-value step a lane forms its partial int32 dot of 16 values with four
-// dot4 instructions, the group's lanes add theirs into the exact int32 group dot, and the group's first lane adds
-// ((float)dot * ws) * xs to its FP32 accumulator (the reference's per-group expression, src/gemv.c:428). A wave
-// reduction and the epilogue finish each row.
-template <int MAXC, int ROWS, bool SWIGLU>
-struct RowSet {
-  int4 w[ROWS][MAXC], w3[ROWS][MAXC];
-  float ws[ROWS][MAXC], w3s[ROWS][MAXC];
+// Streaming W8A8 GEMV on a persistent grid of 8-wave blocks, about two per CU. KS waves share a row: wave `part` of
+// the KS takes the row's 1024-byte chunks part, part + KS, part + 2 KS, ... (at most CH of them), so a long row (W2's
+// 14336 inputs) is streamed by several waves at once and a block works on 8 / KS rows per step. Blocks take steps
+// blockIdx.x, blockIdx.x + gridDim.x, ... and stage (or, FUSED, quantize) the input into LDS once for all of them.
+//
+// The weight loads are software-pipelined: a wave holds two register sets and issues the loads of its next step
+// before it computes the current one, so every wave keeps a step's worth of HBM reads in flight while it works. For
+// the first step they are issued before the input is staged. Per 1024-value chunk a lane forms its partial int32 dot
+// of 16 values with four dot4 instructions, the group's lanes add theirs into the exact int32 group dot, and the
+// group's first lane adds ((float)dot * ws) * xs to its FP32 accumulator (the reference's per-group expression,
+// src/gemv.c:428). A wave reduction gives the wave's part of the row; with KS > 1 the parts meet in LDS and the first
+// wave of the row adds them in part order and applies the epilogue.
+template <int CH, int KS, bool SWIGLU>
+struct RowPart {
+  int4 w[CH], w3[CH];
+  float ws[CH], w3s[CH];
+  float prior; // ADD: the output's current value, loaded with the weights
   GemvSeg seg;
-  int s, r0, nrows;
+  int s, row;
+  bool own;
 
-  // Every load is issued unconditionally through per-row buffer resources: a row past nrows has a zero bound, and
-  // lanes or chunk slots past n fall outside the row's bound, so all of them read zero with no memory access. With no
-  // branch around any load the compiler can count them and wait for each only when it is used.
-  __device__ __forceinline__ void load(const GemvParams &p, int gw, int lane) {
-    const int gl = gw < p.total_waves ? gw : p.total_waves - 1;
+  // Every load is issued unconditionally through per-row buffer resources: a row past total_rows has a zero bound,
+  // and chunks past n fall outside the row's bound, so all of them read zero with no memory access. With no branch
+  // around any load the compiler can count them and wait for each only when it is used.
+  __device__ __forceinline__ void load(const GemvParams &p, int index, int part, int lane) {
+    own = index < p.total_rows;
+    const int gl = own ? index : p.total_rows - 1;
     s = 0;
-    while (s + 1 < p.nseg && gl >= p.seg[s + 1].first_wave)
+    while (s + 1 < p.nseg && gl >= p.seg[s + 1].first_row)
       s++;
     seg = pick(p.seg, s);
-    r0 = (gl - seg.first_wave) * ROWS;
-    nrows = gw < p.total_waves ? min(ROWS, seg.rows - r0) : 0;
-    const unsigned wbytes = (unsigned)p.n, sbytes = (unsigned)(p.n / p.gs) * 4u;
-    __amdgpu_buffer_rsrc_t rw[ROWS], rs[ROWS], rw3[ROWS], rs3[ROWS];
+    row = gl - seg.first_row;
+    const unsigned wbytes = own ? (unsigned)p.n : 0u, sbytes = own ? (unsigned)(p.n / p.gs) * 4u : 0u;
+    const __amdgpu_buffer_rsrc_t rw = buffer(seg.wq + (long long)row * p.ld, wbytes);
+    const __amdgpu_buffer_rsrc_t rs = buffer(seg.ws + (long long)row * p.sld, sbytes);
+    __amdgpu_buffer_rsrc_t rw3 = rw, rs3 = rs;
+    if (SWIGLU) {
+      rw3 = buffer(seg.w3q + (long long)row * p.ld, wbytes);
+      rs3 = buffer(seg.w3s + (long long)row * p.sld, sbytes);
+    }
 #pragma unroll
-    for (int i = 0; i < ROWS; i++) {
-      const long long row = r0 + i;
-      const bool own = i < nrows;
-      rw[i] = buffer(seg.wq + row * p.ld, own ? wbytes : 0u);
-      rs[i] = buffer(seg.ws + row * p.sld, own ? sbytes : 0u);
+    for (int c = 0; c < CH; c++) {
+      const int off = ((c * KS + part) << 10) + lane * 16;
+      const int soff = (off / p.gs) * 4;
+      w[c] = load16(rw, off, 1);
+      ws[c] = load4(rs, soff);
       if (SWIGLU) {
-        rw3[i] = buffer(seg.w3q + row * p.ld, own ? wbytes : 0u);
-        rs3[i] = buffer(seg.w3s + row * p.sld, own ? sbytes : 0u);
+        w3[c] = load16(rw3, off, 1);
+        w3s[c] = load4(rs3, soff);
       }
     }
-    // chunk-major, the order finish() consumes them in
-#pragma unroll
-    for (int c = 0; c < MAXC; c++)
-#pragma unroll
-      for (int i = 0; i < ROWS; i++) {
-        const int off = (c << 10) + lane * 16;
-        const int soff = (off / p.gs) * 4;
-        w[i][c] = load16(rw[i], off, 1);
-        ws[i][c] = load4(rs[i], soff);
-        if (SWIGLU) {
-          w3[i][c] = load16(rw3[i], off, 1);
-          w3s[i][c] = load4(rs3[i], soff);
-        } else {
-          w3[i][c] = int4{0, 0, 0, 0};
-          w3s[i][c] = 0.0f;
-        }
-      }
+    // The residual read of ADD is issued here, after this step's weights: loads complete in issue order for the
+    // counter the waits use, so reading it when the step's weights have arrived never waits on the loads of the
+    // step issued after this one (a read issued at store time would).
+    if (!SWIGLU)
+      prior = load4(buffer(seg.out + row, own && part == 0 && p.epi == EPI_ADD ? 4u : 0u), 0);
   }
 
-  // Fully unrolled over compile-time indices (guards, not early exits), so the arrays stay in registers. Rows past
-  // nrows and steps past nchunks hold zeros from load() and add nothing.
-  __device__ __forceinline__ void finish(const GemvParams &p, const int8_t *sxq, const float *sxs, int lane) {
+  // This wave's part of the row (and of the gate row), reduced over the wave. Fully unrolled over compile-time
+  // indices with guards, not early exits, so the arrays stay in registers.
+  __device__ __forceinline__ float2 dot(const GemvParams &p, const int8_t *sxq, const float *sxs, int part,
+                                        int lane) const {
     const bool leader = (lane & (p.lpg - 1)) == 0;
-    int32_t *probe = (s == 0) ? p.probe : nullptr;
-    float acc[ROWS], gacc[ROWS];
+    int32_t *probe = (s == 0 && own) ? p.probe : nullptr;
+    float acc = 0.0f, gacc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < ROWS; i++)
-      acc[i] = gacc[i] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < MAXC; c++) {
-      if (c < p.nchunks) {
-        const int off = (c << 10) + lane * 16;
+    for (int c = 0; c < CH; c++) {
+      if (c * KS + part < p.nchunks) {
+        const int off = ((c * KS + part) << 10) + lane * 16;
         const bool active = off < p.n;
         const int4 xv = active ? *reinterpret_cast<const int4 *>(sxq + off) : int4{0, 0, 0, 0};
         const int g = off / p.gs;
         const float xsg = active ? sxs[g] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < ROWS; i++) {
-          const int d = group_reduce_add(dot16(w[i][c], xv), p.lpg);
-          if (probe && active && leader && i < nrows)
-            probe[(long long)g * seg.rows + r0 + i] = d;
-          acc[i] += leader ? ((float)d * ws[i][c]) * xsg : 0.0f;
-          if (SWIGLU) {
-            const int d3 = group_reduce_add(dot16(w3[i][c], xv), p.lpg);
-            gacc[i] += leader ? ((float)d3 * w3s[i][c]) * xsg : 0.0f;
-          }
+        const int d = group_reduce_add(dot16(w[c], xv), p.lpg);
+        if (probe && active && leader)
+          probe[(long long)g * seg.rows + row] = d;
+        acc += leader ? ((float)d * ws[c]) * xsg : 0.0f;
+        if (SWIGLU) {
+          const int d3 = group_reduce_add(dot16(w3[c], xv), p.lpg);
+          gacc += leader ? ((float)d3 * w3s[c]) * xsg : 0.0f;
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < ROWS; i++) {
-      const float total = wave_sum(acc[i]);
-      const float gate = SWIGLU ? wave_sum(gacc[i]) : 0.0f;
-      if (lane == 0 && i < nrows) {
-        float *o = seg.out + r0 + i;
-        if (SWIGLU)
-          *o = silu_gate(total, gate);
-        else if (p.epi == EPI_ADD)
-          *o += total;
-        else
-          *o = total;
-      }
-    }
+    return float2{wave_sum(acc), SWIGLU ? wave_sum(gacc) : 0.0f};
+  }
+
+  __device__ __forceinline__ void store(const GemvParams &p, float total, float gate) const {
+    if (!own)
+      return;
+    float *o = seg.out + row;
+    if (SWIGLU)
+      *o = silu_gate(total, gate);
+    else if (p.epi == EPI_ADD)
+      *o = prior + total;
+    else
+      *o = total;
   }
 };
 
-template <int MAXC, int ROWS, bool SWIGLU, bool FUSED, int WAVES>
+constexpr int kMaxGemvWaves = 16;
+
+template <int WAVES, int CH, int KS, bool SWIGLU>
+__device__ __forceinline__ void gemv_step(const GemvParams &p, const RowPart<CH, KS, SWIGLU> &set,
+                                          const int8_t *sxq, const float *sxs, float2 *red, int wave, int part,
+                                          int lane, int &parity) {
+  const float2 r = set.dot(p, sxq, sxs, part, lane);
+  if (KS == 1) {
+    if (lane == 0)
+      set.store(p, r.x, r.y);
+    return;
+  }
+  // Partials of step t go to half t % 2 of `red`: a half is rewritten two steps later, after the barrier of the step
+  // in between, by which time its readers are done.
+  float2 *half = red + parity * WAVES;
+  if (lane == 0)
+    half[wave] = r;
+  __syncthreads();
+  if (part == 0 && lane == 0) {
+    float total = 0.0f, gate = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KS; j++) {
+      total += half[wave + j].x;
+      gate += half[wave + j].y;
+    }
+    set.store(p, total, gate);
+  }
+  parity ^= 1;
+}
+
+template <int WAVES, int CH, int KS, bool SWIGLU, bool FUSED>
 __global__ __launch_bounds__(WAVES * 64) void q8_gemv(GemvParams p) {
+  constexpr int kRows = WAVES / KS; // rows per block step
   extern __shared__ __align__(16) unsigned char smem[];
   int8_t *sxq = reinterpret_cast<int8_t *>(smem);
   float *sxs = reinterpret_cast<float *>(smem + ((p.n + 15) & ~15));
+  float2 *red = reinterpret_cast<float2 *>(sxs + ((p.n / p.gs + 1) & ~1));
   const int lane = threadIdx.x & (kWave - 1);
-  const int stride = gridDim.x * WAVES;
   // wave-uniform by construction; readfirstlane lets the compiler keep row indices and pointers in scalar registers
-  int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * WAVES + (threadIdx.x >> 6));
-  Input<FUSED, WAVES * 64, MAXC> in;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slot = wave / KS, part = wave % KS;
+  const int steps = (p.total_rows + kRows - 1) / kRows;
+  const int stride = gridDim.x;
+  int step = blockIdx.x; // block-uniform, < steps (the grid never exceeds the step count)
+  int parity = 0;
+  Input<FUSED, WAVES * 64, CH * KS> in;
   in.load(p);
   __builtin_amdgcn_sched_barrier(0);
-  RowSet<MAXC, ROWS, SWIGLU> set;
-  set.load(p, gw, lane);
+  // the first two steps' weights are in flight while the block stages its input
+  RowPart<CH, KS, SWIGLU> a, b;
+  a.load(p, step * kRows + slot, part, lane);
+  b.load(p, (step + stride) * kRows + slot, part, lane);
   __builtin_amdgcn_sched_barrier(0);
   in.stage(p, sxq, sxs);
   __syncthreads();
-  while (gw < p.total_waves) {
-    set.finish(p, sxq, sxs, lane);
-    gw += stride;
-    if (gw < p.total_waves)
-      set.load(p, gw, lane);
+  while (true) {
+    gemv_step<WAVES>(p, a, sxq, sxs, red, wave, part, lane, parity);
+    step += stride;
+    if (step >= steps)
+      break;
+    a.load(p, (step + stride) * kRows + slot, part, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    gemv_step<WAVES>(p, b, sxq, sxs, red, wave, part, lane, parity);
+    step += stride;
+    if (step >= steps)
+      break;
+    b.load(p, (step + stride) * kRows + slot, part, lane);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -512,10 +565,10 @@ __global__ __launch_bounds__(kBlock) void q8_gemv_generic(GemvGenericParams p) {
   if (row >= p.total_rows)
     return;
   int s = 0;
-  while (s + 1 < p.nseg && row >= p.seg[s + 1].first_wave)
+  while (s + 1 < p.nseg && row >= p.seg[s + 1].first_row)
     s++;
   const GemvSeg seg = pick(p.seg, s);
-  const long long r = row - seg.first_wave;
+  const long long r = row - seg.first_row;
   int32_t *probe = s == 0 ? p.probe : nullptr;
   const float total = generic_row(seg.wq + r * p.ld, seg.ws + r * p.sld, p, lane, probe, r, seg.rows);
   float gate = 0.0f;
@@ -659,6 +712,9 @@ bool launch_quantize(const QuantizeJob &job, hipStream_t stream) {
   return true;
 }
 
+// Launch-shape overrides set by llhip_set_gemv_shape (0: the default, or the environment's).
+static std::atomic<int> forced_split{0}, forced_blocks{0}, forced_waves{0};
+
 // Blocks per CU of the persistent GEMV grid (LLAMA_HIP_GEMV_BLOCKS_PER_CU overrides, for sweeps).
 static int gemv_blocks_per_cu() {
   static const int value = [] {
@@ -666,48 +722,109 @@ static int gemv_blocks_per_cu() {
     const int v = env && *env ? atoi(env) : 0;
     return v >= 1 && v <= 64 ? v : 2;
   }();
-  return value;
+  const int forced = forced_blocks.load(std::memory_order_relaxed);
+  return forced ? forced : value;
 }
 
-// 8-wave blocks on a grid of a few blocks per CU: every block stages (or quantizes) the input once, however many row
-// sets its waves stream.
-template <int MAXC, int ROWS, bool SWIGLU>
-static void launch_fast(const GemvParams &p, bool fused, hipStream_t stream) {
-  const size_t lds = ((size_t)(p.n + 15) & ~(size_t)15) + (size_t)(p.n / p.gs) * sizeof(float);
-  const int want = (p.total_waves + 7) / 8;
-  const int cap = device().cu_count * gemv_blocks_per_cu();
-  const int blocks = want < cap ? want : cap;
-  if (fused)
-    hipLaunchKernelGGL((q8_gemv<MAXC, ROWS, SWIGLU, true, 8>), dim3(blocks), dim3(512), lds, stream, p);
-  else
-    hipLaunchKernelGGL((q8_gemv<MAXC, ROWS, SWIGLU, false, 8>), dim3(blocks), dim3(512), lds, stream, p);
+// Dynamic LDS of the fast GEMV: the int8 input (rounded to 16 bytes), its scales (rounded to an even count) and the
+// two halves of the per-wave partial sums.
+static size_t gemv_lds_bytes(int n, int gs) {
+  return ((size_t)(n + 15) & ~(size_t)15) + (size_t)((n / gs + 1) & ~1) * sizeof(float) + 2 * kMaxGemvWaves * 8;
 }
 
-// Rows per wave: one. More rows per wave carry more bytes per wave, but measured on MI355X the 8B shapes stream best
-// with one row per wave and more waves (W1/W3 5.5 vs 4.8 TB/s, the classifier 6.5 vs 6.3). LLAMA_HIP_GEMV_ROWS=2 or 4
-// selects the multi-row kernels (for sweeps); the register budget caps ROWS * MAXC.
-static int rows_per_wave(int total_rows, int maxc, bool swiglu) {
-  (void)total_rows;
-  static const int forced = [] {
-    const char *env = getenv("LLAMA_HIP_GEMV_ROWS");
-    return env && *env ? atoi(env) : 0;
+// Waves per block: 16 (one block per CU stages the input once for all its waves) unless set otherwise.
+static int gemv_block_waves() {
+  static const int value = [] {
+    const char *env = getenv("LLAMA_HIP_GEMV_BLOCK_WAVES");
+    const int v = env && *env ? atoi(env) : 0;
+    return v == 8 || v == 16 ? v : 16;
   }();
-  if ((forced == 2 && maxc <= 8 && !(swiglu && maxc > 4)) || (forced == 4 && maxc <= 4 && !swiglu))
+  const int forced = forced_waves.load(std::memory_order_relaxed);
+  return forced ? forced : value;
+}
+
+template <int WAVES, int CH, int KS, bool SWIGLU>
+static void launch_shape(const GemvParams &p, bool fused, int per_cu, hipStream_t stream) {
+  const size_t lds = gemv_lds_bytes(p.n, p.gs);
+  const int steps = (p.total_rows + WAVES / KS - 1) / (WAVES / KS);
+  const int cap = device().cu_count * per_cu;
+  const int blocks = steps < cap ? steps : cap;
+  if (fused)
+    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
+  else
+    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, false>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
+}
+
+template <int CH, int KS, bool SWIGLU>
+static void launch_fast(const GemvParams &p, bool fused, hipStream_t stream) {
+  // blocks per CU counts 8-wave blocks: a 16-wave block stands for two
+  const int bpc = gemv_blocks_per_cu();
+  if (gemv_block_waves() == 16 && bpc % 2 == 0)
+    launch_shape<16, CH, KS, SWIGLU>(p, fused, bpc / 2, stream);
+  else
+    launch_shape<8, CH, KS, SWIGLU>(p, fused, bpc, stream);
+}
+
+// Waves per row: two for K <= 8192 (at most four 1024-byte chunks per wave), four above (W2's 14336). Two waves per
+// K = 4096 row measured fastest on MI355X for every 8B shape: the block steps then divide evenly over two blocks per
+// CU (QKV 6144 rows: 1536 steps, W1/W3 14336: 3584, Wo 4096: 1024). LLAMA_HIP_GEMV_KSPLIT=1|2|4|8 forces a split.
+static int waves_per_row(int nchunks) {
+  static const int from_env = [] {
+    const char *env = getenv("LLAMA_HIP_GEMV_KSPLIT");
+    const int v = env && *env ? atoi(env) : 0;
+    return v == 1 || v == 2 || v == 4 || v == 8 ? v : 0;
+  }();
+  const int forced = forced_split.load(std::memory_order_relaxed);
+  if (forced)
     return forced;
-  return 1;
+  if (from_env)
+    return from_env;
+  return nchunks <= 8 ? 2 : 4;
+}
+
+template <int KS, bool SWIGLU>
+static void launch_split(const GemvParams &p, bool fused, hipStream_t stream) {
+  const int per = (p.nchunks + KS - 1) / KS; // chunks per wave
+  if (per <= 1)
+    launch_fast<1, KS, SWIGLU>(p, fused, stream);
+  else if (per <= 2)
+    launch_fast<2, KS, SWIGLU>(p, fused, stream);
+  else if (per <= 4)
+    launch_fast<4, KS, SWIGLU>(p, fused, stream);
+  else // per <= 16 only with one wave per row: two waves of at most 8 chunks instead (16 would spill registers)
+    launch_fast<8, 2, SWIGLU>(p, fused, stream);
+}
+
+bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves) {
+  if (!(waves_per_row == 0 || waves_per_row == 1 || waves_per_row == 2 || waves_per_row == 4 || waves_per_row == 8))
+    return raise("llhip_set_gemv_shape: waves per row must be 0, 1, 2, 4 or 8, got %d", waves_per_row);
+  if (blocks_per_cu < 0 || blocks_per_cu > 64)
+    return raise("llhip_set_gemv_shape: blocks per CU must be 0..64, got %d", blocks_per_cu);
+  if (!(block_waves == 0 || block_waves == 8 || block_waves == 16))
+    return raise("llhip_set_gemv_shape: waves per block must be 0, 8 or 16, got %d", block_waves);
+  forced_split.store(waves_per_row, std::memory_order_relaxed);
+  forced_blocks.store(blocks_per_cu, std::memory_order_relaxed);
+  forced_waves.store(block_waves, std::memory_order_relaxed);
+  return true;
 }
 
 bool gemv_fast_path(const GemvJob &job) {
   const int lpg = lanes_per_group(job.gs);
-  const size_t lds = job.gs > 0 ? ((size_t)(job.n + 15) & ~(size_t)15) + (size_t)(job.n / job.gs) * sizeof(float) : 0;
+  const size_t lds = job.gs > 0 ? gemv_lds_bytes(job.n, job.gs) : 0;
   bool fast = (job.xq || job.xf_quantize) && lpg && job.n > 0 && job.n % job.gs == 0 && job.ld % 16 == 0 &&
               lds <= 65536 && (job.n + 1023) / 1024 <= 16;
-  // The fused prologue keeps the whole FP32 input in registers while the weights stream: up to 8192 values (K of
-  // the 8B model's QKV, Wo and W1/W3); a longer input (W2's 14336) is quantized by its own launch.
-  fast = fast && (job.xf_quantize ? aligned16(job.xf) && aligned16(job.xq_out) && job.gs <= 256 && job.n <= 8192
-                                  : aligned16(job.xq));
-  for (int s = 0; s < job.nseg && fast; s++)
+  // The fused prologue quantizes the FP32 input 4 values per lane (gs <= 256: a group within a wave).
+  fast = fast && (job.xf_quantize ? aligned16(job.xf) && aligned16(job.xq_out) && job.gs <= 256 : aligned16(job.xq));
+  for (int s = 0; s < job.nseg && fast; s++) {
     fast = aligned16(job.seg[s].wq) && (job.epi != EPI_SWIGLU || aligned16(job.seg[s].w3q));
+    // Fused, every block reads the FP32 input while others already write outputs: an output inside the input would
+    // change what later blocks quantize, so that case quantizes in its own launch first.
+    if (job.xf_quantize) {
+      const uintptr_t o0 = (uintptr_t)job.seg[s].out, o1 = o0 + (size_t)job.seg[s].rows * sizeof(float);
+      const uintptr_t x0 = (uintptr_t)job.xf, x1 = x0 + (size_t)job.n * sizeof(float);
+      fast = fast && (o1 <= x0 || x1 <= o0);
+    }
+  }
   return fast;
 }
 
@@ -719,15 +836,11 @@ bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
     return true;
   if (gemv_fast_path(job)) {
     GemvParams p{};
-    const int nchunks = (job.n + 1023) / 1024;
-    const int maxc = nchunks <= 4 ? 4 : nchunks <= 8 ? 8 : 16;
-    const bool swiglu = job.epi == EPI_SWIGLU;
-    const int rows = rows_per_wave(total_rows, maxc, swiglu);
-    int waves = 0;
+    int rows = 0;
     for (int s = 0; s < job.nseg; s++) {
       const GemvSegment &g = job.seg[s];
-      p.seg[s] = GemvSeg{g.out, g.wq, g.ws, g.w3q, g.w3s, g.rows, waves};
-      waves += (g.rows + rows - 1) / rows;
+      p.seg[s] = GemvSeg{g.out, g.wq, g.ws, g.w3q, g.w3s, g.rows, rows};
+      rows += g.rows;
     }
     p.nseg = job.nseg;
     p.xq = job.xq;
@@ -738,37 +851,27 @@ bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
     p.n = job.n;
     p.gs = job.gs;
     p.lpg = lanes_per_group(job.gs);
-    p.nchunks = nchunks;
+    p.nchunks = (job.n + 1023) / 1024;
     p.ld = (long long)job.ld;
     p.sld = (long long)(job.ld / job.gs);
     p.epi = job.epi;
-    p.total_waves = waves;
+    p.total_rows = rows;
     p.probe = job.probe;
     p.flags = device().error_flags;
-    const bool fused = job.xf_quantize;
-    if (swiglu) {
-      if (maxc == 4 && rows == 2)
-        launch_fast<4, 2, true>(p, fused, stream);
-      else if (maxc == 4)
-        launch_fast<4, 1, true>(p, fused, stream);
-      else if (maxc == 8)
-        launch_fast<8, 1, true>(p, fused, stream);
-      else
-        launch_fast<16, 1, true>(p, fused, stream);
-    } else if (maxc == 4) {
-      if (rows == 4)
-        launch_fast<4, 4, false>(p, fused, stream);
-      else if (rows == 2)
-        launch_fast<4, 2, false>(p, fused, stream);
-      else
-        launch_fast<4, 1, false>(p, fused, stream);
-    } else if (maxc == 8) {
-      if (rows == 2)
-        launch_fast<8, 2, false>(p, fused, stream);
-      else
-        launch_fast<8, 1, false>(p, fused, stream);
-    } else {
-      launch_fast<16, 1, false>(p, fused, stream);
+    const bool fused = job.xf_quantize, swiglu = job.epi == EPI_SWIGLU;
+    switch (waves_per_row(p.nchunks)) {
+    case 1:
+      swiglu ? launch_split<1, true>(p, fused, stream) : launch_split<1, false>(p, fused, stream);
+      break;
+    case 2:
+      swiglu ? launch_split<2, true>(p, fused, stream) : launch_split<2, false>(p, fused, stream);
+      break;
+    case 4:
+      swiglu ? launch_split<4, true>(p, fused, stream) : launch_split<4, false>(p, fused, stream);
+      break;
+    default:
+      swiglu ? launch_split<8, true>(p, fused, stream) : launch_split<8, false>(p, fused, stream);
+      break;
     }
     return launch_ok("q8_gemv");
   }

@@ -452,3 +452,84 @@ def test_fused_quantization_flags_nonfinite():
     finally:
         L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
         L.llhip_clear_error()
+
+
+# ---- launch shapes of the streaming GEMV ----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("n", [1088, 4096, 14336])
+def test_gemv_every_launch_shape(n):
+    """Every waves-per-row split (1, 2, 4, 8), block size and grid size gives the same int32 group dots and in-budget
+    outputs, for
+    a three-segment QKV (rows of one step straddle segments), a SwiGLU pair and the ADD epilogue, fused and not."""
+    L = hu.lib()
+    T = hu.torch()
+    gs = 64
+    rng = orc.Rng(orc.SEED + 4242 + n)
+    rows = (200, 56, 40)
+    ws = [synth_weights(rng, d, n, gs) for d in rows]
+    x = rng.normal(n, 0.0, 1.0)
+    xq, xs = orc.quantize(x, gs)
+    refs = [hu.dequant_reference(xq, xs, q, s, gs) for q, s in ws]
+    xd = hu.dev(x)
+    dws = [(hu.dev(q), hu.dev(s)) for q, s in ws]
+    base = rng.uniform(rows[0], 3.0)
+    try:
+        for split in (1, 2, 4, 8):
+            for blocks, waves in ((1, 8), (3, 8), (2, 16), (4, 16)):
+                L.llhip_set_gemv_shape(split, blocks, waves)
+                what = f"n {n} split {split} blocks/CU {blocks} waves/block {waves}"
+                for fused in (True, False):
+                    qd, sd = T.zeros(n, dtype=T.int8, device="cuda"), T.zeros(n // gs, dtype=T.float32, device="cuda")
+                    outs = [hu.empty(d, T.float32) for d in rows]
+                    T.cuda.synchronize()
+                    if fused:
+                        L.k_quantize(lh.ptr(qd), lh.ptr(sd), lh.ptr(xd), n, gs)
+                    else:
+                        qd.copy_(T.from_numpy(xq))
+                        sd.copy_(T.from_numpy(xs))
+                        T.cuda.synchronize()
+                    inp = lh.k8(qd, sd, xd)
+                    L.k_matmul_q8_qkv(lh.ptr(outs[0]), lh.ptr(outs[1]), lh.ptr(outs[2]), inp, lh.w8(*dws[0]),
+                                      lh.w8(*dws[1]), lh.w8(*dws[2]), n, rows[0], rows[1], gs)
+                    for o, (r, mag) in zip(outs, refs):
+                        hu.assert_within_budget(hu.host(o), r, mag, what=f"qkv {what} fused {fused}")
+                    assert np.array_equal(hu.host(qd), xq), what
+                    # SwiGLU with the same matrix as value and gate: silu(r) * r
+                    sw = hu.empty(rows[1], T.float32)
+                    L.k_matmul_q8_swiglu(lh.ptr(sw), inp, lh.w8(*dws[1]), lh.w8(*dws[1]), n, rows[1], gs)
+                    r1, m1 = refs[1]
+                    got = hu.host(sw)
+                    want = r1 / (1.0 + np.exp(-r1)) * r1
+                    tol = 2e-5 * (m1 * (np.abs(r1) + 1) * 2) + 1e-6
+                    assert np.all(np.abs(got - want) <= tol), f"swiglu {what}"
+                    acc = hu.dev(base)
+                    L.k_matmul_q8_add(lh.ptr(acc), inp, lh.w8(*dws[0]), n, rows[0], gs)
+                    hu.assert_within_budget(hu.host(acc), base + refs[0][0], refs[0][1] + np.abs(base), what=f"add {what}")
+                dots = np.zeros((n // gs, rows[0]), np.int32)
+                L.llhip_q8_gemv_group_dots(lh.ptr(dots), lh.ptr(xq), lh.ptr(xs), lh.ptr(ws[0][0]), lh.ptr(ws[0][1]), 0,
+                                           n, rows[0], gs)
+                assert np.array_equal(dots, orc.group_dots(xq.reshape(1, -1), ws[0][0], gs)[:, 0, :]), what
+    finally:
+        L.llhip_set_gemv_shape(0, 0, 0)
+
+
+def test_fused_quantization_with_output_over_its_input():
+    """k_quantize(q, s, x) then k_matmul_q8_add(x, q/s): the residual output is the quantizer's own input. The result
+    is x + W q(x) with q taken from x before any output is written (the fused kernel steps aside for this case)."""
+    L = hu.lib()
+    T = hu.torch()
+    n = d = 4096
+    gs = 64
+    rng = orc.Rng(orc.SEED + 5151)
+    wq, ws = synth_weights(rng, d, n, gs)
+    x = rng.normal(n, 0.0, 1.0)
+    xq, xs = orc.quantize(x, gs)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    xd, dwq, dws = hu.dev(x), hu.dev(wq), hu.dev(ws)
+    qd, sd = T.zeros(n, dtype=T.int8, device="cuda"), T.zeros(n // gs, dtype=T.float32, device="cuda")
+    T.cuda.synchronize()
+    L.k_quantize(lh.ptr(qd), lh.ptr(sd), lh.ptr(xd), n, gs)
+    L.k_matmul_q8_add(lh.ptr(xd), lh.k8(qd, sd, xd), lh.w8(dwq, dws), n, d, gs)
+    hu.assert_within_budget(hu.host(xd), x + ref, mag + np.abs(x), what="residual over the quantized input")
+    assert np.array_equal(hu.host(qd), xq)

@@ -1,11 +1,12 @@
 """The device quantizer's reciprocal shortcut, checked on the CPU against the oracle. CPU only.
 
-The HIP quantizer (llama3.x.c_amd/csrc/gemv.hip, quantize_fast) rounds r = x * rcp(scale) instead of the exact
-quotient x / scale whenever |frac(|r|) - 0.5| >= 2^-12, and falls back to the exact quotient otherwise (and for
-subnormal x, zero or subnormal scales). The argument: |r - fl(x / scale)| < 2.3e-5 when rcp is within 1 ulp, so both
-round to the same integer outside the margin. Here the same steps run in float32 numpy with the reciprocal perturbed by
--1, 0 and +1 ulp, on random groups and on inputs built to sit next to every rounding tie, and must reproduce the
-oracle's k_quantize bit for bit.
+The HIP quantizer (llama3.x.c_amd/csrc/gemv.hip, quantize_fast) forms r = x * rcp(scale) and takes clamp(rint(r))
+instead of rounding the exact quotient x / scale, unless some value of the call has |r - rint(r)| > 0.5 - 2^-12 (r
+within 2^-12 of a rounding tie), is subnormal, or the scale is zero or subnormal: then the exact quotient decides for
+all values of the call. The argument: |r - fl(x / scale)| < 2.3e-5 when rcp is within 1 ulp, so outside the margin
+both round to the same integer. Here the same steps run in float32 numpy with the reciprocal perturbed by -1, 0 and +1
+ulp, on random groups and on inputs built to sit next to every rounding tie, and must reproduce the oracle's
+k_quantize bit for bit.
 """
 import numpy as np
 
@@ -14,7 +15,10 @@ from oracle import pyoracle as orc
 F32_MIN = np.float32(1.17549435e-38)
 
 
-def fast_quantize(x, gs, ulp_shift):
+def fast_quantize(x, gs, ulp_shift, per_call=4):
+    """The device steps: per group the reciprocal of the scale, per value r = x * inv, t = rint(r) (ties to even),
+    q = clamp(t); a call of `per_call` consecutive values of one lane falls back to the exact quotient when any of them
+    is near a tie or subnormal, or the scale is not normal."""
     x = np.asarray(x, np.float32).reshape(-1, gs)
     peak = np.max(np.abs(x), axis=1)
     scale = (peak / np.float32(127.0)).astype(np.float32)
@@ -24,17 +28,16 @@ def fast_quantize(x, gs, ulp_shift):
         for _ in range(abs(ulp_shift)):
             inv = np.nextafter(inv, np.float32(np.inf if ulp_shift > 0 else 0)).astype(np.float32)
         r = (x * inv[:, None]).astype(np.float32)
-        a = np.abs(r)
-        t = np.trunc(a).astype(np.float32)
-        f = (a - t).astype(np.float32)
-        near = np.abs(f - np.float32(0.5)) < np.float32(2.0 ** -12)
+        t = np.rint(r).astype(np.float32)
+        near = np.abs((r - t).astype(np.float32)) > np.float32(0.5 - 2.0 ** -12)
         tiny = (x != 0) & (np.abs(x) < F32_MIN)
-        exact = ~ok[:, None] | tiny | near
-        m = np.minimum(t + (f > 0.5).astype(np.float32), np.float32(127)).astype(np.int32)
-        fast = np.where(r < 0, -m, m)
+        slow_value = near | tiny | ~ok[:, None]
+        # one branch per call: a lane's per_call consecutive values go the exact way together
+        slow = np.repeat(slow_value.reshape(x.shape[0], -1, per_call).any(axis=2), per_call, axis=1)
+        fast = np.clip(t, -127, 127).astype(np.int32)
     q_ref, s_ref = orc.quantize(x, gs)
-    q = np.where(exact, q_ref.astype(np.int32), fast)
-    return q.astype(np.int8), scale, exact.mean()
+    q = np.where(slow, q_ref.astype(np.int32), fast)
+    return q.astype(np.int8), scale, slow.mean()
 
 
 def adversarial(rng, gs, groups):
@@ -64,14 +67,16 @@ def test_fast_path_reproduces_k_quantize_bitwise():
     for x in cases:
         want_q, want_s = orc.quantize(x.reshape(-1, 64), 64)
         for shift in (-1, 0, 1):
-            q, s, exact_share = fast_quantize(x, 64, shift)
-            assert np.array_equal(s.view(np.uint32), want_s.ravel().view(np.uint32))
-            assert np.array_equal(q.ravel(), want_q.ravel()), shift
+            for per_call in (1, 4, 16):
+                q, s, exact_share = fast_quantize(x, 64, shift, per_call)
+                assert np.array_equal(s.view(np.uint32), want_s.ravel().view(np.uint32))
+                assert np.array_equal(q.ravel(), want_q.ravel()), (shift, per_call)
 
 
 def test_margin_catches_a_plausible_slip():
-    """Without the margin (always rounding r), the adversarial inputs disagree with k_quantize for some reciprocal
-    error: the fallback is what makes the shortcut exact."""
+    """Without the margin (always clamp(rint(r))), the adversarial inputs disagree with k_quantize for some reciprocal
+    error: the fallback is what makes the shortcut exact. rint's ties-to-even also differs from roundf's
+    half-away-from-zero on exact ties, which only the fallback resolves."""
     rng = orc.Rng(orc.SEED + 32)
     x = adversarial(rng, 64, 3000).reshape(-1, 64)
     want_q, _ = orc.quantize(x, 64)
@@ -82,9 +87,10 @@ def test_margin_catches_a_plausible_slip():
         inv = (np.float32(1.0) / scale).astype(np.float32)
         inv = np.nextafter(inv, np.float32(np.inf if shift > 0 else 0)).astype(np.float32)
         r = (x * inv[:, None]).astype(np.float32)
-        a = np.abs(r)
-        t = np.trunc(a)
-        m = np.minimum(t + ((a - t) >= 0.5), 127).astype(np.int32)
-        naive = np.where(r < 0, -m, m).astype(np.int8)
+        naive = np.clip(np.rint(r), -127, 127).astype(np.int8)
         mismatches += int(np.sum(naive != want_q))
     assert mismatches > 0
+    ties = np.array([0.5, 1.5, 2.5, -0.5, -2.5, 126.5] + [127.0] * 58, np.float32) * np.float32(0.25)
+    q_ties, _ = orc.quantize(ties.reshape(1, 64), 64)
+    s = np.float32(127.0 * 0.25) / np.float32(127.0)
+    assert not np.array_equal(np.clip(np.rint(ties / s), -127, 127).astype(np.int8), q_ties.ravel())
