@@ -5,6 +5,8 @@
 // grid of 16 x 16 MFMA tiles, and K is staged through double-buffered LDS. MFMA operand loads are symmetric (lane l
 // supplies row l % 16 of A and column l % 16 of W with the same K slice), so the dot products do not depend on how the
 // instruction orders K inside a lane; the 16 x 16 result holds C[4 (l / 16) + e][l % 16] in element e of lane l.
+#include <cstdlib>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -116,23 +118,26 @@ __device__ __forceinline__ void store_tile(const TileSeg &seg, const TilePos &t,
 // 512 threads own a 256 x 128 output tile (a 128-column tile holds 64 columns of W1 and the same 64 of W3 under
 // SWIGLU); eight waves in 4 x 2 each own 64 x 64 as 4 x 4 v_mfma_i32_16x16x64_i8 tiles. A K step is 64 values. Its A
 // and B tiles (256 x 64 and 128 x 64 int8) and their group scales travel from global memory straight into LDS with
-// buffer loads (no register staging), four steps deep: at step s the block waits for step s's loads, then issues step
-// s + 3's into the stage step s - 1 used. In LDS a tile row is 64 bytes whose four 16-byte chunks are XOR-swizzled by
-// (row / 2) % 4, so the MFMA operand reads (16 rows, one chunk each) fall on distinct banks. At a group's last step
-// every output adds ((float)dot * ws) * xs to its FP32 accumulator; two waves per SIMD let one wave's rescale run while
-// the other's MFMAs do.
-constexpr int kQ8Waves = 8, kQ8Threads = kQ8Waves * 64;
-constexpr int kQ8TileM = 256, kQ8TileN = 128, kQ8Stages = 4;
-constexpr int kQ8LoadsPerStep = 4; // per wave: two A, one B and one scale load
-
-struct Q8Stage {
-  int8_t a[kQ8TileM * 64];
-  int8_t b[kQ8TileN * 64];
-  float xs[kQ8TileM];
-  float ws[kQ8TileN];
-  float spare[64]; // where the two waves without a scale share load theirs (zero-length loads)
-};
-constexpr size_t kQ8Lds = kQ8Stages * sizeof(Q8Stage);
+// buffer loads (no register staging), four steps ahead: at step s the block waits for step s + 1's loads, then issues
+// step s + 4's into the stage step s - 1 used.
+//
+// LDS holds 16-row blocks of 1 KB: A block b of stage t at (b * 5 + t) KB, B blocks after the A ones likewise, so a
+// wave's operand reads of any stage are one base register plus an immediate, and the K loop, unrolled by the five
+// stages, spends no vector instructions on addresses. A block row is 64 bytes whose four 16-byte chunks are
+// XOR-swizzled by (row / 2) % 4, so the MFMA operand reads (16 rows, one chunk each) fall on distinct banks.
+//
+// One set of int32 results per wave: at a group's last step, tile by tile, the results are converted, the tile's MFMA
+// of the next step overwrites them, and ((float)dot * ws) * xs is added to the FP32 accumulator from the converted
+// copy, so each wave keeps the matrix pipe and the VALU busy together; inside a group (gs > 64) the next step's MFMA
+// accumulates onto the results instead.
+constexpr int kQ8Waves = 8, kQ8Threads = 64 * kQ8Waves;
+constexpr int kQ8TileM = 256, kQ8TileN = 128, kQ8Stages = 5;
+constexpr int kQ8LoadsPerStep = 4;                                   // per wave: two A, one B, one scale load
+constexpr int kQ8ABlocks = kQ8TileM / 16, kQ8BBlocks = kQ8TileN / 16; // 1 KB blocks per stage
+constexpr int kQ8BOff = kQ8ABlocks * kQ8Stages * 1024;               // B blocks after the A blocks
+constexpr int kQ8SOff = kQ8BOff + kQ8BBlocks * kQ8Stages * 1024;     // then the scales, a group per stage
+constexpr int kQ8SStride = (kQ8TileM + kQ8TileN + 64) * 4;            // xs, ws, spare (zero-length loads land there)
+constexpr size_t kQ8Lds = (size_t)kQ8SOff + (size_t)kQ8Stages * kQ8SStride;
 
 __device__ __forceinline__ int q8_swizzle(int row) { return (row >> 1) & 3; }
 
@@ -168,64 +173,106 @@ __device__ __forceinline__ TileSeg q8_seg_of(const Q8Grid &g, int s) {
   return s == 0 ? g.seg[0] : s == 1 ? g.seg[1] : g.seg[2];
 }
 
+// A buffer resource from wave-uniform values, built from scalar registers (readfirstlane states the uniformity the
+// compiler cannot always prove; a resource in vector registers would make every load a loop over lanes).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t q8_buffer(const void *base, long long bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)(bytes > 0 ? bytes : 0),
+  const unsigned long long b = (unsigned long long)(uintptr_t)base;
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)b);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(b >> 32));
+  const int n = __builtin_amdgcn_readfirstlane((int)(bytes > 0 ? bytes : 0));
+  return __builtin_amdgcn_make_buffer_rsrc((void *)(uintptr_t)(((unsigned long long)hi << 32) | lo), (short)0, n,
                                            0x00020000);
 }
 
-template <bool PROBE>
+// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+template <bool PROBE, bool GS64>
 __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
   extern __shared__ __align__(16) unsigned char q8_smem[];
-  Q8Stage *stage = reinterpret_cast<Q8Stage *>(q8_smem);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const TilePos t = q8_tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
   const TileSeg seg = q8_seg_of(p.grid, t.s);
-  const int groups = p.k / p.gs, spg = p.gs / 64, steps = p.k / 64;
+  const int groups = p.k / p.gs, spg = GS64 ? 1 : p.gs / 64, steps = p.k / 64;
   const long long k = p.k;
 
-  // This wave's share of every step's loads, as buffer resources bounded to the rows that exist (rows past m or n
-  // read zeros) and per-lane offsets that place lane l's 16 bytes at l * 16 of the wave's 1 KB of LDS.
-  const int ra = 32 * wave + (lane >> 2); // A rows ra and ra + 16
+  // This wave's loads of every step, as buffer resources bounded to the rows that exist (rows past m or n read zeros)
+  // and per-lane offsets that place lane l's 16 bytes at l * 16 of a 1 KB block (row l / 4, swizzled chunk l % 4).
+  const int lrow4 = lane >> 2, chunk = lane & 3;
+  const int ra = 32 * wave + lrow4; // A rows ra (block 2 wave) and ra + 16 (block 2 wave + 1)
   const __amdgpu_buffer_rsrc_t rA = q8_buffer(p.xq + (long long)t.m0 * k, (long long)min(kQ8TileM, p.m - t.m0) * k);
-  const int offA0 = (int)(ra * k) + (((lane & 3) ^ q8_swizzle(ra)) << 4);
-  const int offA1 = (int)((ra + 16) * k) + (((lane & 3) ^ q8_swizzle(ra + 16)) << 4);
-  const int rb = 16 * wave + (lane >> 2); // B tile row
-  const bool second = t.swiglu && wave >= 4;
-  const int col0 = t.swiglu ? t.n0 + ((16 * wave) & 63) : t.n0 + 16 * wave;
-  const int8_t *wmat = (const int8_t *)(second ? seg.w3 : seg.w);
-  const __amdgpu_buffer_rsrc_t rB = q8_buffer(wmat + (long long)col0 * k, (long long)min(16, seg.n - col0) * k);
-  const int offB = (int)((lane >> 2) * k) + (((lane & 3) ^ q8_swizzle(rb)) << 4);
-  // scale loads: waves 0-3 the 256 xs rows, waves 4-5 the 128 ws rows, waves 6-7 nothing
+  const int offA0 = (int)(ra * k) + ((chunk ^ q8_swizzle(ra)) << 4);
+  const int offA1 = (int)((ra + 16) * k) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
+  const int rb0 = 16 * wave; // B tile rows rb0 .. rb0 + 15 (block `wave`), all of one matrix
+  const int colB = t.swiglu ? t.n0 + (rb0 & 63) : t.n0 + rb0;
+  const int8_t *wmat = (const int8_t *)((t.swiglu && rb0 >= 64) ? seg.w3 : seg.w);
+  const __amdgpu_buffer_rsrc_t rB = q8_buffer(wmat + (long long)colB * k, (long long)min(16, seg.n - colB) * k);
+  const int offB = (int)(lrow4 * k) + ((chunk ^ q8_swizzle(rb0 + lrow4)) << 4);
+  // scale loads: waves 0-3 the 256 xs rows (64 each), waves 4-5 the 128 ws rows, waves 6-7 nothing
   __amdgpu_buffer_rsrc_t rS;
-  int scale_dst; // float index in the stage: xs at 0, ws at kQ8TileM, spare after
+  int scale_dst; // byte offset inside a stage's scales: xs, then ws, then spare
   if (wave < 4) {
     const int r0 = t.m0 + 64 * wave;
     rS = q8_buffer(p.xs + (long long)r0 * groups, (long long)min(64, p.m - r0) * groups * 4);
-    scale_dst = 64 * wave;
+    scale_dst = 64 * wave * 4;
   } else if (wave < 6) {
     const int h = wave - 4;
     const float *src = t.swiglu ? (h ? seg.w3s : seg.ws) : seg.ws;
     const int c0 = t.swiglu ? t.n0 : t.n0 + 64 * h;
     rS = q8_buffer(src + (long long)c0 * groups, (long long)min(64, seg.n - c0) * groups * 4);
-    scale_dst = kQ8TileM + 64 * h;
+    scale_dst = (kQ8TileM + 64 * h) * 4;
   } else {
     rS = q8_buffer(p.xs, 0);
-    scale_dst = kQ8TileM + kQ8TileN;
+    scale_dst = (kQ8TileM + kQ8TileN) * 4;
   }
   const int offS = lane * groups * 4;
   const __amdgpu_buffer_rsrc_t none = q8_buffer(p.xq, 0);
 
-  // Issue the loads of K step `step` into stage `st`; a step past the end loads nothing (zero-length resources).
-  auto issue = [&](int step, int st) {
+  // The loads of K step `step` into stage ST; a step past the end loads nothing (zero-length resources). The K offset
+  // goes in the scalar offset operand.
+  auto issue = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value;
     const bool live = step < steps;
     const int k0 = step * 64, g = step / spg;
-    Q8Stage &S = stage[st];
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, &S.a[(32 * wave) * 64], 16, offA0 + k0, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, &S.a[(32 * wave + 16) * 64], 16, offA1 + k0, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB : none, &S.b[(16 * wave) * 64], 16, offB + k0, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rS : none, &S.xs[scale_dst], 4, offS + g * 4, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, (void *)(q8_smem + ((2 * wave) * kQ8Stages + st) * 1024),
+                                             16, offA0, k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
+                                             (void *)(q8_smem + ((2 * wave + 1) * kQ8Stages + st) * 1024), 16, offA1,
+                                             k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB : none,
+                                             (void *)(q8_smem + kQ8BOff + (wave * kQ8Stages + st) * 1024), 16, offB, k0,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rS : none,
+                                             (void *)(q8_smem + kQ8SOff + st * kQ8SStride + scale_dst), 4, offS,
+                                             g * 4, 0, 0);
+  };
+
+  // Per-lane LDS read bases; the stage and the 16-row block add immediates.
+  const int lrow = lane & 15, lq = lane >> 4, lr4 = (lane >> 4) * 4;
+  const int lane_part = lrow * 64 + ((lq ^ q8_swizzle(lrow)) << 4);
+  const unsigned char *abase = q8_smem + (4 * wm) * kQ8Stages * 1024 + lane_part;
+  const unsigned char *bbase[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    bbase[j] = q8_smem + kQ8BOff + (b_row(t.swiglu, wn, j) / 16) * kQ8Stages * 1024 + lane_part;
+  const unsigned char *xsbase = q8_smem + kQ8SOff + (wm * 64 + lr4) * 4;
+  const unsigned char *wsbase[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    wsbase[j] = q8_smem + kQ8SOff + (kQ8TileM + b_row(t.swiglu, wn, j) + lrow) * 4;
+
+  auto operands = [&](auto ST, v4i (&a)[4], v4i (&b)[4]) {
+    constexpr int st = decltype(ST)::value;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      a[i] = *reinterpret_cast<const v4i *>(abase + (i * kQ8Stages + st) * 1024);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      b[j] = *reinterpret_cast<const v4i *>(bbase[j] + st * 1024);
   };
 
   v4f acc[4][4];
@@ -233,52 +280,35 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < 4; j++)
       acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-      dot[i][j] = v4i{0, 0, 0, 0};
-    }
 
-#pragma unroll
-  for (int s = 0; s < kQ8Stages - 1; s++)
-    issue(s, s);
-  const int lrow = lane & 15, lq = lane >> 4, lr4 = (lane >> 4) * 4;
-  for (int step = 0; step < steps; step++) {
-    // this wave's loads of `step` have landed once no more than those of the (kQ8Stages - 2) later steps are
-    // outstanding; the barrier then makes every wave's landed
-    __builtin_amdgcn_s_waitcnt((((kQ8Stages - 2) * kQ8LoadsPerStep) & 15) | (0x7 << 4) | (0xF << 8) |
-                               ((((kQ8Stages - 2) * kQ8LoadsPerStep) >> 4) << 14));
+  // One step in stage ST: step + 1's loads have landed once only the two later steps' may be outstanding; the barrier
+  // makes that true of every wave and means every wave is done with the stage step - 1 used, which step + 4 now
+  // fills. Then the next step's MFMAs and, at a group's end, this step's rescale. After the last step the MFMAs run
+  // on stale operands whose products are never used.
+  auto advance = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value, nst = (st + 1) % kQ8Stages, fill = (st + kQ8Stages - 1) % kQ8Stages;
+    wait_vmcnt<(kQ8Stages - 3) * kQ8LoadsPerStep>();
     __builtin_amdgcn_s_barrier();
-    issue(step + kQ8Stages - 1, (step + kQ8Stages - 1) % kQ8Stages);
-    const Q8Stage &S = stage[step % kQ8Stages];
+    issue(step + kQ8Stages - 1, std::integral_constant<int, fill>{});
     v4i a[4], b[4];
+    operands(std::integral_constant<int, nst>{}, a, b);
+    if (GS64 || step % spg == spg - 1) {
+      v4f xsv[4];
+      float wsc[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = wm * 64 + 16 * i + lrow;
-      a[i] = *reinterpret_cast<const v4i *>(&S.a[row * 64 + ((lq ^ q8_swizzle(row)) << 4)]);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int row = b_row(t.swiglu, wn, j) + lrow;
-      b[j] = *reinterpret_cast<const v4i *>(&S.b[row * 64 + ((lq ^ q8_swizzle(row)) << 4)]);
-    }
-    const bool first = step % spg == 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 4; i++)
+        xsv[i] = *reinterpret_cast<const v4f *>(xsbase + st * kQ8SStride + i * 64);
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], first ? v4i{0, 0, 0, 0} : dot[i][j], 0, 0, 0);
-    if (step % spg == spg - 1) {
-      const int g = step / spg;
+        wsc[j] = *reinterpret_cast<const float *>(wsbase[j] + st * kQ8SStride);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const v4f xsv = *reinterpret_cast<const v4f *>(&S.xs[wm * 64 + 16 * i + lr4]);
+      for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const float wsc = S.ws[b_row(t.swiglu, wn, j) + lrow];
-#pragma unroll
-          for (int e = 0; e < 4; e++)
-            acc[i][j][e] = fmaf((float)dot[i][j][e] * wsc, xsv[e], acc[i][j][e]);
           if (PROBE) {
+            const int g = step / spg;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
               const int row = t.m0 + wm * 64 + 16 * i + lr4 + e, col = t.n0 + 64 * wn + 16 * j + lrow;
@@ -286,9 +316,54 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
                 p.probe[((long long)g * p.m + row) * seg.n + col] = dot[i][j][e];
             }
           }
+          float f[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            f[e] = (float)dot[i][j][e];
+          dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            acc[i][j][e] = fmaf(f[e] * wsc[j], xsv[i][e], acc[i][j][e]);
         }
-      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], dot[i][j], 0, 0, 0);
     }
+  };
+
+  issue(0, std::integral_constant<int, 0>{});
+  issue(1, std::integral_constant<int, 1>{});
+  issue(2, std::integral_constant<int, 2>{});
+  issue(3, std::integral_constant<int, 3>{});
+  wait_vmcnt<(kQ8Stages - 2) * kQ8LoadsPerStep>(); // step 0 has landed for this wave
+  __builtin_amdgcn_s_barrier();                      // ... and for every wave
+  {
+    v4i a[4], b[4];
+    operands(std::integral_constant<int, 0>{}, a, b);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+  }
+  // the K loop unrolled by the five stages, so every stage index is a constant
+  for (int step = 0; step < steps; step += kQ8Stages) {
+    advance(step, std::integral_constant<int, 0>{});
+    if (step + 1 >= steps)
+      break;
+    advance(step + 1, std::integral_constant<int, 1>{});
+    if (step + 2 >= steps)
+      break;
+    advance(step + 2, std::integral_constant<int, 2>{});
+    if (step + 3 >= steps)
+      break;
+    advance(step + 3, std::integral_constant<int, 3>{});
+    if (step + 4 >= steps)
+      break;
+    advance(step + 4, std::integral_constant<int, 4>{});
   }
   // the loads issued for steps past the end still target this block's LDS: let them land before the block exits
   __builtin_amdgcn_s_waitcnt(0);
@@ -546,17 +621,24 @@ Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m) {
 }
 
 // The pipelined kernel takes more than the default 64 KB of dynamic LDS: raised once per instantiation.
-template <bool PROBE> bool q8_lds_ready() {
-  static const hipError_t status =
-      hipFuncSetAttribute((const void *)q8_gemm_lds<PROBE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ8Lds);
+template <bool PROBE, bool GS64> bool q8_ready() {
+  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_lds<PROBE, GS64>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ8Lds);
   return check_hip(status, "allowing the Q8 GEMM its LDS");
 }
 
-template <bool PROBE> bool launch_q8_lds(const Q8Params &p, hipStream_t stream) {
-  if (!q8_lds_ready<PROBE>())
+template <bool PROBE, bool GS64> bool q8_launch(const Q8Params &p, hipStream_t stream) {
+  if (!q8_ready<PROBE, GS64>())
     return false;
-  hipLaunchKernelGGL(q8_gemm_lds<PROBE>, dim3(p.grid.total), dim3(kQ8Threads), kQ8Lds, stream, p);
+  hipLaunchKernelGGL((q8_gemm_lds<PROBE, GS64>), dim3(p.grid.total), dim3(kQ8Threads), kQ8Lds, stream, p);
   return launch_ok("q8_gemm_lds");
+}
+
+template <bool PROBE> bool launch_q8_lds(Q8Params p, const GemmSegmentDev *segs, int nseg, hipStream_t stream) {
+  p.grid = make_q8_grid(segs, nseg, p.m);
+  if (p.grid.total <= 0)
+    return true;
+  return p.gs == 64 ? q8_launch<PROBE, true>(p, stream) : q8_launch<PROBE, false>(p, stream);
 }
 
 } // namespace
@@ -571,15 +653,12 @@ bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream) {
   if (job.m <= 0 || job.k <= 0)
     return true;
   Q8Params p{};
-  p.grid = make_q8_grid(job.seg, job.nseg, job.m);
   p.xq = job.xq;
   p.xs = job.xs;
   p.m = job.m;
   p.k = job.k;
   p.gs = job.gs;
-  if (p.grid.total <= 0)
-    return true;
-  return launch_q8_lds<false>(p, stream);
+  return launch_q8_lds<false>(p, job.seg, job.nseg, stream);
 }
 
 bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream) {
@@ -613,14 +692,13 @@ bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs,
     return false;
   GemmSegmentDev seg{scratch, n, wq, nullptr, ones, nullptr, (size_t)k, n, EPI_STORE};
   Q8Params p{};
-  p.grid = make_q8_grid(&seg, 1, m);
   p.xq = xq;
   p.xs = ones;
   p.m = m;
   p.k = k;
   p.gs = gs;
   p.probe = dots;
-  bool ok = launch_q8_lds<true>(p, stream);
+  bool ok = launch_q8_lds<true>(p, &seg, 1, stream);
   (void)hipFreeAsync(scratch, stream);
   (void)hipFreeAsync(ones, stream);
   return ok;

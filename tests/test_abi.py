@@ -38,6 +38,13 @@ def test_every_declared_function_is_exported(L):
     assert not sorted(names - set(lh._SIGNATURES)), sorted(names - set(lh._SIGNATURES))
 
 
+def test_library_resolves_every_symbol_of_its_own():
+    """A kernel whose host-side stub the compiler dropped shows up as an undefined llhip symbol in the library."""
+    out = subprocess.run(["nm", "-D", lh.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    undefined = [line.split()[-1] for line in out.splitlines() if line.split()[:1] == ["U"] and "llhip" in line]
+    assert not undefined, undefined
+
+
 def test_struct_layouts_match_the_reference():
     """Sizes and offsets on x86-64 of the reference's structs (kernels.h:101-109, gemm.h:22-30, 89-96, 118-125,
     runtime.h:9-16, 87-97), restated field by field."""
