@@ -361,10 +361,14 @@ template <bool FUSED, int BLOCK, int MAXC> struct Input {
 // group's first lane adds ((float)dot * ws) * xs to its FP32 accumulator (the reference's per-group expression,
 // src/gemv.c:428). A wave reduction gives the wave's part of the row; with KS > 1 the parts meet in LDS and the first
 // wave of the row adds them in part order and applies the epilogue.
-template <int CH, int KS, bool SWIGLU>
+template <int CH, int KS, bool SWIGLU, bool SG>
 struct RowPart {
+  // SG (gs = 64, 16 groups per 1024-byte chunk): scale register h of lane l holds the scale of group l % 16 of the
+  // wave's chunk 4 h + l / 16, one load for four chunks, and each chunk's group leaders fetch theirs from the lane that
+  // holds it (ds_bpermute); otherwise every lane loads its group's scale for every chunk.
+  static constexpr int kScaleRegs = SG ? (CH + 3) / 4 : CH;
   int4 w[CH], w3[CH];
-  float ws[CH], w3s[CH];
+  float ws[kScaleRegs], w3s[kScaleRegs];
   float prior; // ADD: the output's current value, loaded with the weights
   GemvSeg seg;
   int s, row;
@@ -392,12 +396,25 @@ struct RowPart {
 #pragma unroll
     for (int c = 0; c < CH; c++) {
       const int off = ((c * KS + part) << 10) + lane * 16;
-      const int soff = (off / p.gs) * 4;
       w[c] = load16(rw, off, 1);
-      ws[c] = load4(rs, soff);
-      if (SWIGLU) {
+      if (SWIGLU)
         w3[c] = load16(rw3, off, 1);
-        w3s[c] = load4(rs3, soff);
+      if (!SG) {
+        const int soff = (off / p.gs) * 4;
+        ws[c] = load4(rs, soff);
+        if (SWIGLU)
+          w3s[c] = load4(rs3, soff);
+      }
+    }
+    if (SG) {
+#pragma unroll
+      for (int h = 0; h < kScaleRegs; h++) {
+        const int j = 4 * h + (lane >> 4); // the wave's chunk this lane's scale belongs to
+        // past the wave's chunks the offset lies beyond every row's scales: zero, no access
+        const int soff = j < CH ? (((j * KS + part) << 4) + (lane & 15)) * 4 : 0x7ffffff0;
+        ws[h] = load4(rs, soff);
+        if (SWIGLU)
+          w3s[h] = load4(rs3, soff);
       }
     }
     // The residual read of ADD is issued here, after this step's weights: loads complete in issue order for the
@@ -425,10 +442,14 @@ struct RowPart {
         const int d = group_reduce_add(dot16(w[c], xv), p.lpg);
         if (probe && active && leader)
           probe[(long long)g * seg.rows + row] = d;
-        acc += leader ? ((float)d * ws[c]) * xsg : 0.0f;
+        // the scale of this lane's group in chunk c: from lane (c % 4) * 16 + lane / 4 under SG
+        const int src = ((c & 3) * 16 + (lane >> 2)) * 4;
+        const float wsc = SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ws[c / 4 < kScaleRegs ? c / 4 : 0]))) : ws[c < kScaleRegs ? c : 0];
+        acc += leader ? ((float)d * wsc) * xsg : 0.0f;
         if (SWIGLU) {
           const int d3 = group_reduce_add(dot16(w3[c], xv), p.lpg);
-          gacc += leader ? ((float)d3 * w3s[c]) * xsg : 0.0f;
+          const float w3sc = SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(w3s[c / 4 < kScaleRegs ? c / 4 : 0]))) : w3s[c < kScaleRegs ? c : 0];
+          gacc += leader ? ((float)d3 * w3sc) * xsg : 0.0f;
         }
       }
     }
@@ -450,8 +471,8 @@ struct RowPart {
 
 constexpr int kMaxGemvWaves = 16;
 
-template <int WAVES, int CH, int KS, bool SWIGLU>
-__device__ __forceinline__ void gemv_step(const GemvParams &p, const RowPart<CH, KS, SWIGLU> &set,
+template <int WAVES, int CH, int KS, bool SWIGLU, bool SG>
+__device__ __forceinline__ void gemv_step(const GemvParams &p, const RowPart<CH, KS, SWIGLU, SG> &set,
                                           const int8_t *sxq, const float *sxs, float2 *red, int wave, int part,
                                           int lane, int &parity) {
   const float2 r = set.dot(p, sxq, sxs, part, lane);
@@ -478,7 +499,7 @@ __device__ __forceinline__ void gemv_step(const GemvParams &p, const RowPart<CH,
   parity ^= 1;
 }
 
-template <int WAVES, int CH, int KS, bool SWIGLU, bool FUSED>
+template <int WAVES, int CH, int KS, bool SWIGLU, bool FUSED, bool SG>
 __global__ __launch_bounds__(WAVES * 64) void q8_gemv(GemvParams p) {
   constexpr int kRows = WAVES / KS; // rows per block step
   extern __shared__ __align__(16) unsigned char smem[];
@@ -497,7 +518,7 @@ __global__ __launch_bounds__(WAVES * 64) void q8_gemv(GemvParams p) {
   in.load(p);
   __builtin_amdgcn_sched_barrier(0);
   // the first two steps' weights are in flight while the block stages its input
-  RowPart<CH, KS, SWIGLU> a, b;
+  RowPart<CH, KS, SWIGLU, SG> a, b;
   a.load(p, step * kRows + slot, part, lane);
   b.load(p, (step + stride) * kRows + slot, part, lane);
   __builtin_amdgcn_sched_barrier(0);
@@ -715,15 +736,11 @@ bool launch_quantize(const QuantizeJob &job, hipStream_t stream) {
 // Launch-shape overrides set by llhip_set_gemv_shape (0: the default, or the environment's).
 static std::atomic<int> forced_split{0}, forced_blocks{0}, forced_waves{0};
 
-// Blocks per CU of the persistent GEMV grid (LLAMA_HIP_GEMV_BLOCKS_PER_CU overrides, for sweeps).
-static int gemv_blocks_per_cu() {
-  static const int value = [] {
-    const char *env = getenv("LLAMA_HIP_GEMV_BLOCKS_PER_CU");
-    const int v = env && *env ? atoi(env) : 0;
-    return v >= 1 && v <= 64 ? v : 2;
-  }();
-  const int forced = forced_blocks.load(std::memory_order_relaxed);
-  return forced ? forced : value;
+// Launch-shape overrides from the environment, read once (0: none).
+static int env_shape(const char *name, int lo, int hi) {
+  const char *env = getenv(name);
+  const int v = env && *env ? atoi(env) : 0;
+  return v >= lo && v <= hi ? v : 0;
 }
 
 // Dynamic LDS of the fast GEMV: the int8 input (rounded to 16 bytes), its scales (rounded to an even count) and the
@@ -732,67 +749,74 @@ static size_t gemv_lds_bytes(int n, int gs) {
   return ((size_t)(n + 15) & ~(size_t)15) + (size_t)((n / gs + 1) & ~1) * sizeof(float) + 2 * kMaxGemvWaves * 8;
 }
 
-// Waves per block: 16 (one block per CU stages the input once for all its waves) unless set otherwise.
-static int gemv_block_waves() {
-  static const int value = [] {
-    const char *env = getenv("LLAMA_HIP_GEMV_BLOCK_WAVES");
-    const int v = env && *env ? atoi(env) : 0;
-    return v == 8 || v == 16 ? v : 16;
-  }();
-  const int forced = forced_waves.load(std::memory_order_relaxed);
-  return forced ? forced : value;
-}
-
 template <int WAVES, int CH, int KS, bool SWIGLU>
 static void launch_shape(const GemvParams &p, bool fused, int per_cu, hipStream_t stream) {
   const size_t lds = gemv_lds_bytes(p.n, p.gs);
   const int steps = (p.total_rows + WAVES / KS - 1) / (WAVES / KS);
   const int cap = device().cu_count * per_cu;
   const int blocks = steps < cap ? steps : cap;
-  if (fused)
-    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
+  const bool sg = p.gs == 64;
+  if (fused && sg)
+    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true, true>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
+  else if (fused)
+    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true, false>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
+  else if (sg)
+    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, false, true>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
   else
-    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, false>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
+    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, false, false>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
+}
+
+// The launch shape of one GEMV: waves per row (split of K), resident 8-wave block equivalents per CU, waves per block.
+struct GemvShape {
+  int split, per_cu, waves;
+};
+
+// Measured on MI355X over the 8B shapes (the 16-wave block stages the input once for twice the waves):
+//   - rows of K <= 8192 take two waves each (at most four 1024-byte chunks per wave), longer rows four (W2's 14336);
+//   - the SwiGLU pair (twice the registers per row) streams best from three 8-wave blocks per CU;
+//   - a long matrix (the 128256-row classifier) from one wave per row and four block equivalents per CU;
+//   - everything else from one 16-wave block per CU.
+// llhip_set_gemv_shape and LLAMA_HIP_GEMV_KSPLIT / _BLOCKS_PER_CU / _BLOCK_WAVES override each part.
+static GemvShape gemv_shape(int total_rows, int nchunks, bool swiglu) {
+  static const int env_split = env_shape("LLAMA_HIP_GEMV_KSPLIT", 1, 8);
+  static const int env_per_cu = env_shape("LLAMA_HIP_GEMV_BLOCKS_PER_CU", 1, 64);
+  static const int env_waves = env_shape("LLAMA_HIP_GEMV_BLOCK_WAVES", 8, 16);
+  GemvShape g{nchunks <= 8 ? 2 : 4, 2, 16};
+  if (swiglu) {
+    g.per_cu = 3;
+    g.waves = 8;
+  } else if (total_rows >= 32768) {
+    g.split = nchunks <= 4 ? 1 : g.split;
+    g.per_cu = 4;
+  }
+  const int split = forced_split.load(std::memory_order_relaxed), per_cu = forced_blocks.load(std::memory_order_relaxed),
+            waves = forced_waves.load(std::memory_order_relaxed);
+  g.split = split ? split : (env_split == 1 || env_split == 2 || env_split == 4 || env_split == 8) ? env_split : g.split;
+  g.per_cu = per_cu ? per_cu : env_per_cu ? env_per_cu : g.per_cu;
+  g.waves = waves ? waves : (env_waves == 8 || env_waves == 16) ? env_waves : g.waves;
+  return g;
 }
 
 template <int CH, int KS, bool SWIGLU>
-static void launch_fast(const GemvParams &p, bool fused, hipStream_t stream) {
-  // blocks per CU counts 8-wave blocks: a 16-wave block stands for two
-  const int bpc = gemv_blocks_per_cu();
-  if (gemv_block_waves() == 16 && bpc % 2 == 0)
-    launch_shape<16, CH, KS, SWIGLU>(p, fused, bpc / 2, stream);
+static void launch_fast(const GemvParams &p, bool fused, const GemvShape &g, hipStream_t stream) {
+  // per_cu counts 8-wave blocks: a 16-wave block stands for two
+  if (g.waves == 16 && g.per_cu % 2 == 0)
+    launch_shape<16, CH, KS, SWIGLU>(p, fused, g.per_cu / 2, stream);
   else
-    launch_shape<8, CH, KS, SWIGLU>(p, fused, bpc, stream);
-}
-
-// Waves per row: two for K <= 8192 (at most four 1024-byte chunks per wave), four above (W2's 14336). Two waves per
-// K = 4096 row measured fastest on MI355X for every 8B shape: the block steps then divide evenly over two blocks per
-// CU (QKV 6144 rows: 1536 steps, W1/W3 14336: 3584, Wo 4096: 1024). LLAMA_HIP_GEMV_KSPLIT=1|2|4|8 forces a split.
-static int waves_per_row(int nchunks) {
-  static const int from_env = [] {
-    const char *env = getenv("LLAMA_HIP_GEMV_KSPLIT");
-    const int v = env && *env ? atoi(env) : 0;
-    return v == 1 || v == 2 || v == 4 || v == 8 ? v : 0;
-  }();
-  const int forced = forced_split.load(std::memory_order_relaxed);
-  if (forced)
-    return forced;
-  if (from_env)
-    return from_env;
-  return nchunks <= 8 ? 2 : 4;
+    launch_shape<8, CH, KS, SWIGLU>(p, fused, g.per_cu, stream);
 }
 
 template <int KS, bool SWIGLU>
-static void launch_split(const GemvParams &p, bool fused, hipStream_t stream) {
+static void launch_split(const GemvParams &p, bool fused, const GemvShape &g, hipStream_t stream) {
   const int per = (p.nchunks + KS - 1) / KS; // chunks per wave
   if (per <= 1)
-    launch_fast<1, KS, SWIGLU>(p, fused, stream);
+    launch_fast<1, KS, SWIGLU>(p, fused, g, stream);
   else if (per <= 2)
-    launch_fast<2, KS, SWIGLU>(p, fused, stream);
+    launch_fast<2, KS, SWIGLU>(p, fused, g, stream);
   else if (per <= 4)
-    launch_fast<4, KS, SWIGLU>(p, fused, stream);
+    launch_fast<4, KS, SWIGLU>(p, fused, g, stream);
   else // per <= 16 only with one wave per row: two waves of at most 8 chunks instead (16 would spill registers)
-    launch_fast<8, 2, SWIGLU>(p, fused, stream);
+    launch_fast<8, 2, SWIGLU>(p, fused, g, stream);
 }
 
 bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves) {
@@ -859,18 +883,19 @@ bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
     p.probe = job.probe;
     p.flags = device().error_flags;
     const bool fused = job.xf_quantize, swiglu = job.epi == EPI_SWIGLU;
-    switch (waves_per_row(p.nchunks)) {
+    const GemvShape g = gemv_shape(rows, p.nchunks, swiglu);
+    switch (g.split) {
     case 1:
-      swiglu ? launch_split<1, true>(p, fused, stream) : launch_split<1, false>(p, fused, stream);
+      swiglu ? launch_split<1, true>(p, fused, g, stream) : launch_split<1, false>(p, fused, g, stream);
       break;
     case 2:
-      swiglu ? launch_split<2, true>(p, fused, stream) : launch_split<2, false>(p, fused, stream);
+      swiglu ? launch_split<2, true>(p, fused, g, stream) : launch_split<2, false>(p, fused, g, stream);
       break;
     case 4:
-      swiglu ? launch_split<4, true>(p, fused, stream) : launch_split<4, false>(p, fused, stream);
+      swiglu ? launch_split<4, true>(p, fused, g, stream) : launch_split<4, false>(p, fused, g, stream);
       break;
     default:
-      swiglu ? launch_split<8, true>(p, fused, stream) : launch_split<8, false>(p, fused, stream);
+      swiglu ? launch_split<8, true>(p, fused, g, stream) : launch_split<8, false>(p, fused, g, stream);
       break;
     }
     return launch_ok("q8_gemv");
