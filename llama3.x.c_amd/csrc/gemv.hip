@@ -439,17 +439,25 @@ struct RowPart {
         const int4 xv = active ? *reinterpret_cast<const int4 *>(sxq + off) : int4{0, 0, 0, 0};
         const int g = off / p.gs;
         const float xsg = active ? sxs[g] : 0.0f;
-        const int d = group_reduce_add(dot16(w[c], xv), p.lpg);
-        if (probe && active && leader)
-          probe[(long long)g * seg.rows + row] = d;
+        // this lane's int32 dot of its 16 values (exact); the group's lanes add theirs for the probe only
+        const int pd = dot16(w[c], xv);
+        if (probe) {
+          const int d = group_reduce_add(pd, p.lpg);
+          if (active && leader)
+            probe[(long long)g * seg.rows + row] = d;
+        }
         // the scale of this lane's group in chunk c: from lane (c % 4) * 16 + lane / 4 under SG
         const int src = ((c & 3) * 16 + (lane >> 2)) * 4;
-        const float wsc = SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ws[c / 4 < kScaleRegs ? c / 4 : 0]))) : ws[c < kScaleRegs ? c : 0];
-        acc += leader ? ((float)d * wsc) * xsg : 0.0f;
+        const float wsc = SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ws[c / 4 < kScaleRegs ? c / 4 : 0])))
+                             : ws[c < kScaleRegs ? c : 0];
+        // every lane scales its partial: sum over the group's lanes of (float)partial * ws * xs, which differs from
+        // ((float)dot * ws) * xs only in FP32 rounding
+        acc = fmaf((float)pd, wsc * xsg, acc);
         if (SWIGLU) {
-          const int d3 = group_reduce_add(dot16(w3[c], xv), p.lpg);
-          const float w3sc = SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(w3s[c / 4 < kScaleRegs ? c / 4 : 0]))) : w3s[c < kScaleRegs ? c : 0];
-          gacc += leader ? ((float)d3 * w3sc) * xsg : 0.0f;
+          const int pd3 = dot16(w3[c], xv);
+          const float w3sc = SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(w3s[c / 4 < kScaleRegs ? c / 4 : 0])))
+                                : w3s[c < kScaleRegs ? c : 0];
+          gacc = fmaf((float)pd3, w3sc * xsg, gacc);
         }
       }
     }
