@@ -298,7 +298,8 @@ def gemm_case(m, n, k, gs, seed):
 
 @pytest.mark.parametrize("m,n,k,gs", [(1, 64, 64, 64), (33, 20, 128, 64), (40, 33, 192, 64), (130, 257, 1024, 64),
                                       (256, 384, 4096, 64), (77, 200, 2048, 128), (64, 96, 512, 32), (5, 7, 16, 4),
-                                      (129, 129, 640, 64)])
+                                      (129, 129, 640, 64), (600, 200, 1024, 64), (300, 136, 14336, 64),
+                                      (50, 70, 1024, 256), (513, 65, 320, 64)])
 def test_gemm_q8_all_kinds_within_budget(m, n, k, gs):
     L = hu.lib()
     T = hu.torch()
@@ -348,7 +349,8 @@ def test_gemm_q8_qkv_segments_and_gemv_agreement():
             hu.assert_within_budget(hu.host(row), got[i], mag[i] * 2, what="gemm row vs gemv")
 
 
-@pytest.mark.parametrize("m,n,k,gs", [(33, 20, 128, 64), (130, 200, 1024, 64), (64, 64, 512, 128)])
+@pytest.mark.parametrize("m,n,k,gs", [(33, 20, 128, 64), (130, 200, 1024, 64), (64, 64, 512, 128), (300, 130, 448, 64),
+                                      (40, 24, 768, 256)])
 def test_gemm_q8_int32_probe_bitwise(m, n, k, gs):
     L = hu.lib()
     xq, _, wq, _, _, _, _ = gemm_case(m, n, k, gs, 808 + m)
