@@ -29,6 +29,8 @@ for p in (ROOT, PKG):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA
+F32_PEAK_TFS = 157.3  # MI355X fp32 matrix
 
 # Llama-3.1-8B
 DIM, KV_DIM, HIDDEN, VOCAB, LAYERS, GS = 4096, 1024, 14336, 128256, 32, 64
@@ -237,6 +239,84 @@ def prefill_set(torch, lh, model, seed):
     return run, gemms, ops
 
 
+def prefill_3b(torch, lh, seed, steps=3):
+    """The FP32 / BF16 batched-prefill GEMMs on the Llama-3.2-3B shapes: 512 tokens, dim 3072, kv_dim 1024, hidden
+    8192, 28 layers of QKV (three segments), Wo (+residual), W1/W3 (SwiGLU) and W2 (+residual). Weights ~N(0, 0.02)
+    drawn on the device, BF16 weights packed on the device into the pack_bf16_vnni layout (16-row tiles, K pairs;
+    torch's float -> bfloat16 cast rounds to nearest even like bf16_from_f32 for finite values)."""
+    L = lh.load()
+    T, D, KVD, H, NL = 512, 3072, 1024, 8192, 28
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 3)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    shapes = [("wq", D, D), ("wk", KVD, D), ("wv", KVD, D), ("wo", D, D), ("w1", H, D), ("w3", H, D), ("w2", D, H)]
+
+    def vnni(w):
+        n, k = w.shape
+        b = w.to(torch.bfloat16).view(torch.int16).reshape(n // 16, 16, k // 2, 2).permute(0, 2, 1, 3)
+        return b.contiguous().reshape(-1)
+
+    layers = []
+    for _ in range(NL):
+        lay = {}
+        for name, n, k in shapes:
+            w = torch.empty(n, k, **f32)
+            w.normal_(0.0, 0.02, generator=gen)
+            lay[name] = (w, vnni(w))
+        layers.append(lay)
+    x, h = torch.randn(T, D, generator=gen, **f32), torch.randn(T, H, generator=gen, **f32)
+    q, kk, v = torch.empty(T, D, **f32), torch.empty(T, KVD, **f32), torch.empty(T, KVD, **f32)
+    resid, hb = torch.zeros(T, D, **f32), torch.empty(T, H, **f32)
+    panel = lh.AlignedBuffer()
+    L.aligned_buffer_alloc(panel, L.k_gemm_bf16_panel_bytes(T, H), 1)
+    torch.cuda.synchronize()
+    P = lh.ptr
+    flops = 2 * T * NL * sum(n * k for _, n, k in shapes)
+
+    def f32seg(c, w, n, k, kind, w3=None):
+        return lh.GemmSegment(P(c), n, P(w), P(w3) if w3 is not None else None, k, n, kind)
+
+    def bfseg(c, pw, n, kind, pw3=None):
+        return lh.GemmBf16Segment(P(c), n, P(pw), P(pw3) if pw3 is not None else None, n, kind)
+
+    def run(mode):
+        for lay in layers:
+            if mode == "f32":
+                qkv = (lh.GemmSegment * 3)(f32seg(q, lay["wq"][0], D, D, 0), f32seg(kk, lay["wk"][0], KVD, D, 0),
+                                           f32seg(v, lay["wv"][0], KVD, D, 0))
+                L.k_gemm_f32(P(x), D, T, D, qkv, 3)
+                L.k_gemm_f32(P(x), D, T, D, f32seg(resid, lay["wo"][0], D, D, 1), 1)
+                L.k_gemm_f32(P(x), D, T, D, f32seg(hb, lay["w1"][0], H, D, 2, lay["w3"][0]), 1)
+                L.k_gemm_f32(P(h), H, T, H, f32seg(resid, lay["w2"][0], D, H, 1), 1)
+            else:
+                qkv = (lh.GemmBf16Segment * 3)(bfseg(q, lay["wq"][1], D, 0), bfseg(kk, lay["wk"][1], KVD, 0),
+                                               bfseg(v, lay["wv"][1], KVD, 0))
+                L.k_gemm_bf16(P(x), D, T, D, qkv, 3, panel)
+                L.k_gemm_bf16(P(x), D, T, D, bfseg(resid, lay["wo"][1], D, 1), 1, panel)
+                L.k_gemm_bf16(P(x), D, T, D, bfseg(hb, lay["w1"][1], H, 2, lay["w3"][1]), 1, panel)
+                L.k_gemm_bf16(P(h), H, T, H, bfseg(resid, lay["w2"][1], D, 1), 1, panel)
+
+    out = {}
+    for mode, peak in (("bf16", BF16_PEAK_TFS), ("f32", F32_PEAK_TFS)):
+        run(mode)
+        L.llhip_synchronize()
+        assert L.llhip_graph_begin() == 0
+        run(mode)
+        graph = L.llhip_graph_end()
+        sec = time_graph(torch, L, graph, steps, 1) / steps
+        L.llhip_graph_destroy(graph)
+        tf = flops / sec / 1e12
+        out[mode] = {"value": round(T / sec, 1), "unit": "tok/s", "ms_per_prompt": round(sec * 1e3, 3),
+                     "tflops": round(tf, 1), "peak_tflops": peak, "frac": round(tf / peak, 4)}
+        print(f"# 3B {mode} prefill: {sec * 1e3:.2f} ms/prompt, {T / sec:.0f} tok/s, {tf:.0f} TFLOP/s",
+              file=sys.stderr, flush=True)
+    L.aligned_buffer_free(panel)
+    out["workload"] = ("Llama-3.2-3B FP32 / BF16 batched prefill GEMMs, 512 tokens, 28 layers (QKV, Wo +resid, W1/W3 "
+                       "SwiGLU, W2 +resid), FP32 activations")
+    out["flops_per_prompt"] = flops
+    return out
+
+
 def cpu_baseline(threads, budget_s=30.0):
     """The reference's own instrument, gemm-bench --gemv (tests/gemm_bench.c), on the five 8B decode shapes with cold
     weights, scaled to one token (32 x the layer set + the classifier). Falls back to the oracle's threaded scalar GEMV
@@ -298,6 +378,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--seed", type=int, default=88172645463325252 % (1 << 31))
+    ap.add_argument("--c3", action="store_true",
+                    help="also measure the FP32 / BF16 prefill GEMMs on the Llama-3.2-3B shapes (512 tokens)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also launch a plain copy kernel of this many MiB (counter calibration for --pmc runs)")
     args = ap.parse_args()
@@ -404,6 +486,8 @@ def main():
               f"{ach:.0f} TOP/s in the W1/W3 GEMM", file=sys.stderr, flush=True)
     L.llhip_graph_destroy(graph)
 
+    if args.c3:
+        result["prefill_3b"] = prefill_3b(torch, lh, args.seed)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_threads)
     print(json.dumps(result), flush=True)

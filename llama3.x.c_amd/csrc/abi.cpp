@@ -566,8 +566,13 @@ void k_gemm_bf16(const float *a, int lda, int m, int k, const GemmBf16Segment *s
   if (!panel || panel->bytes < k_gemm_bf16_panel_bytes(m, k))
     return (void)raise("BF16 activation panel holds %zu bytes but %zu are needed", panel ? panel->bytes : (size_t)0,
                        k_gemm_bf16_panel_bytes(m, k));
+  if (!panel->data)
+    return (void)raise("BF16 activation panel has no memory");
   Call call("k_gemm_bf16");
   Ref A = call.in2d(a, (size_t)k * sizeof(float), (size_t)lda * sizeof(float), (size_t)m);
+  // the rounded activations, m rows of K rounded up to 32 values (device memory from aligned_buffer_alloc is used in
+  // place; a host panel is staged like any other host buffer)
+  Ref PANEL = call.out(panel->data, (size_t)m * (size_t)((k + 31) / 32 * 32) * sizeof(uint16_t), false);
   Ref W[3], W3[3], C[3];
   for (int s = 0; s < count; s++) {
     const GemmBf16Segment &g = segments[s];
@@ -599,6 +604,7 @@ void k_gemm_bf16(const float *a, int lda, int m, int k, const GemmBf16Segment *s
   job.m = m;
   job.k = k;
   job.bf16 = true;
+  job.panel = call.ptr<unsigned short>(PANEL);
   if (launch_f32_gemm(job, call.stream()))
     call.finish();
 }

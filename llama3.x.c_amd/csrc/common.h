@@ -175,6 +175,7 @@ struct GemmF32Job {
   GemmSegmentDev seg[3];
   int nseg;
   bool bf16; // BF16 mode: seg[].w are packed bf16 (pack_bf16_vnni layout), A is rounded to bf16 on the fly
+  unsigned short *panel; // BF16 mode: device panel of m x (K rounded up to 32) for the pipelined kernel, or null
 };
 bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream);
 

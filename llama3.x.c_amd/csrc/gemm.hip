@@ -370,6 +370,156 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
+// Round to nearest even on the 16 dropped bits, NaN quieted with its sign and top payload bits, denormals kept,
+// overflow to infinity: the conversion of the reference's bf16_from_f32 (src/gemm.c:335-342), as an integer formula.
+__device__ __forceinline__ unsigned short to_bf16(float x) {
+  unsigned u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u)
+    return (unsigned short)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (unsigned short)(u >> 16);
+}
+
+// ---- BF16: the activation panel and the pipelined BF16-MFMA kernel -----------------------------------------------------
+//
+// k_gemm_bf16 rounds A to BF16 once per call into the caller's panel (the reference's bf16_convert_rows,
+// src/gemm.c:693-706): rows of kp = K rounded up to 32 values, zero past K. The GEMM then has the structure of the int8
+// kernel above: a 256 x 128 output tile over eight waves of 64 x 64, v_mfma_f32_16x16x32_bf16 per 16 x 16 tile and K
+// step of 32, A and B tiles going straight from global memory into LDS five stages deep, 1 KB blocks of 16 rows
+// interleaved by stage. A block row is the 64 bytes of one step (32 BF16 values), XOR-swizzled in 16-byte chunks like
+// the int8 tiles. B arrives in the pack_bf16_vnni layout, whose 16-row tile and 32-value K step is exactly one
+// contiguous 1 KB block (16 K pairs of 16 rows x 2 values), copied verbatim. MFMA operands take K values 8 q .. 8 q + 7
+// for lane group q: 16 contiguous bytes of an A row, and four 4-byte K pairs of a B tile (two ds_read2_b32). The
+// FP32 sums stay in the MFMA accumulators: no per-step vector work.
+__global__ __launch_bounds__(256) void bf16_panel(const float *__restrict__ a, long long lda, int m, int k, int kp,
+                                                  unsigned short *__restrict__ panel) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x; // 8 values per thread
+  const int per_row = kp / 8;
+  if (idx >= (long long)m * per_row)
+    return;
+  const int row = (int)(idx / per_row), c0 = (int)(idx % per_row) * 8;
+  const float *src = a + row * lda;
+  unsigned packed[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = c0 + 2 * i;
+    const unsigned lo = c < k ? to_bf16(src[c]) : 0u, hi = c + 1 < k ? to_bf16(src[c + 1]) : 0u;
+    packed[i] = lo | (hi << 16);
+  }
+  *reinterpret_cast<uint4 *>(panel + (long long)row * kp + c0) = uint4{packed[0], packed[1], packed[2], packed[3]};
+}
+
+typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
+
+struct Bf16Params {
+  Q8Grid grid;
+  const unsigned short *panel; // m x kp BF16 activations
+  int m, k, kp;
+};
+
+constexpr int kBfLoadsPerStep = 3; // per wave: two A and one B load
+
+__global__ __launch_bounds__(kQ8Threads, 2) void bf16_gemm_lds(Bf16Params p) {
+  extern __shared__ __align__(16) unsigned char q8_smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const TilePos t = q8_tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
+  const TileSeg seg = q8_seg_of(p.grid, t.s);
+  const int steps = p.kp / 32;
+  const long long rowb = (long long)p.kp * 2; // panel row bytes
+
+  const int lrow4 = lane >> 2, chunk = lane & 3;
+  const int ra = 32 * wave + lrow4;
+  const __amdgpu_buffer_rsrc_t rA =
+      q8_buffer(p.panel + (long long)t.m0 * p.kp, (long long)min(kQ8TileM, p.m - t.m0) * rowb);
+  const int offA0 = (int)(ra * rowb) + ((chunk ^ q8_swizzle(ra)) << 4);
+  const int offA1 = (int)((ra + 16) * rowb) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
+  // B: this wave's 16-row tile (one VNNI tile of one matrix); step s is bytes [s * 1024, s * 1024 + 1024) of it
+  const int rb0 = 16 * wave;
+  const int colB = t.swiglu ? t.n0 + (rb0 & 63) : t.n0 + rb0;
+  const unsigned short *wmat = (const unsigned short *)((t.swiglu && rb0 >= 64) ? seg.w3 : seg.w);
+  const long long tile_bytes = (long long)p.kp * 32; // 16 rows x kp values x 2 bytes
+  const __amdgpu_buffer_rsrc_t rB =
+      q8_buffer((const unsigned char *)wmat + (long long)(colB / 16) * tile_bytes, colB < seg.n ? tile_bytes : 0);
+  const int offB = lane * 16;
+  const __amdgpu_buffer_rsrc_t none = q8_buffer(p.panel, 0);
+
+  auto issue = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value;
+    const bool live = step < steps;
+    const int k0 = step * 64;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, (void *)(q8_smem + ((2 * wave) * kQ8Stages + st) * 1024),
+                                             16, offA0, k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
+                                             (void *)(q8_smem + ((2 * wave + 1) * kQ8Stages + st) * 1024), 16, offA1,
+                                             k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB : none,
+                                             (void *)(q8_smem + kQ8BOff + (wave * kQ8Stages + st) * 1024), 16, offB,
+                                             step * 1024, 0, 0);
+  };
+
+  const int lrow = lane & 15, lq = lane >> 4;
+  const unsigned char *abase = q8_smem + (4 * wm) * kQ8Stages * 1024 + lrow * 64 + ((lq ^ q8_swizzle(lrow)) << 4);
+  const unsigned char *bbase[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    bbase[j] = q8_smem + kQ8BOff + (b_row(t.swiglu, wn, j) / 16) * kQ8Stages * 1024 + lq * 256 + lrow * 4;
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto advance = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value, fill = (st + kQ8Stages - 1) % kQ8Stages;
+    wait_vmcnt<(kQ8Stages - 2) * kBfLoadsPerStep>(); // this wave's loads of `step` have landed
+    __builtin_amdgcn_s_barrier();                     // ... every wave's; the stage of step - 1 is free
+    issue(step + kQ8Stages - 1, std::integral_constant<int, fill>{});
+    v8bf_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      a[i] = *reinterpret_cast<const v8bf_t *>(abase + (i * kQ8Stages + st) * 1024);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const unsigned char *bp = bbase[j] + st * 1024;
+      typedef unsigned v4u __attribute__((ext_vector_type(4)));
+      const v4u pairs = v4u{*reinterpret_cast<const unsigned *>(bp), *reinterpret_cast<const unsigned *>(bp + 64),
+                            *reinterpret_cast<const unsigned *>(bp + 128), *reinterpret_cast<const unsigned *>(bp + 192)};
+      b[j] = __builtin_bit_cast(v8bf_t, pairs);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  };
+
+  issue(0, std::integral_constant<int, 0>{});
+  issue(1, std::integral_constant<int, 1>{});
+  issue(2, std::integral_constant<int, 2>{});
+  issue(3, std::integral_constant<int, 3>{});
+  for (int step = 0; step < steps; step += kQ8Stages) {
+    advance(step, std::integral_constant<int, 0>{});
+    if (step + 1 >= steps)
+      break;
+    advance(step + 1, std::integral_constant<int, 1>{});
+    if (step + 2 >= steps)
+      break;
+    advance(step + 2, std::integral_constant<int, 2>{});
+    if (step + 3 >= steps)
+      break;
+    advance(step + 3, std::integral_constant<int, 3>{});
+    if (step + 4 >= steps)
+      break;
+    advance(step + 4, std::integral_constant<int, 4>{});
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  store_tile(seg, t, acc, wm, wn, lane, p.m);
+}
+
 // Any group size (gs % 64 != 0): one thread per output, the per-group int32 dot in plain integer arithmetic.
 __global__ __launch_bounds__(kBlock) void q8_gemm_generic(TileGrid g, const int8_t *xq, const float *xs, int m, int k,
                                                           int gs) {
@@ -490,15 +640,6 @@ __global__ __launch_bounds__(kBlock) void f32_gemm_mfma(F32Params p) {
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
-// Round to nearest even on the 16 dropped bits, NaN quieted with its sign and top payload bits, denormals kept,
-// overflow to infinity: the conversion of the reference's bf16_from_f32 (src/gemm.c:335-342), as an integer formula.
-__device__ __forceinline__ unsigned short to_bf16(float x) {
-  unsigned u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u)
-    return (unsigned short)((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (unsigned short)(u >> 16);
-}
 
 // BF16: activations rounded to BF16 while staged, weights read from the pack_bf16_vnni layout (16-row tiles, K pairs:
 // element ((tile * kp / 2 + pair) * 16 + row) * 2 + e), v_mfma_f32_16x16x32_bf16 per 16 x 16 tile and 32 values of K.
@@ -715,6 +856,27 @@ bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream) {
   p.k = job.k;
   if (p.grid.total <= 0)
     return true;
+  if (job.bf16 && job.panel) {
+    // round A into the panel, then the pipelined kernel
+    const int kp = (job.k + 31) / 32 * 32;
+    const long long threads = (long long)job.m * (kp / 8);
+    hipLaunchKernelGGL(bf16_panel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, job.a,
+                       (long long)job.lda, job.m, job.k, kp, job.panel);
+    if (!launch_ok("bf16_panel"))
+      return false;
+    Bf16Params b{};
+    b.grid = make_q8_grid(job.seg, job.nseg, job.m);
+    b.panel = job.panel;
+    b.m = job.m;
+    b.k = job.k;
+    b.kp = kp;
+    static const hipError_t status = hipFuncSetAttribute((const void *)bf16_gemm_lds,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ8Lds);
+    if (!check_hip(status, "allowing the BF16 GEMM its LDS"))
+      return false;
+    hipLaunchKernelGGL(bf16_gemm_lds, dim3(b.grid.total), dim3(kQ8Threads), kQ8Lds, stream, b);
+    return launch_ok("bf16_gemm_lds");
+  }
   if (job.bf16) {
     hipLaunchKernelGGL(bf16_gemm_mfma, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
     return launch_ok("bf16_gemm_mfma");

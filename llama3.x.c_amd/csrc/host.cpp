@@ -189,20 +189,23 @@ PackS8 pack_s8_job_from_shard(int8_t *dst, const Shard *shard) {
 
 // ---- aligned workspace (gemm.c:400-411) ----------------------------------------------------------------------------
 
+// The reference allocates these only for the BF16 GEMM's activation panel (tp.c:920, 1001), which the GPU kernel
+// fills and reads: device memory here, zeroed, at least 256-byte aligned (hipMalloc).
 void aligned_buffer_alloc(AlignedBuffer *buffer, size_t bytes, MemoryKind kind) {
   (void)kind;
-  void *base = calloc(bytes + 63, 1);
-  if (!base) {
-    raise("out of memory: %zu bytes for an aligned buffer", bytes + 63);
+  buffer->base = buffer->data = nullptr;
+  buffer->bytes = 0;
+  void *p = nullptr;
+  if (!ensure_device() || !check_hip(hipMalloc(&p, bytes ? bytes : 1), "allocating an aligned buffer") ||
+      !check_hip(hipMemset(p, 0, bytes ? bytes : 1), "clearing an aligned buffer"))
     return;
-  }
-  buffer->base = base;
-  buffer->data = (void *)(((uintptr_t)base + 63) & ~(uintptr_t)63);
+  buffer->base = buffer->data = p;
   buffer->bytes = bytes;
 }
 
 void aligned_buffer_free(AlignedBuffer *buffer) {
-  free(buffer->base);
+  if (buffer->base)
+    (void)check_hip(hipFree(buffer->base), "freeing an aligned buffer");
   buffer->base = buffer->data = nullptr;
   buffer->bytes = 0;
 }
