@@ -501,19 +501,13 @@ __global__ __launch_bounds__(kQ8Threads, 2) void bf16_gemm_lds(Bf16Params p) {
   issue(1, std::integral_constant<int, 1>{});
   issue(2, std::integral_constant<int, 2>{});
   issue(3, std::integral_constant<int, 3>{});
+  // Whole rounds of five steps, with no exit between them: steps past the end load zeros (an empty buffer) and add
+  // nothing, and the accumulators stay in place across the unrolled body instead of being copied at every exit.
   for (int step = 0; step < steps; step += kQ8Stages) {
     advance(step, std::integral_constant<int, 0>{});
-    if (step + 1 >= steps)
-      break;
     advance(step + 1, std::integral_constant<int, 1>{});
-    if (step + 2 >= steps)
-      break;
     advance(step + 2, std::integral_constant<int, 2>{});
-    if (step + 3 >= steps)
-      break;
     advance(step + 3, std::integral_constant<int, 3>{});
-    if (step + 4 >= steps)
-      break;
     advance(step + 4, std::integral_constant<int, 4>{});
   }
   __builtin_amdgcn_s_waitcnt(0);
