@@ -26,7 +26,12 @@ struct Device {
   int *error_flags = nullptr; // device: [0] non-finite activation seen by a quantizer
   int cu_count = 0;
   bool capturing = false;
+  void *split_partial = nullptr;  // split-K partial tiles: LLHIP_SPLIT_SLOTS x 256 x 128 floats
+  unsigned *split_count = nullptr; // split-K arrivals per tile, zero between launches
 };
+// Partial tiles of the split-K workspace (one per block of a split launch): 512 x 128 KB = 64 MB of HBM. Launches on
+// the library's stream are ordered, so one workspace per device serves them all.
+#define LLHIP_SPLIT_SLOTS 512
 Device &device();
 bool ensure_device(); // opens the device on first use; false (after raise) when none is usable
 // Waits for the stream and turns a device-side error flag into a failure (the reference fails at once; a device
@@ -129,6 +134,7 @@ struct GemvJob {
   float *xs_out;
 };
 bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves);
+void set_gemm_splits(int splits); // FP32 / BF16 GEMM blocks per tile; 0 = chosen from the grid
 bool gemv_fast_path(const GemvJob &job);
 bool launch_q8_gemv(const GemvJob &job, hipStream_t stream);
 

@@ -5,6 +5,7 @@
 // grid of 16 x 16 MFMA tiles, and K is staged through double-buffered LDS. MFMA operand loads are symmetric (lane l
 // supplies row l % 16 of A and column l % 16 of W with the same K slice), so the dot products do not depend on how the
 // instruction orders K inside a lane; the 16 x 16 result holds C[4 (l / 16) + e][l % 16] in element e of lane l.
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 #include <vector>
@@ -19,7 +20,6 @@ constexpr int kTile = 128; // block tile rows and columns
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ float silu_gate(float value, float gate) {
   value *= (1.0f / (1.0f + expf(-value)));
@@ -380,17 +380,25 @@ __device__ __forceinline__ unsigned short to_bf16(float x) {
   return (unsigned short)(u >> 16);
 }
 
-// ---- BF16: the activation panel and the pipelined BF16-MFMA kernel -----------------------------------------------------
+// ---- FP32 and BF16: the pipelined MFMA kernel, with split K for short grids ---------------------------------------------
 //
 // k_gemm_bf16 rounds A to BF16 once per call into the caller's panel (the reference's bf16_convert_rows,
-// src/gemm.c:693-706): rows of kp = K rounded up to 32 values, zero past K. The GEMM then has the structure of the int8
-// kernel above: a 256 x 128 output tile over eight waves of 64 x 64, v_mfma_f32_16x16x32_bf16 per 16 x 16 tile and K
-// step of 32, A and B tiles going straight from global memory into LDS five stages deep, 1 KB blocks of 16 rows
-// interleaved by stage. A block row is the 64 bytes of one step (32 BF16 values), XOR-swizzled in 16-byte chunks like
-// the int8 tiles. B arrives in the pack_bf16_vnni layout, whose 16-row tile and 32-value K step is exactly one
-// contiguous 1 KB block (16 K pairs of 16 rows x 2 values), copied verbatim. MFMA operands take K values 8 q .. 8 q + 7
-// for lane group q: 16 contiguous bytes of an A row, and four 4-byte K pairs of a B tile (two ds_read2_b32). The
-// FP32 sums stay in the MFMA accumulators: no per-step vector work.
+// src/gemm.c:693-706): rows of kp = K rounded up to 32 values, zero past K. Both modes then share the structure of the
+// int8 kernel above: a 256 x 128 output tile over eight waves of 64 x 64, 4 x 4 MFMA tiles of 16 x 16 per wave, and a
+// K step of 64 bytes per row (32 BF16 or 16 FP32 values) whose A and B tiles go straight from global memory into LDS
+// five stages deep, in 1 KB blocks of 16 rows interleaved by stage. A block row is XOR-swizzled in 16-byte chunks like
+// the int8 tiles. MFMA operands take 16 contiguous bytes of a row per lane group q = lane / 16:
+//   BF16: v_mfma_f32_16x16x32_bf16, K values 8 q .. 8 q + 7. B arrives in the pack_bf16_vnni layout, whose 16-row
+//         tile and 32-value K step is one contiguous 1 KB block (16 K pairs of 16 rows x 2 values), copied verbatim;
+//         a lane's four K pairs are four 4-byte reads of it.
+//   FP32: four v_mfma_f32_16x16x4_f32 per tile and step; lane group q holds K values 4 q .. 4 q + 3 of A and W and
+//         feeds value s to the s-th instruction. W rows are read like A rows (row pitch ldw).
+// The FP32 sums stay in the MFMA accumulators: no per-step vector work.
+//
+// Split K: a grid with fewer tiles than CUs runs each tile as `splits` blocks over consecutive K ranges. Each block
+// writes its 256 x 128 partial sums to a device workspace and counts itself in at the tile's counter; the last to
+// arrive adds the partials in split order (the same order whichever block is last, so results do not depend on
+// timing), puts the counter back to zero and applies the epilogue.
 __global__ __launch_bounds__(256) void bf16_panel(const float *__restrict__ a, long long lda, int m, int k, int kp,
                                                   unsigned short *__restrict__ panel) {
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x; // 8 values per thread
@@ -411,60 +419,116 @@ __global__ __launch_bounds__(256) void bf16_panel(const float *__restrict__ a, l
 
 typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
 
-struct Bf16Params {
-  Q8Grid grid;
-  const unsigned short *panel; // m x kp BF16 activations
-  int m, k, kp;
+constexpr int kMmLoadsPerStep = 3;                   // per wave: two A and one B load
+constexpr size_t kMmLds = (size_t)kQ8SOff;           // A and B blocks of five stages, no scales
+constexpr int kSplitSlots = LLHIP_SPLIT_SLOTS;       // partial tiles the workspace holds
+constexpr int kSplitTileFloats = kQ8TileM * kQ8TileN; // one partial tile
+
+struct SplitK {
+  v4f *partial;    // [tile * splits + split][16][512] partial sums, in the accumulators' register order
+  unsigned *count; // [tile] blocks arrived; zero between launches
+  int splits;      // blocks per tile (1: no split)
+  int per;         // K steps per split
 };
 
-constexpr int kBfLoadsPerStep = 3; // per wave: two A and one B load
+struct MmParams {
+  Q8Grid grid;
+  const unsigned char *a; // BF16 panel or FP32 rows
+  long long arow;         // bytes per A row
+  int m, steps;           // rows; K steps of 64 bytes per row
+  SplitK sk;
+};
 
-__global__ __launch_bounds__(kQ8Threads, 2) void bf16_gemm_lds(Bf16Params p) {
+// The last of a tile's blocks to arrive gets true with acc holding the whole sum; the others get false.
+__device__ __forceinline__ bool split_combine(const SplitK &sk, int tile, int split, v4f (&acc)[4][4]) {
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  v4f *mine = sk.partial + (size_t)(tile * sk.splits + split) * 16 * kQ8Threads;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      mine[(i * 4 + j) * kQ8Threads + tid] = acc[i][j];
+  __threadfence(); // the partial tile is visible device-wide before the count says so
+  __syncthreads();
+  if (tid == 0)
+    last = atomicAdd(&sk.count[tile], 1u) == (unsigned)(sk.splits - 1);
+  __syncthreads();
+  if (!last)
+    return false;
+  __threadfence(); // every other split's partial tile is visible from here on
+  v4f own[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      own[i][j] = acc[i][j];
+  for (int s = 0; s < sk.splits; s++) {
+    const v4f *part = sk.partial + (size_t)(tile * sk.splits + s) * 16 * kQ8Threads;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const v4f v = s == split ? own[i][j] : part[(i * 4 + j) * kQ8Threads + tid];
+        acc[i][j] = s == 0 ? v : acc[i][j] + v;
+      }
+  }
+  if (tid == 0)
+    atomicExch(&sk.count[tile], 0u);
+  return true;
+}
+
+template <bool F32> __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_lds(MmParams p) {
   extern __shared__ __align__(16) unsigned char q8_smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const TilePos t = q8_tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
+  const int logical = xcd_logical(blockIdx.x, p.grid.total * p.sk.splits);
+  const int tile = logical / p.sk.splits, split = logical % p.sk.splits;
+  const TilePos t = q8_tile_of(p.grid, tile);
   const TileSeg seg = q8_seg_of(p.grid, t.s);
-  const int steps = p.kp / 32;
-  const long long rowb = (long long)p.kp * 2; // panel row bytes
+  const int s0 = split * p.sk.per, s1 = min(p.steps, s0 + p.sk.per);
 
   const int lrow4 = lane >> 2, chunk = lane & 3;
   const int ra = 32 * wave + lrow4;
-  const __amdgpu_buffer_rsrc_t rA =
-      q8_buffer(p.panel + (long long)t.m0 * p.kp, (long long)min(kQ8TileM, p.m - t.m0) * rowb);
-  const int offA0 = (int)(ra * rowb) + ((chunk ^ q8_swizzle(ra)) << 4);
-  const int offA1 = (int)((ra + 16) * rowb) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
-  // B: this wave's 16-row tile (one VNNI tile of one matrix); step s is bytes [s * 1024, s * 1024 + 1024) of it
+  const __amdgpu_buffer_rsrc_t rA = q8_buffer(p.a + (long long)t.m0 * p.arow, (long long)min(kQ8TileM, p.m - t.m0) * p.arow);
+  const int offA0 = (int)(ra * p.arow) + ((chunk ^ q8_swizzle(ra)) << 4);
+  const int offA1 = (int)((ra + 16) * p.arow) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
+  // B: this wave's 16 rows of one matrix. BF16: one VNNI tile, step s at bytes [s * 1024, s * 1024 + 1024); FP32: 16
+  // weight rows, read like the A rows.
   const int rb0 = 16 * wave;
   const int colB = t.swiglu ? t.n0 + (rb0 & 63) : t.n0 + rb0;
-  const unsigned short *wmat = (const unsigned short *)((t.swiglu && rb0 >= 64) ? seg.w3 : seg.w);
-  const long long tile_bytes = (long long)p.kp * 32; // 16 rows x kp values x 2 bytes
+  const unsigned char *wmat = (const unsigned char *)((t.swiglu && rb0 >= 64) ? seg.w3 : seg.w);
+  const long long brow = F32 ? seg.ldw * 4 : 0;
+  const long long tile_bytes = (long long)p.steps * 1024;
   const __amdgpu_buffer_rsrc_t rB =
-      q8_buffer((const unsigned char *)wmat + (long long)(colB / 16) * tile_bytes, colB < seg.n ? tile_bytes : 0);
-  const int offB = lane * 16;
-  const __amdgpu_buffer_rsrc_t none = q8_buffer(p.panel, 0);
+      F32 ? q8_buffer(wmat + (long long)colB * brow, (long long)min(16, seg.n - colB) * brow)
+          : q8_buffer(wmat + (long long)(colB / 16) * tile_bytes, colB < seg.n ? tile_bytes : 0);
+  const int offB = F32 ? (int)(lrow4 * brow) + ((chunk ^ q8_swizzle(lrow4)) << 4) : lane * 16;
+  const int bstep = F32 ? 64 : 1024; // B bytes per K step
+  const __amdgpu_buffer_rsrc_t none = q8_buffer(p.a, 0);
 
   auto issue = [&](int step, auto ST) {
     constexpr int st = decltype(ST)::value;
-    const bool live = step < steps;
-    const int k0 = step * 64;
+    const bool live = step < s1;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, (void *)(q8_smem + ((2 * wave) * kQ8Stages + st) * 1024),
-                                             16, offA0, k0, 0, 0);
+                                             16, offA0, step * 64, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
                                              (void *)(q8_smem + ((2 * wave + 1) * kQ8Stages + st) * 1024), 16, offA1,
-                                             k0, 0, 0);
+                                             step * 64, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB : none,
                                              (void *)(q8_smem + kQ8BOff + (wave * kQ8Stages + st) * 1024), 16, offB,
-                                             step * 1024, 0, 0);
+                                             step * bstep, 0, 0);
   };
 
   const int lrow = lane & 15, lq = lane >> 4;
-  const unsigned char *abase = q8_smem + (4 * wm) * kQ8Stages * 1024 + lrow * 64 + ((lq ^ q8_swizzle(lrow)) << 4);
+  const int lane_part = lrow * 64 + ((lq ^ q8_swizzle(lrow)) << 4);
+  const unsigned char *abase = q8_smem + (4 * wm) * kQ8Stages * 1024 + lane_part;
   const unsigned char *bbase[4];
 #pragma unroll
   for (int j = 0; j < 4; j++)
-    bbase[j] = q8_smem + kQ8BOff + (b_row(t.swiglu, wn, j) / 16) * kQ8Stages * 1024 + lq * 256 + lrow * 4;
+    bbase[j] = q8_smem + kQ8BOff + (b_row(t.swiglu, wn, j) / 16) * kQ8Stages * 1024 +
+               (F32 ? lane_part : lq * 256 + lrow * 4);
 
   v4f acc[4][4];
 #pragma unroll
@@ -475,35 +539,53 @@ __global__ __launch_bounds__(kQ8Threads, 2) void bf16_gemm_lds(Bf16Params p) {
 
   auto advance = [&](int step, auto ST) {
     constexpr int st = decltype(ST)::value, fill = (st + kQ8Stages - 1) % kQ8Stages;
-    wait_vmcnt<(kQ8Stages - 2) * kBfLoadsPerStep>(); // this wave's loads of `step` have landed
-    __builtin_amdgcn_s_barrier();                     // ... every wave's; the stage of step - 1 is free
+    wait_vmcnt<(kQ8Stages - 2) * kMmLoadsPerStep>(); // this wave's loads of `step` have landed
+    __builtin_amdgcn_s_barrier();                    // ... every wave's; the stage of step - 1 is free
     issue(step + kQ8Stages - 1, std::integral_constant<int, fill>{});
-    v8bf_t a[4], b[4];
+    if constexpr (F32) {
+      v4f a[4], b[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      a[i] = *reinterpret_cast<const v8bf_t *>(abase + (i * kQ8Stages + st) * 1024);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const unsigned char *bp = bbase[j] + st * 1024;
-      typedef unsigned v4u __attribute__((ext_vector_type(4)));
-      const v4u pairs = v4u{*reinterpret_cast<const unsigned *>(bp), *reinterpret_cast<const unsigned *>(bp + 64),
-                            *reinterpret_cast<const unsigned *>(bp + 128), *reinterpret_cast<const unsigned *>(bp + 192)};
-      b[j] = __builtin_bit_cast(v8bf_t, pairs);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 4; i++)
+        a[i] = *reinterpret_cast<const v4f *>(abase + (i * kQ8Stages + st) * 1024);
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        b[j] = *reinterpret_cast<const v4f *>(bbase[j] + st * 1024);
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+    } else {
+      v8bf_t a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        a[i] = *reinterpret_cast<const v8bf_t *>(abase + (i * kQ8Stages + st) * 1024);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const unsigned char *bp = bbase[j] + st * 1024;
+        typedef unsigned v4u __attribute__((ext_vector_type(4)));
+        const v4u pairs = v4u{*reinterpret_cast<const unsigned *>(bp), *reinterpret_cast<const unsigned *>(bp + 64),
+                              *reinterpret_cast<const unsigned *>(bp + 128),
+                              *reinterpret_cast<const unsigned *>(bp + 192)};
+        b[j] = __builtin_bit_cast(v8bf_t, pairs);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
   };
 
-  issue(0, std::integral_constant<int, 0>{});
-  issue(1, std::integral_constant<int, 1>{});
-  issue(2, std::integral_constant<int, 2>{});
-  issue(3, std::integral_constant<int, 3>{});
+  issue(s0, std::integral_constant<int, 0>{});
+  issue(s0 + 1, std::integral_constant<int, 1>{});
+  issue(s0 + 2, std::integral_constant<int, 2>{});
+  issue(s0 + 3, std::integral_constant<int, 3>{});
   // Whole rounds of five steps, with no exit between them: steps past the end load zeros (an empty buffer) and add
   // nothing, and the accumulators stay in place across the unrolled body instead of being copied at every exit.
-  for (int step = 0; step < steps; step += kQ8Stages) {
+  for (int step = s0; step < s1; step += kQ8Stages) {
     advance(step, std::integral_constant<int, 0>{});
     advance(step + 1, std::integral_constant<int, 1>{});
     advance(step + 2, std::integral_constant<int, 2>{});
@@ -511,6 +593,8 @@ __global__ __launch_bounds__(kQ8Threads, 2) void bf16_gemm_lds(Bf16Params p) {
     advance(step + 4, std::integral_constant<int, 4>{});
   }
   __builtin_amdgcn_s_waitcnt(0);
+  if (p.sk.splits > 1 && !split_combine(p.sk, tile, split, acc))
+    return;
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
@@ -557,7 +641,6 @@ __global__ __launch_bounds__(kBlock) void q8_gemm_generic(TileGrid g, const int8
 
 constexpr int kF32Slice = 16; // K values staged per step
 constexpr int kF32Pitch = 17; // floats per LDS row of a K slice, padded against bank conflicts
-constexpr int kBf16Pitch = 40; // bf16 values per LDS row of a 32-wide K slice (80 bytes)
 
 struct F32Params {
   TileGrid grid;
@@ -634,89 +717,6 @@ __global__ __launch_bounds__(kBlock) void f32_gemm_mfma(F32Params p) {
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
-
-// BF16: activations rounded to BF16 while staged, weights read from the pack_bf16_vnni layout (16-row tiles, K pairs:
-// element ((tile * kp / 2 + pair) * 16 + row) * 2 + e), v_mfma_f32_16x16x32_bf16 per 16 x 16 tile and 32 values of K.
-__global__ __launch_bounds__(kBlock) void bf16_gemm_mfma(F32Params p) {
-  __shared__ __align__(16) unsigned short sa[2][kTile * kBf16Pitch];
-  __shared__ __align__(16) unsigned short sb[2][kTile * kBf16Pitch];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-  const TilePos t = tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
-  const TileSeg seg = seg_of(p.grid, t.s);
-  const unsigned short *w1 = (const unsigned short *)seg.w, *w3 = (const unsigned short *)seg.w3;
-  const long long kp = (p.k + 31) / 32 * 32;
-  const int steps = (int)(kp / 32);
-  // Thread t stages row t / 2 of both tiles, K values (t % 2) * 16 .. + 15 of the slice: 16 activations rounded to
-  // BF16, and the weight row's 8 K pairs gathered from the packed layout.
-  float ra[16];
-  unsigned rbp[8]; // 8 pairs of bf16 for one weight row
-  auto load = [&](int step) {
-    const int k0 = step * 32;
-    const int r = tid >> 1, half = (tid & 1) * 16;
-    const int row = t.m0 + r;
-#pragma unroll
-    for (int e = 0; e < 16; e++) {
-      const int kk = k0 + half + e;
-      ra[e] = (row < p.m && kk < p.k) ? p.a[(long long)row * p.lda + kk] : 0.0f;
-    }
-    const int wc = b_col(t, r);
-    const unsigned short *src = (t.swiglu && r >= 64) ? w3 : w1;
-    if (wc < seg.n) {
-      const long long tile = wc / 16, c = wc % 16;
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const long long pair = (k0 + half) / 2 + q;
-        rbp[q] = *reinterpret_cast<const unsigned *>(src + ((tile * (kp / 2) + pair) * 16 + c) * 2);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 8; q++)
-        rbp[q] = 0u;
-    }
-  };
-  auto store = [&](int buf) {
-    const int r = tid >> 1, half = (tid & 1) * 16;
-    unsigned short *arow = &sa[buf][r * kBf16Pitch + half];
-#pragma unroll
-    for (int e = 0; e < 16; e += 2)
-      *reinterpret_cast<unsigned *>(arow + e) = (unsigned)to_bf16(ra[e]) | ((unsigned)to_bf16(ra[e + 1]) << 16);
-    unsigned *brow = reinterpret_cast<unsigned *>(&sb[buf][r * kBf16Pitch + half]);
-#pragma unroll
-    for (int q = 0; q < 8; q++)
-      brow[q] = rbp[q];
-  };
-  v4f acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  load(0);
-  store(0);
-  __syncthreads();
-  const int lrow = lane & 15, lk = (lane >> 4) * 8;
-  for (int step = 0; step < steps; step++) {
-    const int buf = step & 1;
-    if (step + 1 < steps)
-      load(step + 1);
-    v8bf a[4], b[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      a[i] = *reinterpret_cast<const v8bf *>(&sa[buf][(wm * 64 + 16 * i + lrow) * kBf16Pitch + lk]);
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      b[j] = *reinterpret_cast<const v8bf *>(&sb[buf][(b_row(t.swiglu, wn, j) + lrow) * kBf16Pitch + lk]);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    if (step + 1 < steps)
-      store(buf ^ 1);
-    __syncthreads();
-  }
-  store_tile(seg, t, acc, wm, wn, lane, p.m);
-}
 
 bool launch_ok(const char *what) {
   hipError_t e = hipGetLastError();
@@ -839,43 +839,95 @@ bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs,
   return ok;
 }
 
+namespace {
+
+std::atomic<int> forced_splits{0};
+
+// Blocks per tile: one when the tiles fill the CUs (one 256 x 128 block per CU fits in LDS), else enough to reach
+// about one block per CU, keeping at least eight K steps per block and within the workspace's partial tiles.
+int choose_splits(int tiles, int steps, int *per) {
+  int s = forced_splits.load();
+  if (s <= 0) {
+    const int cus = device().cu_count > 0 ? device().cu_count : 256;
+    s = tiles < cus ? cus / tiles : 1;
+    s = min(s, steps / 8);
+  }
+  s = max(1, min(s, min(kSplitSlots / max(tiles, 1), steps)));
+  *per = (steps + s - 1) / s;
+  return (steps + *per - 1) / *per; // no empty split
+}
+
+template <bool F32> bool mm_launch(MmParams p, hipStream_t stream) {
+  static const hipError_t status =
+      hipFuncSetAttribute((const void *)mm_gemm_lds<F32>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMmLds);
+  if (!check_hip(status, "allowing the FP32 / BF16 GEMM its LDS"))
+    return false;
+  p.sk.splits = p.grid.total > kSplitSlots ? 1 : choose_splits(p.grid.total, p.steps, &p.sk.per);
+  if (p.sk.splits == 1)
+    p.sk.per = p.steps;
+  p.sk.partial = (v4f *)device().split_partial;
+  p.sk.count = device().split_count;
+  hipLaunchKernelGGL(mm_gemm_lds<F32>, dim3((unsigned)(p.grid.total * p.sk.splits)), dim3(kQ8Threads), kMmLds, stream,
+                     p);
+  return launch_ok(F32 ? "mm_gemm_lds<fp32>" : "mm_gemm_lds<bf16>");
+}
+
+bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+// Shapes the pipelined FP32 kernel takes: K a multiple of 16 and 16-byte aligned rows whose 32-bit buffer offsets fit.
+bool f32_fast_path(const GemmF32Job &job) {
+  if (job.k % 16 || job.lda % 4 || !aligned16(job.a) || (long long)kQ8TileM * job.lda * 4 >= (1LL << 31))
+    return false;
+  for (int s = 0; s < job.nseg; s++) {
+    const GemmSegmentDev &g = job.seg[s];
+    if (g.ldw % 4 || !aligned16(g.w) || (g.w3 && !aligned16(g.w3)) || 16LL * (long long)g.ldw * 4 >= (1LL << 31))
+      return false;
+  }
+  return true;
+}
+
+} // namespace
+
+void set_gemm_splits(int splits) { forced_splits.store(splits > 0 ? splits : 0); }
+
 bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream) {
   if (job.m <= 0 || job.k <= 0)
     return true;
-  F32Params p{};
-  p.grid = make_grid(job.seg, job.nseg, job.m);
-  p.a = job.a;
-  p.lda = job.lda;
+  MmParams p{};
+  p.grid = make_q8_grid(job.seg, job.nseg, job.m);
   p.m = job.m;
-  p.k = job.k;
   if (p.grid.total <= 0)
     return true;
-  if (job.bf16 && job.panel) {
+  if (job.bf16) {
     // round A into the panel, then the pipelined kernel
     const int kp = (job.k + 31) / 32 * 32;
+    if (!job.panel)
+      return raise("k_gemm_bf16 needs a device panel");
+    if ((long long)kQ8TileM * kp * 2 >= (1LL << 31))
+      return raise("k_gemm_bf16: K = %d is beyond the kernel's 32-bit offsets", job.k);
     const long long threads = (long long)job.m * (kp / 8);
     hipLaunchKernelGGL(bf16_panel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, job.a,
                        (long long)job.lda, job.m, job.k, kp, job.panel);
     if (!launch_ok("bf16_panel"))
       return false;
-    Bf16Params b{};
-    b.grid = make_q8_grid(job.seg, job.nseg, job.m);
-    b.panel = job.panel;
-    b.m = job.m;
-    b.k = job.k;
-    b.kp = kp;
-    static const hipError_t status = hipFuncSetAttribute((const void *)bf16_gemm_lds,
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ8Lds);
-    if (!check_hip(status, "allowing the BF16 GEMM its LDS"))
-      return false;
-    hipLaunchKernelGGL(bf16_gemm_lds, dim3(b.grid.total), dim3(kQ8Threads), kQ8Lds, stream, b);
-    return launch_ok("bf16_gemm_lds");
+    p.a = (const unsigned char *)job.panel;
+    p.arow = (long long)kp * 2;
+    p.steps = kp / 32;
+    return mm_launch<false>(p, stream);
   }
-  if (job.bf16) {
-    hipLaunchKernelGGL(bf16_gemm_mfma, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
-    return launch_ok("bf16_gemm_mfma");
+  if (f32_fast_path(job)) {
+    p.a = (const unsigned char *)job.a;
+    p.arow = (long long)job.lda * 4;
+    p.steps = job.k / 16;
+    return mm_launch<true>(p, stream);
   }
-  hipLaunchKernelGGL(f32_gemm_mfma, dim3(p.grid.total), dim3(kBlock), 0, stream, p);
+  F32Params f{};
+  f.grid = make_grid(job.seg, job.nseg, job.m);
+  f.a = job.a;
+  f.lda = job.lda;
+  f.m = job.m;
+  f.k = job.k;
+  hipLaunchKernelGGL(f32_gemm_mfma, dim3(f.grid.total), dim3(kBlock), 0, stream, f);
   return launch_ok("f32_gemm_mfma");
 }
 

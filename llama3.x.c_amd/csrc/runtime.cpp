@@ -89,6 +89,14 @@ bool ensure_device() {
   int zero[16] = {0};
   if (!LLHIP_CHECK(hipMemcpy(flags, zero, sizeof(zero), hipMemcpyHostToDevice)))
     return false;
+  void *partial;
+  unsigned *arrivals;
+  if (!LLHIP_CHECK(hipMalloc(&partial, (size_t)LLHIP_SPLIT_SLOTS * 256 * 128 * sizeof(float))) ||
+      !LLHIP_CHECK(hipMalloc((void **)&arrivals, LLHIP_SPLIT_SLOTS * sizeof(unsigned))) ||
+      !LLHIP_CHECK(hipMemset(arrivals, 0, LLHIP_SPLIT_SLOTS * sizeof(unsigned))))
+    return false;
+  the_device.split_partial = partial;
+  the_device.split_count = arrivals;
   the_device.ordinal = ordinal;
   the_device.stream = stream;
   the_device.error_flags = flags;

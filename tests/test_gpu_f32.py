@@ -234,3 +234,85 @@ def test_bf16_gemm_reference_golden():
                 extra = np.abs(base[:, :n]) if kname == "add" else 0
                 hu.assert_within_budget(c[:, :n], want[:, :n], mag + extra, rel=4e-6, what=f"{key} {kname}")
         L.aligned_buffer_free(panel)
+
+
+# ---- pipelined FP32 / BF16 kernels: aligned shapes, split K --------------------------------------------------------
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 200, 1024), (513, 136, 3072), (40, 130, 16 * 37), (256, 256, 8192)])
+@pytest.mark.parametrize("mode", ["f32", "bf16"])
+def test_pipelined_gemm_split_k(m, n, k, mode):
+    """Rows 16-byte aligned and K a multiple of 16 take the pipelined kernel. Every split count (0 = the automatic
+    choice) meets the budget for every kind and for three segments sharing A; a repeated call with the same split count
+    gives the same bits (the arrival counters are back at zero and partial sums are added in split order)."""
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 81 * m + n + k)
+    lda, ldc = k + 4, n + 7
+    a = rng.uniform(m * lda, 2.0).reshape(m, lda)
+    w, w3 = rng.uniform(n * k).reshape(n, k), rng.uniform(n * k).reshape(n, k)
+    base = rng.uniform(m * ldc, 4.0).reshape(m, ldc)
+    da = hu.dev(a)
+    panel = lh.AlignedBuffer()
+    if mode == "bf16":
+        pw, pw3 = np.zeros(L.bf16_vnni_elements(n, k), np.uint16), np.zeros(L.bf16_vnni_elements(n, k), np.uint16)
+        L.pack_bf16_vnni(lh.ptr(pw), lh.ptr(w), n, k, k)
+        L.pack_bf16_vnni(lh.ptr(pw3), lh.ptr(w3), n, k, k)
+        dw, dw3 = hu.dev(pw), hu.dev(pw3)
+        ab, wb, w3b = bf16_round(a[:, :k].copy()), bf16_round(w), bf16_round(w3)
+        r, mag = ref_f32(ab, wb)
+        r3, mag3 = ref_f32(ab, w3b)
+        rel = 2e-6
+        L.aligned_buffer_alloc(panel, L.k_gemm_bf16_panel_bytes(m, k), 1)
+    else:
+        dw, dw3 = hu.dev(w), hu.dev(w3)
+        r, mag = ref_f32(a[:, :k], w)
+        r3, mag3 = ref_f32(a[:, :k], w3)
+        rel = 2e-5
+
+    def gemm(c, kind, splits):
+        L.llhip_set_gemm_splits(splits)
+        if mode == "bf16":
+            seg = lh.GemmBf16Segment(lh.ptr(c), ldc, lh.ptr(dw), lh.ptr(dw3), n, kind)
+            L.k_gemm_bf16(lh.ptr(da), lda, m, k, seg, 1, panel)
+        else:
+            seg = lh.GemmSegment(lh.ptr(c), ldc, lh.ptr(dw), lh.ptr(dw3), k, n, kind)
+            L.k_gemm_f32(lh.ptr(da), lda, m, k, seg, 1)
+
+    try:
+        for splits in (0, 1, 2, 3, 7):
+            for kind in (lh.GEMM_STORE, lh.GEMM_ADD, lh.GEMM_SWIGLU):
+                c = hu.dev(base)
+                gemm(c, kind, splits)
+                got = hu.host(c)
+                assert lh.last_error() == "", lh.last_error()
+                assert np.array_equal(hu.bits(got[:, n:]), hu.bits(base[:, n:])), "row padding was written"
+                check_kind(got[:, :n], base[:, :n], r, mag, r3, mag3, kind, rel=rel,
+                           what=f"{mode} {m}x{n}x{k} kind {kind} splits {splits}")
+                if kind == lh.GEMM_STORE:
+                    again = hu.dev(base)
+                    gemm(again, kind, splits)
+                    assert np.array_equal(hu.bits(hu.host(again)), hu.bits(got)), f"splits {splits} not repeatable"
+        # three segments sharing A (QKV), automatic splits
+        L.llhip_set_gemm_splits(0)
+        widths = (n, max(16, n // 4), max(16, n // 4))
+        outs = [hu.dev(np.zeros((m, nn), np.float32)) for nn in widths]
+        wts = [w[:nn] for nn in widths]
+        if mode == "bf16":
+            packed = []
+            for nn, wt in zip(widths, wts):
+                pk = np.zeros(L.bf16_vnni_elements(nn, k), np.uint16)
+                L.pack_bf16_vnni(lh.ptr(pk), lh.ptr(np.ascontiguousarray(wt)), nn, k, k)
+                packed.append(hu.dev(pk))
+            segs = (lh.GemmBf16Segment * 3)(*[lh.GemmBf16Segment(lh.ptr(o), nn, lh.ptr(p), None, nn, lh.GEMM_STORE)
+                                              for o, p, nn in zip(outs, packed, widths)])
+            L.k_gemm_bf16(lh.ptr(da), lda, m, k, segs, 3, panel)
+        else:
+            dws = [hu.dev(np.ascontiguousarray(wt)) for wt in wts]
+            segs = (lh.GemmSegment * 3)(*[lh.GemmSegment(lh.ptr(o), nn, lh.ptr(d), None, k, nn, lh.GEMM_STORE)
+                                          for o, d, nn in zip(outs, dws, widths)])
+            L.k_gemm_f32(lh.ptr(da), lda, m, k, segs, 3)
+        for o, nn in zip(outs, widths):
+            hu.assert_within_budget(hu.host(o), r[:, :nn], mag[:, :nn], rel=rel, what=f"{mode} segment of {nn}")
+    finally:
+        L.llhip_set_gemm_splits(0)
+        L.aligned_buffer_free(panel)
