@@ -389,8 +389,8 @@ __device__ __forceinline__ unsigned short to_bf16(float x) {
 // five stages deep, in 1 KB blocks of 16 rows interleaved by stage. A block row is XOR-swizzled in 16-byte chunks like
 // the int8 tiles. MFMA operands take 16 contiguous bytes of a row per lane group q = lane / 16:
 //   BF16: v_mfma_f32_16x16x32_bf16, K values 8 q .. 8 q + 7. B arrives in the pack_bf16_vnni layout, whose 16-row
-//         tile and 32-value K step is one contiguous 1 KB block (16 K pairs of 16 rows x 2 values), copied verbatim;
-//         a lane's four K pairs are four 4-byte reads of it.
+//         tile and 32-value K step is one contiguous 1 KB block (16 K pairs of 16 rows x 2 values), copied with its
+//         16-byte chunks reordered so that a lane's four K pairs are four conflict-free 4-byte reads.
 //   FP32: four v_mfma_f32_16x16x4_f32 per tile and step; lane group q holds K values 4 q .. 4 q + 3 of A and W and
 //         feeds value s to the s-th instruction. W rows are read like A rows (row pitch ldw).
 // The FP32 sums stay in the MFMA accumulators: no per-step vector work.
@@ -439,24 +439,33 @@ struct MmParams {
   SplitK sk;
 };
 
+// Cache policy of the partial tiles' stores and loads: device-coherent (sc1), so a store is written through past the
+// XCD's L2 before its completion is counted, and a load reads from past it. No cache-wide write-back or invalidate is
+// needed, which would also evict the operands of every other block on the XCD.
+constexpr int kDeviceCoherent = 16;
+
 // The last of a tile's blocks to arrive gets true with acc holding the whole sum; the others get false.
 __device__ __forceinline__ bool split_combine(const SplitK &sk, int tile, int split, v4f (&acc)[4][4]) {
   __shared__ int last;
   const int tid = threadIdx.x;
-  v4f *mine = sk.partial + (size_t)(tile * sk.splits + split) * 16 * kQ8Threads;
+  constexpr int kSlotBytes = 16 * kQ8Threads * 16; // one partial tile
+  const __amdgpu_buffer_rsrc_t r =
+      q8_buffer((const unsigned char *)sk.partial + (size_t)tile * sk.splits * kSlotBytes, (long long)sk.splits * kSlotBytes);
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++)
-      mine[(i * 4 + j) * kQ8Threads + tid] = acc[i][j];
-  __threadfence(); // the partial tile is visible device-wide before the count says so
-  __syncthreads();
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, acc[i][j]), r,
+                                             split * kSlotBytes + ((i * 4 + j) * kQ8Threads + tid) * 16, 0,
+                                             kDeviceCoherent);
+  __builtin_amdgcn_s_waitcnt(0); // this thread's partial sums have reached the device-coherent level
+  __syncthreads();               // ... and every thread's
   if (tid == 0)
-    last = atomicAdd(&sk.count[tile], 1u) == (unsigned)(sk.splits - 1);
+    last = __hip_atomic_fetch_add(&sk.count[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (unsigned)(sk.splits - 1);
   __syncthreads();
   if (!last)
     return false;
-  __threadfence(); // every other split's partial tile is visible from here on
   v4f own[4][4];
 #pragma unroll
   for (int i = 0; i < 4; i++)
@@ -464,17 +473,19 @@ __device__ __forceinline__ bool split_combine(const SplitK &sk, int tile, int sp
     for (int j = 0; j < 4; j++)
       own[i][j] = acc[i][j];
   for (int s = 0; s < sk.splits; s++) {
-    const v4f *part = sk.partial + (size_t)(tile * sk.splits + s) * 16 * kQ8Threads;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const v4f v = s == split ? own[i][j] : part[(i * 4 + j) * kQ8Threads + tid];
+        const v4f v = s == split ? own[i][j]
+                                 : __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               r, s * kSlotBytes + ((i * 4 + j) * kQ8Threads + tid) * 16,
+                                                               0, kDeviceCoherent));
         acc[i][j] = s == 0 ? v : acc[i][j] + v;
       }
   }
   if (tid == 0)
-    atomicExch(&sk.count[tile], 0u);
+    __hip_atomic_store(&sk.count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return true;
 }
 
@@ -504,7 +515,12 @@ template <bool F32> __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_lds
   const __amdgpu_buffer_rsrc_t rB =
       F32 ? q8_buffer(wmat + (long long)colB * brow, (long long)min(16, seg.n - colB) * brow)
           : q8_buffer(wmat + (long long)(colB / 16) * tile_bytes, colB < seg.n ? tile_bytes : 0);
-  const int offB = F32 ? (int)(lrow4 * brow) + ((chunk ^ q8_swizzle(lrow4)) << 4) : lane * 16;
+  // BF16: the 1 KB VNNI block holds 16-byte chunks of one K pair for four rows (chunk 4 P + rg: pair P, rows
+  // 4 rg .. 4 rg + 3). Lane l copies chunk (pair 4 q + p, rows 4 rg ..) with p = l / 16, q = (l / 4) % 4, rg = l % 4
+  // to LDS position l = 16 p + 4 q + rg, so the MFMA lane (row r, group q) finds its pair 4 q + p at byte
+  // 256 p + 64 q + 4 r: one 4-byte read per p, on 64 distinct banks across the wave.
+  const int offB = F32 ? (int)(lrow4 * brow) + ((chunk ^ q8_swizzle(lrow4)) << 4)
+                       : ((4 * ((lane >> 2) & 3) + (lane >> 4)) << 6) + ((lane & 3) << 4);
   const int bstep = F32 ? 64 : 1024; // B bytes per K step
   const __amdgpu_buffer_rsrc_t none = q8_buffer(p.a, 0);
 
@@ -528,7 +544,7 @@ template <bool F32> __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_lds
 #pragma unroll
   for (int j = 0; j < 4; j++)
     bbase[j] = q8_smem + kQ8BOff + (b_row(t.swiglu, wn, j) / 16) * kQ8Stages * 1024 +
-               (F32 ? lane_part : lq * 256 + lrow * 4);
+               (F32 ? lane_part : lq * 64 + lrow * 4);
 
   v4f acc[4][4];
 #pragma unroll
@@ -537,52 +553,66 @@ template <bool F32> __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_lds
     for (int j = 0; j < 4; j++)
       acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto advance = [&](int step, auto ST) {
-    constexpr int st = decltype(ST)::value, fill = (st + kQ8Stages - 1) % kQ8Stages;
-    wait_vmcnt<(kQ8Stages - 2) * kMmLoadsPerStep>(); // this wave's loads of `step` have landed
-    __builtin_amdgcn_s_barrier();                    // ... every wave's; the stage of step - 1 is free
-    issue(step + kQ8Stages - 1, std::integral_constant<int, fill>{});
-    if constexpr (F32) {
-      v4f a[4], b[4];
+  // MFMA operands of one step, read from LDS a step ahead of their use
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  struct Operands {
+    v4u a[4], b[4];
+  };
+  auto operands = [&](auto ST, Operands &o) {
+    constexpr int st = decltype(ST)::value;
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        a[i] = *reinterpret_cast<const v4f *>(abase + (i * kQ8Stages + st) * 1024);
+    for (int i = 0; i < 4; i++)
+      o.a[i] = *reinterpret_cast<const v4u *>(abase + (i * kQ8Stages + st) * 1024);
 #pragma unroll
-      for (int j = 0; j < 4; j++)
-        b[j] = *reinterpret_cast<const v4f *>(bbase[j] + st * 1024);
+    for (int j = 0; j < 4; j++) {
+      const unsigned char *bp = bbase[j] + st * 1024;
+      if constexpr (F32)
+        o.b[j] = *reinterpret_cast<const v4u *>(bp);
+      else
+        o.b[j] = v4u{*reinterpret_cast<const unsigned *>(bp), *reinterpret_cast<const unsigned *>(bp + 256),
+                     *reinterpret_cast<const unsigned *>(bp + 512), *reinterpret_cast<const unsigned *>(bp + 768)};
+    }
+  };
+  auto mfmas = [&](const Operands &o) {
 #pragma unroll
-      for (int s = 0; s < 4; s++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int j = 0; j < 4; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
-    } else {
-      v8bf_t a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        a[i] = *reinterpret_cast<const v8bf_t *>(abase + (i * kQ8Stages + st) * 1024);
+    for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const unsigned char *bp = bbase[j] + st * 1024;
-        typedef unsigned v4u __attribute__((ext_vector_type(4)));
-        const v4u pairs = v4u{*reinterpret_cast<const unsigned *>(bp), *reinterpret_cast<const unsigned *>(bp + 64),
-                              *reinterpret_cast<const unsigned *>(bp + 128),
-                              *reinterpret_cast<const unsigned *>(bp + 192)};
-        b[j] = __builtin_bit_cast(v8bf_t, pairs);
+        if constexpr (F32) {
+          const v4f a = __builtin_bit_cast(v4f, o.a[i]), b = __builtin_bit_cast(v4f, o.b[j]);
+#pragma unroll
+          for (int s = 0; s < 4; s++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], acc[i][j], 0, 0, 0);
+        } else {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf_t, o.a[i]),
+                                                              __builtin_bit_cast(v8bf_t, o.b[j]), acc[i][j], 0, 0, 0);
+        }
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
+  };
+
+  // One step in stage ST: step + 1's loads have landed once only the two later steps' may be outstanding; the barrier
+  // makes that true of every wave and means every wave is done with the stage step - 1 used, which step + 4 now
+  // fills. The operands of step + 1 are read while this step's MFMAs (on operands read one step earlier) run.
+  Operands cur, next;
+  auto advance = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value, nst = (st + 1) % kQ8Stages, fill = (st + kQ8Stages - 1) % kQ8Stages;
+    wait_vmcnt<(kQ8Stages - 3) * kMmLoadsPerStep>();
+    __builtin_amdgcn_s_barrier();
+    issue(step + kQ8Stages - 1, std::integral_constant<int, fill>{});
+    operands(std::integral_constant<int, nst>{}, next);
+    __builtin_amdgcn_sched_barrier(0); // keep the reads ahead of the MFMAs that do not need them
+    mfmas(cur);
+    __builtin_amdgcn_sched_barrier(0);
+    cur = next;
   };
 
   issue(s0, std::integral_constant<int, 0>{});
   issue(s0 + 1, std::integral_constant<int, 1>{});
   issue(s0 + 2, std::integral_constant<int, 2>{});
   issue(s0 + 3, std::integral_constant<int, 3>{});
+  wait_vmcnt<(kQ8Stages - 2) * kMmLoadsPerStep>(); // step s0 has landed for this wave
+  __builtin_amdgcn_s_barrier();                    // ... and for every wave
+  operands(std::integral_constant<int, 0>{}, cur);
   // Whole rounds of five steps, with no exit between them: steps past the end load zeros (an empty buffer) and add
   // nothing, and the accumulators stay in place across the unrolled body instead of being copied at every exit.
   for (int step = s0; step < s1; step += kQ8Stages) {
