@@ -139,6 +139,26 @@ constexpr int kQ8SOff = kQ8BOff + kQ8BBlocks * kQ8Stages * 1024;     // then the
 constexpr int kQ8SStride = (kQ8TileM + kQ8TileN + 64) * 4;            // xs, ws, spare (zero-length loads land there)
 constexpr size_t kQ8Lds = (size_t)kQ8SOff + (size_t)kQ8Stages * kQ8SStride;
 
+// The int8 kernel's tile shapes: WM rows of 64 x 64 wave tiles over 128 columns. WM = 4 is the layout above (one
+// 129 KB block per CU); WM = 2 is a 128 x 128 tile of four waves with four stages (69 KB), two blocks per CU, so a
+// block waiting at its barrier or for its loads leaves the SIMDs to the other block's waves.
+template <int WM_, int STAGES_> struct Q8Cfg {
+  static constexpr int WM = WM_, Waves = 2 * WM, Threads = 64 * Waves;
+  static constexpr int TileM = 64 * WM, TileN = 128, Stages = STAGES_;
+  static constexpr int ABlocks = TileM / 16, BBlocks = TileN / 16;
+  static constexpr int BPerWave = BBlocks / Waves;         // B blocks each wave loads per step
+  static constexpr int LoadsPerStep = 2 + BPerWave + 1;    // two A, the B blocks, one scale load
+  static constexpr int BOff = ABlocks * Stages * 1024;
+  static constexpr int SOff = BOff + BBlocks * Stages * 1024;
+  static constexpr int SStride = (TileM + TileN + 64) * 4; // xs, ws, spare (zero-length loads land there)
+  static constexpr size_t Lds = (size_t)SOff + (size_t)Stages * SStride;
+  static_assert(BBlocks % Waves == 0 && (TileM + TileN) / 64 <= Waves, "every load has a wave");
+};
+using Q8Wide = Q8Cfg<4, 5>;
+using Q8Pair = Q8Cfg<2, 4>;
+static_assert(Q8Wide::Lds == kQ8Lds, "the 256 x 128 layout");
+static_assert(2 * Q8Pair::Lds <= 160 * 1024, "two 128 x 128 blocks fit one CU's LDS");
+
 __device__ __forceinline__ int q8_swizzle(int row) { return (row >> 1) & 3; }
 
 struct Q8Grid {
@@ -156,7 +176,7 @@ struct Q8Params {
   int32_t *probe; // optional (one segment, no SWIGLU): probe[(g * m + r) * n + c]
 };
 
-__device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical) {
+__device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical, int tile_m = kQ8TileM) {
   int s = 0;
   while (s + 1 < g.nseg && logical >= g.seg[s + 1].first_tile)
     s++;
@@ -164,7 +184,7 @@ __device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical) {
   TilePos t;
   t.s = s;
   t.swiglu = g.seg[s].epi == EPI_SWIGLU;
-  t.m0 = (local % g.mtiles) * kQ8TileM;
+  t.m0 = (local % g.mtiles) * tile_m;
   t.n0 = (local / g.mtiles) * (t.swiglu ? kQ8TileN / 2 : kQ8TileN);
   return t;
 }
@@ -189,13 +209,32 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
-template <bool PROBE, bool GS64>
-__global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
+// The K loop unrolled by the stages (every stage index a constant), leaving after the last step.
+template <int I, int N, class F> __device__ __forceinline__ bool unrolled_steps(F &f, int step, int steps) {
+  if constexpr (I < N) {
+    f(step + I, std::integral_constant<int, I>{});
+    if (I + 1 < N && step + I + 1 >= steps)
+      return false;
+    return unrolled_steps<I + 1, N>(f, step, steps);
+  }
+  return true;
+}
+
+// The loads of steps 0 .. N - 1 into stages 0 .. N - 1.
+template <int I, int N, class F> __device__ __forceinline__ void issue_first(F &f) {
+  if constexpr (I < N) {
+    f(I, std::integral_constant<int, I>{});
+    issue_first<I + 1, N>(f);
+  }
+}
+
+template <class C, bool PROBE, bool GS64>
+__global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
   extern __shared__ __align__(16) unsigned char q8_smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const TilePos t = q8_tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total));
+  const TilePos t = q8_tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total), C::TileM);
   const TileSeg seg = q8_seg_of(p.grid, t.s);
   const int groups = p.k / p.gs, spg = GS64 ? 1 : p.gs / 64, steps = p.k / 64;
   const long long k = p.k;
@@ -204,30 +243,38 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
   // and per-lane offsets that place lane l's 16 bytes at l * 16 of a 1 KB block (row l / 4, swizzled chunk l % 4).
   const int lrow4 = lane >> 2, chunk = lane & 3;
   const int ra = 32 * wave + lrow4; // A rows ra (block 2 wave) and ra + 16 (block 2 wave + 1)
-  const __amdgpu_buffer_rsrc_t rA = q8_buffer(p.xq + (long long)t.m0 * k, (long long)min(kQ8TileM, p.m - t.m0) * k);
+  const __amdgpu_buffer_rsrc_t rA = q8_buffer(p.xq + (long long)t.m0 * k, (long long)min(C::TileM, p.m - t.m0) * k);
   const int offA0 = (int)(ra * k) + ((chunk ^ q8_swizzle(ra)) << 4);
   const int offA1 = (int)((ra + 16) * k) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
-  const int rb0 = 16 * wave; // B tile rows rb0 .. rb0 + 15 (block `wave`), all of one matrix
-  const int colB = t.swiglu ? t.n0 + (rb0 & 63) : t.n0 + rb0;
-  const int8_t *wmat = (const int8_t *)((t.swiglu && rb0 >= 64) ? seg.w3 : seg.w);
-  const __amdgpu_buffer_rsrc_t rB = q8_buffer(wmat + (long long)colB * k, (long long)min(16, seg.n - colB) * k);
-  const int offB = (int)(lrow4 * k) + ((chunk ^ q8_swizzle(rb0 + lrow4)) << 4);
-  // scale loads: waves 0-3 the 256 xs rows (64 each), waves 4-5 the 128 ws rows, waves 6-7 nothing
+  // B tile rows 16 bb .. 16 bb + 15 (block bb = BPerWave wave + b, b < 2), all of one matrix. Two named resources, not
+  // an array: the host compilation silently drops a kernel that holds an array of buffer resources.
+  static_assert(C::BPerWave == 1 || C::BPerWave == 2, "one or two B blocks per wave");
+  auto b_resource = [&](int b, int &off) {
+    const int rb0 = 16 * (C::BPerWave * wave + b);
+    const int colB = t.swiglu ? t.n0 + (rb0 & 63) : t.n0 + rb0;
+    const int8_t *wmat = (const int8_t *)((t.swiglu && rb0 >= 64) ? seg.w3 : seg.w);
+    off = (int)(lrow4 * k) + ((chunk ^ q8_swizzle(rb0 + lrow4)) << 4);
+    return q8_buffer(wmat + (long long)colB * k, (long long)min(16, seg.n - colB) * k);
+  };
+  int offB0, offB1 = 0;
+  const __amdgpu_buffer_rsrc_t rB0 = b_resource(0, offB0);
+  const __amdgpu_buffer_rsrc_t rB1 = C::BPerWave == 2 ? b_resource(1, offB1) : rB0;
+  // scale loads: waves 0 .. WM - 1 the xs rows (64 each), the next two the 128 ws rows, any others nothing
   __amdgpu_buffer_rsrc_t rS;
   int scale_dst; // byte offset inside a stage's scales: xs, then ws, then spare
-  if (wave < 4) {
+  if (wave < C::WM) {
     const int r0 = t.m0 + 64 * wave;
     rS = q8_buffer(p.xs + (long long)r0 * groups, (long long)min(64, p.m - r0) * groups * 4);
     scale_dst = 64 * wave * 4;
-  } else if (wave < 6) {
-    const int h = wave - 4;
+  } else if (wave < C::WM + 2) {
+    const int h = wave - C::WM;
     const float *src = t.swiglu ? (h ? seg.w3s : seg.ws) : seg.ws;
     const int c0 = t.swiglu ? t.n0 : t.n0 + 64 * h;
     rS = q8_buffer(src + (long long)c0 * groups, (long long)min(64, seg.n - c0) * groups * 4);
-    scale_dst = (kQ8TileM + 64 * h) * 4;
+    scale_dst = (C::TileM + 64 * h) * 4;
   } else {
     rS = q8_buffer(p.xs, 0);
-    scale_dst = (kQ8TileM + kQ8TileN) * 4;
+    scale_dst = (C::TileM + C::TileN) * 4;
   }
   const int offS = lane * groups * 4;
   const __amdgpu_buffer_rsrc_t none = q8_buffer(p.xq, 0);
@@ -238,38 +285,42 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
     constexpr int st = decltype(ST)::value;
     const bool live = step < steps;
     const int k0 = step * 64, g = step / spg;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, (void *)(q8_smem + ((2 * wave) * kQ8Stages + st) * 1024),
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, (void *)(q8_smem + ((2 * wave) * C::Stages + st) * 1024),
                                              16, offA0, k0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
-                                             (void *)(q8_smem + ((2 * wave + 1) * kQ8Stages + st) * 1024), 16, offA1,
+                                             (void *)(q8_smem + ((2 * wave + 1) * C::Stages + st) * 1024), 16, offA1,
                                              k0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB : none,
-                                             (void *)(q8_smem + kQ8BOff + (wave * kQ8Stages + st) * 1024), 16, offB, k0,
-                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        live ? rB0 : none, (void *)(q8_smem + C::BOff + (C::BPerWave * wave * C::Stages + st) * 1024), 16, offB0, k0,
+        0, 0);
+    if constexpr (C::BPerWave == 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          live ? rB1 : none, (void *)(q8_smem + C::BOff + ((2 * wave + 1) * C::Stages + st) * 1024), 16, offB1, k0,
+          0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rS : none,
-                                             (void *)(q8_smem + kQ8SOff + st * kQ8SStride + scale_dst), 4, offS,
+                                             (void *)(q8_smem + C::SOff + st * C::SStride + scale_dst), 4, offS,
                                              g * 4, 0, 0);
   };
 
   // Per-lane LDS read bases; the stage and the 16-row block add immediates.
   const int lrow = lane & 15, lq = lane >> 4, lr4 = (lane >> 4) * 4;
   const int lane_part = lrow * 64 + ((lq ^ q8_swizzle(lrow)) << 4);
-  const unsigned char *abase = q8_smem + (4 * wm) * kQ8Stages * 1024 + lane_part;
+  const unsigned char *abase = q8_smem + (4 * wm) * C::Stages * 1024 + lane_part;
   const unsigned char *bbase[4];
 #pragma unroll
   for (int j = 0; j < 4; j++)
-    bbase[j] = q8_smem + kQ8BOff + (b_row(t.swiglu, wn, j) / 16) * kQ8Stages * 1024 + lane_part;
-  const unsigned char *xsbase = q8_smem + kQ8SOff + (wm * 64 + lr4) * 4;
+    bbase[j] = q8_smem + C::BOff + (b_row(t.swiglu, wn, j) / 16) * C::Stages * 1024 + lane_part;
+  const unsigned char *xsbase = q8_smem + C::SOff + (wm * 64 + lr4) * 4;
   const unsigned char *wsbase[4];
 #pragma unroll
   for (int j = 0; j < 4; j++)
-    wsbase[j] = q8_smem + kQ8SOff + (kQ8TileM + b_row(t.swiglu, wn, j) + lrow) * 4;
+    wsbase[j] = q8_smem + C::SOff + (C::TileM + b_row(t.swiglu, wn, j) + lrow) * 4;
 
   auto operands = [&](auto ST, v4i (&a)[4], v4i (&b)[4]) {
     constexpr int st = decltype(ST)::value;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-      a[i] = *reinterpret_cast<const v4i *>(abase + (i * kQ8Stages + st) * 1024);
+      a[i] = *reinterpret_cast<const v4i *>(abase + (i * C::Stages + st) * 1024);
 #pragma unroll
     for (int j = 0; j < 4; j++)
       b[j] = *reinterpret_cast<const v4i *>(bbase[j] + st * 1024);
@@ -288,10 +339,10 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
   // fills. Then the next step's MFMAs and, at a group's end, this step's rescale. After the last step the MFMAs run
   // on stale operands whose products are never used.
   auto advance = [&](int step, auto ST) {
-    constexpr int st = decltype(ST)::value, nst = (st + 1) % kQ8Stages, fill = (st + kQ8Stages - 1) % kQ8Stages;
-    wait_vmcnt<(kQ8Stages - 3) * kQ8LoadsPerStep>();
+    constexpr int st = decltype(ST)::value, nst = (st + 1) % C::Stages, fill = (st + C::Stages - 1) % C::Stages;
+    wait_vmcnt<(C::Stages - 3) * C::LoadsPerStep>();
     __builtin_amdgcn_s_barrier();
-    issue(step + kQ8Stages - 1, std::integral_constant<int, fill>{});
+    issue(step + C::Stages - 1, std::integral_constant<int, fill>{});
     v4i a[4], b[4];
     operands(std::integral_constant<int, nst>{}, a, b);
     if (GS64 || step % spg == spg - 1) {
@@ -299,10 +350,10 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
       float wsc[4];
 #pragma unroll
       for (int i = 0; i < 4; i++)
-        xsv[i] = *reinterpret_cast<const v4f *>(xsbase + st * kQ8SStride + i * 64);
+        xsv[i] = *reinterpret_cast<const v4f *>(xsbase + st * C::SStride + i * 64);
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        wsc[j] = *reinterpret_cast<const float *>(wsbase[j] + st * kQ8SStride);
+        wsc[j] = *reinterpret_cast<const float *>(wsbase[j] + st * C::SStride);
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -334,11 +385,8 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
     }
   };
 
-  issue(0, std::integral_constant<int, 0>{});
-  issue(1, std::integral_constant<int, 1>{});
-  issue(2, std::integral_constant<int, 2>{});
-  issue(3, std::integral_constant<int, 3>{});
-  wait_vmcnt<(kQ8Stages - 2) * kQ8LoadsPerStep>(); // step 0 has landed for this wave
+  issue_first<0, C::Stages - 1>(issue);
+  wait_vmcnt<(C::Stages - 2) * C::LoadsPerStep>(); // step 0 has landed for this wave
   __builtin_amdgcn_s_barrier();                      // ... and for every wave
   {
     v4i a[4], b[4];
@@ -349,22 +397,10 @@ __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_lds(Q8Params p) {
       for (int j = 0; j < 4; j++)
         dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], v4i{0, 0, 0, 0}, 0, 0, 0);
   }
-  // the K loop unrolled by the five stages, so every stage index is a constant
-  for (int step = 0; step < steps; step += kQ8Stages) {
-    advance(step, std::integral_constant<int, 0>{});
-    if (step + 1 >= steps)
+  // the K loop unrolled by the stages, so every stage index is a constant
+  for (int step = 0; step < steps; step += C::Stages)
+    if (!unrolled_steps<0, C::Stages>(advance, step, steps))
       break;
-    advance(step + 1, std::integral_constant<int, 1>{});
-    if (step + 2 >= steps)
-      break;
-    advance(step + 2, std::integral_constant<int, 2>{});
-    if (step + 3 >= steps)
-      break;
-    advance(step + 3, std::integral_constant<int, 3>{});
-    if (step + 4 >= steps)
-      break;
-    advance(step + 4, std::integral_constant<int, 4>{});
-  }
   // the loads issued for steps past the end still target this block's LDS: let them land before the block exits
   __builtin_amdgcn_s_waitcnt(0);
   store_tile(seg, t, acc, wm, wn, lane, p.m);
@@ -770,10 +806,10 @@ TileGrid make_grid(const GemmSegmentDev *segs, int nseg, int m) {
   return g;
 }
 
-Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m) {
+Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m, int tile_m = kQ8TileM) {
   Q8Grid g{};
   g.nseg = nseg;
-  g.mtiles = (m + kQ8TileM - 1) / kQ8TileM;
+  g.mtiles = (m + tile_m - 1) / tile_m;
   int tiles = 0;
   for (int s = 0; s < nseg; s++) {
     const GemmSegmentDev &d = segs[s];
@@ -785,25 +821,43 @@ Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m) {
   return g;
 }
 
+struct SegList {
+  const GemmSegmentDev *seg;
+  int nseg;
+};
+
 // The pipelined kernel takes more than the default 64 KB of dynamic LDS: raised once per instantiation.
-template <bool PROBE, bool GS64> bool q8_ready() {
-  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_lds<PROBE, GS64>,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ8Lds);
+template <class C, bool PROBE, bool GS64> bool q8_ready() {
+  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_lds<C, PROBE, GS64>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::Lds);
   return check_hip(status, "allowing the Q8 GEMM its LDS");
 }
 
-template <bool PROBE, bool GS64> bool q8_launch(const Q8Params &p, hipStream_t stream) {
-  if (!q8_ready<PROBE, GS64>())
+template <class C, bool PROBE, bool GS64> bool q8_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
+  if (!q8_ready<C, PROBE, GS64>())
     return false;
-  hipLaunchKernelGGL((q8_gemm_lds<PROBE, GS64>), dim3(p.grid.total), dim3(kQ8Threads), kQ8Lds, stream, p);
+  p.grid = make_q8_grid(segs.seg, segs.nseg, p.m, C::TileM);
+  if (p.grid.total <= 0)
+    return true;
+  hipLaunchKernelGGL((q8_gemm_lds<C, PROBE, GS64>), dim3(p.grid.total), dim3(C::Threads), C::Lds, stream, p);
   return launch_ok("q8_gemm_lds");
 }
 
+// Tile shape: 256 x 128 unless LLAMA_HIP_Q8_TILE_M = 128 (read once). On the 8B W1/W3 shape the 128-row tiles with
+// two blocks per CU measured about 5% slower: the extra A traffic costs more than the second block's overlap gains.
+int q8_tile_m() {
+  static const int tile = [] {
+    const char *env = getenv("LLAMA_HIP_Q8_TILE_M");
+    return env && atoi(env) == 128 ? 128 : 256;
+  }();
+  return tile;
+}
+
 template <bool PROBE> bool launch_q8_lds(Q8Params p, const GemmSegmentDev *segs, int nseg, hipStream_t stream) {
-  p.grid = make_q8_grid(segs, nseg, p.m);
-  if (p.grid.total <= 0)
-    return true;
-  return p.gs == 64 ? q8_launch<PROBE, true>(p, stream) : q8_launch<PROBE, false>(p, stream);
+  const SegList list{segs, nseg};
+  if (q8_tile_m() == 256)
+    return p.gs == 64 ? q8_launch<Q8Wide, PROBE, true>(p, list, stream) : q8_launch<Q8Wide, PROBE, false>(p, list, stream);
+  return p.gs == 64 ? q8_launch<Q8Pair, PROBE, true>(p, list, stream) : q8_launch<Q8Pair, PROBE, false>(p, list, stream);
 }
 
 } // namespace
