@@ -80,10 +80,10 @@ void llhip_clear_error(void);
  * start-up. */
 void llhip_set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves);
 
-/* Blocks per 256 x 128 output tile of the FP32 / BF16 prefill GEMMs (split K; 0 = chosen from the grid: about one
- * block per CU when the tiles are fewer than the CUs, at least eight K steps per block, at most 512 blocks). Partial
- * sums are added in split order, so results depend on it only through FP32 summation order, never on timing. For
- * tuning and tests. */
+/* Blocks per output tile of the prefill GEMMs, FP32, BF16 and INT8 (split K; 0 = chosen from the grid: about one
+ * block per CU when the tiles are fewer than the CUs, at least eight K steps per block, at most 512 blocks; INT8
+ * splits keep whole scale groups). Partial sums are added in split order, so results depend on it only through FP32
+ * summation order, never on timing; INT8 group dots are exact either way. For tuning and tests. */
 void llhip_set_gemm_splits(int splits);
 
 /* The int32 probe of the decode GEMV: dots[g * d + r] = the exact int32 dot of group g of input row xq and weight

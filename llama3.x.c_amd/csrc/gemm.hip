@@ -168,12 +168,22 @@ struct Q8Grid {
   int total;
 };
 
+constexpr int kSplitSlots = LLHIP_SPLIT_SLOTS; // partial tiles the workspace holds
+
+struct SplitK {
+  v4f *partial;    // [tile * splits + split][16][threads] partial sums, in the accumulators' register order
+  unsigned *count; // [tile] blocks arrived; zero between launches
+  int splits;      // blocks per tile (1: no split)
+  int per;         // K steps per split
+};
+
 struct Q8Params {
   Q8Grid grid;
   const int8_t *xq;
   const float *xs;
   int m, k, gs;
   int32_t *probe; // optional (one segment, no SWIGLU): probe[(g * m + r) * n + c]
+  SplitK sk;
 };
 
 __device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical, int tile_m = kQ8TileM) {
@@ -209,6 +219,62 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
+// Split K (the GEMM kernels here): a grid with fewer tiles than CUs runs each tile as `splits` blocks over consecutive K
+// ranges. Each block writes its partial tile to a device workspace and counts itself in at the tile's counter; the
+// last to arrive adds the partials in split order (the same order whichever block is last, so results do not depend
+// on timing), puts the counter back to zero and applies the epilogue.
+
+// Cache policy of the partial tiles' stores and loads: device-coherent (sc1), so a store is written through past the
+// XCD's L2 before its completion is counted, and a load reads from past it. No cache-wide write-back or invalidate is
+// needed, which would also evict the operands of every other block on the XCD.
+constexpr int kDeviceCoherent = 16;
+
+// The last of a tile's blocks to arrive gets true with acc holding the whole sum; the others get false.
+template <int THREADS>
+__device__ __forceinline__ bool split_combine(const SplitK &sk, int tile, int split, v4f (&acc)[4][4]) {
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  constexpr int kSlotBytes = 16 * THREADS * 16; // one partial tile
+  const __amdgpu_buffer_rsrc_t r =
+      q8_buffer((const unsigned char *)sk.partial + (size_t)tile * sk.splits * kSlotBytes, (long long)sk.splits * kSlotBytes);
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, acc[i][j]), r,
+                                             split * kSlotBytes + ((i * 4 + j) * THREADS + tid) * 16, 0,
+                                             kDeviceCoherent);
+  __builtin_amdgcn_s_waitcnt(0); // this thread's partial sums have reached the device-coherent level
+  __syncthreads();               // ... and every thread's
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(&sk.count[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (unsigned)(sk.splits - 1);
+  __syncthreads();
+  if (!last)
+    return false;
+  v4f own[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      own[i][j] = acc[i][j];
+  for (int s = 0; s < sk.splits; s++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const v4f v = s == split ? own[i][j]
+                                 : __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               r, s * kSlotBytes + ((i * 4 + j) * THREADS + tid) * 16,
+                                                               0, kDeviceCoherent));
+        acc[i][j] = s == 0 ? v : acc[i][j] + v;
+      }
+  }
+  if (tid == 0)
+    __hip_atomic_store(&sk.count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 // The K loop unrolled by the stages (every stage index a constant), leaving after the last step.
 template <int I, int N, class F> __device__ __forceinline__ bool unrolled_steps(F &f, int step, int steps) {
   if constexpr (I < N) {
@@ -220,23 +286,32 @@ template <int I, int N, class F> __device__ __forceinline__ bool unrolled_steps(
   return true;
 }
 
-// The loads of steps 0 .. N - 1 into stages 0 .. N - 1.
-template <int I, int N, class F> __device__ __forceinline__ void issue_first(F &f) {
+// The loads of steps first .. first + N - 1 into stages 0 .. N - 1.
+template <int I, int N, class F> __device__ __forceinline__ void issue_first(F &f, int first) {
   if constexpr (I < N) {
-    f(I, std::integral_constant<int, I>{});
-    issue_first<I + 1, N>(f);
+    f(first + I, std::integral_constant<int, I>{});
+    issue_first<I + 1, N>(f, first);
   }
 }
 
-template <class C, bool PROBE, bool GS64>
+template <class C, bool PROBE, bool GS64, bool SPLIT>
 __global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
   extern __shared__ __align__(16) unsigned char q8_smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const TilePos t = q8_tile_of(p.grid, xcd_logical(blockIdx.x, p.grid.total), C::TileM);
+  // readfirstlane: the divisions run on the vector unit, and a step base the compiler cannot prove uniform would
+  // turn every buffer load (the step is its scalar offset) into a loop over lanes
+  // SPLIT is its own instantiation: the unsplit kernel sits at the register limit, and a K range that does not start
+  // at 0 pushes it into spilling.
+  const int logical = xcd_logical(blockIdx.x, p.grid.total * (SPLIT ? p.sk.splits : 1));
+  const int tile = SPLIT ? __builtin_amdgcn_readfirstlane(logical / p.sk.splits) : logical;
+  const int split = SPLIT ? __builtin_amdgcn_readfirstlane(logical % p.sk.splits) : 0;
+  const TilePos t = q8_tile_of(p.grid, tile, C::TileM);
   const TileSeg seg = q8_seg_of(p.grid, t.s);
   const int groups = p.k / p.gs, spg = GS64 ? 1 : p.gs / 64, steps = p.k / 64;
+  // this block's K steps [s0, s1): whole groups (per is a multiple of the steps per group)
+  const int s0 = SPLIT ? split * p.sk.per : 0, s1 = SPLIT ? min(steps, s0 + p.sk.per) : steps;
   const long long k = p.k;
 
   // This wave's loads of every step, as buffer resources bounded to the rows that exist (rows past m or n read zeros)
@@ -283,7 +358,7 @@ __global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
   // goes in the scalar offset operand.
   auto issue = [&](int step, auto ST) {
     constexpr int st = decltype(ST)::value;
-    const bool live = step < steps;
+    const bool live = step < s1;
     const int k0 = step * 64, g = step / spg;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, (void *)(q8_smem + ((2 * wave) * C::Stages + st) * 1024),
                                              16, offA0, k0, 0, 0);
@@ -385,8 +460,8 @@ __global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
     }
   };
 
-  issue_first<0, C::Stages - 1>(issue);
-  wait_vmcnt<(C::Stages - 2) * C::LoadsPerStep>(); // step 0 has landed for this wave
+  issue_first<0, C::Stages - 1>(issue, s0);
+  wait_vmcnt<(C::Stages - 2) * C::LoadsPerStep>(); // step s0 has landed for this wave
   __builtin_amdgcn_s_barrier();                      // ... and for every wave
   {
     v4i a[4], b[4];
@@ -398,11 +473,43 @@ __global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
         dot[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], v4i{0, 0, 0, 0}, 0, 0, 0);
   }
   // the K loop unrolled by the stages, so every stage index is a constant
-  for (int step = 0; step < steps; step += C::Stages)
-    if (!unrolled_steps<0, C::Stages>(advance, step, steps))
+  for (int step = s0; step < s1; step += C::Stages)
+    if (!unrolled_steps<0, C::Stages>(advance, step, s1))
       break;
   // the loads issued for steps past the end still target this block's LDS: let them land before the block exits
   __builtin_amdgcn_s_waitcnt(0);
+  if (SPLIT) { // a partial tile for q8_split_reduce (the register budget leaves no room for an in-kernel sum)
+    v4f *slot = p.sk.partial + (size_t)(tile * p.sk.splits + split) * 16 * C::Threads + threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        slot[(i * 4 + j) * C::Threads] = acc[i][j];
+    return;
+  }
+  store_tile(seg, t, acc, wm, wn, lane, p.m);
+}
+
+// The split int8 launch's second kernel: one block per tile adds the tile's partials in split order and applies the
+// epilogue, with the thread layout of q8_gemm_lds.
+template <class C> __global__ __launch_bounds__(C::Threads) void q8_split_reduce(Q8Params p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
+  const int tile = blockIdx.x;
+  const TilePos t = q8_tile_of(p.grid, tile, C::TileM);
+  const TileSeg seg = q8_seg_of(p.grid, t.s);
+  const v4f *part = p.sk.partial + (size_t)tile * p.sk.splits * 16 * C::Threads + threadIdx.x;
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      acc[i][j] = part[(i * 4 + j) * C::Threads];
+  for (int s = 1; s < p.sk.splits; s++)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] += part[((size_t)s * 16 + i * 4 + j) * C::Threads];
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
@@ -431,10 +538,7 @@ __device__ __forceinline__ unsigned short to_bf16(float x) {
 //         feeds value s to the s-th instruction. W rows are read like A rows (row pitch ldw).
 // The FP32 sums stay in the MFMA accumulators: no per-step vector work.
 //
-// Split K: a grid with fewer tiles than CUs runs each tile as `splits` blocks over consecutive K ranges. Each block
-// writes its 256 x 128 partial sums to a device workspace and counts itself in at the tile's counter; the last to
-// arrive adds the partials in split order (the same order whichever block is last, so results do not depend on
-// timing), puts the counter back to zero and applies the epilogue.
+// Short grids split K as the int8 kernel does.
 __global__ __launch_bounds__(256) void bf16_panel(const float *__restrict__ a, long long lda, int m, int k, int kp,
                                                   unsigned short *__restrict__ panel) {
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x; // 8 values per thread
@@ -457,15 +561,6 @@ typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
 
 constexpr int kMmLoadsPerStep = 3;                   // per wave: two A and one B load
 constexpr size_t kMmLds = (size_t)kQ8SOff;           // A and B blocks of five stages, no scales
-constexpr int kSplitSlots = LLHIP_SPLIT_SLOTS;       // partial tiles the workspace holds
-constexpr int kSplitTileFloats = kQ8TileM * kQ8TileN; // one partial tile
-
-struct SplitK {
-  v4f *partial;    // [tile * splits + split][16][512] partial sums, in the accumulators' register order
-  unsigned *count; // [tile] blocks arrived; zero between launches
-  int splits;      // blocks per tile (1: no split)
-  int per;         // K steps per split
-};
 
 struct MmParams {
   Q8Grid grid;
@@ -475,63 +570,14 @@ struct MmParams {
   SplitK sk;
 };
 
-// Cache policy of the partial tiles' stores and loads: device-coherent (sc1), so a store is written through past the
-// XCD's L2 before its completion is counted, and a load reads from past it. No cache-wide write-back or invalidate is
-// needed, which would also evict the operands of every other block on the XCD.
-constexpr int kDeviceCoherent = 16;
-
-// The last of a tile's blocks to arrive gets true with acc holding the whole sum; the others get false.
-__device__ __forceinline__ bool split_combine(const SplitK &sk, int tile, int split, v4f (&acc)[4][4]) {
-  __shared__ int last;
-  const int tid = threadIdx.x;
-  constexpr int kSlotBytes = 16 * kQ8Threads * 16; // one partial tile
-  const __amdgpu_buffer_rsrc_t r =
-      q8_buffer((const unsigned char *)sk.partial + (size_t)tile * sk.splits * kSlotBytes, (long long)sk.splits * kSlotBytes);
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, acc[i][j]), r,
-                                             split * kSlotBytes + ((i * 4 + j) * kQ8Threads + tid) * 16, 0,
-                                             kDeviceCoherent);
-  __builtin_amdgcn_s_waitcnt(0); // this thread's partial sums have reached the device-coherent level
-  __syncthreads();               // ... and every thread's
-  if (tid == 0)
-    last = __hip_atomic_fetch_add(&sk.count[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           (unsigned)(sk.splits - 1);
-  __syncthreads();
-  if (!last)
-    return false;
-  v4f own[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      own[i][j] = acc[i][j];
-  for (int s = 0; s < sk.splits; s++) {
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const v4f v = s == split ? own[i][j]
-                                 : __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                                                               r, s * kSlotBytes + ((i * 4 + j) * kQ8Threads + tid) * 16,
-                                                               0, kDeviceCoherent));
-        acc[i][j] = s == 0 ? v : acc[i][j] + v;
-      }
-  }
-  if (tid == 0)
-    __hip_atomic_store(&sk.count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return true;
-}
-
 template <bool F32> __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_lds(MmParams p) {
   extern __shared__ __align__(16) unsigned char q8_smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int logical = xcd_logical(blockIdx.x, p.grid.total * p.sk.splits);
-  const int tile = logical / p.sk.splits, split = logical % p.sk.splits;
+  const int tile = __builtin_amdgcn_readfirstlane(logical / p.sk.splits); // uniform (see q8_gemm_lds)
+  const int split = __builtin_amdgcn_readfirstlane(logical % p.sk.splits);
   const TilePos t = q8_tile_of(p.grid, tile);
   const TileSeg seg = q8_seg_of(p.grid, t.s);
   const int s0 = split * p.sk.per, s1 = min(p.steps, s0 + p.sk.per);
@@ -659,7 +705,7 @@ template <bool F32> __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_lds
     advance(step + 4, std::integral_constant<int, 4>{});
   }
   __builtin_amdgcn_s_waitcnt(0);
-  if (p.sk.splits > 1 && !split_combine(p.sk, tile, split, acc))
+  if (p.sk.splits > 1 && !split_combine<kQ8Threads>(p.sk, tile, split, acc))
     return;
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
@@ -821,26 +867,60 @@ Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m, int tile_m = kQ
   return g;
 }
 
+std::atomic<int> forced_splits{0};
+
+// Blocks per tile: one when the tiles fill the CUs (one 256 x 128 block per CU fits in LDS), else enough to reach
+// about one block per CU, keeping at least eight K steps per block and within the workspace's partial tiles. A
+// block's steps are a multiple of `unit` (the int8 kernel's steps per scale group).
+int choose_splits(int tiles, int steps, int *per, int unit = 1) {
+  int s = forced_splits.load();
+  if (s <= 0) {
+    const int cus = device().cu_count > 0 ? device().cu_count : 256;
+    s = tiles < cus ? cus / tiles : 1;
+    s = min(s, steps / 8);
+  }
+  s = max(1, min(s, min(kSplitSlots / max(tiles, 1), steps)));
+  *per = ((steps + s - 1) / s + unit - 1) / unit * unit;
+  return (steps + *per - 1) / *per; // no empty split
+}
+
 struct SegList {
   const GemmSegmentDev *seg;
   int nseg;
 };
 
 // The pipelined kernel takes more than the default 64 KB of dynamic LDS: raised once per instantiation.
-template <class C, bool PROBE, bool GS64> bool q8_ready() {
-  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_lds<C, PROBE, GS64>,
+template <class C, bool PROBE, bool GS64, bool SPLIT> bool q8_ready() {
+  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_lds<C, PROBE, GS64, SPLIT>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::Lds);
   return check_hip(status, "allowing the Q8 GEMM its LDS");
 }
 
 template <class C, bool PROBE, bool GS64> bool q8_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
-  if (!q8_ready<C, PROBE, GS64>())
-    return false;
   p.grid = make_q8_grid(segs.seg, segs.nseg, p.m, C::TileM);
   if (p.grid.total <= 0)
     return true;
-  hipLaunchKernelGGL((q8_gemm_lds<C, PROBE, GS64>), dim3(p.grid.total), dim3(C::Threads), C::Lds, stream, p);
-  return launch_ok("q8_gemm_lds");
+  const int steps = p.k / 64;
+  p.sk.splits = p.grid.total > kSplitSlots ? 1 : choose_splits(p.grid.total, steps, &p.sk.per, p.gs / 64);
+  if (p.sk.splits == 1)
+    p.sk.per = steps;
+  p.sk.partial = (v4f *)device().split_partial;
+  p.sk.count = device().split_count;
+  if (p.sk.splits == 1) {
+    if (!q8_ready<C, PROBE, GS64, false>())
+      return false;
+    hipLaunchKernelGGL((q8_gemm_lds<C, PROBE, GS64, false>), dim3((unsigned)p.grid.total), dim3(C::Threads), C::Lds,
+                       stream, p);
+    return launch_ok("q8_gemm_lds");
+  }
+  if (!q8_ready<C, PROBE, GS64, true>())
+    return false;
+  hipLaunchKernelGGL((q8_gemm_lds<C, PROBE, GS64, true>), dim3((unsigned)(p.grid.total * p.sk.splits)),
+                     dim3(C::Threads), C::Lds, stream, p);
+  if (!launch_ok("q8_gemm_lds"))
+    return false;
+  hipLaunchKernelGGL(q8_split_reduce<C>, dim3((unsigned)p.grid.total), dim3(C::Threads), 0, stream, p);
+  return launch_ok("q8_split_reduce");
 }
 
 // Tile shape: 256 x 128 unless LLAMA_HIP_Q8_TILE_M = 128 (read once). On the 8B W1/W3 shape the 128-row tiles with
@@ -924,22 +1004,6 @@ bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs,
 }
 
 namespace {
-
-std::atomic<int> forced_splits{0};
-
-// Blocks per tile: one when the tiles fill the CUs (one 256 x 128 block per CU fits in LDS), else enough to reach
-// about one block per CU, keeping at least eight K steps per block and within the workspace's partial tiles.
-int choose_splits(int tiles, int steps, int *per) {
-  int s = forced_splits.load();
-  if (s <= 0) {
-    const int cus = device().cu_count > 0 ? device().cu_count : 256;
-    s = tiles < cus ? cus / tiles : 1;
-    s = min(s, steps / 8);
-  }
-  s = max(1, min(s, min(kSplitSlots / max(tiles, 1), steps)));
-  *per = (steps + s - 1) / s;
-  return (steps + *per - 1) / *per; // no empty split
-}
 
 template <bool F32> bool mm_launch(MmParams p, hipStream_t stream) {
   static const hipError_t status =

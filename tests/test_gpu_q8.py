@@ -327,6 +327,51 @@ def test_gemm_q8_all_kinds_within_budget(m, n, k, gs):
     del T
 
 
+@pytest.mark.parametrize("m,n,k,gs", [(5, 300, 4096, 64), (40, 136, 14336, 256), (257, 70, 2048, 128)])
+def test_gemm_q8_split_k(m, n, k, gs):
+    """Grids of few tiles split K over several blocks per tile (partials added in split order by a second kernel).
+    Every forced split count meets the budget for every kind, repeats bit for bit, and leaves the int32 group dots of
+    the probe exact; 0 is the automatic choice."""
+    L = hu.lib()
+    xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 909 + m)
+    ldc = n + 3
+    base = rng.uniform(m * ldc, 3.0).reshape(m, ldc)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    r3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
+    dx = [hu.dev(a) for a in (xq, xs, wq, ws, w3q, w3s)]
+    want_dots = orc.group_dots(xq, wq, gs)
+    try:
+        for splits in (0, 1, 2, 3, 7):
+            L.llhip_set_gemm_splits(splits)
+            for kind in (lh.GEMM_STORE, lh.GEMM_ADD, lh.GEMM_SWIGLU):
+                c = hu.dev(base)
+                seg = lh.GemmQ8Segment(lh.ptr(c), ldc, lh.w8(dx[2], dx[3]), lh.w8(dx[4], dx[5]), None, None, n, kind)
+                L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+                got = hu.host(c)
+                assert lh.last_error() == "", lh.last_error()
+                assert np.array_equal(hu.bits(got[:, n:]), hu.bits(base[:, n:])), "row padding was written"
+                what = f"{m}x{n}x{k} gs {gs} kind {kind} splits {splits}"
+                if kind == lh.GEMM_ADD:
+                    hu.assert_within_budget(got[:, :n], base[:, :n] + ref, mag + np.abs(base[:, :n]), what=what)
+                elif kind == lh.GEMM_SWIGLU:
+                    want = ref / (1 + np.exp(-ref)) * r3
+                    tol = 2e-5 * (mag * (np.abs(r3) + 1) + mag3 * (np.abs(ref) + 1)) + 1e-6
+                    assert np.all(np.abs(got[:, :n] - want) <= tol), what
+                else:
+                    hu.assert_within_budget(got[:, :n], ref, mag, what=what)
+                    again = hu.dev(base)
+                    seg = lh.GemmQ8Segment(lh.ptr(again), ldc, lh.w8(dx[2], dx[3]), lh.K8Weight(), None, None, n,
+                                           kind)
+                    L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+                    assert np.array_equal(hu.bits(hu.host(again)), hu.bits(got)), what + " not repeatable"
+            dots = np.zeros((k // gs, m, n), np.int32)
+            L.llhip_q8_group_dots(lh.ptr(dots), lh.ptr(xq), m, k, gs, lh.ptr(wq), n)
+            assert lh.last_error() == ""
+            assert np.array_equal(dots, want_dots), f"probe splits {splits}"
+    finally:
+        L.llhip_set_gemm_splits(0)
+
+
 def test_gemm_q8_qkv_segments_and_gemv_agreement():
     """Three segments sharing the activations (QKV), and each GEMM row against the GEMV of that row."""
     L = hu.lib()
