@@ -378,8 +378,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--seed", type=int, default=88172645463325252 % (1 << 31))
-    ap.add_argument("--c3", action="store_true",
-                    help="also measure the FP32 / BF16 prefill GEMMs on the Llama-3.2-3B shapes (512 tokens)")
+    ap.add_argument("--no-c3", action="store_true",
+                    help="skip the FP32 / BF16 prefill GEMMs on the Llama-3.2-3B shapes (512 tokens)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also launch a plain copy kernel of this many MiB (counter calibration for --pmc runs)")
     args = ap.parse_args()
@@ -486,7 +486,7 @@ def main():
               f"{ach:.0f} TOP/s in the W1/W3 GEMM", file=sys.stderr, flush=True)
     L.llhip_graph_destroy(graph)
 
-    if args.c3:
+    if not args.no_c3:
         result["prefill_3b"] = prefill_3b(torch, lh, args.seed)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_threads)
