@@ -7,6 +7,7 @@
 // instruction orders K inside a lane; the 16 x 16 result holds C[4 (l / 16) + e][l % 16] in element e of lane l.
 #include <atomic>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <vector>
 
@@ -113,6 +114,41 @@ __device__ __forceinline__ void store_tile(const TileSeg &seg, const TilePos &t,
     }
 }
 
+// The wide BF16 tile's epilogue: rows 64 wm + 16 i + 4 (l / 16) + e, columns 128 wn + 16 j + l % 16, or under SWIGLU
+// silu(W1 column 64 wn + 16 j + l % 16) * (the same W3 column) from tiles j and j + 4.
+__device__ __forceinline__ void store_tile_wide(const TileSeg &seg, const TilePos &t, const v4f (&acc)[4][8], int wm,
+                                                int wn, int lane, int m) {
+  const int lc = lane & 15, lr = (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int row = t.m0 + wm * 64 + 16 * i + lr + e;
+      if (row >= m)
+        continue;
+      float *crow = seg.c + (long long)row * seg.ldc;
+      if (t.swiglu) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int col = t.n0 + 64 * wn + 16 * j + lc;
+          if (col < seg.n)
+            crow[col] = silu_gate(acc[i][j][e], acc[i][j + 4][e]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int col = t.n0 + 128 * wn + 16 * j + lc;
+          if (col >= seg.n)
+            continue;
+          if (seg.epi == EPI_ADD)
+            crow[col] += acc[i][j][e];
+          else
+            crow[col] = acc[i][j][e];
+        }
+      }
+    }
+}
+
 // ---- W8A8 Q8_0: the pipelined int8-MFMA kernel ------------------------------------------------------------------------
 //
 // 512 threads own a 256 x 128 output tile (a 128-column tile holds 64 columns of W1 and the same 64 of W3 under
@@ -186,7 +222,8 @@ struct Q8Params {
   SplitK sk;
 };
 
-__device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical, int tile_m = kQ8TileM) {
+__device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical, int tile_m = kQ8TileM,
+                                              int tile_n = kQ8TileN) {
   int s = 0;
   while (s + 1 < g.nseg && logical >= g.seg[s + 1].first_tile)
     s++;
@@ -195,7 +232,7 @@ __device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical, int 
   t.s = s;
   t.swiglu = g.seg[s].epi == EPI_SWIGLU;
   t.m0 = (local % g.mtiles) * tile_m;
-  t.n0 = (local / g.mtiles) * (t.swiglu ? kQ8TileN / 2 : kQ8TileN);
+  t.n0 = (local / g.mtiles) * (t.swiglu ? tile_n / 2 : tile_n);
   return t;
 }
 
@@ -273,6 +310,54 @@ __device__ __forceinline__ bool split_combine(const SplitK &sk, int tile, int sp
   if (tid == 0)
     __hip_atomic_store(&sk.count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return true;
+}
+
+// The second kernel of a split launch whose kernel wrote partial tiles (the int8 and the wide BF16 kernels): thread by
+// thread over every tile's partial sums. A thread takes one accumulator pair, tiles j and j + J/2 of row tile i of
+// one lane of the block layout (the SWIGLU pair, or two plain column tiles), adds the splits in order and applies the
+// epilogue to its four rows. Partial tile layout: [tile][split][i * J + j][THREADS] v4f.
+struct SplitOut {
+  Q8Grid grid;
+  const v4f *partial;
+  int splits, m, tile_m, tile_n;
+};
+
+template <int J, int THREADS> __global__ __launch_bounds__(256) void split_reduce(SplitOut p) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long per_tile = 4LL * (J / 2) * THREADS;
+  if (idx >= per_tile * p.grid.total)
+    return;
+  const int tile = (int)(idx / per_tile), rest = (int)(idx % per_tile);
+  const int tid = rest % THREADS, jp = (rest / THREADS) % (J / 2), i = rest / THREADS / (J / 2);
+  const TilePos t = q8_tile_of(p.grid, tile, p.tile_m, p.tile_n);
+  const TileSeg seg = q8_seg_of(p.grid, t.s);
+  const v4f *part = p.partial + (size_t)tile * p.splits * (4 * J * THREADS) + tid;
+  v4f lo = part[(i * J + jp) * THREADS], hi = part[(i * J + jp + J / 2) * THREADS];
+  for (int s = 1; s < p.splits; s++) {
+    lo += part[(size_t)s * (4 * J * THREADS) + (i * J + jp) * THREADS];
+    hi += part[(size_t)s * (4 * J * THREADS) + (i * J + jp + J / 2) * THREADS];
+  }
+  const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  const int lc = lane & 15, lr = (lane >> 4) * 4;
+  constexpr int kSpan = 16 * J; // columns a wave covers
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int row = t.m0 + wm * 64 + 16 * i + lr + e;
+    if (row >= p.m)
+      continue;
+    float *crow = seg.c + (long long)row * seg.ldc;
+    if (t.swiglu) {
+      const int col = t.n0 + (kSpan / 2) * wn + 16 * jp + lc;
+      if (col < seg.n)
+        crow[col] = silu_gate(lo[e], hi[e]);
+    } else {
+      const int c0 = t.n0 + kSpan * wn + 16 * jp + lc, c1 = c0 + 16 * (J / 2);
+      if (c0 < seg.n)
+        crow[c0] = seg.epi == EPI_ADD ? crow[c0] + lo[e] : lo[e];
+      if (c1 < seg.n)
+        crow[c1] = seg.epi == EPI_ADD ? crow[c1] + hi[e] : hi[e];
+    }
+  }
 }
 
 // The K loop unrolled by the stages (every stage index a constant), leaving after the last step.
@@ -478,7 +563,7 @@ __global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
       break;
   // the loads issued for steps past the end still target this block's LDS: let them land before the block exits
   __builtin_amdgcn_s_waitcnt(0);
-  if (SPLIT) { // a partial tile for q8_split_reduce (the register budget leaves no room for an in-kernel sum)
+  if (SPLIT) { // a partial tile for split_reduce (the register budget leaves no room for an in-kernel sum)
     v4f *slot = p.sk.partial + (size_t)(tile * p.sk.splits + split) * 16 * C::Threads + threadIdx.x;
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -490,28 +575,6 @@ __global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
-// The split int8 launch's second kernel: one block per tile adds the tile's partials in split order and applies the
-// epilogue, with the thread layout of q8_gemm_lds.
-template <class C> __global__ __launch_bounds__(C::Threads) void q8_split_reduce(Q8Params p) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
-  const int tile = blockIdx.x;
-  const TilePos t = q8_tile_of(p.grid, tile, C::TileM);
-  const TileSeg seg = q8_seg_of(p.grid, t.s);
-  const v4f *part = p.sk.partial + (size_t)tile * p.sk.splits * 16 * C::Threads + threadIdx.x;
-  v4f acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      acc[i][j] = part[(i * 4 + j) * C::Threads];
-  for (int s = 1; s < p.sk.splits; s++)
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        acc[i][j] += part[((size_t)s * 16 + i * 4 + j) * C::Threads];
-  store_tile(seg, t, acc, wm, wn, lane, p.m);
-}
 
 // Round to nearest even on the 16 dropped bits, NaN quieted with its sign and top payload bits, denormals kept,
 // overflow to infinity: the conversion of the reference's bf16_from_f32 (src/gemm.c:335-342), as an integer formula.
@@ -710,6 +773,142 @@ template <bool F32> __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_lds
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
+// ---- BF16, wide tiles ---------------------------------------------------------------------------------------------
+//
+// The BF16 kernel above waits on L2: its operands arrive at about 18 bytes per clock per CU, far below the L1's rate,
+// because the misses a CU keeps in flight bound it (TCP_PENDING_STALL_CYCLES 62% of the time, MFMA pipe 38% busy).
+// This one owns a 256 x 256 tile, which needs a third fewer operand bytes per flop: eight waves in 4 x 2, each
+// 64 x 128 as 4 x 8 MFMA tiles (128 accumulators, which the compiler keeps in AGPRs), four stages of 32 KB. Under
+// SWIGLU the tile holds 128 columns of W1 and the same 128 of W3, a wave's j = 0..3 and 4..7. Short grids split K;
+// the partial tiles are added in split order by split_reduce.
+constexpr int kWStages = 4, kWLoadsPerStep = 4; // per wave: two A and two B blocks
+constexpr int kWTileM = 256, kWTileN = 256;
+constexpr int kWBOff = 16 * kWStages * 1024;                      // 16 A blocks per stage, then 16 B blocks
+constexpr size_t kWLds = (size_t)kWBOff + 16 * kWStages * 1024;  // 128 KB
+constexpr int kWSlotV4 = 32 * kQ8Threads;                         // v4f per partial tile
+
+// The B-tile row (0..255) that a wave's column tile j reads.
+__device__ __forceinline__ int b_row_wide(bool swiglu, int wn, int j) {
+  return swiglu ? (j < 4 ? 64 * wn + 16 * j : 128 + 64 * wn + 16 * (j - 4)) : 128 * wn + 16 * j;
+}
+
+template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void bf16_gemm_wide(MmParams p) {
+  extern __shared__ __align__(16) unsigned char q8_smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int logical = xcd_logical(blockIdx.x, p.grid.total * (SPLIT ? p.sk.splits : 1));
+  const int tile = SPLIT ? __builtin_amdgcn_readfirstlane(logical / p.sk.splits) : logical;
+  const int split = SPLIT ? __builtin_amdgcn_readfirstlane(logical % p.sk.splits) : 0;
+  const TilePos t = q8_tile_of(p.grid, tile, kWTileM, kWTileN);
+  const TileSeg seg = q8_seg_of(p.grid, t.s);
+  const int s0 = SPLIT ? split * p.sk.per : 0, s1 = SPLIT ? min(p.steps, s0 + p.sk.per) : p.steps;
+
+  const int lrow4 = lane >> 2, chunk = lane & 3;
+  const int ra = 32 * wave + lrow4;
+  const __amdgpu_buffer_rsrc_t rA =
+      q8_buffer(p.a + (long long)t.m0 * p.arow, (long long)min(kWTileM, p.m - t.m0) * p.arow);
+  const int offA0 = (int)(ra * p.arow) + ((chunk ^ q8_swizzle(ra)) << 4);
+  const int offA1 = (int)((ra + 16) * p.arow) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
+  // B blocks 2 wave and 2 wave + 1: one VNNI tile of one matrix each (chunks reordered as in mm_gemm_lds)
+  const long long tile_bytes = (long long)p.steps * 1024;
+  auto b_resource = [&](int blk) {
+    const int rb = 16 * blk;
+    const int colB = t.swiglu ? t.n0 + (rb & 127) : t.n0 + rb;
+    const unsigned char *wmat = (const unsigned char *)((t.swiglu && rb >= 128) ? seg.w3 : seg.w);
+    return q8_buffer(wmat + (long long)(colB / 16) * tile_bytes, colB < seg.n ? tile_bytes : 0);
+  };
+  const __amdgpu_buffer_rsrc_t rB0 = b_resource(2 * wave), rB1 = b_resource(2 * wave + 1);
+  const int offB = ((4 * ((lane >> 2) & 3) + (lane >> 4)) << 6) + ((lane & 3) << 4);
+  const __amdgpu_buffer_rsrc_t none = q8_buffer(p.a, 0);
+
+  auto issue = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value;
+    const bool live = step < s1;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, (void *)(q8_smem + ((2 * wave) * kWStages + st) * 1024),
+                                             16, offA0, step * 64, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
+                                             (void *)(q8_smem + ((2 * wave + 1) * kWStages + st) * 1024), 16, offA1,
+                                             step * 64, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB0 : none,
+                                             (void *)(q8_smem + kWBOff + ((2 * wave) * kWStages + st) * 1024), 16,
+                                             offB, step * 1024, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB1 : none,
+                                             (void *)(q8_smem + kWBOff + ((2 * wave + 1) * kWStages + st) * 1024), 16,
+                                             offB, step * 1024, 0, 0);
+  };
+
+  const int lrow = lane & 15, lq = lane >> 4;
+  const unsigned char *abase = q8_smem + (4 * wm) * kWStages * 1024 + lrow * 64 + ((lq ^ q8_swizzle(lrow)) << 4);
+  const unsigned char *bbase = q8_smem + kWBOff + lq * 64 + lrow * 4;
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  struct Operands {
+    v4u a[4], b[8];
+  };
+  auto operands = [&](auto ST, Operands &o) {
+    constexpr int st = decltype(ST)::value;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      o.a[i] = *reinterpret_cast<const v4u *>(abase + (i * kWStages + st) * 1024);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const unsigned char *bp = bbase + ((b_row_wide(t.swiglu, wn, j) / 16) * kWStages + st) * 1024;
+      o.b[j] = v4u{*reinterpret_cast<const unsigned *>(bp), *reinterpret_cast<const unsigned *>(bp + 256),
+                   *reinterpret_cast<const unsigned *>(bp + 512), *reinterpret_cast<const unsigned *>(bp + 768)};
+    }
+  };
+  v4f acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  auto mfmas = [&](const Operands &o) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf_t, o.a[i]),
+                                                            __builtin_bit_cast(v8bf_t, o.b[j]), acc[i][j], 0, 0, 0);
+  };
+
+  Operands cur, next;
+  auto advance = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value, nst = (st + 1) % kWStages, fill = (st + kWStages - 1) % kWStages;
+    wait_vmcnt<(kWStages - 3) * kWLoadsPerStep>(); // step + 1 has landed for this wave
+    __builtin_amdgcn_s_barrier();                 // ... and every wave; the stage of step - 1 is free
+    issue(step + kWStages - 1, std::integral_constant<int, fill>{});
+    operands(std::integral_constant<int, nst>{}, next);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(cur);
+    __builtin_amdgcn_sched_barrier(0);
+    cur = next;
+  };
+
+  issue_first<0, kWStages - 1>(issue, s0);
+  wait_vmcnt<(kWStages - 2) * kWLoadsPerStep>();
+  __builtin_amdgcn_s_barrier();
+  operands(std::integral_constant<int, 0>{}, cur);
+  for (int step = s0; step < s1; step += kWStages) { // whole rounds: steps past the end load zeros
+    advance(step, std::integral_constant<int, 0>{});
+    advance(step + 1, std::integral_constant<int, 1>{});
+    advance(step + 2, std::integral_constant<int, 2>{});
+    advance(step + 3, std::integral_constant<int, 3>{});
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if (SPLIT) {
+    v4f *slot = p.sk.partial + (size_t)(tile * p.sk.splits + split) * kWSlotV4 + threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        slot[(i * 8 + j) * kQ8Threads] = acc[i][j];
+    return;
+  }
+  store_tile_wide(seg, t, acc, wm, wn, lane, p.m);
+}
+
+
 // Any group size (gs % 64 != 0): one thread per output, the per-group int32 dot in plain integer arithmetic.
 __global__ __launch_bounds__(kBlock) void q8_gemm_generic(TileGrid g, const int8_t *xq, const float *xs, int m, int k,
                                                           int gs) {
@@ -837,6 +1036,14 @@ bool launch_ok(const char *what) {
   return raise("launching %s failed: %s", what, hipGetErrorString(e));
 }
 
+template <int J, int THREADS> bool launch_split_reduce(const Q8Grid &grid, const SplitK &sk, int m, int tile_m,
+                                                       int tile_n, hipStream_t stream) {
+  SplitOut o{grid, sk.partial, sk.splits, m, tile_m, tile_n};
+  const long long threads = 4LL * (J / 2) * THREADS * grid.total;
+  hipLaunchKernelGGL((split_reduce<J, THREADS>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, o);
+  return launch_ok("split_reduce");
+}
+
 TileGrid make_grid(const GemmSegmentDev *segs, int nseg, int m) {
   TileGrid g{};
   g.nseg = nseg;
@@ -852,14 +1059,14 @@ TileGrid make_grid(const GemmSegmentDev *segs, int nseg, int m) {
   return g;
 }
 
-Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m, int tile_m = kQ8TileM) {
+Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m, int tile_m = kQ8TileM, int tile_n = kQ8TileN) {
   Q8Grid g{};
   g.nseg = nseg;
   g.mtiles = (m + tile_m - 1) / tile_m;
   int tiles = 0;
   for (int s = 0; s < nseg; s++) {
     const GemmSegmentDev &d = segs[s];
-    const int width = d.epi == EPI_SWIGLU ? kQ8TileN / 2 : kQ8TileN;
+    const int width = d.epi == EPI_SWIGLU ? tile_n / 2 : tile_n;
     g.seg[s] = TileSeg{d.c, d.ldc, d.w, d.w3, d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width};
     tiles += g.seg[s].ntiles * g.mtiles;
   }
@@ -872,14 +1079,14 @@ std::atomic<int> forced_splits{0};
 // Blocks per tile: one when the tiles fill the CUs (one 256 x 128 block per CU fits in LDS), else enough to reach
 // about one block per CU, keeping at least eight K steps per block and within the workspace's partial tiles. A
 // block's steps are a multiple of `unit` (the int8 kernel's steps per scale group).
-int choose_splits(int tiles, int steps, int *per, int unit = 1) {
+int choose_splits(int tiles, int steps, int *per, int unit = 1, int slots = kSplitSlots) {
   int s = forced_splits.load();
   if (s <= 0) {
     const int cus = device().cu_count > 0 ? device().cu_count : 256;
     s = tiles < cus ? cus / tiles : 1;
     s = min(s, steps / 8);
   }
-  s = max(1, min(s, min(kSplitSlots / max(tiles, 1), steps)));
+  s = max(1, min(s, min(slots / max(tiles, 1), steps)));
   *per = ((steps + s - 1) / s + unit - 1) / unit * unit;
   return (steps + *per - 1) / *per; // no empty split
 }
@@ -919,8 +1126,7 @@ template <class C, bool PROBE, bool GS64> bool q8_launch(Q8Params p, const SegLi
                      dim3(C::Threads), C::Lds, stream, p);
   if (!launch_ok("q8_gemm_lds"))
     return false;
-  hipLaunchKernelGGL(q8_split_reduce<C>, dim3((unsigned)p.grid.total), dim3(C::Threads), 0, stream, p);
-  return launch_ok("q8_split_reduce");
+  return launch_split_reduce<4, C::Threads>(p.grid, p.sk, p.m, C::TileM, kQ8TileN, stream);
 }
 
 // Tile shape: 256 x 128 unless LLAMA_HIP_Q8_TILE_M = 128 (read once). On the 8B W1/W3 shape the 128-row tiles with
@@ -1020,6 +1226,50 @@ template <bool F32> bool mm_launch(MmParams p, hipStream_t stream) {
   return launch_ok(F32 ? "mm_gemm_lds<fp32>" : "mm_gemm_lds<bf16>");
 }
 
+// The wide BF16 kernel (256 x 256 tiles); its partial tiles are twice the size, so half as many fit the workspace.
+bool wide_launch(MmParams p, const GemmF32Job &job, hipStream_t stream) {
+  constexpr int kWideSlots = kSplitSlots / 2;
+  p.grid = make_q8_grid(job.seg, job.nseg, job.m, kWTileM, kWTileN);
+  p.sk.splits = p.grid.total > kWideSlots ? 1 : choose_splits(p.grid.total, p.steps, &p.sk.per, 1, kWideSlots);
+  if (p.sk.splits == 1)
+    p.sk.per = p.steps;
+  p.sk.partial = (v4f *)device().split_partial;
+  p.sk.count = device().split_count;
+  static const hipError_t s0 =
+      hipFuncSetAttribute((const void *)bf16_gemm_wide<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWLds);
+  static const hipError_t s1 =
+      hipFuncSetAttribute((const void *)bf16_gemm_wide<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWLds);
+  if (!check_hip(s0, "allowing the BF16 GEMM its LDS") || !check_hip(s1, "allowing the BF16 GEMM its LDS"))
+    return false;
+  if (p.sk.splits == 1) {
+    hipLaunchKernelGGL(bf16_gemm_wide<false>, dim3((unsigned)p.grid.total), dim3(kQ8Threads), kWLds, stream, p);
+    return launch_ok("bf16_gemm_wide");
+  }
+  hipLaunchKernelGGL(bf16_gemm_wide<true>, dim3((unsigned)(p.grid.total * p.sk.splits)), dim3(kQ8Threads), kWLds,
+                     stream, p);
+  if (!launch_ok("bf16_gemm_wide"))
+    return false;
+  return launch_split_reduce<8, kQ8Threads>(p.grid, p.sk, p.m, kWTileM, kWTileN, stream);
+}
+
+// BF16 tile: LLAMA_HIP_BF16_TILE = wide (256 x 256) or narrow (256 x 128), read once; by default wide when the grid
+// has at least four 256 x 128 tiles per CU. Measured: 2048 x 28672 x 4096 SwiGLU 886 TF/s wide, 754 narrow; with fewer
+// tiles the wide grid's quantization and split cost more than its operand savings (2048 x 4096 x 4096: 677 vs 757,
+// the 512-token 3B shapes 10-15% slower).
+std::atomic<int> forced_bf16_tile{0}; // llhip_set_bf16_tile: 0 unset, 1 narrow, 2 wide
+
+bool bf16_wide(int narrow_tiles) {
+  static const int env_tile = [] {
+    const char *env = getenv("LLAMA_HIP_BF16_TILE");
+    return env && !strcmp(env, "wide") ? 2 : env && !strcmp(env, "narrow") ? 1 : 0;
+  }();
+  const int forced = forced_bf16_tile.load() ? forced_bf16_tile.load() : env_tile;
+  if (forced)
+    return forced == 2;
+  const int cus = device().cu_count > 0 ? device().cu_count : 256;
+  return narrow_tiles >= 4 * cus;
+}
+
 bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 // Shapes the pipelined FP32 kernel takes: K a multiple of 16 and 16-byte aligned rows whose 32-bit buffer offsets fit.
@@ -1037,6 +1287,8 @@ bool f32_fast_path(const GemmF32Job &job) {
 } // namespace
 
 void set_gemm_splits(int splits) { forced_splits.store(splits > 0 ? splits : 0); }
+
+void set_bf16_tile(int tile) { forced_bf16_tile.store(tile == 1 || tile == 2 ? tile : 0); }
 
 bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream) {
   if (job.m <= 0 || job.k <= 0)
@@ -1061,7 +1313,7 @@ bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream) {
     p.a = (const unsigned char *)job.panel;
     p.arow = (long long)kp * 2;
     p.steps = kp / 32;
-    return mm_launch<false>(p, stream);
+    return bf16_wide(p.grid.total) ? wide_launch(p, job, stream) : mm_launch<false>(p, stream);
   }
   if (f32_fast_path(job)) {
     p.a = (const unsigned char *)job.a;

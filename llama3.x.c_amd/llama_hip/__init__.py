@@ -197,6 +197,7 @@ _SIGNATURES = {
     "llhip_q8_gemv_group_dots": (None, [P, P, P, P, P, SZ, I32, I32, I32]),
     "llhip_set_gemv_shape": (None, [I32, I32, I32]),
     "llhip_set_gemm_splits": (None, [I32]),
+    "llhip_set_bf16_tile": (None, [I32]),
 }
 
 _lib = None

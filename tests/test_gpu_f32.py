@@ -239,13 +239,16 @@ def test_bf16_gemm_reference_golden():
 # ---- pipelined FP32 / BF16 kernels: aligned shapes, split K --------------------------------------------------------
 
 
-@pytest.mark.parametrize("m,n,k", [(300, 200, 1024), (513, 136, 3072), (40, 130, 16 * 37), (256, 256, 8192)])
-@pytest.mark.parametrize("mode", ["f32", "bf16"])
+@pytest.mark.parametrize("m,n,k", [(300, 200, 1024), (513, 136, 3072), (40, 130, 16 * 37), (256, 256, 8192),
+                                   (600, 600, 512)])
+@pytest.mark.parametrize("mode", ["f32", "bf16", "bf16-wide"])
 def test_pipelined_gemm_split_k(m, n, k, mode):
     """Rows 16-byte aligned and K a multiple of 16 take the pipelined kernel. Every split count (0 = the automatic
     choice) meets the budget for every kind and for three segments sharing A; a repeated call with the same split count
     gives the same bits (the arrival counters are back at zero and partial sums are added in split order)."""
     L = hu.lib()
+    L.llhip_set_bf16_tile(2 if mode == "bf16-wide" else 1)
+    mode = mode[:4]
     rng = orc.Rng(orc.SEED + 81 * m + n + k)
     lda, ldc = k + 4, n + 7
     a = rng.uniform(m * lda, 2.0).reshape(m, lda)
@@ -315,4 +318,5 @@ def test_pipelined_gemm_split_k(m, n, k, mode):
             hu.assert_within_budget(hu.host(o), r[:, :nn], mag[:, :nn], rel=rel, what=f"{mode} segment of {nn}")
     finally:
         L.llhip_set_gemm_splits(0)
+        L.llhip_set_bf16_tile(0)
         L.aligned_buffer_free(panel)
