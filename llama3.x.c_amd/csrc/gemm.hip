@@ -1,10 +1,19 @@
 // Batched-prefill GEMMs for gfx950 on MFMA: W8A8 Q8_0 on int8 MFMA, FP32 on FP32 MFMA, BF16 on BF16 MFMA.
 //
-// All three compute C[m][n] (op)= A[m][k] . W[n][k]^T over up to three segments that share A. A block owns a
-// 128 x 128 output tile (64 columns of W1 plus the same 64 of W3 for SWIGLU), four waves each own 64 x 64 as a 4 x 4
-// grid of 16 x 16 MFMA tiles, and K is staged through double-buffered LDS. MFMA operand loads are symmetric (lane l
-// supplies row l % 16 of A and column l % 16 of W with the same K slice), so the dot products do not depend on how the
-// instruction orders K inside a lane; the 16 x 16 result holds C[4 (l / 16) + e][l % 16] in element e of lane l.
+// All compute C[m][n] (op)= A[m][k] . W[n][k]^T over up to three segments that share A, with the epilogues STORE,
+// ADD and SWIGLU (a column tile then holds columns of W1 and the same columns of W3, so the gate is applied in
+// registers). The kernels, each described where it is defined:
+//   q8_gemm_lds     int8, 256 x 128 tiles (or 128 x 128), A/B/scales streamed into LDS five stages deep;
+//   mm_gemm_lds     FP32 and BF16, 256 x 128 tiles, the same pipeline;
+//   bf16_gemm_wide  BF16, 256 x 256 tiles for large grids;
+//   split_reduce    the second kernel of a split-K launch of the int8 and wide kernels;
+//   f32_gemm_mfma   FP32 shapes the pipeline does not take (K % 16 != 0, unaligned rows): 128 x 128 tiles staged
+//                   through registers into double-buffered LDS;
+//   q8_gemm_generic int8 with a group size that is not a multiple of 64.
+// Each wave owns 64 x 64 (64 x 128 in the wide kernel) as a grid of 16 x 16 MFMA tiles. MFMA operand loads are
+// symmetric (lane l supplies row l % 16 of A and column l % 16 of W with the same K slice), so the dot products do not
+// depend on how the instruction orders K inside a lane; the 16 x 16 result holds C[4 (l / 16) + e][l % 16] in element
+// e of lane l.
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
@@ -17,7 +26,7 @@ namespace llhip {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kTile = 128; // block tile rows and columns
+constexpr int kTile = 128; // block tile rows and columns of f32_gemm_mfma
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -256,10 +265,11 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
-// Split K (the GEMM kernels here): a grid with fewer tiles than CUs runs each tile as `splits` blocks over consecutive K
-// ranges. Each block writes its partial tile to a device workspace and counts itself in at the tile's counter; the
-// last to arrive adds the partials in split order (the same order whichever block is last, so results do not depend
-// on timing), puts the counter back to zero and applies the epilogue.
+// Split K: a grid with fewer tiles than CUs runs each tile as `splits` blocks over consecutive K ranges, each writing
+// its partial tile to a device workspace. The partials are added in split order, so results do not depend on timing:
+// by split_reduce, a second kernel (int8 and wide BF16 kernels, which have no registers to spare), or by the last of
+// the tile's blocks to arrive (split_combine, the FP32 / BF16 kernel), which counts the arrivals and puts the counter
+// back to zero.
 
 // Cache policy of the partial tiles' stores and loads: device-coherent (sc1), so a store is written through past the
 // XCD's L2 before its completion is counted, and a load reads from past it. No cache-wide write-back or invalidate is
@@ -601,7 +611,8 @@ __device__ __forceinline__ unsigned short to_bf16(float x) {
 //         feeds value s to the s-th instruction. W rows are read like A rows (row pitch ldw).
 // The FP32 sums stay in the MFMA accumulators: no per-step vector work.
 //
-// Short grids split K as the int8 kernel does.
+// Short grids split K; this kernel's register budget leaves room to add the partial tiles in the last block to
+// arrive (split_combine) instead of a second kernel.
 __global__ __launch_bounds__(256) void bf16_panel(const float *__restrict__ a, long long lda, int m, int k, int kp,
                                                   unsigned short *__restrict__ panel) {
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x; // 8 values per thread
