@@ -781,7 +781,8 @@ struct GemvShape {
 
 // Measured on MI355X over the 8B shapes (the 16-wave block stages the input once for twice the waves):
 //   - rows of K <= 8192 take two waves each (at most four 1024-byte chunks per wave), longer rows four (W2's 14336);
-//   - the SwiGLU pair (twice the registers per row) streams best from three 8-wave blocks per CU;
+//   - the SwiGLU pair (twice the registers per row) streams best from two 8-wave blocks per CU (21.9 us against
+//     22.6 with three, 14336 x 4096 twice, in the 8B decode step);
 //   - a long matrix (the 128256-row classifier) from one wave per row and four block equivalents per CU;
 //   - everything else from one 16-wave block per CU.
 // llhip_set_gemv_shape and LLAMA_HIP_GEMV_KSPLIT / _BLOCKS_PER_CU / _BLOCK_WAVES override each part.
@@ -791,7 +792,7 @@ static GemvShape gemv_shape(int total_rows, int nchunks, bool swiglu) {
   static const int env_waves = env_shape("LLAMA_HIP_GEMV_BLOCK_WAVES", 8, 16);
   GemvShape g{nchunks <= 8 ? 2 : 4, 2, 16};
   if (swiglu) {
-    g.per_cu = 3;
+    g.per_cu = 2;
     g.waves = 8;
   } else if (total_rows >= 32768) {
     g.split = nchunks <= 4 ? 1 : g.split;
