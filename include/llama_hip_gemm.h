@@ -170,14 +170,18 @@ PackS8 pack_s8_job_from_shard(int8_t *dst, const Shard *shard);
 
 /* testing.h:27, 61-69 analogues. k_gemm_f32_portable runs the device FP32 GEMM (kc is ignored: no K blocking);
  * k_gemm_f32_simd_test returns 0 (no CPU SIMD kernel here); k_gemv_force_hybrid is accepted (one device schedule).
- * k_gemm_q8_backend_test runs one named backend (Q8_GEMM_HIP_MFMA or Q8_GEMM_PORTABLE; returns 0 for the CPU ones). llhip_q8_group_dots is the int32 probe: the exact group dots the MFMA kernel forms,
- * dots[(g * m + r) * n + c], from row-major xq (m x k) and wq (n x k). */
+ * k_gemm_q8_backend_test runs one named backend (Q8_GEMM_HIP_MFMA or Q8_GEMM_PORTABLE; returns 0 for the CPU ones).
+ * llhip_q8_group_dots is the int32 probe: the exact group dots the MFMA kernel forms, dots[(g * m + r) * n + c], from
+ * row-major xq (m x k) and wq (n x k). k_gemm_q8_amx_dots_test (testing.h:69) returns the same dots from weights in
+ * the pack_s8_vnni layout, as the reference's AMX probe does: 1 when it ran, 0 for shapes the MFMA probe does not take
+ * (gs % 64 != 0 or k % gs != 0), as a build without AMX returns 0. */
 void k_gemm_f32_portable(const float *a, int lda, int m, int k, const GemmSegment *segments, int count, int kc);
 int k_gemm_f32_simd_test(const float *a, int lda, int m, int k, const GemmSegment *segments, int count, int kc);
 void k_gemv_force_hybrid(int on);
 int k_gemm_q8_backend_test(Q8GemmBackend backend, const int8_t *xq, const float *xs, int m, int k, int gs,
                            const GemmQ8Segment *segments, int count);
 void llhip_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs, const int8_t *wq, int n);
+int k_gemm_q8_amx_dots_test(int32_t *dots, const int8_t *xq, int m, int k, int gs, const int8_t *packed, int n);
 
 #ifdef __cplusplus
 }

@@ -505,6 +505,39 @@ void llhip_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs, 
     call.finish();
 }
 
+// testing.h:69: the reference's AMX probe reads the weights in the pack_s8_vnni layout (K padded to 64); here they are
+// unpacked on the device and the MFMA kernel's probe forms the dots.
+int k_gemm_q8_amx_dots_test(int32_t *dots, const int8_t *xq, int m, int k, int gs, const int8_t *packed, int n) {
+  if (gs <= 0 || gs % 64 || k <= 0 || k % gs)
+    return 0;
+  if (m <= 0 || n <= 0)
+    return 1;
+  Call call("k_gemm_q8_amx_dots_test");
+  Ref XQ = call.in(xq, (size_t)m * k), PK = call.in(packed, s8_vnni_bytes(n, k));
+  Ref D = call.out(dots, (size_t)(k / gs) * m * n * sizeof(int32_t), false);
+  if (!call.ready())
+    return 0;
+  if (!q8_gemm_fast_path(call.ptr<const int8_t>(XQ), m, k, gs)) {
+    raise("k_gemm_q8_amx_dots_test: the shape (m %d, K %d) is outside the MFMA kernel's range", m, k);
+    return 0;
+  }
+  if ((uintptr_t)call.ptr<const int8_t>(PK) & 3) {
+    raise("k_gemm_q8_amx_dots_test: the packed weights must be 4-byte aligned");
+    return 0;
+  }
+  int8_t *wq = nullptr;
+  if (!LLHIP_CHECK(hipMallocAsync((void **)&wq, (size_t)n * k, call.stream())))
+    return 0;
+  const bool ok = launch_s8_vnni_unpack(wq, call.ptr<const int8_t>(PK), n, k, call.stream()) &&
+                  launch_q8_group_dots(call.ptr<int32_t>(D), call.ptr<const int8_t>(XQ), m, k, gs, wq, n,
+                                       call.stream());
+  (void)hipFreeAsync(wq, call.stream());
+  if (!ok)
+    return 0;
+  call.finish();
+  return 1;
+}
+
 void llhip_set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves) {
   // the next launches use it: launch any recorded quantization under the shape it was recorded with
   if (ensure_device() && flush_pending_quantize())

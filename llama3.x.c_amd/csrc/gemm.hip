@@ -1191,6 +1191,29 @@ bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream) {
   return launch_ok("q8_gemm_generic");
 }
 
+namespace {
+// The pack_s8_vnni layout (16-row tiles, K in quads: byte ((t * quads + q) * 16 + c) * 4 + e holds row 16 t + c,
+// column 4 q + e) back to row-major n x k; one thread per quad of one row.
+__global__ __launch_bounds__(kBlock) void s8_vnni_unpack(int8_t *__restrict__ w, const int8_t *__restrict__ packed,
+                                                         int n, int k) {
+  const long long idx = (long long)blockIdx.x * kBlock + threadIdx.x;
+  const int quads = k / 4;
+  if (idx >= (long long)n * quads)
+    return;
+  const int row = (int)(idx / quads), q = (int)(idx % quads);
+  const int t = row / 16, c = row % 16;
+  *reinterpret_cast<int *>(w + (long long)row * k + 4 * q) =
+      *reinterpret_cast<const int *>(packed + (((long long)t * quads + q) * 16 + c) * 4);
+}
+} // namespace
+
+bool launch_s8_vnni_unpack(int8_t *w, const int8_t *packed, int n, int k, hipStream_t stream) {
+  const long long threads = (long long)n * (k / 4);
+  hipLaunchKernelGGL(s8_vnni_unpack, dim3((unsigned)((threads + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream, w,
+                     packed, n, k);
+  return launch_ok("s8_vnni_unpack");
+}
+
 bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs, const int8_t *wq, int n,
                           hipStream_t stream) {
   if (m <= 0 || n <= 0 || k <= 0)

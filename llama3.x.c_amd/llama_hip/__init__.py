@@ -166,6 +166,7 @@ _SIGNATURES = {
     "k_gemm_q8_pick": (I32, [I32, ctypes.POINTER(GemmQ8Segment), I32]),
     "k_gemm_q8_backend_test": (I32, [I32, P, P, I32, I32, I32, ctypes.POINTER(GemmQ8Segment), I32]),
     "llhip_q8_group_dots": (None, [P, P, I32, I32, I32, P, I32]),
+    "k_gemm_q8_amx_dots_test": (I32, [P, P, I32, I32, I32, P, I32]),
     # prefill.h surface
     "prefill_precision": (I32, [I32]),
     "prefill_configure": (None, [ctypes.POINTER(Model), I32]),

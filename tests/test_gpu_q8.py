@@ -405,6 +405,20 @@ def test_gemm_q8_int32_probe_bitwise(m, n, k, gs):
     assert np.array_equal(dots, orc.group_dots(xq, wq, gs))
 
 
+@pytest.mark.parametrize("m,n,k,gs", [(33, 20, 128, 64), (70, 130, 1024, 128), (5, 17, 256, 256)])
+def test_amx_dots_probe_from_packed_weights(m, n, k, gs):
+    """testing.h:69 k_gemm_q8_amx_dots_test: the exact int32 group dots from weights in the pack_s8_vnni layout
+    (unpacked on the device, then the MFMA probe); 0 for a group size the MFMA probe does not take."""
+    L = hu.lib()
+    xq, _, wq, _, _, _, _ = gemm_case(m, n, k, gs, 1111 + m)
+    packed = np.zeros(L.s8_vnni_bytes(n, k), np.int8)
+    L.pack_s8_vnni(lh.ptr(packed), lh.ptr(wq), n, k, k)
+    dots = np.zeros((k // gs, m, n), np.int32)
+    assert L.k_gemm_q8_amx_dots_test(lh.ptr(dots), lh.ptr(xq), m, k, gs, lh.ptr(packed), n) == 1, lh.last_error()
+    assert np.array_equal(dots, orc.group_dots(xq, wq, gs))
+    assert L.k_gemm_q8_amx_dots_test(lh.ptr(dots), lh.ptr(xq), m, k, 32, lh.ptr(packed), n) == 0
+
+
 def test_gemm_q8_reference_golden_and_backends():
     """The reference's golden portable-GEMM cases: the MFMA backend (gs % 64 == 0) and the generic one, each within
     budget of the reference's outputs; the probe equals the reference's AMX int32 dots where the fixture has them."""
