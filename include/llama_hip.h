@@ -83,7 +83,8 @@ void llhip_set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves)
 /* Blocks per output tile of the prefill GEMMs, FP32, BF16 and INT8 (split K; 0 = chosen from the grid: about one
  * block per CU when the tiles are fewer than the CUs, at least eight K steps per block, at most 512 blocks; INT8
  * splits keep whole scale groups). Partial sums are added in split order, so results depend on it only through FP32
- * summation order, never on timing; INT8 group dots are exact either way. For tuning and tests. */
+ * summation order, never on timing; INT8 group dots are exact either way. A forced count also sends INT8 calls of at
+ * most 32 rows to the tiled kernel instead of the weight-streaming one. For tuning and tests. */
 void llhip_set_gemm_splits(int splits);
 
 /* Output tile of the BF16 prefill GEMM: 1 = 256 x 128, 2 = 256 x 256, 0 = by grid (256 x 256 when the grid has at

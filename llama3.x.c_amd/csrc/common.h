@@ -172,6 +172,8 @@ struct GemmQ8Job {
 };
 bool q8_gemm_fast_path(const int8_t *xq, int m, int k, int gs); // the pipelined int8-MFMA kernel takes the shape
 bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream);
+bool q8_gemm_skinny_path(const int8_t *xq, int m, int k, int gs); // at most 32 rows: stream the weights once
+bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream);
 bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream);
 bool launch_s8_vnni_unpack(int8_t *w, const int8_t *packed, int n, int k, hipStream_t stream); // k % 64 == 0
 bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs, const int8_t *wq, int n,

@@ -177,7 +177,6 @@ __device__ __forceinline__ void store_tile_wide(const TileSeg &seg, const TilePo
 // accumulates onto the results instead.
 constexpr int kQ8Waves = 8, kQ8Threads = 64 * kQ8Waves;
 constexpr int kQ8TileM = 256, kQ8TileN = 128, kQ8Stages = 5;
-constexpr int kQ8LoadsPerStep = 4;                                   // per wave: two A, one B, one scale load
 constexpr int kQ8ABlocks = kQ8TileM / 16, kQ8BBlocks = kQ8TileN / 16; // 1 KB blocks per stage
 constexpr int kQ8BOff = kQ8ABlocks * kQ8Stages * 1024;               // B blocks after the A blocks
 constexpr int kQ8SOff = kQ8BOff + kQ8BBlocks * kQ8Stages * 1024;     // then the scales, a group per stage
@@ -1168,6 +1167,8 @@ bool q8_gemm_fast_path(const int8_t *xq, int m, int k, int gs) {
 bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream) {
   if (job.m <= 0 || job.k <= 0)
     return true;
+  if (q8_gemm_skinny_path(job.xq, job.m, job.k, job.gs) && !forced_splits.load())
+    return launch_q8_gemm_skinny(job, stream);
   Q8Params p{};
   p.xq = job.xq;
   p.xs = job.xs;

@@ -1,0 +1,235 @@
+// The int8 GEMM for short batches: k_gemm_q8 with at most 32 activation rows (a prompt of a few tokens, or a batch of
+// decode steps that share one pass over the weights).
+//
+// The tiled kernel (gemm.hip) computes 256 activation rows per tile whatever m is, so below a few dozen rows its time
+// is that of m = 256, about three times the time to stream the weights. Here the weights are streamed once, as in the
+// decode GEMV: a block owns 16 weight rows (16 output columns, and the same 16 of W3 under SWIGLU) and its eight waves
+// split K into consecutive ranges. Per 64-value K step a wave loads its 1 KB of weights (16 bytes per lane) straight
+// into the B operand of v_mfma_i32_16x16x64_i8 and the activations (16 rows per MFMA tile, MT = 1 or 2 tiles) into
+// the A operand, four steps ahead. At a group's last step the exact int32 dots are rescaled,
+// acc += ((float)dot * ws) * xs, from scales staged in LDS. The eight partial sums of an output meet in LDS and are
+// added in wave order; the epilogue (STORE, ADD, SWIGLU) follows.
+#include <atomic>
+
+#include "common.h"
+
+namespace llhip {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kSkWaves = 8, kSkThreads = 64 * kSkWaves;
+constexpr int kSkDepth = 4; // K steps in flight per wave
+
+struct SkSeg {
+  float *c;
+  int ldc;
+  const int8_t *w, *w3;
+  const float *ws, *w3s;
+  int n, epi;
+  int first_tile;
+};
+
+struct SkParams {
+  SkSeg seg[3];
+  int nseg;
+  const int8_t *xq;
+  const float *xs;
+  int m, k, gs, groups, steps, per; // per: K steps of each wave (a multiple of the steps per group)
+};
+
+__device__ __forceinline__ SkSeg sk_pick(const SkParams &p, int s) { return s == 0 ? p.seg[0] : s == 1 ? p.seg[1] : p.seg[2]; }
+
+// A raw buffer resource from wave-uniform values (readfirstlane keeps it in scalar registers); loads past `bytes` read
+// zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_buffer(const void *base, long long bytes) {
+  const unsigned long long b = (unsigned long long)(uintptr_t)base;
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)b);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(b >> 32));
+  const int n = __builtin_amdgcn_readfirstlane((int)(bytes > 0 ? bytes : 0));
+  return __builtin_amdgcn_make_buffer_rsrc((void *)(uintptr_t)(((unsigned long long)hi << 32) | lo), (short)0, n,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ float sk_silu_gate(float value, float gate) {
+  value *= (1.0f / (1.0f + expf(-value)));
+  return value * gate;
+}
+
+constexpr int kStream = 2; // cache policy nt for the weights, read once
+
+template <int MT> __global__ __launch_bounds__(kSkThreads) void q8_gemm_skinny(SkParams p) {
+  extern __shared__ __align__(16) float sk_smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = blockIdx.x;
+  int s = 0;
+  while (s + 1 < p.nseg && tile >= p.seg[s + 1].first_tile)
+    s++;
+  const SkSeg seg = sk_pick(p, s);
+  const bool swiglu = seg.epi == EPI_SWIGLU;
+  const int col0 = (tile - seg.first_tile) * 16;
+  const int G = p.groups, spg = p.gs / 64;
+
+  // scales of the block's 16 weight rows (and their W3 rows) and of the activation rows, all groups
+  float *sws = sk_smem, *sw3s = sws + 16 * G, *sxs = sw3s + 16 * G;
+  for (int i = tid; i < 16 * G; i += kSkThreads) {
+    const int r = i / G, g = i % G, col = col0 + r;
+    sws[i] = col < seg.n ? seg.ws[(long long)col * G + g] : 0.0f;
+    sw3s[i] = swiglu && col < seg.n ? seg.w3s[(long long)col * G + g] : 0.0f;
+  }
+  for (int i = tid; i < 16 * MT * G; i += kSkThreads) {
+    const int r = i / G, g = i % G;
+    sxs[i] = r < p.m ? p.xs[(long long)r * G + g] : 0.0f;
+  }
+
+  // this wave's K steps [s0, s1); steps past s1 load zeros
+  const int s0 = wave * p.per, s1 = min(p.steps, s0 + p.per);
+  const long long k = p.k;
+  const long long wrows = (long long)min(16, seg.n - col0);
+  const __amdgpu_buffer_rsrc_t rB = sk_buffer(seg.w + (long long)col0 * k, wrows * k);
+  const __amdgpu_buffer_rsrc_t rB3 = sk_buffer(swiglu ? seg.w3 + (long long)col0 * k : seg.w, swiglu ? wrows * k : 0);
+  const __amdgpu_buffer_rsrc_t rA = sk_buffer(p.xq, (long long)p.m * k);
+  const __amdgpu_buffer_rsrc_t none = sk_buffer(p.xq, 0);
+  const int off = (int)((lane & 15) * k) + (lane >> 4) * 16; // MFMA operand: row lane % 16, K bytes 16 (lane / 16) ..
+
+  v4i b[kSkDepth], b3[kSkDepth], a[kSkDepth][MT];
+  auto issue = [&](int step, int slot_unused, v4i &bb, v4i &bb3, v4i (&aa)[MT]) {
+    const bool live = step < s1;
+    const int k0 = step * 64;
+    bb = __builtin_amdgcn_raw_buffer_load_b128(live ? rB : none, off, k0, kStream);
+    bb3 = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3 : none, off, k0, kStream);
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+      aa[t] = __builtin_amdgcn_raw_buffer_load_b128(live ? rA : none, off + (int)(16 * t * k), k0, 0);
+    (void)slot_unused;
+  };
+#pragma unroll
+  for (int d = 0; d < kSkDepth; d++)
+    issue(s0 + d, d, b[d], b3[d], a[d]);
+  __syncthreads(); // the scales are staged
+
+  v4f acc[MT], acc3[MT];
+  v4i dot[MT], dot3[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++) {
+    acc[t] = acc3[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    dot[t] = dot3[t] = v4i{0, 0, 0, 0};
+  }
+  const int lr = (lane >> 4) * 4, lc = lane & 15;
+  // whole rounds of kSkDepth steps (the ring's slots are constants); steps past s1 add zero dots
+  for (int step = s0; step < s1; step += kSkDepth) {
+#pragma unroll
+    for (int d = 0; d < kSkDepth; d++) {
+      const int st = step + d;
+      const bool first = st % spg == 0, last = st % spg == spg - 1;
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        dot[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][t], b[d], first ? v4i{0, 0, 0, 0} : dot[t], 0, 0, 0);
+        if (swiglu)
+          dot3[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][t], b3[d], first ? v4i{0, 0, 0, 0} : dot3[t], 0, 0, 0);
+      }
+      issue(st + kSkDepth, d, b[d], b3[d], a[d]);
+      if (last) {
+        const int g = min(st / spg, G - 1); // past the end the dots are zero; any group's scales will do
+        const float wsc = sws[lc * G + g], w3sc = sw3s[lc * G + g];
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float xsc = sxs[(16 * t + lr + e) * G + g];
+            acc[t][e] = fmaf((float)dot[t][e] * wsc, xsc, acc[t][e]);
+            if (swiglu)
+              acc3[t][e] = fmaf((float)dot3[t][e] * w3sc, xsc, acc3[t][e]);
+          }
+      }
+    }
+  }
+
+  // the eight waves' partial sums, added in wave order
+  float *red = sxs + 16 * MT * G; // [wave][t][e][lane], then the same for W3
+  const int red3 = kSkWaves * MT * 4 * 64;
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      red[((wave * MT + t) * 4 + e) * 64 + lane] = acc[t][e];
+      if (swiglu)
+        red[red3 + ((wave * MT + t) * 4 + e) * 64 + lane] = acc3[t][e];
+    }
+  __syncthreads();
+  if (wave >= MT * 4)
+    return;
+  // wave w finishes activation tile t = w / 4, element e = w % 4 of every lane
+  const int t = wave / 4, e = wave % 4;
+  float total = 0.0f, gate = 0.0f;
+  for (int w = 0; w < kSkWaves; w++) {
+    total += red[((w * MT + t) * 4 + e) * 64 + lane];
+    if (swiglu)
+      gate += red[red3 + ((w * MT + t) * 4 + e) * 64 + lane];
+  }
+  const int row = 16 * t + lr + e, col = col0 + lc;
+  if (row >= p.m || col >= seg.n)
+    return;
+  float *o = seg.c + (long long)row * seg.ldc + col;
+  if (swiglu)
+    *o = sk_silu_gate(total, gate);
+  else if (seg.epi == EPI_ADD)
+    *o += total;
+  else
+    *o = total;
+}
+
+size_t skinny_lds(int mt, int groups) {
+  return ((size_t)(32 + 16 * mt) * groups + 2 * (size_t)kSkWaves * mt * 4 * 64) * sizeof(float);
+}
+
+} // namespace
+
+// Shapes the skinny kernel takes: at most 32 rows, gs a multiple of 64, 16-byte aligned rows, scales that fit LDS.
+bool q8_gemm_skinny_path(const int8_t *xq, int m, int k, int gs) {
+  return m > 0 && m <= 32 && gs > 0 && gs % 64 == 0 && k % gs == 0 && ((uintptr_t)xq & 15) == 0 &&
+         32LL * k < (1LL << 31) && skinny_lds(m > 16 ? 2 : 1, k / gs) <= 160 * 1024;
+}
+
+bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream) {
+  SkParams p{};
+  int tiles = 0;
+  for (int s = 0; s < job.nseg; s++) {
+    const GemmSegmentDev &d = job.seg[s];
+    p.seg[s] = SkSeg{d.c, d.ldc, (const int8_t *)d.w, (const int8_t *)d.w3, d.ws, d.w3s, d.n, d.epi, tiles};
+    tiles += (d.n + 15) / 16;
+  }
+  if (tiles <= 0)
+    return true;
+  p.nseg = job.nseg;
+  p.xq = job.xq;
+  p.xs = job.xs;
+  p.m = job.m;
+  p.k = job.k;
+  p.gs = job.gs;
+  p.groups = job.k / job.gs;
+  p.steps = job.k / 64;
+  const int spg = job.gs / 64;
+  p.per = ((p.steps + kSkWaves - 1) / kSkWaves + spg - 1) / spg * spg;
+  const int mt = job.m > 16 ? 2 : 1;
+  const size_t lds = skinny_lds(mt, p.groups);
+  if (mt == 1) {
+    static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<1>,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
+      return false;
+    hipLaunchKernelGGL(q8_gemm_skinny<1>, dim3((unsigned)tiles), dim3(kSkThreads), lds, stream, p);
+  } else {
+    static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<2>,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
+      return false;
+    hipLaunchKernelGGL(q8_gemm_skinny<2>, dim3((unsigned)tiles), dim3(kSkThreads), lds, stream, p);
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess || raise("launching q8_gemm_skinny failed: %s", hipGetErrorString(e));
+}
+
+} // namespace llhip

@@ -327,6 +327,59 @@ def test_gemm_q8_all_kinds_within_budget(m, n, k, gs):
     del T
 
 
+@pytest.mark.parametrize("m", [1, 2, 7, 16, 17, 32])
+@pytest.mark.parametrize("n,k,gs", [(300, 4096, 64), (136, 14336, 256), (70, 2048, 128)])
+def test_gemm_q8_short_batches(m, n, k, gs):
+    """At most 32 rows take the skinny kernel (weights streamed once, K split over a block's waves): every kind and a
+    three-segment QKV call within the budget, and each output equal to the tiled kernel's within the budget (a forced
+    split count selects the tiled kernel)."""
+    L = hu.lib()
+    xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 1212 + m + n)
+    ldc = n + 3
+    base = rng.uniform(m * ldc, 3.0).reshape(m, ldc)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    r3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
+    dx = [hu.dev(a) for a in (xq, xs, wq, ws, w3q, w3s)]
+
+    def run(kind, splits):
+        L.llhip_set_gemm_splits(splits)
+        c = hu.dev(base)
+        seg = lh.GemmQ8Segment(lh.ptr(c), ldc, lh.w8(dx[2], dx[3]), lh.w8(dx[4], dx[5]), None, None, n, kind)
+        L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+        got = hu.host(c)
+        assert lh.last_error() == "", lh.last_error()
+        assert np.array_equal(hu.bits(got[:, n:]), hu.bits(base[:, n:])), "row padding was written"
+        return got[:, :n]
+
+    try:
+        for kind in (lh.GEMM_STORE, lh.GEMM_ADD, lh.GEMM_SWIGLU):
+            got, tiled = run(kind, 0), run(kind, 1)
+            what = f"skinny m {m} {n}x{k} gs {gs} kind {kind}"
+            if kind == lh.GEMM_ADD:
+                hu.assert_within_budget(got, base[:, :n] + ref, mag + np.abs(base[:, :n]), what=what)
+                hu.assert_within_budget(got, tiled, 2 * (mag + np.abs(base[:, :n])), what=what + " vs tiled")
+            elif kind == lh.GEMM_SWIGLU:
+                want = ref / (1 + np.exp(-ref)) * r3
+                tol = 2e-5 * (mag * (np.abs(r3) + 1) + mag3 * (np.abs(ref) + 1)) + 1e-6
+                assert np.all(np.abs(got - want) <= tol), what
+                assert np.all(np.abs(got - tiled) <= 2 * tol), what + " vs tiled"
+            else:
+                hu.assert_within_budget(got, ref, mag, what=what)
+                hu.assert_within_budget(got, tiled, 2 * mag, what=what + " vs tiled")
+        # three segments sharing the activations
+        L.llhip_set_gemm_splits(0)
+        widths = (n, max(16, n // 4), max(16, n // 4))
+        outs = [hu.dev(np.zeros((m, nn), np.float32)) for nn in widths]
+        mats = [(hu.dev(wq[:nn]), hu.dev(ws[:nn])) for nn in widths]  # kept alive across the call
+        segs = (lh.GemmQ8Segment * 3)(*[lh.GemmQ8Segment(lh.ptr(o), nn, lh.w8(*w), lh.K8Weight(), None, None, nn,
+                                                         lh.GEMM_STORE) for o, w, nn in zip(outs, mats, widths)])
+        L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, segs, 3)
+        for o, nn in zip(outs, widths):
+            hu.assert_within_budget(hu.host(o), ref[:, :nn], mag[:, :nn], what=f"skinny segment of {nn}")
+    finally:
+        L.llhip_set_gemm_splits(0)
+
+
 @pytest.mark.parametrize("m,n,k,gs", [(5, 300, 4096, 64), (40, 136, 14336, 256), (257, 70, 2048, 128)])
 def test_gemm_q8_split_k(m, n, k, gs):
     """Grids of few tiles split K over several blocks per tile (partials added in split order by a second kernel).
