@@ -3,11 +3,11 @@
 //
 // The tiled kernel (gemm.hip) computes 256 activation rows per tile whatever m is, so below a few dozen rows its time
 // is that of m = 256, about three times the time to stream the weights. Here the weights are streamed once, as in the
-// decode GEMV: a block owns 16 weight rows (16 output columns, and the same 16 of W3 under SWIGLU) and its eight waves
-// split K into consecutive ranges. Per 64-value K step a wave loads its 1 KB of weights (16 bytes per lane) straight
-// into the B operand of v_mfma_i32_16x16x64_i8 and the activations (16 rows per MFMA tile, MT = 1 or 2 tiles) into
-// the A operand, four steps ahead. At a group's last step the exact int32 dots are rescaled,
-// acc += ((float)dot * ws) * xs, from scales staged in LDS. The eight partial sums of an output meet in LDS and are
+// decode GEMV: a block owns 16 weight rows (16 output columns, and the same 16 of W3 under SWIGLU) and its waves (four
+// or eight) split K into consecutive ranges. Per 64-value K step a wave loads its 1 KB of weights (16 bytes per lane)
+// straight into the B operand of v_mfma_i32_16x16x64_i8 and the activations (16 rows per MFMA tile, MT = 1 or 2
+// tiles) into the A operand, four steps ahead. At a group's last step the exact int32 dots are rescaled,
+// acc += ((float)dot * ws) * xs, from scales staged in LDS. The waves' partial sums of an output meet in LDS and are
 // added in wave order; the epilogue (STORE, ADD, SWIGLU) follows.
 #include <atomic>
 
@@ -19,7 +19,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kSkWaves = 8, kSkThreads = 64 * kSkWaves;
 constexpr int kSkDepth = 4; // K steps in flight per wave
 
 struct SkSeg {
@@ -59,7 +58,7 @@ __device__ __forceinline__ float sk_silu_gate(float value, float gate) {
 
 constexpr int kStream = 2; // cache policy nt for the weights, read once
 
-template <int MT> __global__ __launch_bounds__(kSkThreads) void q8_gemm_skinny(SkParams p) {
+template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_gemm_skinny(SkParams p) {
   extern __shared__ __align__(16) float sk_smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -74,12 +73,12 @@ template <int MT> __global__ __launch_bounds__(kSkThreads) void q8_gemm_skinny(S
 
   // scales of the block's 16 weight rows (and their W3 rows) and of the activation rows, all groups
   float *sws = sk_smem, *sw3s = sws + 16 * G, *sxs = sw3s + 16 * G;
-  for (int i = tid; i < 16 * G; i += kSkThreads) {
+  for (int i = tid; i < 16 * G; i += 64 * WAVES) {
     const int r = i / G, g = i % G, col = col0 + r;
     sws[i] = col < seg.n ? seg.ws[(long long)col * G + g] : 0.0f;
     sw3s[i] = swiglu && col < seg.n ? seg.w3s[(long long)col * G + g] : 0.0f;
   }
-  for (int i = tid; i < 16 * MT * G; i += kSkThreads) {
+  for (int i = tid; i < 16 * MT * G; i += 64 * WAVES) {
     const int r = i / G, g = i % G;
     sxs[i] = r < p.m ? p.xs[(long long)r * G + g] : 0.0f;
   }
@@ -95,7 +94,7 @@ template <int MT> __global__ __launch_bounds__(kSkThreads) void q8_gemm_skinny(S
   const int off = (int)((lane & 15) * k) + (lane >> 4) * 16; // MFMA operand: row lane % 16, K bytes 16 (lane / 16) ..
 
   v4i b[kSkDepth], b3[kSkDepth], a[kSkDepth][MT];
-  auto issue = [&](int step, int slot_unused, v4i &bb, v4i &bb3, v4i (&aa)[MT]) {
+  auto issue = [&](int step, v4i &bb, v4i &bb3, v4i (&aa)[MT]) {
     const bool live = step < s1;
     const int k0 = step * 64;
     bb = __builtin_amdgcn_raw_buffer_load_b128(live ? rB : none, off, k0, kStream);
@@ -103,11 +102,10 @@ template <int MT> __global__ __launch_bounds__(kSkThreads) void q8_gemm_skinny(S
 #pragma unroll
     for (int t = 0; t < MT; t++)
       aa[t] = __builtin_amdgcn_raw_buffer_load_b128(live ? rA : none, off + (int)(16 * t * k), k0, 0);
-    (void)slot_unused;
   };
 #pragma unroll
   for (int d = 0; d < kSkDepth; d++)
-    issue(s0 + d, d, b[d], b3[d], a[d]);
+    issue(s0 + d, b[d], b3[d], a[d]);
   __syncthreads(); // the scales are staged
 
   v4f acc[MT], acc3[MT];
@@ -130,7 +128,7 @@ template <int MT> __global__ __launch_bounds__(kSkThreads) void q8_gemm_skinny(S
         if (swiglu)
           dot3[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][t], b3[d], first ? v4i{0, 0, 0, 0} : dot3[t], 0, 0, 0);
       }
-      issue(st + kSkDepth, d, b[d], b3[d], a[d]);
+      issue(st + kSkDepth, b[d], b3[d], a[d]);
       if (last) {
         const int g = min(st / spg, G - 1); // past the end the dots are zero; any group's scales will do
         const float wsc = sws[lc * G + g], w3sc = sw3s[lc * G + g];
@@ -147,9 +145,9 @@ template <int MT> __global__ __launch_bounds__(kSkThreads) void q8_gemm_skinny(S
     }
   }
 
-  // the eight waves' partial sums, added in wave order
+  // the waves' partial sums, added in wave order
   float *red = sxs + 16 * MT * G; // [wave][t][e][lane], then the same for W3
-  const int red3 = kSkWaves * MT * 4 * 64;
+  const int red3 = WAVES * MT * 4 * 64;
 #pragma unroll
   for (int t = 0; t < MT; t++)
 #pragma unroll
@@ -159,30 +157,41 @@ template <int MT> __global__ __launch_bounds__(kSkThreads) void q8_gemm_skinny(S
         red[red3 + ((wave * MT + t) * 4 + e) * 64 + lane] = acc3[t][e];
     }
   __syncthreads();
-  if (wave >= MT * 4)
-    return;
-  // wave w finishes activation tile t = w / 4, element e = w % 4 of every lane
-  const int t = wave / 4, e = wave % 4;
-  float total = 0.0f, gate = 0.0f;
-  for (int w = 0; w < kSkWaves; w++) {
-    total += red[((w * MT + t) * 4 + e) * 64 + lane];
+  // wave w finishes (activation tile t, element e) = (te / 4, te % 4) for te = w, w + WAVES, ... of every lane
+  for (int te = wave; te < MT * 4; te += WAVES) {
+    const int t = te / 4, e = te % 4;
+    float total = 0.0f, gate = 0.0f;
+    for (int w = 0; w < WAVES; w++) {
+      total += red[((w * MT + t) * 4 + e) * 64 + lane];
+      if (swiglu)
+        gate += red[red3 + ((w * MT + t) * 4 + e) * 64 + lane];
+    }
+    const int row = 16 * t + lr + e, col = col0 + lc;
+    if (row >= p.m || col >= seg.n)
+      continue;
+    float *o = seg.c + (long long)row * seg.ldc + col;
     if (swiglu)
-      gate += red[red3 + ((w * MT + t) * 4 + e) * 64 + lane];
+      *o = sk_silu_gate(total, gate);
+    else if (seg.epi == EPI_ADD)
+      *o += total;
+    else
+      *o = total;
   }
-  const int row = 16 * t + lr + e, col = col0 + lc;
-  if (row >= p.m || col >= seg.n)
-    return;
-  float *o = seg.c + (long long)row * seg.ldc + col;
-  if (swiglu)
-    *o = sk_silu_gate(total, gate);
-  else if (seg.epi == EPI_ADD)
-    *o += total;
-  else
-    *o = total;
 }
 
-size_t skinny_lds(int mt, int groups) {
-  return ((size_t)(32 + 16 * mt) * groups + 2 * (size_t)kSkWaves * mt * 4 * 64) * sizeof(float);
+size_t skinny_lds(int mt, int waves, int groups) {
+  return ((size_t)(32 + 16 * mt) * groups + 2 * (size_t)waves * mt * 4 * 64) * sizeof(float);
+}
+
+template <int MT, int WAVES> bool skinny_launch(const SkParams &p, int tiles, hipStream_t stream) {
+  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<MT, WAVES>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
+    return false;
+  hipLaunchKernelGGL((q8_gemm_skinny<MT, WAVES>), dim3((unsigned)tiles), dim3(64 * WAVES),
+                     skinny_lds(MT, WAVES, p.groups), stream, p);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess || raise("launching q8_gemm_skinny failed: %s", hipGetErrorString(e));
 }
 
 } // namespace
@@ -190,7 +199,7 @@ size_t skinny_lds(int mt, int groups) {
 // Shapes the skinny kernel takes: at most 32 rows, gs a multiple of 64, 16-byte aligned rows, scales that fit LDS.
 bool q8_gemm_skinny_path(const int8_t *xq, int m, int k, int gs) {
   return m > 0 && m <= 32 && gs > 0 && gs % 64 == 0 && k % gs == 0 && ((uintptr_t)xq & 15) == 0 &&
-         32LL * k < (1LL << 31) && skinny_lds(m > 16 ? 2 : 1, k / gs) <= 160 * 1024;
+         32LL * k < (1LL << 31) && skinny_lds(m > 16 ? 2 : 1, 8, k / gs) <= 160 * 1024;
 }
 
 bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream) {
@@ -211,25 +220,14 @@ bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream) {
   p.gs = job.gs;
   p.groups = job.k / job.gs;
   p.steps = job.k / 64;
-  const int spg = job.gs / 64;
-  p.per = ((p.steps + kSkWaves - 1) / kSkWaves + spg - 1) / spg * spg;
+  // Waves per block split K: eight for grids of fewer than 512 column tiles (W2, Wo: 256), four otherwise (W1/W3: 896),
+  // which measured best on the 8B shapes (W2 17.5 vs 24.0 us with four; W1/W3 29.4 vs 31.6 with eight).
+  const int waves = tiles < 512 ? 8 : 4, spg = job.gs / 64;
+  p.per = ((p.steps + waves - 1) / waves + spg - 1) / spg * spg;
   const int mt = job.m > 16 ? 2 : 1;
-  const size_t lds = skinny_lds(mt, p.groups);
-  if (mt == 1) {
-    static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<1>,
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
-      return false;
-    hipLaunchKernelGGL(q8_gemm_skinny<1>, dim3((unsigned)tiles), dim3(kSkThreads), lds, stream, p);
-  } else {
-    static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<2>,
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
-      return false;
-    hipLaunchKernelGGL(q8_gemm_skinny<2>, dim3((unsigned)tiles), dim3(kSkThreads), lds, stream, p);
-  }
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess || raise("launching q8_gemm_skinny failed: %s", hipGetErrorString(e));
+  if (mt == 1)
+    return waves == 8 ? skinny_launch<1, 8>(p, tiles, stream) : skinny_launch<1, 4>(p, tiles, stream);
+  return waves == 8 ? skinny_launch<2, 8>(p, tiles, stream) : skinny_launch<2, 4>(p, tiles, stream);
 }
 
 } // namespace llhip
