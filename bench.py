@@ -327,7 +327,8 @@ def cpu_baseline(threads, budget_s=30.0):
                  (VOCAB, DIM): 1}
     if os.path.exists(exe):
         env = dict(os.environ, LLAMA_THREADS=str(threads), LLAMA_KERNELS="auto")
-        cmd = [exe, "--kernel", "q8", "--gemv", "--m", "1", "--reps", "25", "--cold-mib", "1200", "--shapes",
+        reps = 100  # about 10 s of wall time on 16 host threads
+        cmd = [exe, "--kernel", "q8", "--gemv", "--m", "1", "--reps", str(reps), "--cold-mib", "1200", "--shapes",
                ",".join(f"{n}x{k}" for n, k in shapes)]
         t0 = time.time()
         r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
@@ -341,7 +342,7 @@ def cpu_baseline(threads, budget_s=30.0):
                     isa = rec["isa"]
             token_s = sum(med[s] * c for s, c in per_token.items())
             return {"value": round(1.0 / token_s, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-                    "sample": f"reference gemm-bench --kernel q8 --gemv (isa {isa}, {threads} threads, 25 reps, cold "
+                    "sample": f"reference gemm-bench --kernel q8 --gemv (isa {isa}, {threads} threads, {reps} reps, cold "
                               f"copies over 1200 MiB) on the 8B shapes 4096x4096, 1024x4096, 14336x4096, 4096x14336, "
                               f"128256x4096; per-token time = 32 x (2 wq/wo + 2 wk/wv + 2 w1/w3 + w2) + classifier "
                               f"= {token_s * 1e3:.2f} ms; wall {time.time() - t0:.1f} s",
