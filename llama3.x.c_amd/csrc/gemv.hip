@@ -636,7 +636,8 @@ struct F32Params {
 template <int ROWS>
 __global__ __launch_bounds__(kBlock) void f32_gemv(F32Params p) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int gw = blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6);
+  // wave-uniform: readfirstlane keeps the row pointers, and so the buffer resources, in scalar registers
+  const int gw = blockIdx.x * (kBlock / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (gw >= p.total_waves)
     return;
   int s = 0;
@@ -651,19 +652,36 @@ __global__ __launch_bounds__(kBlock) void f32_gemv(F32Params p) {
   for (int i = 0; i < ROWS; i++)
     acc[i] = gacc[i] = 0.0f;
   if (p.vec4) {
-    for (int off = lane * 4; off < p.n; off += kWave * 4) {
-      const float4 xv = *reinterpret_cast<const float4 *>(p.x + off);
+    // U 1 KB steps of every row in flight at once, the weights streamed past the caches (nt); rows and columns past
+    // the end read zero through bounded buffer resources, so no load is conditional
+    constexpr int U = ROWS >= 4 ? 2 : 4;
+    const unsigned rowb = (unsigned)p.n * 4u;
+    for (int off = lane * 4; off < p.n; off += kWave * 4 * U) {
+      float4 wv[U][ROWS], gv[U][ROWS], xv[U];
 #pragma unroll
-      for (int i = 0; i < ROWS; i++) {
-        if (i >= nrows)
-          break;
-        const float4 wv = *reinterpret_cast<const float4 *>(seg.w + (r0 + i) * p.ld + off);
-        acc[i] = fmaf(wv.x, xv.x, fmaf(wv.y, xv.y, fmaf(wv.z, xv.z, fmaf(wv.w, xv.w, acc[i]))));
-        if (swiglu) {
-          const float4 gv = *reinterpret_cast<const float4 *>(seg.w3 + (r0 + i) * p.ld + off);
-          gacc[i] = fmaf(gv.x, xv.x, fmaf(gv.y, xv.y, fmaf(gv.z, xv.z, fmaf(gv.w, xv.w, gacc[i]))));
+      for (int u = 0; u < U; u++) {
+        const int o = off + u * kWave * 4;
+        const int4 xi = load16(buffer(p.x, rowb), o * 4, 0);
+        xv[u] = float4{__int_as_float(xi.x), __int_as_float(xi.y), __int_as_float(xi.z), __int_as_float(xi.w)};
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) {
+          const unsigned bytes = i < nrows ? rowb : 0u;
+          const int4 a = load16(buffer(seg.w + (r0 + i) * p.ld, bytes), o * 4, 1);
+          wv[u][i] = float4{__int_as_float(a.x), __int_as_float(a.y), __int_as_float(a.z), __int_as_float(a.w)};
+          if (swiglu) {
+            const int4 g = load16(buffer(seg.w3 + (r0 + i) * p.ld, bytes), o * 4, 1);
+            gv[u][i] = float4{__int_as_float(g.x), __int_as_float(g.y), __int_as_float(g.z), __int_as_float(g.w)};
+          }
         }
       }
+#pragma unroll
+      for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) {
+          acc[i] = fmaf(wv[u][i].x, xv[u].x, fmaf(wv[u][i].y, xv[u].y, fmaf(wv[u][i].z, xv[u].z, fmaf(wv[u][i].w, xv[u].w, acc[i]))));
+          if (swiglu)
+            gacc[i] = fmaf(gv[u][i].x, xv[u].x, fmaf(gv[u][i].y, xv[u].y, fmaf(gv[u][i].z, xv[u].z, fmaf(gv[u][i].w, xv[u].w, gacc[i]))));
+        }
     }
   } else {
     for (int off = lane; off < p.n; off += kWave) {
