@@ -273,6 +273,22 @@ __device__ __forceinline__ int dot16(int4 w, int4 x) {
   return __builtin_amdgcn_sdot4(w.w, x.w, d, false);
 }
 
+// W8A32: the FP32 dot of 16 int8 weights (byte j of the int4 is weight j) with 16 FP32 inputs, each weight widened
+// exactly to FP32; two accumulators halve the FMA dependency chain.
+__device__ __forceinline__ float dot16f(int4 w, const float4 (&x)[4]) {
+  const int words[4] = {w.x, w.y, w.z, w.w};
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int v = words[q];
+    a = fmaf((float)((v << 24) >> 24), x[q].x, a);
+    b = fmaf((float)((v << 16) >> 24), x[q].y, b);
+    a = fmaf((float)((v << 8) >> 24), x[q].z, a);
+    b = fmaf((float)(v >> 24), x[q].w, b);
+  }
+  return a + b;
+}
+
 // The block's copy of the input in LDS: the int8 activations and their scales, copied from (xq, xs), or (FUSED) made
 // here from the FP32 input with the k_quantize rule, block 0 also storing them for the caller. load() only issues the
 // global loads into registers; the kernel issues it before the weight loads, so waiting for the input does not wait
@@ -424,6 +440,36 @@ struct RowPart {
       prior = load4(buffer(seg.out + row, own && part == 0 && p.epi == EPI_ADD ? 4u : 0u), 0);
   }
 
+  // The scale of this lane's group in the wave's chunk c (and of the gate row's): under SG from lane
+  // (c % 4) * 16 + lane / 4, which loaded it.
+  __device__ __forceinline__ float scale(int c, int lane) const {
+    const int src = ((c & 3) * 16 + (lane >> 2)) * 4;
+    return SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ws[c / 4 < kScaleRegs ? c / 4 : 0])))
+              : ws[c < kScaleRegs ? c : 0];
+  }
+  __device__ __forceinline__ float gate_scale(int c, int lane) const {
+    const int src = ((c & 3) * 16 + (lane >> 2)) * 4;
+    return SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(w3s[c / 4 < kScaleRegs ? c / 4 : 0])))
+              : w3s[c < kScaleRegs ? c : 0];
+  }
+
+  // W8A32: this wave's part of the row against the FP32 input the wave holds in registers (x[c]: its 16 values of
+  // chunk c). Per chunk a lane forms the FP32 dot of its 16 widened weights and adds it times the group scale: the
+  // reference's per-group sum times ws (src/gemv.c:141-181) up to FP32 rounding order.
+  __device__ __forceinline__ float2 dot_f32(const GemvParams &p, const float4 (&x)[CH][4], int part, int lane) const {
+    float acc = 0.0f, gacc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+      if (c * KS + part < p.nchunks) {
+        // lanes past n read zero weights, inputs and scales
+        acc = fmaf(dot16f(w[c], x[c]), scale(c, lane), acc);
+        if (SWIGLU)
+          gacc = fmaf(dot16f(w3[c], x[c]), gate_scale(c, lane), gacc);
+      }
+    }
+    return float2{wave_sum(acc), SWIGLU ? wave_sum(gacc) : 0.0f};
+  }
+
   // This wave's part of the row (and of the gate row), reduced over the wave. Fully unrolled over compile-time
   // indices with guards, not early exits, so the arrays stay in registers.
   __device__ __forceinline__ float2 dot(const GemvParams &p, const int8_t *sxq, const float *sxs, int part,
@@ -446,19 +492,11 @@ struct RowPart {
           if (active && leader)
             probe[(long long)g * seg.rows + row] = d;
         }
-        // the scale of this lane's group in chunk c: from lane (c % 4) * 16 + lane / 4 under SG
-        const int src = ((c & 3) * 16 + (lane >> 2)) * 4;
-        const float wsc = SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ws[c / 4 < kScaleRegs ? c / 4 : 0])))
-                             : ws[c < kScaleRegs ? c : 0];
         // every lane scales its partial: sum over the group's lanes of (float)partial * ws * xs, which differs from
         // ((float)dot * ws) * xs only in FP32 rounding
-        acc = fmaf((float)pd, wsc * xsg, acc);
-        if (SWIGLU) {
-          const int pd3 = dot16(w3[c], xv);
-          const float w3sc = SG ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(w3s[c / 4 < kScaleRegs ? c / 4 : 0])))
-                                : w3s[c < kScaleRegs ? c : 0];
-          gacc = fmaf((float)pd3, w3sc * xsg, gacc);
-        }
+        acc = fmaf((float)pd, scale(c, lane) * xsg, acc);
+        if (SWIGLU)
+          gacc = fmaf((float)dot16(w3[c], xv), gate_scale(c, lane) * xsg, gacc);
       }
     }
     return float2{wave_sum(acc), SWIGLU ? wave_sum(gacc) : 0.0f};
@@ -479,11 +517,10 @@ struct RowPart {
 
 constexpr int kMaxGemvWaves = 16;
 
+// One row step: the wave's part r of the row (and gate row) is combined with the row's other parts and stored.
 template <int WAVES, int CH, int KS, bool SWIGLU, bool SG>
-__device__ __forceinline__ void gemv_step(const GemvParams &p, const RowPart<CH, KS, SWIGLU, SG> &set,
-                                          const int8_t *sxq, const float *sxs, float2 *red, int wave, int part,
-                                          int lane, int &parity) {
-  const float2 r = set.dot(p, sxq, sxs, part, lane);
+__device__ __forceinline__ void gemv_step(const GemvParams &p, const RowPart<CH, KS, SWIGLU, SG> &set, float2 r,
+                                          float2 *red, int wave, int part, int lane, int &parity) {
   if (KS == 1) {
     if (lane == 0)
       set.store(p, r.x, r.y);
@@ -533,13 +570,60 @@ __global__ __launch_bounds__(WAVES * 64) void q8_gemv(GemvParams p) {
   in.stage(p, sxq, sxs);
   __syncthreads();
   while (true) {
-    gemv_step<WAVES>(p, a, sxq, sxs, red, wave, part, lane, parity);
+    gemv_step<WAVES>(p, a, a.dot(p, sxq, sxs, part, lane), red, wave, part, lane, parity);
     step += stride;
     if (step >= steps)
       break;
     a.load(p, (step + stride) * kRows + slot, part, lane);
     __builtin_amdgcn_sched_barrier(0);
-    gemv_step<WAVES>(p, b, sxq, sxs, red, wave, part, lane, parity);
+    gemv_step<WAVES>(p, b, b.dot(p, sxq, sxs, part, lane), red, wave, part, lane, parity);
+    step += stride;
+    if (step >= steps)
+      break;
+    b.load(p, (step + stride) * kRows + slot, part, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// W8A32 (FP32 input, src/gemv.c:141-181): the same persistent, software-pipelined row stream, the input not staged
+// in LDS but held in registers. A wave's chunks (part, part + KS, ...) are the same for every row it takes, so each
+// wave loads its 16 inputs per chunk and lane once (L2-resident after the first blocks) and keeps them for all its
+// rows; LDS only carries the partial sums of a split row.
+template <int WAVES, int CH, int KS, bool SWIGLU, bool SG>
+__global__ __launch_bounds__(WAVES * 64) void q8_gemv_a32(GemvParams p) {
+  constexpr int kRows = WAVES / KS;
+  __shared__ float2 red[2 * WAVES];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slot = wave / KS, part = wave % KS;
+  const int steps = (p.total_rows + kRows - 1) / kRows;
+  const int stride = gridDim.x;
+  int step = blockIdx.x; // block-uniform, < steps (the grid never exceeds the step count)
+  int parity = 0;
+  float4 x[CH][4];
+  {
+    // bounded to the n inputs: chunks and lanes past n read zero
+    const __amdgpu_buffer_rsrc_t r = buffer(p.xf, (unsigned)p.n * 4u);
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int4 v = load16(r, ((((c * KS + part) << 10) + lane * 16) << 2) + q * 16, 0);
+        x[c][q] = float4{__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w)};
+      }
+  }
+  RowPart<CH, KS, SWIGLU, SG> a, b;
+  a.load(p, step * kRows + slot, part, lane);
+  b.load(p, (step + stride) * kRows + slot, part, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  while (true) {
+    gemv_step<WAVES>(p, a, a.dot_f32(p, x, part, lane), red, wave, part, lane, parity);
+    step += stride;
+    if (step >= steps)
+      break;
+    a.load(p, (step + stride) * kRows + slot, part, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    gemv_step<WAVES>(p, b, b.dot_f32(p, x, part, lane), red, wave, part, lane, parity);
     step += stride;
     if (step >= steps)
       break;
@@ -775,14 +859,26 @@ static size_t gemv_lds_bytes(int n, int gs) {
   return ((size_t)(n + 15) & ~(size_t)15) + (size_t)((n / gs + 1) & ~1) * sizeof(float) + 2 * kMaxGemvWaves * 8;
 }
 
+// The input a fast GEMV takes: int8 (xq, xs), FP32 quantized in the prologue, or FP32 as it is (W8A32).
+enum GemvInput { IN_Q8, IN_FUSED, IN_F32 };
+
 template <int WAVES, int CH, int KS, bool SWIGLU>
-static void launch_shape(const GemvParams &p, bool fused, int per_cu, hipStream_t stream) {
+static void launch_shape(const GemvParams &p, GemvInput in, int per_cu, hipStream_t stream) {
   const size_t lds = gemv_lds_bytes(p.n, p.gs);
   const int steps = (p.total_rows + WAVES / KS - 1) / (WAVES / KS);
   const int cap = device().cu_count * per_cu;
   const int blocks = steps < cap ? steps : cap;
-  const bool sg = p.gs == 64;
-  if (fused && sg)
+  const bool sg = p.gs == 64, fused = in == IN_FUSED;
+  if (in == IN_F32) {
+    if constexpr (CH <= 4) {
+      if (sg)
+        hipLaunchKernelGGL((q8_gemv_a32<WAVES, CH, KS, SWIGLU, true>), dim3(blocks), dim3(WAVES * 64), 0, stream, p);
+      else
+        hipLaunchKernelGGL((q8_gemv_a32<WAVES, CH, KS, SWIGLU, false>), dim3(blocks), dim3(WAVES * 64), 0, stream, p);
+    } else {
+      raise("internal: a W8A32 GEMV of more than four chunks per wave");
+    }
+  } else if (fused && sg)
     hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true, true>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
   else if (fused)
     hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true, false>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
@@ -802,9 +898,11 @@ struct GemvShape {
 //   - the SwiGLU pair (twice the registers per row) streams best from two 8-wave blocks per CU (21.9 us against
 //     22.6 with three, 14336 x 4096 twice, in the 8B decode step);
 //   - a long matrix (the 128256-row classifier) from one wave per row and four block equivalents per CU;
-//   - everything else from one 16-wave block per CU.
+//   - everything else from one 16-wave block per CU;
+//   - W8A32 (inputs in registers) from three 8-wave blocks per CU, at most two chunks per wave (W2 14.6 us against
+//     17.2 with one 16-wave block of four-chunk waves, the SwiGLU pair 22.8 against 24.3), the classifier as above.
 // llhip_set_gemv_shape and LLAMA_HIP_GEMV_KSPLIT / _BLOCKS_PER_CU / _BLOCK_WAVES override each part.
-static GemvShape gemv_shape(int total_rows, int nchunks, bool swiglu) {
+static GemvShape gemv_shape(int total_rows, int nchunks, bool swiglu, bool f32_input) {
   static const int env_split = env_shape("LLAMA_HIP_GEMV_KSPLIT", 1, 8);
   static const int env_per_cu = env_shape("LLAMA_HIP_GEMV_BLOCKS_PER_CU", 1, 64);
   static const int env_waves = env_shape("LLAMA_HIP_GEMV_BLOCK_WAVES", 8, 16);
@@ -816,34 +914,45 @@ static GemvShape gemv_shape(int total_rows, int nchunks, bool swiglu) {
     g.split = nchunks <= 4 ? 1 : g.split;
     g.per_cu = 4;
   }
+  if (f32_input && total_rows < 32768) {
+    g.per_cu = 3;
+    g.waves = 8;
+  }
   const int split = forced_split.load(std::memory_order_relaxed), per_cu = forced_blocks.load(std::memory_order_relaxed),
             waves = forced_waves.load(std::memory_order_relaxed);
   g.split = split ? split : (env_split == 1 || env_split == 2 || env_split == 4 || env_split == 8) ? env_split : g.split;
   g.per_cu = per_cu ? per_cu : env_per_cu ? env_per_cu : g.per_cu;
   g.waves = waves ? waves : (env_waves == 8 || env_waves == 16) ? env_waves : g.waves;
+  // W8A32 holds 16 FP32 inputs per chunk and lane in registers: at most four chunks per wave, two where the gate row
+  // doubles the weight registers or more than two 8-wave blocks share a CU (spill-free and resident, as compiled)
+  const int max_per = swiglu || g.per_cu > 2 ? 2 : 4;
+  while (f32_input && g.split < 8 && (nchunks + g.split - 1) / g.split > max_per)
+    g.split *= 2;
   return g;
 }
 
 template <int CH, int KS, bool SWIGLU>
-static void launch_fast(const GemvParams &p, bool fused, const GemvShape &g, hipStream_t stream) {
+static void launch_fast(const GemvParams &p, GemvInput in, const GemvShape &g, hipStream_t stream) {
   // per_cu counts 8-wave blocks: a 16-wave block stands for two
   if (g.waves == 16 && g.per_cu % 2 == 0)
-    launch_shape<16, CH, KS, SWIGLU>(p, fused, g.per_cu / 2, stream);
+    launch_shape<16, CH, KS, SWIGLU>(p, in, g.per_cu / 2, stream);
   else
-    launch_shape<8, CH, KS, SWIGLU>(p, fused, g.per_cu, stream);
+    launch_shape<8, CH, KS, SWIGLU>(p, in, g.per_cu, stream);
 }
 
 template <int KS, bool SWIGLU>
-static void launch_split(const GemvParams &p, bool fused, const GemvShape &g, hipStream_t stream) {
+static void launch_split(const GemvParams &p, GemvInput in, const GemvShape &g, hipStream_t stream) {
   const int per = (p.nchunks + KS - 1) / KS; // chunks per wave
   if (per <= 1)
-    launch_fast<1, KS, SWIGLU>(p, fused, g, stream);
+    launch_fast<1, KS, SWIGLU>(p, in, g, stream);
   else if (per <= 2)
-    launch_fast<2, KS, SWIGLU>(p, fused, g, stream);
+    launch_fast<2, KS, SWIGLU>(p, in, g, stream);
   else if (per <= 4)
-    launch_fast<4, KS, SWIGLU>(p, fused, g, stream);
+    launch_fast<4, KS, SWIGLU>(p, in, g, stream);
+  else if (in == IN_F32) // (gemv_shape keeps W8A32 at <= 4 chunks per wave) four waves of four cover 16 chunks
+    launch_fast<4, 4, SWIGLU>(p, in, g, stream);
   else // per <= 16 only with one wave per row: two waves of at most 8 chunks instead (16 would spill registers)
-    launch_fast<8, 2, SWIGLU>(p, fused, g, stream);
+    launch_fast<8, 2, SWIGLU>(p, in, g, stream);
 }
 
 bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves) {
@@ -861,16 +970,21 @@ bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves) {
 
 bool gemv_fast_path(const GemvJob &job) {
   const int lpg = lanes_per_group(job.gs);
-  const size_t lds = job.gs > 0 ? gemv_lds_bytes(job.n, job.gs) : 0;
-  bool fast = (job.xq || job.xf_quantize) && lpg && job.n > 0 && job.n % job.gs == 0 && job.ld % 16 == 0 &&
-              lds <= 65536 && (job.n + 1023) / 1024 <= 16;
+  // W8A32: the FP32 input as it is (the int32 probe needs int8 activations: the generic kernel records none either)
+  const bool f32_input = !job.xq && !job.xf_quantize && job.xf && !job.probe;
+  const size_t lds = job.gs > 0 && !f32_input ? gemv_lds_bytes(job.n, job.gs) : 0;
+  bool fast = (job.xq || job.xf_quantize || f32_input) && lpg && job.n > 0 && job.n % job.gs == 0 &&
+              job.ld % 16 == 0 && lds <= 65536 && (job.n + 1023) / 1024 <= 16;
   // The fused prologue quantizes the FP32 input 4 values per lane (gs <= 256: a group within a wave).
-  fast = fast && (job.xf_quantize ? aligned16(job.xf) && aligned16(job.xq_out) && job.gs <= 256 : aligned16(job.xq));
+  fast = fast && (job.xf_quantize ? aligned16(job.xf) && aligned16(job.xq_out) && job.gs <= 256
+                  : f32_input     ? aligned16(job.xf)
+                                  : aligned16(job.xq));
   for (int s = 0; s < job.nseg && fast; s++) {
     fast = aligned16(job.seg[s].wq) && (job.epi != EPI_SWIGLU || aligned16(job.seg[s].w3q));
-    // Fused, every block reads the FP32 input while others already write outputs: an output inside the input would
-    // change what later blocks quantize, so that case quantizes in its own launch first.
-    if (job.xf_quantize) {
+    // With an FP32 input every block reads it while others already write outputs: an output inside the input would
+    // change what later blocks read (fused: quantize), so that case takes the quantization's own launch first, or
+    // (W8A32) the generic kernel.
+    if (job.xf_quantize || f32_input) {
       const uintptr_t o0 = (uintptr_t)job.seg[s].out, o1 = o0 + (size_t)job.seg[s].rows * sizeof(float);
       const uintptr_t x0 = (uintptr_t)job.xf, x1 = x0 + (size_t)job.n * sizeof(float);
       fast = fast && (o1 <= x0 || x1 <= o0);
@@ -909,23 +1023,24 @@ bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
     p.total_rows = rows;
     p.probe = job.probe;
     p.flags = device().error_flags;
-    const bool fused = job.xf_quantize, swiglu = job.epi == EPI_SWIGLU;
-    const GemvShape g = gemv_shape(rows, p.nchunks, swiglu);
+    const GemvInput in = job.xf_quantize ? IN_FUSED : job.xq ? IN_Q8 : IN_F32;
+    const bool swiglu = job.epi == EPI_SWIGLU;
+    const GemvShape g = gemv_shape(rows, p.nchunks, swiglu, in == IN_F32);
     switch (g.split) {
     case 1:
-      swiglu ? launch_split<1, true>(p, fused, g, stream) : launch_split<1, false>(p, fused, g, stream);
+      swiglu ? launch_split<1, true>(p, in, g, stream) : launch_split<1, false>(p, in, g, stream);
       break;
     case 2:
-      swiglu ? launch_split<2, true>(p, fused, g, stream) : launch_split<2, false>(p, fused, g, stream);
+      swiglu ? launch_split<2, true>(p, in, g, stream) : launch_split<2, false>(p, in, g, stream);
       break;
     case 4:
-      swiglu ? launch_split<4, true>(p, fused, g, stream) : launch_split<4, false>(p, fused, g, stream);
+      swiglu ? launch_split<4, true>(p, in, g, stream) : launch_split<4, false>(p, in, g, stream);
       break;
     default:
-      swiglu ? launch_split<8, true>(p, fused, g, stream) : launch_split<8, false>(p, fused, g, stream);
+      swiglu ? launch_split<8, true>(p, in, g, stream) : launch_split<8, false>(p, in, g, stream);
       break;
     }
-    return launch_ok("q8_gemv");
+    return launch_ok(in == IN_F32 ? "q8_gemv_a32" : "q8_gemv");
   }
   if (job.xf_quantize)
     return raise("internal: a fused quantization was routed to the generic GEMV");

@@ -142,6 +142,51 @@ def test_gemv_shapes_budget_and_probe(d, n, gs):
     assert np.array_equal(dots, orc.group_dots(xq.reshape(1, -1), wq, gs)[:, 0, :])
 
 
+def f32_input_reference(x, wq, ws, gs):
+    """float64 sum and magnitude of W.x for the W8A32 GEMV: dequantized weights, the FP32 input as it is."""
+    wd = wq.astype(np.float64) * np.repeat(ws.astype(np.float64), gs, axis=-1)
+    xd = x.astype(np.float64)
+    return wd @ xd, np.abs(wd) @ np.abs(xd)
+
+
+@pytest.mark.parametrize("d,n,gs", [(4096, 4096, 64), (1024, 14336, 64), (512, 16384, 64), (333, 4096, 128),
+                                    (77, 2048, 32), (64, 1088, 64), (5, 256, 16), (17, 320, 64), (40, 8192, 256)])
+def test_w8a32_gemv_shapes_budget(d, n, gs):
+    """W8A32 (FP32 activations, src/gemv.c:141-181) through every epilogue: store and add within the budget of the
+    float64 reference, SwiGLU and the three-matrix QKV form against the oracle (the reference's scalar loop)."""
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 3 * d + n + gs)
+    wq, ws = synth_weights(rng, d, n, gs)
+    w3q, w3s = synth_weights(rng, d, n, gs)
+    x = rng.normal(n, 0.0, 1.0)
+    base = rng.normal(d, 0.0, 1.0)
+    ref, mag = f32_input_reference(x, wq, ws, gs)
+    dx, dwq, dws, dw3q, dw3s = hu.dev(x), hu.dev(wq), hu.dev(ws), hu.dev(w3q), hu.dev(w3s)
+    inp = lh.k8(None, None, dx)
+    out = hu.empty(d, hu.torch().float32)
+    L.k_matmul_q8(lh.ptr(out), inp, lh.w8(dwq, dws), n, d, gs)
+    hu.assert_within_budget(hu.host(out), ref, mag, what=f"w8a32 store {d}x{n} gs {gs}")
+    acc = hu.dev(base)
+    L.k_matmul_q8_add(lh.ptr(acc), inp, lh.w8(dwq, dws), n, d, gs)
+    hu.assert_within_budget(hu.host(acc), ref + base, mag + np.abs(base), what=f"w8a32 add {d}x{n}")
+    sw = hu.empty(d, hu.torch().float32)
+    L.k_matmul_q8_swiglu(lh.ptr(sw), inp, lh.w8(dwq, dws), lh.w8(dw3q, dw3s), n, d, gs)
+    got = hu.host(sw).astype(np.float64)
+    ref3, mag3 = f32_input_reference(x, w3q, w3s, gs)
+    # silu(a) * b with both dots inside their budgets t: the error carries through |silu'| <= 1.1
+    ta, tb = 2e-5 * mag + 1e-6, 2e-5 * mag3 + 1e-6
+    silu = ref / (1.0 + np.exp(-ref))
+    tol = 1.1 * np.abs(ref3) * ta + np.abs(silu) * tb + 1.1 * ta * tb + 1e-6
+    assert np.all(np.abs(got - silu * ref3) <= tol), f"w8a32 swiglu {d}x{n}"
+    want = orc.matmul_q8(None, None, wq, ws, gs, orc.K_SWIGLU, w3q=w3q, w3s=w3s, xf=x)
+    assert np.all(np.abs(got - want) <= 2 * tol), f"w8a32 swiglu {d}x{n} vs oracle"
+    qkv = [hu.empty(d, hu.torch().float32) for _ in range(3)]
+    L.k_matmul_q8_qkv(lh.ptr(qkv[0]), lh.ptr(qkv[1]), lh.ptr(qkv[2]), inp, lh.w8(dwq, dws), lh.w8(dw3q, dw3s),
+                      lh.w8(dwq, dws), n, d, d, gs)
+    for j, (r, m) in enumerate([(ref, mag), (ref3, mag3), (ref, mag)]):
+        hu.assert_within_budget(hu.host(qkv[j]), r, m, what=f"w8a32 qkv[{j}] {d}x{n}")
+
+
 def test_gemv_entry_points_against_reference_golden():
     """Every GEMV entry point, W8A8 and W8A32, on the reference's own golden small cases (host buffers)."""
     g = np.load(os.path.join(GOLDEN, "gemv_q8.npz"))
