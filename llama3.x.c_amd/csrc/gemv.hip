@@ -81,35 +81,43 @@ __device__ __forceinline__ int quantize_one(float x, float scale) {
   return (int)roundf(fmaxf(-127.0f, fminf(127.0f, ratio)));
 }
 
-// Values through the reciprocal, for normal scales: r = x * rcp(scale) lies within 127 * 3 * 2^-24 < 2.3e-5 of the
-// correctly rounded quotient fl(x / scale) (v_rcp_f32 is within 1 ulp, the product rounds once, |x / scale| <=
-// 127 (1 + 2^-23)). roundf changes value only at k + 0.5 and the clamp only binds above 127, so wherever r is at least
-// 2^-12 from every k + 0.5, i.e. |r - rint(r)| <= 0.5 - 2^-12 (an exact subtraction), both give clamp(rint(r)). If any
-// value of the call is inside that margin, is subnormal (a flushing multiply would lose it) or the scale is 0 or not
-// normal, the exact quotient decides for all of them: one branch per call, rarely taken.
+// Values through the reciprocal, for normal finite scales: r = x * rcp(scale) lies within 127 * 3 * 2^-24 < 2.3e-5 of
+// the correctly rounded quotient fl(x / scale) (v_rcp_f32 is within 1 ulp, the product rounds once, |x / scale| <=
+// 127 (1 + 2^-23)). The kernels keep FP32 denormals (the compiler's default mode), so a subnormal x or r changes this
+// only by an absolute 2^-150. roundf changes value only at k + 0.5 and the clamp binds only from 127.5, which r never
+// reaches, so wherever r is at least 2^-12 from every k + 0.5, i.e. |r - rint(r)| <= 0.5 - 2^-12 (an exact
+// subtraction), both give rint(r). rint is r + M - M with M = 1.5 * 2^23: for |r| < 2^22 the sum rounds r to the
+// nearest integer (ties to even) in the low mantissa bits, so the low byte of the sum's bits is rint(r) as int8, with
+// no conversion. If any value of the call is inside the margin or not finite (r is then NaN or infinite, and the test
+// fails), or the scale is 0, not normal or infinite, the exact quotient decides for all of them, and the non-finite
+// values are flagged: one branch per call, rarely taken.
 constexpr float kTieGuard = 0.5f - 0x1p-12f;
-constexpr int kSubnormal = 0x090; // v_cmp_class mask: negative and positive denormals
+constexpr float kRoundMagic = 12582912.0f; // 1.5 * 2^23
 
+// q[j]'s low byte is the int8 value of x[j].
 template <int N>
-__device__ __forceinline__ void quantize_fast(const float (&x)[N], float scale, float inv, bool inv_ok, int (&q)[N]) {
-#pragma clang fp contract(off) // r is the rounded product: the margin test must see the value rint() rounded
+__device__ __forceinline__ void quantize_fast(const float (&x)[N], float scale, float inv, bool inv_ok, int (&q)[N],
+                                              bool &bad) {
+#pragma clang fp contract(off) // r is the rounded product: the margin test must see the value that was rounded
   bool slow = !inv_ok;
 #pragma unroll
   for (int j = 0; j < N; j++) {
     const float r = x[j] * inv;
-    const float t = __builtin_rintf(r);
-    slow |= fabsf(r - t) > kTieGuard || __builtin_amdgcn_class(x[j], kSubnormal);
-    q[j] = (int)__builtin_amdgcn_fmed3f(t, -127.0f, 127.0f);
+    const float t = r + kRoundMagic;
+    slow |= !(fabsf(r - (t - kRoundMagic)) <= kTieGuard);
+    q[j] = __float_as_int(t);
   }
   if (slow) {
 #pragma unroll
-    for (int j = 0; j < N; j++)
+    for (int j = 0; j < N; j++) {
+      bad |= !isfinite(x[j]);
       q[j] = quantize_one(x[j], scale);
+    }
   }
 }
 
 __device__ __forceinline__ float group_reciprocal(float scale, bool &ok) {
-  ok = scale >= 1.17549435e-38f; // normal (finite: |x| is finite, so scale <= FLT_MAX / 127)
+  ok = scale >= 1.17549435e-38f && scale <= 3.40282347e+38f; // normal and finite
   return ok ? __builtin_amdgcn_rcpf(scale) : 0.0f;
 }
 
@@ -120,40 +128,20 @@ __device__ __forceinline__ int pack_bytes(int a, int b, int c, int d) {
 // Quantizes the 16 values a lane holds; every lane of the wave must call it (the group max is a lane reduction).
 // Returns the packed int8 values and the group's scale; flags a non-finite input.
 __device__ __forceinline__ int4 quantize_slice(const float4 (&v)[4], int lpg, float &scale, bool &bad) {
+  const float e[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
+                       v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};
   float peak = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      bad |= !isfinite(e[j]);
-      peak = fmaxf(peak, fabsf(e[j]));
-    }
-  }
+  for (int j = 0; j < 16; j++)
+    peak = fmaxf(peak, fabsf(e[j])); // a NaN is skipped here and caught by quantize_fast
   peak = group_reduce_max(peak, lpg);
   scale = peak / 127.0f;
   bool ok;
   const float inv = group_reciprocal(scale, ok);
-  const float e[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
-                       v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};
   int q[16];
-  quantize_fast(e, scale, inv, ok, q);
+  quantize_fast(e, scale, inv, ok, q, bad);
   return int4{pack_bytes(q[0], q[1], q[2], q[3]), pack_bytes(q[4], q[5], q[6], q[7]),
               pack_bytes(q[8], q[9], q[10], q[11]), pack_bytes(q[12], q[13], q[14], q[15])};
-}
-
-// Four values per lane (one float4): the group spans gs / 4 lanes (lpg4, a power of two <= 64).
-__device__ __forceinline__ int quantize_quad(float4 v, int lpg4, float &scale, bool &bad) {
-  bad |= !isfinite(v.x) || !isfinite(v.y) || !isfinite(v.z) || !isfinite(v.w);
-  float peak = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  peak = group_reduce_max(peak, lpg4);
-  scale = peak / 127.0f;
-  bool ok;
-  const float inv = group_reciprocal(scale, ok);
-  const float e[4] = {v.x, v.y, v.z, v.w};
-  int q[4];
-  quantize_fast(e, scale, inv, ok, q);
-  return pack_bytes(q[0], q[1], q[2], q[3]);
 }
 
 // k_quantize / k_quantize_rows, fast form: gs = 16 * lpg with lpg a power of two <= 64, n % 16 == 0, 16-byte aligned
@@ -294,10 +282,10 @@ __device__ __forceinline__ float dot16f(int4 w, const float4 (&x)[4]) {
 // global loads into registers; the kernel issues it before the weight loads, so waiting for the input does not wait
 // for the weights (loads complete in issue order for the counter the waits use).
 template <bool FUSED, int BLOCK, int MAXC> struct Input {
-  static constexpr int kFusedPasses = (MAXC * 1024 + BLOCK * 4 - 1) / (BLOCK * 4); // 4 values per thread and pass
+  static constexpr int kFusedPasses = (MAXC * 1024 + BLOCK * 16 - 1) / (BLOCK * 16); // 16 values per thread and pass
   static constexpr int kCopyPasses = (MAXC * 1024 + BLOCK * 16 - 1) / (BLOCK * 16);
   static constexpr int kScalePasses = (MAXC * 64 + BLOCK - 1) / BLOCK; // gs >= 16: at most n / 16 scales
-  float4 xf[FUSED ? kFusedPasses : 1];
+  float4 xf[FUSED ? 4 * kFusedPasses : 1];
   int4 xq[FUSED ? 1 : kCopyPasses];
   float xs[FUSED ? 1 : kScalePasses];
 
@@ -307,10 +295,12 @@ template <bool FUSED, int BLOCK, int MAXC> struct Input {
     if (FUSED) {
       const __amdgpu_buffer_rsrc_t r = buffer(p.xf, (unsigned)p.n * 4u);
 #pragma unroll
-      for (int i = 0; i < kFusedPasses; i++) {
-        const int4 v = load16(r, (i * BLOCK * 4 + tid * 4) * 4, 0);
-        xf[i] = float4{__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w)};
-      }
+      for (int i = 0; i < kFusedPasses; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int4 v = load16(r, (i * BLOCK * 16 + tid * 16) * 4 + j * 16, 0);
+          xf[4 * i + j] = float4{__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w)};
+        }
     } else {
       const __amdgpu_buffer_rsrc_t rq = buffer(p.xq, (unsigned)p.n), rs = buffer(p.xs, (unsigned)(p.n / p.gs) * 4u);
 #pragma unroll
@@ -340,21 +330,26 @@ template <bool FUSED, int BLOCK, int MAXC> struct Input {
       return;
     }
     const bool keep = blockIdx.x == 0;
-    const int lpg4 = p.gs >> 2;
     bool bad = false;
-    // every lane takes part in every pass (the group max is a lane reduction); lanes past n hold zeros
+    // 16 values per lane, a group over lpg lanes: one group maximum, division and reciprocal per 16 values. A wave
+    // whose pass lies wholly past n skips it; otherwise all its lanes take part (the group max is a lane reduction),
+    // lanes past n holding zeros (n is a whole number of groups, so no group mixes them with values).
+    const int wave_off = (tid & ~(kWave - 1)) * 16;
 #pragma unroll
     for (int i = 0; i < kFusedPasses; i++) {
-      const int off = i * BLOCK * 4 + tid * 4;
+      if (i * BLOCK * 16 + wave_off >= p.n)
+        continue;
+      const int off = i * BLOCK * 16 + tid * 16;
+      const float4 v[4] = {xf[4 * i], xf[4 * i + 1], xf[4 * i + 2], xf[4 * i + 3]};
       float scale;
-      const int q = quantize_quad(xf[i], lpg4, scale, bad);
+      const int4 q = quantize_slice(v, p.lpg, scale, bad);
       if (off < p.n) {
-        *reinterpret_cast<int *>(sxq + off) = q;
-        const bool first = (tid & (lpg4 - 1)) == 0;
+        *reinterpret_cast<int4 *>(sxq + off) = q;
+        const bool first = (tid & (p.lpg - 1)) == 0;
         if (first)
           sxs[off / p.gs] = scale;
         if (keep) {
-          *reinterpret_cast<int *>(p.xq_out + off) = q;
+          *reinterpret_cast<int4 *>(p.xq_out + off) = q;
           if (first)
             p.xs_out[off / p.gs] = scale;
         }
@@ -975,8 +970,8 @@ bool gemv_fast_path(const GemvJob &job) {
   const size_t lds = job.gs > 0 && !f32_input ? gemv_lds_bytes(job.n, job.gs) : 0;
   bool fast = (job.xq || job.xf_quantize || f32_input) && lpg && job.n > 0 && job.n % job.gs == 0 &&
               job.ld % 16 == 0 && lds <= 65536 && (job.n + 1023) / 1024 <= 16;
-  // The fused prologue quantizes the FP32 input 4 values per lane (gs <= 256: a group within a wave).
-  fast = fast && (job.xf_quantize ? aligned16(job.xf) && aligned16(job.xq_out) && job.gs <= 256
+  // The fused prologue quantizes the FP32 input 16 values per lane, a group within a wave (lpg <= 64).
+  fast = fast && (job.xf_quantize ? aligned16(job.xf) && aligned16(job.xq_out)
                   : f32_input     ? aligned16(job.xf)
                                   : aligned16(job.xq));
   for (int s = 0; s < job.nseg && fast; s++) {
