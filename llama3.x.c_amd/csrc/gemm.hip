@@ -621,11 +621,19 @@ __global__ __launch_bounds__(256) void bf16_panel(const float *__restrict__ a, l
   const int row = (int)(idx / per_row), c0 = (int)(idx % per_row) * 8;
   const float *src = a + row * lda;
   unsigned packed[4];
+  if (c0 + 8 <= k && ((uintptr_t)(src + c0) & 15) == 0) { // eight values in two 16-byte loads
+    const float4 v0 = *reinterpret_cast<const float4 *>(src + c0), v1 = *reinterpret_cast<const float4 *>(src + c0 + 4);
+    packed[0] = to_bf16(v0.x) | ((unsigned)to_bf16(v0.y) << 16);
+    packed[1] = to_bf16(v0.z) | ((unsigned)to_bf16(v0.w) << 16);
+    packed[2] = to_bf16(v1.x) | ((unsigned)to_bf16(v1.y) << 16);
+    packed[3] = to_bf16(v1.z) | ((unsigned)to_bf16(v1.w) << 16);
+  } else { // the row's tail (zeros past k) or an unaligned row
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int c = c0 + 2 * i;
-    const unsigned lo = c < k ? to_bf16(src[c]) : 0u, hi = c + 1 < k ? to_bf16(src[c + 1]) : 0u;
-    packed[i] = lo | (hi << 16);
+    for (int i = 0; i < 4; i++) {
+      const int c = c0 + 2 * i;
+      const unsigned lo = c < k ? to_bf16(src[c]) : 0u, hi = c + 1 < k ? to_bf16(src[c + 1]) : 0u;
+      packed[i] = lo | (hi << 16);
+    }
   }
   *reinterpret_cast<uint4 *>(panel + (long long)row * kp + c0) = uint4{packed[0], packed[1], packed[2], packed[3]};
 }

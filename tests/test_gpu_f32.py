@@ -212,6 +212,44 @@ def test_bf16_gemm_all_kinds(m, n, k):
         L.aligned_buffer_free(panel)
 
 
+@pytest.mark.parametrize("m,k,lda", [(37, 200, 200), (37, 203, 203), (20, 203, 208), (5, 3072, 3072)])
+def test_bf16_panel_bits(m, k, lda):
+    """The activation panel k_gemm_bf16 writes: row r holds bf16_from_f32 of A's row (the oracle's conversion, taken
+    from its VNNI packing so NaN payloads pass unchanged), zeros from k to the padded width; aligned rows take the
+    16-byte path, odd strides and the row tail the per-value one. Specials: NaN payloads, infinities, denormals,
+    rounding ties and values that round up to infinity."""
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 5 * m + k + lda)
+    a = rng.normal(m * lda, 0.0, 3.0).reshape(m, lda)
+    specials = np.array([0x7FC00001, 0xFF800001, 0x7F800001, 0x7F800000, 0xFF800000, 0x00000001, 0x807FFFFF,
+                         0x3F808000, 0x3F818000, 0xBF808000, 0x7F7FFFFF, 0xFF7FFFFF, 0x00000000, 0x80000000],
+                        np.uint32).view(np.float32)
+    flat = a.reshape(-1)
+    idx = (np.arange(specials.size * 7) * 131) % flat.size
+    flat[idx] = np.tile(specials, 7)
+    kpad = (k + 31) // 32 * 32
+    vnni = orc.pack_bf16_vnni(np.ascontiguousarray(a[:, :k]))
+    r, c = np.meshgrid(np.arange(m), np.arange(k), indexing="ij")
+    want = vnni[(r // 16) * 16 * kpad + (c // 2) * 32 + (r % 16) * 2 + c % 2]
+    n = 16
+    w = rng.uniform(n * k).reshape(n, k)
+    pw = np.zeros(L.bf16_vnni_elements(n, k), np.uint16)
+    L.pack_bf16_vnni(lh.ptr(pw), lh.ptr(w), n, k, k)
+    panel = lh.AlignedBuffer()
+    L.aligned_buffer_alloc(panel, L.k_gemm_bf16_panel_bytes(m, k), 1)
+    da, dpw, out = hu.dev(a), hu.dev(pw), hu.empty((m, n), hu.torch().float32)
+    try:
+        seg = lh.GemmBf16Segment(lh.ptr(out), n, lh.ptr(dpw), None, n, lh.GEMM_STORE)
+        L.k_gemm_bf16(lh.ptr(da), lda, m, k, seg, 1, panel)
+        L.llhip_synchronize()
+        got = np.zeros((m, kpad), np.uint16)
+        L.llhip_memcpy_d2h(got.ctypes.data, panel.data, got.nbytes)
+        assert np.array_equal(got[:, :k], want), np.argwhere(got[:, :k] != want)[:5]
+        assert not got[:, k:].any()
+    finally:
+        L.aligned_buffer_free(panel)
+
+
 def test_bf16_gemm_reference_golden():
     g = np.load(os.path.join(GOLDEN, "bf16.npz"))
     L = hu.lib()
