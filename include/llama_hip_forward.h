@@ -1,0 +1,90 @@
+/* The forward around the matmuls, served on an MI355X (gfx950): RMSNorm, RoPE, the K/V cache and causal attention, so
+ * a device-resident engine keeps its activations in HBM between the matmuls. Drop-in for these declarations of the
+ * reference's include/kernels.h (and the layout selectors of include/testing.h): the same names, argument meaning and
+ * struct layouts, with C linkage. Each declaration cites the one it replaces (LucianCrainic/llama3.x.c file:line).
+ *
+ * Pointers follow llama_hip_kernels.h: device memory in place (stream-ordered, no wait), registered host ranges through
+ * their device copies, other host memory copied in and out around a synchronous call. */
+#ifndef LLAMA_HIP_FORWARD_H
+#define LLAMA_HIP_FORWARD_H
+
+#include <stddef.h>
+
+#include "llama_hip_prefill.h" /* Config (include/runtime.h:9-16): k_rope_table reads head_dim and the rope fields */
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* kernels.h:57-60: out = weight * (ss * x) with ss = 1 / sqrtf(mean(x^2) + epsilon), per row; out may equal x. The
+ * products are the reference's; the sum of squares is reduced in another order (within 1e-6 relative of it). */
+void k_rmsnorm(float *out, const float *x, const float *weight, int size, float epsilon);
+void k_rmsnorm_rows(float *out, const float *x, const float *weight, int rows, int size, float epsilon);
+
+/* kernels.h:61-68: one position's table (2 * head_dim floats: cosines duplicated per pair, then -sin, +sin), computed
+ * on the host with the C library as the reference computes it (src/kernels.c:49-61); and the rotation of q's n_heads and
+ * k's n_kv_heads heads by it, bitwise the reference's (products rounded before the sum). */
+void k_rope_table(const Config *p, int position, float *table);
+void k_rope_apply(float *q, float *k, const float *table, int n_heads, int n_kv_heads, int head_dim);
+void k_rope_apply_rows(float *q, size_t q_stride, float *k, size_t k_stride, const float *table, size_t table_stride,
+                       int rows, int n_heads, int n_kv_heads, int head_dim);
+
+/* kernels.h:127-132: the attention workspace record. The device attention keeps its split-K partials in a library
+ * workspace; this record only carries the shapes (partial is never dereferenced). */
+typedef struct {
+  float *partial;
+  int max_chunks, n_heads, head_dim, workers;
+  int external;
+  size_t capacity;
+} AttentionWork;
+void k_attention_init(AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len); /* kernels.h:133 */
+size_t k_attention_bytes(int n_heads, int n_kv_heads, int head_dim, int seq_len);                   /* kernels.h:135 */
+void k_attention_init_in(AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len,
+                         float *memory);                                                             /* kernels.h:136 */
+size_t k_attention_bytes_rows(int n_heads, int n_kv_heads, int head_dim, int seq_len, int rows);    /* kernels.h:139 */
+void k_attention_init_rows(AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int rows,
+                           float *memory);                                                           /* kernels.h:140 */
+int k_attention_chunk_count(const AttentionWork *work, int n_kv_heads, int position);               /* kernels.h:150 */
+void k_attention_free(AttentionWork *work);                                                          /* kernels.h:151 */
+
+/* kernels.h:146-166: causal attention. q and out hold m rows of n_heads * head_dim floats; row i (position pos0 + i)
+ * attends to positions 0..pos0 + i of its KV head (query head h uses KV head h / (n_heads / n_kv_heads)). Scores are
+ * (q . k) / sqrtf(head_dim), softmax-weighted sums of the values, computed over 64-position chunks merged by their
+ * maxima (the reference's split-K form, src/attention.c:664-682, 841-876). The plain forms read the rows layout
+ * [position][kv_head][head_dim]; _layout takes the strides (position t of KV head g at cache + t * pos_stride +
+ * g * head_base). att is the reference's score scratch and is not used. A non-finite score fails with "nonfinite value
+ * in softmax" (at the next host-visible point when the buffers are device memory). */
+void k_attention(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
+                 AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int position);
+void k_attention_layout(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
+                        AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int position,
+                        size_t pos_stride, size_t head_base);
+void k_attention_batch(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
+                       AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int pos0, int m);
+void k_attention_batch_layout(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
+                              AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int pos0,
+                              int m, size_t pos_stride, size_t head_base);
+
+/* kernels.h:52-53, 168-179: the engine-facing K/V cache of one layer in the active layout (LLAMA_KV_LAYOUT=rows|head,
+ * head-major by default), and k_attention / k_attention_batch on it. */
+int kernels_kv_layout_head(void);
+const char *kernels_kv_layout_name(void);
+void k_kv_strides(int n_kv_heads, int head_dim, int seq_len, size_t *pos_stride, size_t *head_base);
+void k_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,
+                int seq_len);
+void k_attention_kv(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
+                    AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int position);
+void k_attention_batch_kv(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
+                          AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int pos0, int m);
+
+/* kernels.h:46-47 and testing.h: the attention kernels' names ("split" for both: one device kernel) and the test-time
+ * selectors, which accept the reference's names (tiled / split, split / group; rows / head). */
+const char *kernels_attention_name(void);
+const char *kernels_attention_decode_name(void);
+int kernels_attention_select(const char *batch, const char *decode);
+int kernels_kv_layout_select(const char *name);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -23,7 +23,7 @@ struct Device {
   bool ready = false;
   int ordinal = 0;
   hipStream_t stream = nullptr;
-  int *error_flags = nullptr; // device: [0] non-finite activation seen by a quantizer
+  int *error_flags = nullptr; // device: [0] non-finite activation seen by a quantizer, [1] non-finite attention score
   int cu_count = 0;
   bool capturing = false;
   void *split_partial = nullptr;  // split-K partial tiles: LLHIP_SPLIT_SLOTS x 256 x 128 floats
@@ -37,6 +37,8 @@ bool ensure_device(); // opens the device on first use; false (after raise) when
 // Waits for the stream and turns a device-side error flag into a failure (the reference fails at once; a device
 // kernel can only report at the next host-visible point).
 bool synchronize_and_check();
+// Host memory that is neither device memory nor inside a registered range: written in place by host-side entry points.
+bool plain_host_memory(const void *p, size_t bytes);
 
 // ---- pointer residency ------------------------------------------------------------------------------------------
 // Every pointer an entry point receives is resolved once per call: device memory is used in place, host memory
@@ -153,6 +155,25 @@ struct F32GemvJob {
   Epilogue epi;
 };
 bool launch_f32_gemv(const F32GemvJob &job, hipStream_t stream);
+
+// ---- the forward around the matmuls (forward.hip) ------------------------------------------------------------------
+bool launch_rmsnorm(float *out, const float *x, const float *weight, int rows, int size, float epsilon,
+                    hipStream_t stream);
+bool launch_rope(float *q, size_t q_stride, float *k, size_t k_stride, const float *table, size_t table_stride,
+                 int rows, int n_heads, int n_kv_heads, int head_dim, hipStream_t stream);
+bool launch_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,
+                     size_t pos_stride, size_t head_base, hipStream_t stream);
+// Causal attention of `rows` query rows at positions pos0 .. pos0 + rows - 1 (q and out: rows x n_heads x head_dim);
+// position t of KV head g at key / value + t * pos_stride + g * head_base.
+struct AttentionJob {
+  float *out;
+  const float *q, *key, *value;
+  int n_heads, n_kv_heads, head_dim, pos0, rows;
+  size_t pos_stride, head_base;
+};
+bool attention_shape_ok(int n_heads, int n_kv_heads, int head_dim); // kv_mul <= 16, head_dim <= 256
+size_t attention_partial_floats(int rows, int n_heads, int head_dim, int last_position);
+bool launch_attention(const AttentionJob &job, float *partial, hipStream_t stream);
 
 struct GemmSegmentDev {
   float *c;

@@ -1,0 +1,316 @@
+// The forward around the matmuls on gfx950: RMSNorm, RoPE, the K/V cache store and causal attention (decode and
+// batched), so activations can stay in HBM between layers. Citations are LucianCrainic/llama3.x.c file:line.
+//
+//   rmsnorm_rows   one block per row: the sum of squares reduced over the block, then out = w * (ss * x) in the
+//                  reference's operation order (src/kernels.c:8-21). HBM-bound: 8 bytes read + 4 written per value.
+//   rope_rows      one thread per (row, head, pair), products rounded before the sum (no fused multiply-add), so the
+//                  result is bitwise the reference's (src/kernels_simd.c:203-225).
+//   kv_store       a strided copy into the rows or head-major cache layout (src/attention.c:1420-1432).
+//   attn_chunks    split-K attention: one block per (query row, KV head, chunk of kChunk positions) scores the
+//                  chunk for every query head of the group (the K row read once serves kv_mul heads), keeps the
+//                  chunk's maximum and sum of exponentials and the unnormalized value sum (src/attention.c:841-876);
+//                  attn_merge rescales the chunks by exp(m_c - M) and normalizes (src/attention.c:664-682).
+//                  HBM-bound on the K/V cache: 8 * kv_dim bytes per position and query row.
+#include <cfloat>
+
+#include "common.h"
+
+namespace llhip {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;
+constexpr int kChunk = 64;      // positions per attention block
+constexpr int kMaxHeadDim = 256;
+constexpr int kMaxGroup = 16;   // query heads per KV head
+
+bool launch_ok(const char *what) {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess || raise("launching %s failed: %s", what, hipGetErrorString(e));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+    v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+    v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// ---- RMSNorm -----------------------------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void rmsnorm_rows(float *__restrict__ out, const float *__restrict__ x,
+                                                         const float *__restrict__ weight, int size, float epsilon) {
+  __shared__ float part[kThreads / kWave];
+  const float *row = x + (size_t)blockIdx.x * size;
+  float *o = out + (size_t)blockIdx.x * size;
+  float ss = 0.0f;
+  for (int j = threadIdx.x; j < size; j += kThreads)
+    ss = fmaf(row[j], row[j], ss);
+  ss = wave_sum(ss);
+  if ((threadIdx.x & (kWave - 1)) == 0)
+    part[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  ss = part[0] + part[1] + part[2] + part[3];
+  // src/kernels.c:15-17, the same three roundings (correctly rounded division and square root)
+  ss /= size;
+  ss += epsilon;
+  ss = 1.0f / sqrtf(ss);
+  // out may be x: each value is read by the thread that writes it, after every thread's sum is in
+  for (int j = threadIdx.x; j < size; j += kThreads)
+    o[j] = weight[j] * (ss * row[j]);
+}
+
+// ---- RoPE ---------------------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ void rotate(float *v, float c, float s) {
+#pragma clang fp contract(off) // a*c - b*s and a*s + b*c with the products rounded, as the reference computes them
+  const float a = v[0], b = v[1];
+  v[0] = a * c - b * s;
+  v[1] = a * s + b * c;
+}
+
+// Thread i: row i / (n_heads * half), head and pair from the rest; k is rotated for heads below n_kv_heads.
+__global__ __launch_bounds__(kThreads) void rope_rows(float *__restrict__ q, size_t q_stride, float *__restrict__ k,
+                                                      size_t k_stride, const float *__restrict__ table,
+                                                      size_t table_stride, int rows, int n_heads, int n_kv_heads,
+                                                      int head_dim) {
+  const int half = head_dim / 2;
+  const long long per_row = (long long)n_heads * half;
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= per_row * rows)
+    return;
+  const int row = (int)(i / per_row), rest = (int)(i % per_row);
+  const int h = rest / half, j = 2 * (rest % half);
+  const float *t = table + (size_t)row * table_stride;
+  const float c = t[j], s = t[head_dim + j + 1];
+  rotate(q + (size_t)row * q_stride + (size_t)h * head_dim + j, c, s);
+  if (h < n_kv_heads)
+    rotate(k + (size_t)row * k_stride + (size_t)h * head_dim + j, c, s);
+}
+
+// ---- K/V cache store ------------------------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void kv_store(float *__restrict__ cache, const float *__restrict__ src,
+                                                     size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,
+                                                     size_t pos_stride, size_t head_base) {
+  const long long kv_dim = (long long)n_kv_heads * head_dim;
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= kv_dim * count)
+    return;
+  const int r = (int)(i / kv_dim), rest = (int)(i % kv_dim);
+  const int g = rest / head_dim, d = rest % head_dim;
+  cache[(size_t)(pos0 + r) * pos_stride + (size_t)g * head_base + d] = src[(size_t)r * src_ld + rest];
+}
+
+// ---- attention ------------------------------------------------------------------------------------------------------
+
+struct AttnParams {
+  float *out;
+  const float *q, *key, *value;
+  float *partial; // [row][head][chunk][head_dim + 2]: unnormalized value sum, chunk maximum, chunk sum
+  int *flags;
+  int n_heads, n_kv_heads, head_dim, pos0, chunks; // chunks: per row, for the last row's position
+  size_t pos_stride, head_base;
+  float divisor; // sqrtf(head_dim)
+};
+
+// Block (chunk c, KV head g, query row r). Waves take positions t0 + w, t0 + w + 4, ...: lane l holds dimensions
+// l, l + 64, ... of the K row, dots it with each query head of the group held the same way, and the wave sum over the
+// lanes gives the score, (dot) / sqrtf(head_dim) like the reference. Then per head the chunk maximum, the
+// exponentials and their sum; then thread i accumulates dimension i % head_dim of the value sum for every head over a
+// share of the positions, the shares meeting in LDS.
+__global__ __launch_bounds__(kThreads) void attn_chunks(AttnParams p) {
+  static_assert(kChunk == kWave, "a chunk's scores are one per lane");
+  __shared__ float score[kMaxGroup][kChunk];
+  __shared__ float acc[kThreads * kMaxGroup]; // the value-sum shares: [share][head][head_dim], shares * head_dim <= 256
+  const int c = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+  const int position = p.pos0 + r, positions = position + 1;
+  const int t0 = c * kChunk;
+  if (t0 >= positions)
+    return; // beyond this row's causal range: the merge reads only the row's own chunks
+  const int t1 = min(positions, t0 + kChunk);
+  const int kv_mul = p.n_heads / p.n_kv_heads, hd = p.head_dim;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const float *qrow = p.q + (size_t)r * p.n_heads * hd + (size_t)g * kv_mul * hd;
+  const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
+  constexpr int kDims = kMaxHeadDim / kWave;
+  float qv[kMaxGroup][kDims];
+#pragma unroll
+  for (int h = 0; h < kMaxGroup; h++)
+#pragma unroll
+    for (int e = 0; e < kDims; e++) {
+      const int d = lane + e * kWave;
+      qv[h][e] = h < kv_mul && d < hd ? qrow[(size_t)h * hd + d] : 0.0f;
+    }
+  bool bad = false;
+  for (int t = t0 + wave; t < t1; t += kThreads / kWave) {
+    const float *krow = kbase + (size_t)t * p.pos_stride;
+    float kd[kDims];
+#pragma unroll
+    for (int e = 0; e < kDims; e++) {
+      const int d = lane + e * kWave;
+      kd[e] = d < hd ? krow[d] : 0.0f;
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) {
+      if (h < kv_mul) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kDims; e++)
+          dot = fmaf(qv[h][e], kd[e], dot);
+        const float s = wave_sum(dot) / p.divisor;
+        bad |= !isfinite(s);
+        if (lane == 0)
+          score[h][t - t0] = s;
+      }
+    }
+  }
+  if (bad && lane == 0)
+    p.flags[1] = 1;
+  __syncthreads();
+  // per head (wave w takes heads w, w + 4, ...): the chunk maximum, the exponentials in place and their sum
+  const int n = t1 - t0;
+  float *part = p.partial + ((size_t)(r * p.n_heads + g * kv_mul) * p.chunks + c) * (hd + 2);
+  for (int h = wave; h < kv_mul; h += kThreads / kWave) {
+    const float s = lane < n ? score[h][lane] : -FLT_MAX;
+    const float m = wave_max(s);
+    const float e = lane < n ? expf(s - m) : 0.0f;
+    score[h][lane] = e;
+    const float l = wave_sum(e);
+    if (lane == 0) {
+      float *ph = part + (size_t)h * p.chunks * (hd + 2);
+      ph[hd] = m;
+      ph[hd + 1] = l;
+    }
+  }
+  __syncthreads();
+  // value sums: thread i owns dimension d = i % hd (hd <= 256) for every head, over positions t0 + share, + shares ...
+  const int shares = kThreads / hd > 0 ? kThreads / hd : 1;
+  const int d = threadIdx.x % hd, share = threadIdx.x / hd;
+  float o[kMaxGroup];
+#pragma unroll
+  for (int h = 0; h < kMaxGroup; h++)
+    o[h] = 0.0f;
+  if (share < shares) {
+    for (int t = t0 + share; t < t1; t += shares) {
+      const float v = vbase[(size_t)t * p.pos_stride + d];
+#pragma unroll
+      for (int h = 0; h < kMaxGroup; h++)
+        if (h < kv_mul)
+          o[h] = fmaf(score[h][t - t0], v, o[h]);
+    }
+  }
+  if (shares == 1) { // hd > 128: threads past hd own nothing
+    if (share == 0) {
+#pragma unroll
+      for (int h = 0; h < kMaxGroup; h++)
+        if (h < kv_mul)
+          part[(size_t)h * p.chunks * (hd + 2) + d] = o[h];
+    }
+    return;
+  }
+  // shares > 1 (hd <= 128): the shares' sums meet in LDS, share order
+  float *sh = acc; // [share][head][hd]
+  if (share < shares) {
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++)
+      if (h < kv_mul)
+        sh[((size_t)share * kv_mul + h) * hd + d] = o[h];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kv_mul * hd; i += kThreads) {
+    const int h = i / hd, dd = i % hd;
+    float total = 0.0f;
+    for (int s2 = 0; s2 < shares; s2++)
+      total += sh[((size_t)s2 * kv_mul + h) * hd + dd];
+    part[(size_t)h * p.chunks * (hd + 2) + dd] = total;
+  }
+}
+
+// Block (head h, query row r): M = max over the row's chunks of m_c, weight_c = expf(m_c - M), L = sum of
+// weight_c * l_c, out = (sum of weight_c * o_c) / L, chunks in order.
+__global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int hd = p.head_dim, chunks = (p.pos0 + r) / kChunk + 1;
+  const float *part = p.partial + ((size_t)(r * p.n_heads + h) * p.chunks) * (hd + 2);
+  float m = part[hd];
+  for (int c = 1; c < chunks; c++)
+    m = fmaxf(m, part[(size_t)c * (hd + 2) + hd]);
+  for (int d = threadIdx.x; d < hd; d += kThreads) {
+    float sum = 0.0f, o = 0.0f;
+    for (int c = 0; c < chunks; c++) {
+      const float *pc = part + (size_t)c * (hd + 2);
+      const float w = expf(pc[hd] - m);
+      sum += w * pc[hd + 1];
+      o += w * pc[d];
+    }
+    p.out[((size_t)r * p.n_heads + h) * hd + d] = o / sum;
+  }
+}
+
+} // namespace
+
+bool launch_rmsnorm(float *out, const float *x, const float *weight, int rows, int size, float epsilon,
+                    hipStream_t stream) {
+  hipLaunchKernelGGL(rmsnorm_rows, dim3((unsigned)rows), dim3(kThreads), 0, stream, out, x, weight, size, epsilon);
+  return launch_ok("rmsnorm_rows");
+}
+
+bool launch_rope(float *q, size_t q_stride, float *k, size_t k_stride, const float *table, size_t table_stride,
+                 int rows, int n_heads, int n_kv_heads, int head_dim, hipStream_t stream) {
+  const long long threads = (long long)rows * n_heads * (head_dim / 2);
+  hipLaunchKernelGGL(rope_rows, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream, q,
+                     q_stride, k, k_stride, table, table_stride, rows, n_heads, n_kv_heads, head_dim);
+  return launch_ok("rope_rows");
+}
+
+bool launch_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,
+                     size_t pos_stride, size_t head_base, hipStream_t stream) {
+  const long long threads = (long long)count * n_kv_heads * head_dim;
+  hipLaunchKernelGGL(kv_store, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream, cache,
+                     src, src_ld, pos0, count, n_kv_heads, head_dim, pos_stride, head_base);
+  return launch_ok("kv_store");
+}
+
+size_t attention_partial_floats(int rows, int n_heads, int head_dim, int last_position) {
+  const size_t chunks = (size_t)last_position / kChunk + 1;
+  return (size_t)rows * n_heads * chunks * ((size_t)head_dim + 2);
+}
+
+bool attention_shape_ok(int n_heads, int n_kv_heads, int head_dim) {
+  return n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= kMaxGroup && head_dim > 0 &&
+         head_dim <= kMaxHeadDim;
+}
+
+bool launch_attention(const AttentionJob &job, float *partial, hipStream_t stream) {
+  AttnParams p{};
+  p.out = job.out;
+  p.q = job.q;
+  p.key = job.key;
+  p.value = job.value;
+  p.partial = partial;
+  p.flags = device().error_flags;
+  p.n_heads = job.n_heads;
+  p.n_kv_heads = job.n_kv_heads;
+  p.head_dim = job.head_dim;
+  p.pos0 = job.pos0;
+  p.chunks = (job.pos0 + job.rows - 1) / kChunk + 1;
+  p.pos_stride = job.pos_stride;
+  p.head_base = job.head_base;
+  p.divisor = sqrtf((float)job.head_dim);
+  hipLaunchKernelGGL(attn_chunks, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, (unsigned)job.rows),
+                     dim3(kThreads), 0, stream, p);
+  if (!launch_ok("attn_chunks"))
+    return false;
+  hipLaunchKernelGGL(attn_merge, dim3((unsigned)job.n_heads, (unsigned)job.rows), dim3(kThreads), 0, stream, p);
+  return launch_ok("attn_merge");
+}
+
+} // namespace llhip

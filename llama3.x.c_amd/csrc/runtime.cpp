@@ -118,10 +118,10 @@ bool synchronize_and_check() {
   int flags[16];
   if (!LLHIP_CHECK(hipMemcpy(flags, dev.error_flags, sizeof(flags), hipMemcpyDeviceToHost)))
     return false;
-  if (flags[0]) {
+  if (flags[0] || flags[1]) {
     int zero[16] = {0};
     (void)hipMemcpy(dev.error_flags, zero, sizeof(zero), hipMemcpyHostToDevice);
-    return raise("nonfinite activation during INT8 quantization");
+    return raise(flags[0] ? "nonfinite activation during INT8 quantization" : "nonfinite value in softmax");
   }
   return true;
 }
@@ -260,6 +260,8 @@ Ref Call::stage(void *host, size_t row_bytes, size_t pitch, size_t rows, bool to
   copies_[ncopies_] = Copy{host, offset, row_bytes, pitch, rows, to_device, to_host};
   return Ref{nullptr, ncopies_++};
 }
+
+bool plain_host_memory(const void *p, size_t bytes) { return !lookup(p) && device_extent(p, bytes) == 0; }
 
 void *Call::address(const Ref &r) const {
   return r.staged < 0 ? r.direct : (void *)((char *)arena + copies_[r.staged].offset);

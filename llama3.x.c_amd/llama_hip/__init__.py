@@ -100,7 +100,39 @@ RowsDoneFn = ctypes.CFUNCTYPE(None, P, I32, I32)
 SegmentFn = ctypes.CFUNCTYPE(None, P, I32, I32, I32)
 FailFn = ctypes.CFUNCTYPE(None, ctypes.c_char_p)
 
+class AttentionWork(ctypes.Structure):  # kernels.h:127-132
+    _fields_ = [("partial", P), ("max_chunks", I32), ("n_heads", I32), ("head_dim", I32), ("workers", I32),
+                ("external", I32), ("capacity", SZ)]
+
+
 _SIGNATURES = {
+    # the forward around the matmuls (llama_hip_forward.h)
+    "k_rmsnorm": (None, [P, P, P, I32, ctypes.c_float]),
+    "k_rmsnorm_rows": (None, [P, P, P, I32, I32, ctypes.c_float]),
+    "k_rope_table": (None, [P, I32, P]),
+    "k_rope_apply": (None, [P, P, P, I32, I32, I32]),
+    "k_rope_apply_rows": (None, [P, SZ, P, SZ, P, SZ, I32, I32, I32, I32]),
+    "kernels_kv_layout_head": (I32, []),
+    "kernels_kv_layout_name": (ctypes.c_char_p, []),
+    "kernels_kv_layout_select": (I32, [ctypes.c_char_p]),
+    "k_kv_strides": (None, [I32, I32, I32, P, P]),
+    "k_kv_store": (None, [P, P, SZ, I32, I32, I32, I32, I32]),
+    "k_attention_init": (None, [P, I32, I32, I32, I32]),
+    "k_attention_bytes": (SZ, [I32, I32, I32, I32]),
+    "k_attention_init_in": (None, [P, I32, I32, I32, I32, P]),
+    "k_attention_bytes_rows": (SZ, [I32, I32, I32, I32, I32]),
+    "k_attention_init_rows": (None, [P, I32, I32, I32, I32, I32, P]),
+    "k_attention_chunk_count": (I32, [P, I32, I32]),
+    "k_attention_free": (None, [P]),
+    "k_attention": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32]),
+    "k_attention_layout": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, SZ, SZ]),
+    "k_attention_batch": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, I32]),
+    "k_attention_batch_layout": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, SZ, SZ]),
+    "k_attention_kv": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32]),
+    "k_attention_batch_kv": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, I32]),
+    "kernels_attention_name": (ctypes.c_char_p, []),
+    "kernels_attention_decode_name": (ctypes.c_char_p, []),
+    "kernels_attention_select": (I32, [ctypes.c_char_p, ctypes.c_char_p]),
     # kernels.h surface
     "kernels_init": (None, []),
     "kernels_select": (I32, [I32]),

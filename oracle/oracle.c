@@ -304,6 +304,98 @@ void orc_matmul_q8_threads(float *out, const int8_t *xq, const float *xs, const 
   free(jobs);
 }
 
+/* ---- the forward around the matmuls ------------------------------------------------------------------------- */
+
+/* src/kernels.c:8-21 */
+void orc_rmsnorm(float *out, const float *x, const float *weight, int size, float epsilon) {
+  float ss = 0.0f;
+  for (int j = 0; j < size; j++)
+    ss += x[j] * x[j];
+  ss /= size;
+  ss += epsilon;
+  ss = 1.0f / sqrtf(ss);
+  for (int j = 0; j < size; j++)
+    out[j] = weight[j] * (ss * x[j]);
+}
+
+/* src/kernels_simd.c:212-225 (the products round before the sum: this file is built with -ffp-contract=off). */
+static void rope_pair(float *v, int i, float c, float s) {
+  const float a = v[i], b = v[i + 1];
+  v[i] = a * c - b * s;
+  v[i + 1] = a * s + b * c;
+}
+
+void orc_rope_apply(float *q, float *k, const float *table, int n_heads, int n_kv_heads, int head_dim) {
+  const float *sines = table + head_dim;
+  for (int h = 0; h < n_heads; h++)
+    for (int j = 0; j < head_dim; j += 2) {
+      const float c = table[j], s = sines[j + 1];
+      rope_pair(q, h * head_dim + j, c, s);
+      if (h < n_kv_heads)
+        rope_pair(k, h * head_dim + j, c, s);
+    }
+}
+
+/* src/attention.c:1420-1432 */
+void orc_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,
+                  size_t pos_stride, size_t head_base) {
+  for (int r = 0; r < count; r++)
+    for (int g = 0; g < n_kv_heads; g++)
+      memcpy(cache + (size_t)(pos0 + r) * pos_stride + (size_t)g * head_base, src + (size_t)r * src_ld + (size_t)g * head_dim,
+             (size_t)head_dim * sizeof(float));
+}
+
+/* src/kernels.c:23-45 */
+static int softmax(float *x, int size) {
+  float max_val = x[0];
+  if (!isfinite(max_val))
+    return -1;
+  for (int i = 1; i < size; i++) {
+    if (!isfinite(x[i]))
+      return -1;
+    if (x[i] > max_val)
+      max_val = x[i];
+  }
+  float sum = 0.0f;
+  for (int i = 0; i < size; i++) {
+    x[i] = expf(x[i] - max_val);
+    sum += x[i];
+  }
+  for (int i = 0; i < size; i++)
+    x[i] /= sum;
+  return 0;
+}
+
+/* src/attention.c:606-641 */
+int orc_attention(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
+                  int n_heads, int n_kv_heads, int head_dim, int seq_len, int position, size_t pos_stride,
+                  size_t head_base) {
+  const int kv_mul = n_heads / n_kv_heads;
+  for (int h = 0; h < n_heads; h++) {
+    const float *qh = q + (size_t)h * head_dim;
+    float *a = att + (size_t)h * seq_len;
+    for (int t = 0; t <= position; t++) {
+      const float *k = key_cache + (size_t)t * pos_stride + (size_t)(h / kv_mul) * head_base;
+      float score = 0.0f;
+      for (int i = 0; i < head_dim; i++)
+        score += qh[i] * k[i];
+      score /= sqrtf(head_dim);
+      a[t] = score;
+    }
+    if (softmax(a, position + 1))
+      return -1;
+    float *xb = out + (size_t)h * head_dim;
+    memset(xb, 0, (size_t)head_dim * sizeof(float));
+    for (int t = 0; t <= position; t++) {
+      const float *v = value_cache + (size_t)t * pos_stride + (size_t)(h / kv_mul) * head_base;
+      const float w = a[t];
+      for (int i = 0; i < head_dim; i++)
+        xb[i] += w * v[i];
+    }
+  }
+  return 0;
+}
+
 /* ---- seeded synthetic inputs ------------------------------------------------------------------------------------- */
 
 uint64_t orc_rng_next(uint64_t *state) {

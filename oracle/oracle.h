@@ -91,6 +91,28 @@ void orc_matmul_q8_threads(float *out, const int8_t *xq, const float *xs, const 
                            int d, int gs, int threads);
 
 
+/* ---- the device-resident forward around the matmuls (RMSNorm, RoPE, the K/V cache, attention) ------------------- */
+
+/* src/kernels.c:8-21 (rmsnorm_eps): ss = sum of x[j] * x[j] in index order, ss /= size, ss += epsilon,
+ * ss = 1 / sqrtf(ss); out[j] = weight[j] * (ss * x[j]). out may equal x. */
+void orc_rmsnorm(float *out, const float *x, const float *weight, int size, float epsilon);
+/* src/kernels_simd.c:203-225 (scalar k_rope_apply): per head and pair j, c = table[j], s = table[head_dim + j + 1],
+ * (a, b) -> (a*c - b*s, a*s + b*c), products rounded before the sum (no fused multiply-add); k for the first
+ * n_kv_heads heads. */
+void orc_rope_apply(float *q, float *k, const float *table, int n_heads, int n_kv_heads, int head_dim);
+/* src/attention.c:1420-1432: `count` rows of n_kv_heads * head_dim floats (row stride src_ld) to positions pos0..,
+ * at cache + t * pos_stride + g * head_base for KV head g (rows layout: pos_stride = kv_dim, head_base = head_dim;
+ * head-major: pos_stride = head_dim, head_base = seq_len * head_dim). */
+void orc_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,
+                  size_t pos_stride, size_t head_base);
+/* src/attention.c:606-641 with softmax src/kernels.c:23-45 (the scalar decode): per head h (KV head h / kv_mul),
+ * score[t] = (sum_i q[i] * k_t[i]) / sqrtf(head_dim) for t = 0..position in index order, softmax (max, expf(x - max),
+ * their sum, then each divided by it), out = sum_t w_t * v_t accumulated in t order. Returns -1 (the reference's fail)
+ * when a score is not finite. att holds n_heads rows of seq_len scores. */
+int orc_attention(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
+                  int n_heads, int n_kv_heads, int head_dim, int seq_len, int position, size_t pos_stride,
+                  size_t head_base);
+
 /* ---- seeded synthetic inputs (shared by the golden-vector script, the tests and bench.py's CPU leg) ---------------
  * The reference tests' generator, tests/q8.c:19-30: xorshift64 (shifts 13, 7, 17) from seed 88172645463325252, and
  * uniform() = (float)((double)(x >> 40) / 2^24) * 2 - 1. orc_fill_normal draws N(mean, std) by Box-Muller from pairs

@@ -58,6 +58,10 @@ def _declare(L):
         "orc_pack_s8_vnni": (None, [P, P, i32, i32, sz]),
         "orc_gemm_bf16": (None, [P, i32, i32, i32, P, i32, P, P, i32, i32]),
         "orc_matmul_q8_threads": (None, [P, P, P, P, P, i32, i32, i32, i32]),
+        "orc_rmsnorm": (None, [P, P, P, i32, f32]),
+        "orc_rope_apply": (None, [P, P, P, i32, i32, i32]),
+        "orc_kv_store": (None, [P, P, sz, i32, i32, i32, i32, sz, sz]),
+        "orc_attention": (i32, [P, P, P, P, P, i32, i32, i32, i32, i32, sz, sz]),
         "orc_rng_next": (u64, [P]),
         "orc_rng_uniform": (f32, [P]),
         "orc_fill_uniform": (None, [P, sz, P, f32]),
@@ -179,6 +183,38 @@ def gemm_bf16(a, pw, n, kind=GEMM_STORE, c=None, pw3=None):
     c = np.zeros((m, n), np.float32) if c is None else c
     lib().orc_gemm_bf16(ptr(a), a.strides[0] // 4, m, k, ptr(c), c.strides[0] // 4, ptr(pw), ptr(pw3), n, kind)
     return c
+
+
+def rmsnorm(x, weight, eps=1e-5):
+    """k_rmsnorm / k_rmsnorm_rows (src/kernels.c:8-21), row by row; x (size,) or (rows, size)."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    rows = x.reshape(-1, x.shape[-1])
+    o = out.reshape(rows.shape)
+    for r in range(rows.shape[0]):
+        lib().orc_rmsnorm(ptr(o[r]), ptr(rows[r]), ptr(weight), rows.shape[1], eps)
+    return out
+
+
+def rope_apply(q, k, table, n_heads, n_kv_heads, head_dim):
+    """k_rope_apply (src/kernels_simd.c:203-225) on copies of one row's q and k."""
+    q, k = np.array(q, np.float32), np.array(k, np.float32)
+    lib().orc_rope_apply(ptr(q), ptr(k), ptr(np.ascontiguousarray(table, np.float32)), n_heads, n_kv_heads, head_dim)
+    return q, k
+
+
+def kv_strides(n_kv_heads, head_dim, seq_len, head_major):
+    """(pos_stride, head_base) of the rows or head-major K/V layout (src/attention.c:1415-1418)."""
+    return (head_dim, seq_len * head_dim) if head_major else (n_kv_heads * head_dim, head_dim)
+
+
+def attention(q, key_cache, value_cache, n_heads, n_kv_heads, head_dim, seq_len, position, pos_stride, head_base):
+    """The scalar decode attention (src/attention.c:606-641) for one position; None where the reference fails."""
+    out = np.zeros(n_heads * head_dim, np.float32)
+    att = np.zeros(n_heads * seq_len, np.float32)
+    rc = lib().orc_attention(ptr(out), ptr(np.ascontiguousarray(q, np.float32)), ptr(key_cache), ptr(value_cache),
+                             ptr(att), n_heads, n_kv_heads, head_dim, seq_len, position, pos_stride, head_base)
+    return None if rc else out
 
 
 def quantize_weights(w, gs):

@@ -305,11 +305,102 @@ def bf16_cases(L):
     return out
 
 
+class Config(ctypes.Structure):  # include/runtime.h:9-16
+    _fields_ = [(f, ctypes.c_int) for f in ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size",
+                                           "seq_len", "format", "max_seq_len", "shared", "head_dim")] + \
+               [(f, ctypes.c_float) for f in ("norm_eps", "rope_theta", "rope_factor", "rope_low", "rope_high")] + \
+               [(f, ctypes.c_int) for f in ("rope_type", "rope_original", "bos_id", "eos_id", "eot_id", "eom_id")] + \
+               [("name", ctypes.c_char * 128)]
+
+
+class AttentionWork(ctypes.Structure):  # include/kernels.h:127-132
+    _fields_ = [("partial", P), ("max_chunks", ctypes.c_int), ("n_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+                ("workers", ctypes.c_int), ("external", ctypes.c_int), ("capacity", ctypes.c_size_t)]
+
+
+def rope_config(head_dim, llama3):
+    c = Config()
+    c.head_dim = head_dim
+    if llama3:  # Llama 3.1 scaling
+        c.rope_theta, c.rope_type, c.rope_factor, c.rope_low, c.rope_high, c.rope_original = 500000.0, 1, 8.0, 1.0, 4.0, 8192
+    else:
+        c.rope_theta, c.rope_type = 10000.0, 0
+    return c
+
+
+def forward_cases(L):
+    """The forward around the matmuls on the scalar instruction set: k_rmsnorm and _rows (src/kernels.c:8-21,
+    src/kernels_simd.c:247-255), k_rope_table and k_rope_apply (src/kernels_simd.c:194-225), the decode attention
+    k_attention / k_attention_layout (src/attention.c:606-641, 1362-1377) and the batched k_attention_batch
+    (src/attention.c:1379-1384)."""
+    rng = orc.Rng(orc.SEED + 900)
+    out = {}
+    assert L.kernels_select(KERNELS_SCALAR)
+    for size in (1, 100, 2048, 3072, 4096):
+        x, w = rng.normal(size, 0.0, 2.0), rng.normal(size, 1.0, 0.1)
+        o = np.zeros(size, np.float32)
+        L.k_rmsnorm(ptr(o), ptr(x), ptr(w), size, ctypes.c_float(1e-5))
+        out[f"rms{size}/x"], out[f"rms{size}/w"], out[f"rms{size}/out"] = x, w, o
+    xr, wr = rng.normal(3 * 512, 0.0, 1.0).reshape(3, 512), rng.normal(512, 1.0, 0.1)
+    orow = np.zeros_like(xr)
+    L.k_rmsnorm_rows(ptr(orow), ptr(xr), ptr(wr), 3, 512, ctypes.c_float(1e-5))
+    out["rmsrows/x"], out["rmsrows/w"], out["rmsrows/out"] = xr, wr, orow
+    for hd, llama3 in ((128, True), (64, False)):
+        cfg = rope_config(hd, llama3)
+        for pos in (0, 1, 7, 1000, 8191, 100000):
+            t = np.zeros(2 * hd, np.float32)
+            L.k_rope_table(ctypes.byref(cfg), pos, ptr(t))
+            out[f"ropetab{hd}_{pos}/table"] = t
+        t = out[f"ropetab{hd}_1000/table"]
+        nh, nkv = 8, 2
+        q, k = rng.normal(nh * hd, 0.0, 1.0), rng.normal(nkv * hd, 0.0, 1.0)
+        out[f"rope{hd}/q"], out[f"rope{hd}/k"] = q.copy(), k.copy()
+        L.k_rope_apply(ptr(q), ptr(k), ptr(t), nh, nkv, hd)
+        out[f"rope{hd}/q_out"], out[f"rope{hd}/k_out"] = q, k
+    for (nh, nkv, hd, seq, pos) in ((4, 2, 16, 8, 0), (4, 2, 16, 8, 7), (8, 2, 64, 48, 47), (32, 8, 128, 20, 19)):
+        key = f"att{nh}_{nkv}_{hd}_{seq}_{pos}"
+        kv_dim = nkv * hd
+        kc, vc = rng.normal(seq * kv_dim, 0.0, 1.0), rng.normal(seq * kv_dim, 0.0, 1.0)
+        q = rng.normal(nh * hd, 0.0, 1.0)
+        work = AttentionWork()
+        L.k_attention_init(ctypes.byref(work), nh, nkv, hd, seq)
+        att = np.zeros(nh * seq, np.float32)
+        o = np.zeros(nh * hd, np.float32)
+        L.k_attention(ptr(o), ptr(q), ptr(kc), ptr(vc), ptr(att), ctypes.byref(work), nh, nkv, hd, seq, pos)
+        # the same cache values in the head-major layout [kv_head][position][head_dim]
+        kh = np.ascontiguousarray(kc.reshape(seq, nkv, hd).transpose(1, 0, 2)).reshape(-1)
+        vh = np.ascontiguousarray(vc.reshape(seq, nkv, hd).transpose(1, 0, 2)).reshape(-1)
+        oh = np.zeros(nh * hd, np.float32)
+        L.k_attention_layout(ptr(oh), ptr(q), ptr(kh), ptr(vh), ptr(att), ctypes.byref(work), nh, nkv, hd, seq, pos,
+                             ctypes.c_size_t(hd), ctypes.c_size_t(seq * hd))
+        assert np.array_equal(o.view(np.uint32), oh.view(np.uint32)), key
+        out[f"{key}/k"], out[f"{key}/v"], out[f"{key}/q"], out[f"{key}/out"] = kc, vc, q, o
+        L.k_attention_free(ctypes.byref(work))
+    # batched: m rows at positions pos0 .. pos0 + m - 1 over a cache holding all of them
+    nh, nkv, hd, seq, pos0, m = 8, 2, 64, 48, 20, 6
+    kv_dim = nkv * hd
+    kc, vc = rng.normal(seq * kv_dim, 0.0, 1.0), rng.normal(seq * kv_dim, 0.0, 1.0)
+    q = rng.normal(m * nh * hd, 0.0, 1.0)
+    work = AttentionWork()
+    L.k_attention_bytes_rows.restype = ctypes.c_size_t
+    mem = np.zeros(L.k_attention_bytes_rows(nh, nkv, hd, seq, m) // 4 + 16, np.float32)
+    L.k_attention_init_rows(ctypes.byref(work), nh, nkv, hd, seq, m, ptr(mem))
+    att = np.zeros(m * nh * seq, np.float32)
+    o = np.zeros(m * nh * hd, np.float32)
+    L.k_attention_batch(ptr(o), ptr(q), ptr(kc), ptr(vc), ptr(att), ctypes.byref(work), nh, nkv, hd, seq, pos0, m)
+    out["attbatch/k"], out["attbatch/v"], out["attbatch/q"], out["attbatch/out"] = kc, vc, q, o
+    out["attbatch/shape"] = np.array([nh, nkv, hd, seq, pos0, m], np.int32)
+    return out
+
+
 def main():
     L = load_reference()
     groups = {"quantize": quantize_cases, "gemv_q8": gemv_cases, "gemm_q8": gemm_q8_cases, "f32": f32_cases,
-              "bf16": bf16_cases}
+              "bf16": bf16_cases, "forward": forward_cases}
+    only = sys.argv[1:]
     for name, fn in groups.items():
+        if only and name not in only:
+            continue
         data = fn(L)
         path = os.path.join(HERE, f"{name}.npz")
         np.savez_compressed(path, **data)

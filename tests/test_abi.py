@@ -56,6 +56,7 @@ def test_struct_layouts_match_the_reference():
     assert ctypes.sizeof(lh.PackBf16) == 32 and ctypes.sizeof(lh.PackS8) == 32
     assert ctypes.sizeof(lh.TensorDesc) == 56 and ctypes.sizeof(lh.Shard) == 80 and lh.Shard.q.offset == 56
     assert ctypes.sizeof(lh.Config) == 44 + 20 + 24 + 128
+    assert ctypes.sizeof(lh.AttentionWork) == 40 and lh.AttentionWork.capacity.offset == 32
     assert lh.Model.max_batch.offset == ctypes.sizeof(lh.Config) + 4 + 8 + 8 + 8 - 4 or lh.Model.max_batch.offset > 0
 
 
@@ -70,11 +71,13 @@ def test_reference_headers_agree_on_layouts():
 #include "gemm.h"
 #include "prefill.h"
 #include "shards.h"
+#include "kernels.h"
 int main(void) {
-  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(K8Weight), sizeof(K8Input),
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(K8Weight), sizeof(K8Input),
          sizeof(GemmSegment), sizeof(GemmBf16Segment), sizeof(GemmQ8Segment), sizeof(AlignedBuffer), sizeof(Config),
          sizeof(Model), sizeof(TensorDesc), sizeof(Shard), sizeof(PackS8), offsetof(Shard, ld),
-         offsetof(Model, max_batch), offsetof(Model, prefill_bf16));
+         offsetof(Model, max_batch), offsetof(Model, prefill_bf16), sizeof(AttentionWork),
+         offsetof(AttentionWork, capacity));
   return 0;
 }
 '''
@@ -88,7 +91,8 @@ int main(void) {
     sizes = [int(v) for v in subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()]
     mine = [ctypes.sizeof(c) for c in (lh.K8Weight, lh.K8Input, lh.GemmSegment, lh.GemmBf16Segment, lh.GemmQ8Segment,
                                        lh.AlignedBuffer, lh.Config, lh.Model, lh.TensorDesc, lh.Shard, lh.PackS8)]
-    mine += [lh.Shard.ld.offset, lh.Model.max_batch.offset, lh.Model.prefill_bf16.offset]
+    mine += [lh.Shard.ld.offset, lh.Model.max_batch.offset, lh.Model.prefill_bf16.offset, ctypes.sizeof(lh.AttentionWork),
+             lh.AttentionWork.capacity.offset]
     assert sizes == mine
 
 

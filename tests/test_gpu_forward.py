@@ -1,0 +1,272 @@
+"""GPU parity of the forward around the matmuls through the C ABI: RMSNorm, RoPE (table and rotation), the K/V cache
+store and causal attention (decode and batched, rows and head-major layouts).
+
+The oracle (oracle/, pinned bitwise to the reference's scalar kernels by tests/test_oracle.py) is the checker. The bar:
+RoPE, its table and the cache store are bitwise the reference's; RMSNorm differs only in the order of its sum of squares
+(relative 1e-5); attention sums scores, exponentials and values in other orders (split over 64-position chunks, as the
+reference's own split-K form does), so it is checked against a float64 evaluation within 1e-5 of sum_t w_t |v_t| plus
+1e-6, and against the oracle within twice that.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import llama_hip as lh
+from oracle import pyoracle as orc
+from tests import hip_util as hu
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    yield L
+
+
+def golden():
+    return np.load(os.path.join(GOLDEN, "forward.npz"))
+
+
+# ---- RMSNorm ---------------------------------------------------------------------------------------------------------
+
+
+def test_rmsnorm_golden_device_host_and_in_place():
+    L = hu.lib()
+    g = golden()
+    for size in (1, 100, 2048, 3072, 4096):
+        x, w, want = g[f"rms{size}/x"], g[f"rms{size}/w"], g[f"rms{size}/out"]
+        tol = 1e-5 * np.abs(want) + 1e-7
+        out = np.zeros_like(x)
+        L.k_rmsnorm(lh.ptr(out), lh.ptr(x), lh.ptr(w), size, 1e-5)  # host buffers
+        assert np.all(np.abs(out - want) <= tol), size
+        dx, dw = hu.dev(x), hu.dev(w)
+        L.k_rmsnorm(lh.ptr(dx), lh.ptr(dx), lh.ptr(dw), size, 1e-5)  # device, in place
+        assert np.all(np.abs(hu.host(dx) - want) <= tol), size
+    x, w, want = g["rmsrows/x"], g["rmsrows/w"], g["rmsrows/out"]
+    dx, dw, do = hu.dev(x), hu.dev(w), hu.empty(x.shape, hu.torch().float32)
+    L.k_rmsnorm_rows(lh.ptr(do), lh.ptr(dx), lh.ptr(dw), 3, 512, 1e-5)
+    assert np.all(np.abs(hu.host(do) - want) <= 1e-5 * np.abs(want) + 1e-7)
+
+
+@pytest.mark.parametrize("rows,size", [(1, 8192), (64, 4096), (7, 1000)])
+def test_rmsnorm_rows_against_oracle(rows, size):
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + rows * 13 + size)
+    x, w = rng.normal(rows * size, 0.0, 2.0).reshape(rows, size), rng.normal(size, 1.0, 0.2)
+    want = orc.rmsnorm(x, w, 1e-6)
+    dx, dw, do = hu.dev(x), hu.dev(w), hu.empty((rows, size), hu.torch().float32)
+    L.k_rmsnorm_rows(lh.ptr(do), lh.ptr(dx), lh.ptr(dw), rows, size, 1e-6)
+    assert np.all(np.abs(hu.host(do) - want) <= 1e-5 * np.abs(want) + 1e-7)
+
+
+# ---- RoPE --------------------------------------------------------------------------------------------------------------
+
+
+def rope_config(head_dim, llama3):
+    c = lh.Config()
+    c.head_dim = head_dim
+    if llama3:
+        c.rope_theta, c.rope_type, c.rope_factor, c.rope_low, c.rope_high, c.rope_original = 500000.0, 1, 8.0, 1.0, 4.0, 8192
+    else:
+        c.rope_theta, c.rope_type = 10000.0, 0
+    return c
+
+
+def test_rope_table_bitwise_host_and_device():
+    """k_rope_table runs on the host with the C library, as the reference does: bitwise its tables (Llama 3.1 scaling at
+    head_dim 128, plain theta 10000 at 64), written to host memory in place and to device memory by a copy."""
+    L = hu.lib()
+    g = golden()
+    for hd, llama3 in ((128, True), (64, False)):
+        cfg = rope_config(hd, llama3)
+        for pos in (0, 1, 7, 1000, 8191, 100000):
+            want = g[f"ropetab{hd}_{pos}/table"]
+            t = np.zeros(2 * hd, np.float32)
+            L.k_rope_table(ctypes.byref(cfg), pos, lh.ptr(t))
+            assert np.array_equal(hu.bits(t), hu.bits(want)), (hd, pos)
+            dt = hu.empty(2 * hd, hu.torch().float32)
+            L.k_rope_table(ctypes.byref(cfg), pos, lh.ptr(dt))
+            assert np.array_equal(hu.bits(hu.host(dt)), hu.bits(want)), (hd, pos)
+
+
+def test_rope_apply_bitwise_golden_and_rows():
+    L = hu.lib()
+    g = golden()
+    for hd in (128, 64):
+        q, k, t = g[f"rope{hd}/q"].copy(), g[f"rope{hd}/k"].copy(), g[f"ropetab{hd}_1000/table"]
+        L.k_rope_apply(lh.ptr(q), lh.ptr(k), lh.ptr(t), 8, 2, hd)  # host buffers
+        assert np.array_equal(hu.bits(q), hu.bits(g[f"rope{hd}/q_out"]))
+        assert np.array_equal(hu.bits(k), hu.bits(g[f"rope{hd}/k_out"]))
+        dq, dk, dt = hu.dev(g[f"rope{hd}/q"]), hu.dev(g[f"rope{hd}/k"]), hu.dev(t)
+        L.k_rope_apply(lh.ptr(dq), lh.ptr(dk), lh.ptr(dt), 8, 2, hd)
+        assert np.array_equal(hu.bits(hu.host(dq)), hu.bits(g[f"rope{hd}/q_out"]))
+        assert np.array_equal(hu.bits(hu.host(dk)), hu.bits(g[f"rope{hd}/k_out"]))
+    # rows with padded strides: each row bitwise the oracle's single-row rotation with its own table
+    rng = orc.Rng(orc.SEED + 505)
+    rows, nh, nkv, hd = 5, 8, 2, 64
+    qs, ks, ts = nh * hd + 16, nkv * hd + 8, 2 * hd + 4
+    q, k, t = rng.normal(rows * qs, 0, 1).reshape(rows, qs), rng.normal(rows * ks, 0, 1).reshape(rows, ks), \
+        rng.normal(rows * ts, 0, 1).reshape(rows, ts)
+    dq, dk, dt = hu.dev(q), hu.dev(k), hu.dev(t)
+    L.k_rope_apply_rows(lh.ptr(dq), qs, lh.ptr(dk), ks, lh.ptr(dt), ts, rows, nh, nkv, hd)
+    gq, gk = hu.host(dq), hu.host(dk)
+    for r in range(rows):
+        wq, wk = orc.rope_apply(q[r, :nh * hd], k[r, :nkv * hd], t[r, :2 * hd], nh, nkv, hd)
+        assert np.array_equal(hu.bits(gq[r, :nh * hd]), hu.bits(wq)) and np.array_equal(hu.bits(gk[r, :nkv * hd]), hu.bits(wk))
+        assert np.array_equal(hu.bits(gq[r, nh * hd:]), hu.bits(q[r, nh * hd:]))  # row padding untouched
+        assert np.array_equal(hu.bits(gk[r, nkv * hd:]), hu.bits(k[r, nkv * hd:]))
+
+
+# ---- the K/V cache -----------------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("layout", ["rows", "head"])
+def test_kv_store_both_layouts(layout):
+    L = hu.lib()
+    assert L.kernels_kv_layout_select(layout.encode()) == 1
+    try:
+        assert L.kernels_kv_layout_name() == layout.encode()
+        nkv, hd, seq, pos0, count, ld = 4, 32, 50, 17, 6, 4 * 32 + 8
+        ps, hb = ctypes.c_size_t(), ctypes.c_size_t()
+        L.k_kv_strides(nkv, hd, seq, ctypes.byref(ps), ctypes.byref(hb))
+        assert (ps.value, hb.value) == orc.kv_strides(nkv, hd, seq, layout == "head")
+        rng = orc.Rng(orc.SEED + 606)
+        cache0 = rng.normal(seq * nkv * hd, 0, 1)
+        src = rng.normal(count * ld, 0, 1).reshape(count, ld)
+        want = cache0.copy()
+        orc.lib().orc_kv_store(orc.ptr(want), orc.ptr(src), ld, pos0, count, nkv, hd, ps.value, hb.value)
+        dc, ds = hu.dev(cache0), hu.dev(src)
+        L.k_kv_store(lh.ptr(dc), lh.ptr(ds), ld, pos0, count, nkv, hd, seq)
+        assert np.array_equal(hu.bits(hu.host(dc)), hu.bits(want))
+        hc = cache0.copy()  # host cache
+        L.k_kv_store(lh.ptr(hc), lh.ptr(src), ld, pos0, count, nkv, hd, seq)
+        assert np.array_equal(hu.bits(hc), hu.bits(want))
+    finally:
+        L.kernels_kv_layout_select(b"head")
+
+
+# ---- attention ---------------------------------------------------------------------------------------------------------
+
+
+def attention_f64(q, kc, vc, nh, nkv, hd, pos, ps, hb):
+    """float64 decode attention and the magnitude sum_t w_t |v_t| per output."""
+    kv_mul = nh // nkv
+    q = q.astype(np.float64).reshape(nh, hd)
+    out, mag = np.zeros((nh, hd)), np.zeros((nh, hd))
+    t = np.arange(pos + 1)
+    for h in range(nh):
+        base = (h // kv_mul) * hb
+        idx = base + t[:, None] * ps + np.arange(hd)[None, :]
+        K, V = kc[idx].astype(np.float64), vc[idx].astype(np.float64)
+        s = K @ q[h] / np.sqrt(hd)
+        w = np.exp(s - s.max())
+        w /= w.sum()
+        out[h], mag[h] = w @ V, w @ np.abs(V)
+    return out.reshape(-1), mag.reshape(-1)
+
+
+def check_attention(got, q, kc, vc, nh, nkv, hd, seq, pos, ps, hb, what):
+    ref, mag = attention_f64(q, kc, vc, nh, nkv, hd, pos, ps, hb)
+    tol = 1e-5 * mag + 1e-6
+    assert np.all(np.abs(got - ref) <= tol), (what, np.max(np.abs(got - ref) - tol))
+    orc_out = orc.attention(q, kc, vc, nh, nkv, hd, seq, pos, ps, hb)
+    assert np.all(np.abs(got - orc_out) <= 2 * tol), what
+
+
+def test_attention_golden_cases_both_layouts():
+    L = hu.lib()
+    g = golden()
+    for key in sorted({k.split("/")[0] for k in g.files if k.startswith("att") and not k.startswith("attbatch")}):
+        nh, nkv, hd, seq, pos = (int(v) for v in key[3:].split("_"))
+        q, kc, vc = g[f"{key}/q"], g[f"{key}/k"], g[f"{key}/v"]
+        work = lh.AttentionWork()
+        L.k_attention_init(ctypes.byref(work), nh, nkv, hd, seq)
+        out = np.zeros(nh * hd, np.float32)
+        L.k_attention(lh.ptr(out), lh.ptr(q), lh.ptr(kc), lh.ptr(vc), None, ctypes.byref(work), nh, nkv, hd, seq, pos)
+        ps, hb = orc.kv_strides(nkv, hd, seq, False)
+        check_attention(out, q, kc, vc, nh, nkv, hd, seq, pos, ps, hb, key)
+        assert np.all(np.abs(out - g[f"{key}/out"]) <= 2e-5 * np.abs(vc).max() + 1e-6), key
+        kh = np.ascontiguousarray(kc.reshape(seq, nkv, hd).transpose(1, 0, 2)).reshape(-1)
+        vh = np.ascontiguousarray(vc.reshape(seq, nkv, hd).transpose(1, 0, 2)).reshape(-1)
+        dq, dk, dv, do = hu.dev(q), hu.dev(kh), hu.dev(vh), hu.empty(nh * hd, hu.torch().float32)
+        L.k_attention_kv(lh.ptr(do), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), None, ctypes.byref(work), nh, nkv, hd, seq,
+                         pos)  # the default head-major layout
+        ps, hb = orc.kv_strides(nkv, hd, seq, True)
+        check_attention(hu.host(do), q, kh, vh, nh, nkv, hd, seq, pos, ps, hb, key + " head")
+        L.k_attention_free(ctypes.byref(work))
+
+
+@pytest.mark.parametrize("nh,nkv,hd,seq,positions", [(32, 8, 128, 600, (0, 63, 64, 65, 599)),
+                                                     (8, 8, 64, 200, (1, 127, 199)), (12, 4, 96, 130, (129,)),
+                                                     (16, 1, 256, 70, (69,)), (4, 2, 32, 40, (39,))])
+def test_attention_decode_shapes(nh, nkv, hd, seq, positions):
+    """Decode attention at chunk boundaries (63, 64, 65) and GQA ratios 1-16, head_dim 32-256, head-major layout."""
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + nh * 31 + hd + seq)
+    kc, vc = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1)
+    dk, dv = hu.dev(kc), hu.dev(vc)
+    ps, hb = orc.kv_strides(nkv, hd, seq, True)
+    for pos in positions:
+        q = rng.normal(nh * hd, 0, 1)
+        dq, do = hu.dev(q), hu.empty(nh * hd, hu.torch().float32)
+        L.k_attention_layout(lh.ptr(do), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), None, None, nh, nkv, hd, seq, pos, ps, hb)
+        check_attention(hu.host(do), q, kc, vc, nh, nkv, hd, seq, pos, ps, hb, f"pos {pos}")
+
+
+@pytest.mark.parametrize("nh,nkv,hd,seq,pos0,m", [(8, 2, 64, 48, 20, 6), (32, 8, 128, 300, 0, 130),
+                                                  (32, 8, 128, 300, 100, 64)])
+def test_attention_batch_rows(nh, nkv, hd, seq, pos0, m):
+    """k_attention_batch: row i attends to positions 0..pos0 + i, each row as the decode attention at its position; the
+    reference's own batched output on the golden case."""
+    L = hu.lib()
+    g = golden()
+    rng = orc.Rng(orc.SEED + 700 + m)
+    if (nh, nkv, hd, seq, pos0, m) == tuple(int(v) for v in g["attbatch/shape"]):
+        kc, vc, q = g["attbatch/k"], g["attbatch/v"], g["attbatch/q"]
+    else:
+        kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(m * nh * hd, 0, 1)
+    dq, dk, dv, do = hu.dev(q), hu.dev(kc), hu.dev(vc), hu.empty(m * nh * hd, hu.torch().float32)
+    L.k_attention_batch(lh.ptr(do), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), None, None, nh, nkv, hd, seq, pos0, m)
+    got = hu.host(do).reshape(m, -1)
+    ps, hb = orc.kv_strides(nkv, hd, seq, False)
+    for i in range(m):
+        check_attention(got[i], q.reshape(m, -1)[i], kc, vc, nh, nkv, hd, seq, pos0 + i, ps, hb, f"row {i}")
+    if (nh, nkv, hd, seq, pos0, m) == tuple(int(v) for v in g["attbatch/shape"]):
+        assert np.all(np.abs(got.reshape(-1) - g["attbatch/out"]) <= 2e-5 * np.abs(vc).max() + 1e-6)
+
+
+def test_attention_nonfinite_score_fails_and_bookkeeping():
+    L = hu.lib()
+    lh.record_failures()
+    try:
+        nh, nkv, hd, seq = 4, 2, 16, 10
+        rng = orc.Rng(orc.SEED + 808)
+        kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(nh * hd, 0, 1)
+        kc[5 * nkv * hd + 3] = np.inf
+        out = np.zeros(nh * hd, np.float32)
+        L.k_attention(lh.ptr(out), lh.ptr(q), lh.ptr(kc), lh.ptr(vc), None, None, nh, nkv, hd, seq, seq - 1)
+        assert "nonfinite value in softmax" in lh.last_error()
+        L.llhip_clear_error()
+        L.k_attention(lh.ptr(out), lh.ptr(q), lh.ptr(kc), lh.ptr(vc), None, None, nh, nkv, hd, seq, 4)  # before it
+        assert lh.last_error() == ""
+        L.k_attention(lh.ptr(out), lh.ptr(q), lh.ptr(kc), lh.ptr(vc), None, None, nh, nkv, hd, seq, seq)
+        assert "outside the cache" in lh.last_error()
+        L.llhip_clear_error()
+        L.k_attention(lh.ptr(out), lh.ptr(q), lh.ptr(kc), lh.ptr(vc), None, None, 6, 4, hd, seq, 3)
+        assert "not supported" in lh.last_error()
+        L.llhip_clear_error()
+    finally:
+        L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+        L.llhip_clear_error()
+    work = lh.AttentionWork()
+    L.k_attention_init(ctypes.byref(work), 32, 8, 128, 8192)
+    assert work.max_chunks == 128 and work.n_heads == 32 and work.head_dim == 128 and not work.partial
+    assert L.k_attention_chunk_count(ctypes.byref(work), 8, 63) == 1 and L.k_attention_chunk_count(None, 8, 64) == 2
+    assert L.k_attention_bytes(32, 8, 128, 8192) == 32 * 128 * 130 * 4
+    L.k_attention_free(ctypes.byref(work))
+    assert L.kernels_attention_select(b"tiled", b"group") == 1 and L.kernels_attention_select(b"x", None) == 0

@@ -16,6 +16,14 @@ How each oracle function is pinned:
   orc_pack_*_vnni       golden packed bytes from the reference's packers.
   orc_gemm_bf16         golden outputs of the reference's portable k_gemm_bf16.
   Rng                   the digest of the regenerated C1 inputs equals the one the reference run stored.
+  orc_rmsnorm           golden outputs of the reference's scalar k_rmsnorm and k_rmsnorm_rows (bitwise); the constant
+                        vector's closed form; a fresh odd size against the live reference.
+  orc_rope_apply        golden outputs of the reference's scalar k_rope_apply on its own k_rope_table (bitwise); pair
+                        norms kept; rotations compose (angle a then b equals a + b).
+  orc_attention         golden outputs of the reference's scalar decode attention in the rows and head-major layouts
+                        and of its batched k_attention_batch, row by row (bitwise); one position returns its value row;
+                        equal keys give the mean value; a non-finite score fails; fresh positions against the live
+                        reference.
 """
 import hashlib
 import os
@@ -300,3 +308,121 @@ def test_oracle_equals_live_reference_on_fresh_inputs():
         L.k_matmul_q8(mg.ptr(y_ref), ctypes.byref(mg.K8Input(mg.ptr(q), mg.ptr(s), mg.ptr(x))),
                       mg.K8Weight(mg.ptr(wq), mg.ptr(ws)), n, d, gs)
         assert np.array_equal(bits(orc.matmul_q8(q, s, wq, ws, gs)), bits(y_ref))
+
+
+# ---- the forward around the matmuls ---------------------------------------------------------------------------------
+
+
+def test_rmsnorm_matches_reference_golden_and_closed_form():
+    """orc_rmsnorm is bitwise the reference's scalar k_rmsnorm / k_rmsnorm_rows (src/kernels.c:8-21); a constant
+    vector c normalizes to w * c / sqrt(c^2 + eps) (float64 within 1e-6)."""
+    g = load("forward")
+    for size in (1, 100, 2048, 3072, 4096):
+        got = orc.rmsnorm(g[f"rms{size}/x"], g[f"rms{size}/w"])
+        assert np.array_equal(bits(got), bits(g[f"rms{size}/out"])), size
+    assert np.array_equal(bits(orc.rmsnorm(g["rmsrows/x"], g["rmsrows/w"])), bits(g["rmsrows/out"]))
+    x, w = np.full(512, 3.0, np.float32), np.linspace(0.5, 1.5, 512).astype(np.float32)
+    want = w.astype(np.float64) * 3.0 / np.sqrt(9.0 + 1e-5)
+    assert np.allclose(orc.rmsnorm(x, w), want, rtol=1e-6, atol=0)
+
+
+def test_rope_matches_reference_golden_and_rotation():
+    """orc_rope_apply is bitwise the reference's scalar k_rope_apply on the reference's own k_rope_table (Llama 3.1
+    scaling at head_dim 128, plain theta 10000 at 64); the rotation keeps each pair's norm and composes: the table of
+    angle a then b equals the table of a + b (float64, 1e-5)."""
+    g = load("forward")
+    for hd in (128, 64):
+        q, k = orc.rope_apply(g[f"rope{hd}/q"], g[f"rope{hd}/k"], g[f"ropetab{hd}_1000/table"], 8, 2, hd)
+        assert np.array_equal(bits(q), bits(g[f"rope{hd}/q_out"])) and np.array_equal(bits(k), bits(g[f"rope{hd}/k_out"]))
+        n0 = np.hypot(g[f"rope{hd}/q"][0::2].astype(np.float64), g[f"rope{hd}/q"][1::2])
+        n1 = np.hypot(q[0::2].astype(np.float64), q[1::2])
+        assert np.allclose(n0, n1, rtol=1e-5)
+    hd = 16
+    ang_a, ang_b = np.linspace(0.1, 1.5, hd // 2), np.linspace(-0.7, 0.9, hd // 2)
+
+    def table(ang):
+        t = np.zeros(2 * hd, np.float32)
+        t[0:hd:2] = t[1:hd:2] = np.cos(ang)
+        t[hd::2], t[hd + 1::2] = -np.sin(ang), np.sin(ang)
+        return t
+
+    v = np.linspace(-1, 1, hd).astype(np.float32)
+    q1, _ = orc.rope_apply(v, v[:0], table(ang_a), 1, 0, hd)
+    q2, _ = orc.rope_apply(q1, v[:0], table(ang_b), 1, 0, hd)
+    q3, _ = orc.rope_apply(v, v[:0], table(ang_a + ang_b), 1, 0, hd)
+    assert np.allclose(q2, q3, atol=1e-5)
+
+
+def test_attention_matches_reference_golden_and_closed_forms():
+    """orc_attention is bitwise the reference's scalar decode attention (src/attention.c:606-641) in the rows and
+    head-major layouts and, row by row, its batched k_attention_batch; closed forms: one position returns its value
+    row, equal keys give the mean of the values, adding a constant to every score (a key component along q) changes
+    nothing, and a non-finite score fails."""
+    g = load("forward")
+    for key in cases(g, "/out"):
+        if not key.startswith("att") or key == "attbatch":
+            continue
+        nh, nkv, hd, seq, pos = (int(v) for v in key[3:].split("_"))
+        for head_major in (False, True):
+            kc, vc = g[f"{key}/k"], g[f"{key}/v"]
+            if head_major:
+                kc = np.ascontiguousarray(kc.reshape(seq, nkv, hd).transpose(1, 0, 2)).reshape(-1)
+                vc = np.ascontiguousarray(vc.reshape(seq, nkv, hd).transpose(1, 0, 2)).reshape(-1)
+            ps, hb = orc.kv_strides(nkv, hd, seq, head_major)
+            got = orc.attention(g[f"{key}/q"], kc, vc, nh, nkv, hd, seq, pos, ps, hb)
+            assert np.array_equal(bits(got), bits(g[f"{key}/out"])), (key, head_major)
+    nh, nkv, hd, seq, pos0, m = (int(v) for v in g["attbatch/shape"])
+    ps, hb = orc.kv_strides(nkv, hd, seq, False)
+    q = g["attbatch/q"].reshape(m, -1)
+    rows = [orc.attention(q[i], g["attbatch/k"], g["attbatch/v"], nh, nkv, hd, seq, pos0 + i, ps, hb) for i in range(m)]
+    assert np.array_equal(bits(np.concatenate(rows)), bits(g["attbatch/out"]))
+    rng = orc.Rng(orc.SEED + 950)
+    nh, nkv, hd, seq = 4, 2, 8, 10
+    kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(nh * hd, 0, 1)
+    ps, hb = orc.kv_strides(nkv, hd, seq, False)
+    out = orc.attention(q, kc, vc, nh, nkv, hd, seq, 0, ps, hb).reshape(nh, hd)
+    v0 = vc.reshape(seq, nkv, hd)[0]
+    assert np.array_equal(out, v0[np.arange(nh) // (nh // nkv)])
+    same = np.tile(kc.reshape(seq, nkv * hd)[:1], (seq, 1)).reshape(-1)
+    out = orc.attention(q, same, vc, nh, nkv, hd, seq, seq - 1, ps, hb).reshape(nh, hd)
+    mean = vc.reshape(seq, nkv, hd).astype(np.float64).mean(axis=0)[np.arange(nh) // (nh // nkv)]
+    assert np.allclose(out, mean, atol=1e-6)
+    bad = kc.copy()
+    bad[3 * nkv * hd] = np.inf
+    assert orc.attention(q, bad, vc, nh, nkv, hd, seq, seq - 1, ps, hb) is None
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(orc.REF_DIR, "libllama_ref.so")),
+                    reason="oracle/_ref not built (the reference sources are absent)")
+def test_forward_oracle_equals_live_reference():
+    """Fresh shapes against the reference built from its sources: rmsnorm (odd size), rope (head_dim 32), decode
+    attention at several positions in both layouts, all bitwise on the scalar instruction set."""
+    import ctypes
+    L = ctypes.CDLL(os.path.join(orc.REF_DIR, "libllama_ref.so"))
+    L.kernels_select.restype = ctypes.c_int
+    assert L.kernels_select(0)
+    P = ctypes.c_void_p
+    ptr = lambda a: a.ctypes.data_as(P)
+    rng = orc.Rng(orc.SEED + 977)
+    x, w = rng.normal(777, 0, 3), rng.normal(777, 1, 0.2)
+    o = np.zeros(777, np.float32)
+    L.k_rmsnorm(ptr(o), ptr(x), ptr(w), 777, ctypes.c_float(1e-6))
+    assert np.array_equal(bits(orc.rmsnorm(x, w, 1e-6)), bits(o))
+    hd, nh, nkv = 32, 6, 3
+    t = rng.normal(2 * hd, 0, 1)
+    q, k = rng.normal(nh * hd, 0, 1), rng.normal(nkv * hd, 0, 1)
+    oq, ok = orc.rope_apply(q, k, t, nh, nkv, hd)
+    L.k_rope_apply(ptr(q), ptr(k), ptr(t), nh, nkv, hd)
+    assert np.array_equal(bits(oq), bits(q)) and np.array_equal(bits(ok), bits(k))
+    nh, nkv, hd, seq = 6, 2, 24, 70
+    kc, vc = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1)
+    att = np.zeros(nh * seq, np.float32)
+    work = (ctypes.c_char * 64)()
+    L.k_attention_init(work, nh, nkv, hd, seq)
+    for pos in (0, 5, 63, 64, 69):
+        q = rng.normal(nh * hd, 0, 1)
+        o = np.zeros(nh * hd, np.float32)
+        L.k_attention(ptr(o), ptr(q), ptr(kc), ptr(vc), ptr(att), work, nh, nkv, hd, seq, pos)
+        ps, hb = orc.kv_strides(nkv, hd, seq, False)
+        assert np.array_equal(bits(orc.attention(q, kc, vc, nh, nkv, hd, seq, pos, ps, hb)), bits(o)), pos
+    L.k_attention_free(work)
