@@ -114,12 +114,106 @@ __global__ __launch_bounds__(kThreads) void kv_store(float *__restrict__ cache, 
 struct AttnParams {
   float *out;
   const float *q, *key, *value;
-  float *partial; // [row][head][chunk][head_dim + 2]: unnormalized value sum, chunk maximum, chunk sum
+  float *partial; // [row][head][chunk][slot]: unnormalized value sum, chunk maximum, chunk sum (slot = head_dim + 2
+                  // rounded up to 4 floats, so every slot starts 16-byte aligned)
   int *flags;
   int n_heads, n_kv_heads, head_dim, pos0, chunks; // chunks: per row, for the last row's position
+  int rows, tile_rows;                              // query rows, and rows per attn_tile block
+  int slot;                                         // floats per partial
   size_t pos_stride, head_base;
   float divisor; // sqrtf(head_dim)
 };
+
+constexpr int kTileThreads = 512;
+constexpr int kTileWaves = kTileThreads / kWave;
+constexpr int kMaxQv = 64; // query vectors (tile rows x the group's query heads) per attn_tile block
+
+// The aligned form (head_dim % 4 == 0, 16-byte aligned rows): block (chunk c, KV head g, tile of tile_rows query rows).
+// The chunk's K rows and the tile's query vectors are staged in LDS (K rows padded to head_dim + 4 floats, so lane t's
+// 16-byte reads of row t fall on distinct banks); wave w scores query vectors w, w + 8, ... with lane t taking position
+// t0 + t (one dot per lane, no cross-lane sum), masks positions past each row's own (causal), and keeps the chunk
+// maximum, the exponentials and their sum; then each work item (query vector, four dimensions) sums the
+// exponential-weighted V rows staged beside K. The K and V rows of a chunk are read once, all loads in flight
+// together, for all tile_rows x kv_mul query vectors.
+__global__ __launch_bounds__(kTileThreads) void attn_tile(AttnParams p) {
+  extern __shared__ __align__(16) float lds[];
+  const int c = blockIdx.x, g = blockIdx.y, r0 = blockIdx.z * p.tile_rows;
+  const int nrows = min(p.tile_rows, p.rows - r0);
+  const int last = p.pos0 + r0 + nrows - 1; // the tile's last position
+  const int t0 = c * kChunk;
+  if (t0 > last)
+    return; // no row of the tile reaches this chunk; the merge reads only each row's own chunks
+  const int n = min(kChunk, last + 1 - t0);
+  const int kv_mul = p.n_heads / p.n_kv_heads, hd = p.head_dim, hd4 = hd / 4, kst = hd + 4;
+  const int nqv = nrows * kv_mul;
+  float *ks = lds, *vs = ks + kChunk * kst, *qs = vs + kChunk * hd, *es = qs + p.tile_rows * kv_mul * hd;
+  const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
+  // every K and V load of the chunk is issued before any is waited for; V lands while the scores are computed
+  for (int i = threadIdx.x; i < n * hd4; i += kTileThreads) {
+    const int t = i / hd4, d4 = i % hd4;
+    const size_t at = (size_t)(t0 + t) * p.pos_stride + 4 * d4;
+    const float4 kv = *reinterpret_cast<const float4 *>(kbase + at), vv = *reinterpret_cast<const float4 *>(vbase + at);
+    *reinterpret_cast<float4 *>(ks + t * kst + 4 * d4) = kv;
+    *reinterpret_cast<float4 *>(vs + t * hd + 4 * d4) = vv;
+  }
+  for (int i = threadIdx.x; i < nqv * hd4; i += kTileThreads) {
+    const int qv = i / hd4, d4 = i % hd4, j = qv / kv_mul, h = qv % kv_mul;
+    *reinterpret_cast<float4 *>(qs + qv * hd + 4 * d4) = *reinterpret_cast<const float4 *>(
+        p.q + ((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * hd + 4 * d4);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  bool bad = false;
+  for (int qv = wave; qv < nqv; qv += kTileWaves) {
+    const int j = qv / kv_mul, h = qv % kv_mul, pos = p.pos0 + r0 + j;
+    const bool live = lane < n && t0 + lane <= pos;
+    float s = -FLT_MAX;
+    if (live) {
+      const float *kr = ks + lane * kst, *qr = qs + qv * hd;
+      float dot = 0.0f;
+      for (int i = 0; i < hd; i += 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(kr + i), b = *reinterpret_cast<const float4 *>(qr + i);
+        dot = fmaf(a.x, b.x, dot);
+        dot = fmaf(a.y, b.y, dot);
+        dot = fmaf(a.z, b.z, dot);
+        dot = fmaf(a.w, b.w, dot);
+      }
+      s = dot / p.divisor;
+      bad |= !isfinite(s);
+    }
+    const float m = wave_max(s);
+    const float e = live ? expf(s - m) : 0.0f;
+    es[qv * kChunk + lane] = e;
+    const float l = wave_sum(e);
+    if (lane == 0 && t0 <= pos) {
+      float *ph = p.partial + (((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * p.chunks + c) * p.slot;
+      ph[hd] = m;
+      ph[hd + 1] = l;
+    }
+  }
+  if (bad)
+    p.flags[1] = 1;
+  __syncthreads();
+  // value sums: work item (query vector, 4 consecutive dimensions), the exponentials of its row against the V rows
+  for (int it = threadIdx.x; it < nqv * hd4; it += kTileThreads) {
+    const int qv = it / hd4, d4 = it % hd4, j = qv / kv_mul, h = qv % kv_mul;
+    if (t0 > p.pos0 + r0 + j)
+      continue; // this row does not reach the chunk
+    const float *er = es + qv * kChunk, *vr = vs + 4 * d4;
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < n; t++) {
+      const float e = er[t];
+      const float4 v = *reinterpret_cast<const float4 *>(vr + t * hd);
+      acc.x = fmaf(e, v.x, acc.x);
+      acc.y = fmaf(e, v.y, acc.y);
+      acc.z = fmaf(e, v.z, acc.z);
+      acc.w = fmaf(e, v.w, acc.w);
+    }
+    *reinterpret_cast<float4 *>(p.partial +
+                                (((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * p.chunks + c) * p.slot +
+                                4 * d4) = acc;
+  }
+}
 
 // Block (chunk c, KV head g, query row r). Waves take positions t0 + w, t0 + w + 4, ...: lane l holds dimensions
 // l, l + 64, ... of the K row, dots it with each query head of the group held the same way, and the wave sum over the
@@ -177,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunks(AttnParams p) {
   __syncthreads();
   // per head (wave w takes heads w, w + 4, ...): the chunk maximum, the exponentials in place and their sum
   const int n = t1 - t0;
-  float *part = p.partial + ((size_t)(r * p.n_heads + g * kv_mul) * p.chunks + c) * (hd + 2);
+  float *part = p.partial + ((size_t)(r * p.n_heads + g * kv_mul) * p.chunks + c) * p.slot;
   for (int h = wave; h < kv_mul; h += kThreads / kWave) {
     const float s = lane < n ? score[h][lane] : -FLT_MAX;
     const float m = wave_max(s);
@@ -185,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunks(AttnParams p) {
     score[h][lane] = e;
     const float l = wave_sum(e);
     if (lane == 0) {
-      float *ph = part + (size_t)h * p.chunks * (hd + 2);
+      float *ph = part + (size_t)h * p.chunks * p.slot;
       ph[hd] = m;
       ph[hd + 1] = l;
     }
@@ -212,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunks(AttnParams p) {
 #pragma unroll
       for (int h = 0; h < kMaxGroup; h++)
         if (h < kv_mul)
-          part[(size_t)h * p.chunks * (hd + 2) + d] = o[h];
+          part[(size_t)h * p.chunks * p.slot + d] = o[h];
     }
     return;
   }
@@ -230,28 +324,59 @@ __global__ __launch_bounds__(kThreads) void attn_chunks(AttnParams p) {
     float total = 0.0f;
     for (int s2 = 0; s2 < shares; s2++)
       total += sh[((size_t)s2 * kv_mul + h) * hd + dd];
-    part[(size_t)h * p.chunks * (hd + 2) + dd] = total;
+    part[(size_t)h * p.chunks * p.slot + dd] = total;
   }
 }
 
 // Block (head h, query row r): M = max over the row's chunks of m_c, weight_c = expf(m_c - M), L = sum of
-// weight_c * l_c, out = (sum of weight_c * o_c) / L, chunks in order.
+// weight_c * l_c, out = (sum of weight_c * o_c) / L. The chunks are spread over the threads (every load in flight at
+// once, not one chunk after another): the maxima and weights by chunk, the value sums by (dimension, chunk group), the
+// groups meeting in LDS.
+constexpr int kMaxMergeChunks = 4096; // 262144 positions
+
+__device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_max) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  if ((threadIdx.x & (kWave - 1)) == 0)
+    scratch[threadIdx.x / kWave] = v;
+  __syncthreads();
+  float r = scratch[0];
+  for (int w = 1; w < kThreads / kWave; w++)
+    r = is_max ? fmaxf(r, scratch[w]) : r + scratch[w];
+  __syncthreads();
+  return r;
+}
+
 __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
+  __shared__ float weight[kMaxMergeChunks];
+  __shared__ float red[kThreads];
   const int h = blockIdx.x, r = blockIdx.y;
   const int hd = p.head_dim, chunks = (p.pos0 + r) / kChunk + 1;
-  const float *part = p.partial + ((size_t)(r * p.n_heads + h) * p.chunks) * (hd + 2);
-  float m = part[hd];
-  for (int c = 1; c < chunks; c++)
-    m = fmaxf(m, part[(size_t)c * (hd + 2) + hd]);
-  for (int d = threadIdx.x; d < hd; d += kThreads) {
-    float sum = 0.0f, o = 0.0f;
-    for (int c = 0; c < chunks; c++) {
-      const float *pc = part + (size_t)c * (hd + 2);
-      const float w = expf(pc[hd] - m);
-      sum += w * pc[hd + 1];
-      o += w * pc[d];
-    }
-    p.out[((size_t)r * p.n_heads + h) * hd + d] = o / sum;
+  const float *part = p.partial + ((size_t)(r * p.n_heads + h) * p.chunks) * p.slot;
+  float m = -FLT_MAX;
+  for (int c = threadIdx.x; c < chunks; c += kThreads)
+    m = fmaxf(m, part[(size_t)c * p.slot + hd]);
+  m = block_reduce(m, red, true);
+  float l = 0.0f;
+  for (int c = threadIdx.x; c < chunks; c += kThreads) {
+    const float w = expf(part[(size_t)c * p.slot + hd] - m);
+    weight[c] = w;
+    l += w * part[(size_t)c * p.slot + hd + 1];
+  }
+  l = block_reduce(l, red, false); // its barriers also publish `weight`
+  const int groups = kThreads / hd > 0 ? kThreads / hd : 1;
+  const int d = threadIdx.x % hd, grp = threadIdx.x / hd;
+  float o = 0.0f;
+  if (grp < groups && d < hd) {
+#pragma unroll 8
+    for (int c = grp; c < chunks; c += groups)
+      o = fmaf(weight[c], part[(size_t)c * p.slot + d], o);
+  }
+  red[threadIdx.x] = o;
+  __syncthreads();
+  if (grp == 0) {
+    for (int g2 = 1; g2 < groups; g2++)
+      o += red[g2 * hd + d];
+    p.out[((size_t)r * p.n_heads + h) * hd + d] = o / l;
   }
 }
 
@@ -279,14 +404,27 @@ bool launch_kv_store(float *cache, const float *src, size_t src_ld, int pos0, in
   return launch_ok("kv_store");
 }
 
+int slot_floats(int head_dim) { return (head_dim + 2 + 3) & ~3; }
+
 size_t attention_partial_floats(int rows, int n_heads, int head_dim, int last_position) {
   const size_t chunks = (size_t)last_position / kChunk + 1;
-  return (size_t)rows * n_heads * chunks * ((size_t)head_dim + 2);
+  return (size_t)rows * n_heads * chunks * (size_t)slot_floats(head_dim);
 }
 
 bool attention_shape_ok(int n_heads, int n_kv_heads, int head_dim) {
   return n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= kMaxGroup && head_dim > 0 &&
          head_dim <= kMaxHeadDim;
+}
+
+// attn_tile's rows per block: as many as keep tile_rows x kv_mul within kMaxQv (16 for head_dim > 128, so LDS fits).
+int attention_tile_rows(int rows, int kv_mul, int head_dim) {
+  const int cap = head_dim > 128 ? kMaxQv / 4 : kMaxQv;
+  const int tile = cap / kv_mul > 1 ? cap / kv_mul : 1;
+  return rows < tile ? rows : tile;
+}
+
+size_t attention_tile_lds(int tile_rows, int kv_mul, int head_dim) {
+  return ((size_t)kChunk * (2 * head_dim + 4) + (size_t)tile_rows * kv_mul * (head_dim + kChunk)) * sizeof(float);
 }
 
 bool launch_attention(const AttentionJob &job, float *partial, hipStream_t stream) {
@@ -302,13 +440,34 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
   p.head_dim = job.head_dim;
   p.pos0 = job.pos0;
   p.chunks = (job.pos0 + job.rows - 1) / kChunk + 1;
+  if (p.chunks > kMaxMergeChunks)
+    return raise("attention over %d positions: at most %d are supported", job.pos0 + job.rows, kMaxMergeChunks * kChunk);
   p.pos_stride = job.pos_stride;
   p.head_base = job.head_base;
   p.divisor = sqrtf((float)job.head_dim);
-  hipLaunchKernelGGL(attn_chunks, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, (unsigned)job.rows),
-                     dim3(kThreads), 0, stream, p);
-  if (!launch_ok("attn_chunks"))
-    return false;
+  p.rows = job.rows;
+  p.slot = slot_floats(job.head_dim);
+  const int kv_mul = job.n_heads / job.n_kv_heads;
+  const bool aligned = job.head_dim % 4 == 0 && job.pos_stride % 4 == 0 && job.head_base % 4 == 0 &&
+                       ((uintptr_t)job.q & 15) == 0 && ((uintptr_t)job.key & 15) == 0;
+  if (aligned) {
+    p.tile_rows = attention_tile_rows(job.rows, kv_mul, job.head_dim);
+    const size_t lds = attention_tile_lds(p.tile_rows, kv_mul, job.head_dim);
+    static const hipError_t allowed =
+        hipFuncSetAttribute((const void *)attn_tile, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (allowed != hipSuccess)
+      return raise("allowing the attention kernel its LDS failed: %s", hipGetErrorString(allowed));
+    const unsigned tiles = (unsigned)((job.rows + p.tile_rows - 1) / p.tile_rows);
+    hipLaunchKernelGGL(attn_tile, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, tiles), dim3(kTileThreads), lds,
+                       stream, p);
+    if (!launch_ok("attn_tile"))
+      return false;
+  } else {
+    hipLaunchKernelGGL(attn_chunks, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, (unsigned)job.rows),
+                       dim3(kThreads), 0, stream, p);
+    if (!launch_ok("attn_chunks"))
+      return false;
+  }
   hipLaunchKernelGGL(attn_merge, dim3((unsigned)job.n_heads, (unsigned)job.rows), dim3(kThreads), 0, stream, p);
   return launch_ok("attn_merge");
 }
