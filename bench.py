@@ -8,6 +8,8 @@ HIP graph with every input already in HBM; attention, RMSNorm and RoPE are not p
 
 Alongside (`prefill`): the 8B INT8 W8A8 prefill of a 2048-token prompt: per layer quantize the 2048 rows and run the
 int8-MFMA GEMMs (QKV, Wo + residual, W1/W3 SwiGLU, W2 + residual), then the last row's classifier GEMV.
+`forward_decode`: the whole 8B decode token on the device (the matmul set plus RMSNorm, RoPE, the K/V cache store and
+attention over 2048 cached positions), also from a HIP graph.
 
 Weights ~N(0, 0.02) and activations ~N(0, 1) are drawn on the device (torch, seeded) and quantized by the library's
 own k_quantize rule; the data is synthetic. `roofline` is the dominant kernel of the decode step (the SwiGLU GEMV),
@@ -121,6 +123,67 @@ def decode_set(torch, lh, model, seed):
         L.k_matmul_q8(P(logits), inputs_d, w8(model.cls), DIM, VOCAB, GS)
 
     return run_step
+
+
+N_HEADS, N_KV_HEADS, HEAD_DIM = 32, 8, 128
+CONTEXT = 2048  # the position the full decode token is measured at (its attention reads 2048 cached positions)
+
+
+def forward_decode_set(torch, lh, model, seed):
+    """One token of the device-resident 8B forward at position CONTEXT - 1, in the reference's decode order
+    (src/tp.c:397-432): per layer RMSNorm, quantize + QKV, RoPE, K/V cache store, attention over the cache, quantize +
+    Wo (+ residual), RMSNorm, quantize + W1/W3 SwiGLU, quantize + W2 (+ residual); then the final RMSNorm and the
+    classifier. Synthetic cache contents, norm weights and rope table; the matmul weights are the decode set's."""
+    import ctypes
+    L = lh.load()
+    P = lh.ptr
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 7)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    cache = [(torch.randn(CONTEXT * KV_DIM, generator=gen, **f32), torch.randn(CONTEXT * KV_DIM, generator=gen, **f32))
+             for _ in range(LAYERS)]
+    norms = torch.rand(2 * LAYERS + 1, DIM, generator=gen, **f32) + 0.5
+    x, xb, att = torch.randn(DIM, generator=gen, **f32) * 0.1, torch.empty(DIM, **f32), torch.empty(DIM, **f32)
+    q, k, v = torch.empty(DIM, **f32), torch.empty(KV_DIM, **f32), torch.empty(KV_DIM, **f32)
+    hb, logits = torch.empty(HIDDEN, **f32), torch.empty(VOCAB, **f32)
+    xq_d, xs_d = torch.empty(DIM, dtype=torch.int8, device="cuda"), torch.empty(DIM // GS, **f32)
+    xq_h, xs_h = torch.empty(HIDDEN, dtype=torch.int8, device="cuda"), torch.empty(HIDDEN // GS, **f32)
+    cfg = lh.Config()
+    cfg.head_dim, cfg.rope_theta, cfg.rope_type = HEAD_DIM, 500000.0, 1
+    cfg.rope_factor, cfg.rope_low, cfg.rope_high, cfg.rope_original = 8.0, 1.0, 4.0, 8192
+    table = torch.empty(2 * HEAD_DIM, **f32)
+    torch.cuda.synchronize()
+    pos = CONTEXT - 1
+    L.k_rope_table(ctypes.byref(cfg), pos, P(table))
+    inputs_d, inputs_h = lh.K8Input(P(xq_d), P(xs_d), None), lh.K8Input(P(xq_h), P(xs_h), None)
+    assert L.kernels_kv_layout_head() == 1
+
+    def w8(pair):
+        return lh.K8Weight(P(pair[0]), P(pair[1]))
+
+    def run_step():
+        for l, lay in enumerate(model.layers):
+            kc, vc = cache[l]
+            L.k_rmsnorm(P(xb), P(x), P(norms[2 * l]), DIM, 1e-5)
+            L.k_quantize(P(xq_d), P(xs_d), P(xb), DIM, GS)
+            L.k_matmul_q8_qkv(P(q), P(k), P(v), inputs_d, w8(lay["wq"]), w8(lay["wk"]), w8(lay["wv"]), DIM, DIM,
+                              KV_DIM, GS)
+            L.k_rope_apply(P(q), P(k), P(table), N_HEADS, N_KV_HEADS, HEAD_DIM)
+            L.k_kv_store(P(kc), P(k), KV_DIM, pos, 1, N_KV_HEADS, HEAD_DIM, CONTEXT)
+            L.k_kv_store(P(vc), P(v), KV_DIM, pos, 1, N_KV_HEADS, HEAD_DIM, CONTEXT)
+            L.k_attention_kv(P(att), P(q), P(kc), P(vc), None, None, N_HEADS, N_KV_HEADS, HEAD_DIM, CONTEXT, pos)
+            L.k_quantize(P(xq_d), P(xs_d), P(att), DIM, GS)
+            L.k_matmul_q8_add(P(x), inputs_d, w8(lay["wo"]), DIM, DIM, GS)
+            L.k_rmsnorm(P(xb), P(x), P(norms[2 * l + 1]), DIM, 1e-5)
+            L.k_quantize(P(xq_d), P(xs_d), P(xb), DIM, GS)
+            L.k_matmul_q8_swiglu(P(hb), inputs_d, w8(lay["w1"]), w8(lay["w3"]), DIM, HIDDEN, GS)
+            L.k_quantize(P(xq_h), P(xs_h), P(hb), HIDDEN, GS)
+            L.k_matmul_q8_add(P(x), inputs_h, w8(lay["w2"]), HIDDEN, DIM, GS)
+        L.k_rmsnorm(P(xb), P(x), P(norms[2 * LAYERS]), DIM, 1e-5)
+        L.k_quantize(P(xq_d), P(xs_d), P(xb), DIM, GS)
+        L.k_matmul_q8(P(logits), inputs_d, w8(model.cls), DIM, VOCAB, GS)
+
+    return run_step, x
 
 
 def time_graph(torch, L, graph, steps, warmup):
@@ -381,6 +444,8 @@ def main():
     ap.add_argument("--seed", type=int, default=88172645463325252 % (1 << 31))
     ap.add_argument("--no-c3", action="store_true",
                     help="skip the FP32 / BF16 prefill GEMMs on the Llama-3.2-3B shapes (512 tokens)")
+    ap.add_argument("--no-forward", action="store_true",
+                    help="skip the full device decode token (matmuls + RMSNorm, RoPE, K/V store, attention)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also launch a plain copy kernel of this many MiB (counter calibration for --pmc runs)")
     args = ap.parse_args()
@@ -457,6 +522,30 @@ def main():
                    "step_hbm_frac": round(step_bytes / (seconds / args.steps) / 1e9 / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
     }
+
+    if not args.no_forward:
+        # the whole decode token on the device, at position CONTEXT - 1 (graph replays rewrite the same cache slot)
+        run_fwd, x_state = forward_decode_set(torch, lh, model, args.seed)
+        x0 = x_state.clone()
+        run_fwd()
+        L.llhip_synchronize()
+        assert L.llhip_graph_begin() == 0
+        run_fwd()
+        fgraph = L.llhip_graph_end()
+        if not fgraph:
+            raise SystemExit(f"graph capture of the forward token failed: {lh.last_error()}")
+        fsteps = max(5, args.steps // 2)
+        x_state.copy_(x0)
+        fsec = time_graph(torch, L, fgraph, fsteps, 2) / fsteps
+        L.llhip_graph_destroy(fgraph)
+        result["forward_decode"] = {
+            "value": round(1.0 / fsec, 2), "unit": "tok/s", "ms_per_token": round(fsec * 1e3, 4),
+            "matmul_share": round((seconds / args.steps) / fsec, 3),
+            "workload": f"Llama-3.1-8B Q8_0 decode token on the device at position {CONTEXT - 1}: 32 x (RMSNorm, "
+                        "quantize + QKV, RoPE, K/V store, attention over the head-major cache, quantize + Wo +resid, "
+                        "RMSNorm, quantize + W1/W3 SwiGLU, quantize + W2 +resid) + RMSNorm + classifier, HIP graph"}
+        print(f"# device decode token at position {CONTEXT - 1}: {fsec * 1e3:.3f} ms, {1 / fsec:.1f} tok/s",
+              file=sys.stderr, flush=True)
 
     if not args.no_prefill:
         run_prefill, gemms, ops = prefill_set(torch, lh, model, args.seed)

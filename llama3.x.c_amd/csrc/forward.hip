@@ -1,7 +1,7 @@
 // The forward around the matmuls on gfx950: RMSNorm, RoPE, the K/V cache store and causal attention (decode and
 // batched), so activations can stay in HBM between layers. Citations are LucianCrainic/llama3.x.c file:line.
 //
-//   rmsnorm_rows   one block per row: the sum of squares reduced over the block, then out = w * (ss * x) in the
+//   rmsnorm_rows   one 1024-thread block per row: the sum of squares reduced over the block, then out = w * (ss * x) in the
 //                  reference's operation order (src/kernels.c:8-21). HBM-bound: 8 bytes read + 4 written per value.
 //   rope_rows      one thread per (row, head, pair), products rounded before the sum (no fused multiply-add), so the
 //                  result is bitwise the reference's (src/kernels_simd.c:203-225).
@@ -45,26 +45,51 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // ---- RMSNorm -----------------------------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void rmsnorm_rows(float *__restrict__ out, const float *__restrict__ x,
-                                                         const float *__restrict__ weight, int size, float epsilon) {
-  __shared__ float part[kThreads / kWave];
+constexpr int kNormThreads = 1024;
+
+// One block per row. Aligned rows (size % 4 == 0, 16-byte aligned) are read as float4, so a 4096-value row is one
+// load per thread, all in flight at once.
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_rows(float *__restrict__ out, const float *__restrict__ x,
+                                                             const float *__restrict__ weight, int size, float epsilon,
+                                                             bool vec4) {
+  __shared__ float part[kNormThreads / kWave];
   const float *row = x + (size_t)blockIdx.x * size;
   float *o = out + (size_t)blockIdx.x * size;
   float ss = 0.0f;
-  for (int j = threadIdx.x; j < size; j += kThreads)
-    ss = fmaf(row[j], row[j], ss);
+  if (vec4) {
+    for (int j = 4 * threadIdx.x; j < size; j += 4 * kNormThreads) {
+      const float4 v = *reinterpret_cast<const float4 *>(row + j);
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+  } else {
+    for (int j = threadIdx.x; j < size; j += kNormThreads)
+      ss = fmaf(row[j], row[j], ss);
+  }
   ss = wave_sum(ss);
   if ((threadIdx.x & (kWave - 1)) == 0)
     part[threadIdx.x / kWave] = ss;
   __syncthreads();
-  ss = part[0] + part[1] + part[2] + part[3];
+  ss = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; w++)
+    ss += part[w];
   // src/kernels.c:15-17, the same three roundings (correctly rounded division and square root)
   ss /= size;
   ss += epsilon;
   ss = 1.0f / sqrtf(ss);
   // out may be x: each value is read by the thread that writes it, after every thread's sum is in
-  for (int j = threadIdx.x; j < size; j += kThreads)
-    o[j] = weight[j] * (ss * row[j]);
+  if (vec4) {
+    for (int j = 4 * threadIdx.x; j < size; j += 4 * kNormThreads) {
+      const float4 v = *reinterpret_cast<const float4 *>(row + j), w = *reinterpret_cast<const float4 *>(weight + j);
+      *reinterpret_cast<float4 *>(o + j) = float4{w.x * (ss * v.x), w.y * (ss * v.y), w.z * (ss * v.z), w.w * (ss * v.w)};
+    }
+  } else {
+    for (int j = threadIdx.x; j < size; j += kNormThreads)
+      o[j] = weight[j] * (ss * row[j]);
+  }
 }
 
 // ---- RoPE ---------------------------------------------------------------------------------------------------------
@@ -384,7 +409,9 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
 
 bool launch_rmsnorm(float *out, const float *x, const float *weight, int rows, int size, float epsilon,
                     hipStream_t stream) {
-  hipLaunchKernelGGL(rmsnorm_rows, dim3((unsigned)rows), dim3(kThreads), 0, stream, out, x, weight, size, epsilon);
+  const bool vec4 = size % 4 == 0 && (((uintptr_t)out | (uintptr_t)x | (uintptr_t)weight) & 15) == 0;
+  hipLaunchKernelGGL(rmsnorm_rows, dim3((unsigned)rows), dim3(kNormThreads), 0, stream, out, x, weight, size, epsilon,
+                     vec4);
   return launch_ok("rmsnorm_rows");
 }
 
