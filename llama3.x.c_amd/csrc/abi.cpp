@@ -22,7 +22,7 @@ void quantize_rows(const char *name, int8_t *q, float *s, const float *x, size_t
     raise("%s: null buffer", name);
     return;
   }
-  Call call(name);
+  Call call(name, true); // a recorded k_rmsnorm of x may be taken along
   const size_t used = (size_t)groups * gs;
   Ref X = call.in2d(x, used * sizeof(float), ldx * sizeof(float), (size_t)m);
   Ref Q = call.out2d(q, used, (size_t)n, (size_t)m, false);
@@ -30,10 +30,14 @@ void quantize_rows(const char *name, int8_t *q, float *s, const float *x, size_t
   if (!call.ready())
     return;
   if (m == 1 && !call.staged() && quantize_fusion_enabled() && n % gs == 0) {
-    // one device-resident row: the next GEMV reading (q, s) quantizes it in its prologue
-    defer_quantize(PendingQuantize{call.ptr<int8_t>(Q), call.ptr<float>(S), call.ptr<const float>(X), n, gs});
+    // one device-resident row: the next GEMV reading (q, s) quantizes it (and normalizes it, when a k_rmsnorm of
+    // this row was recorded) in its prologue
+    defer_quantize(PendingQuantize{call.ptr<int8_t>(Q), call.ptr<float>(S), call.ptr<const float>(X), n, gs, nullptr,
+                                   nullptr, 0.0f});
     return;
   }
+  if (!flush_pending_quantize())
+    return;
   QuantizeJob job{call.ptr<int8_t>(Q), call.ptr<float>(S), call.ptr<const float>(X), ldx, m, n, gs};
   if (launch_quantize(job, call.stream()))
     call.finish();
@@ -122,13 +126,16 @@ void q8_gemv(const char *name, const Q8Member *members, int count, const K8Input
     fused.xs_out = pq.s;
     fused.xq = nullptr;
     fused.xs = nullptr;
+    fused.norm_w = pq.norm_w;
+    fused.norm_out = pq.norm_out;
+    fused.norm_eps = pq.norm_eps;
     if (gemv_fast_path(fused)) {
       if (launch_q8_gemv(fused, call.stream()))
         call.finish();
       return;
     }
-    // not a shape the fused kernel takes: quantize first, as recorded
-    if (!launch_quantize(QuantizeJob{pq.q, pq.s, pq.x, (size_t)pq.n, 1, pq.n, pq.gs}, call.stream()))
+    // not a shape the fused kernel takes: normalize and quantize first, as recorded
+    if (!launch_pending_quantize(pq, call.stream()))
       return;
   } else if (!flush_pending_quantize()) {
     return;

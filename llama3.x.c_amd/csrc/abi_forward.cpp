@@ -71,8 +71,18 @@ void rmsnorm(const char *name, float *out, const float *x, const float *weight, 
   const size_t bytes = (size_t)rows * size * sizeof(float);
   Ref X = call.in(x, bytes), W = call.in(weight, (size_t)size * sizeof(float));
   Ref O = call.out(out, bytes, false);
-  if (call.ready() && launch_rmsnorm(call.ptr<float>(O), call.ptr<const float>(X), call.ptr<const float>(W), rows,
-                                     size, epsilon, call.stream()))
+  if (!call.ready())
+    return;
+  float *o = call.ptr<float>(O);
+  const float *xd = call.ptr<const float>(X);
+  const bool apart = (uintptr_t)(o + size) <= (uintptr_t)xd || (uintptr_t)(xd + size) <= (uintptr_t)o;
+  if (rows == 1 && !call.staged() && apart && quantize_fusion_enabled()) {
+    // one device-resident row into another buffer: recorded, so a k_quantize of the output and the GEMV after it
+    // normalize in the GEMV's prologue (any other call runs it first)
+    defer_norm(PendingNorm{o, xd, call.ptr<const float>(W), size, epsilon});
+    return;
+  }
+  if (launch_rmsnorm(o, xd, call.ptr<const float>(W), rows, size, epsilon, call.stream()))
     call.finish();
 }
 

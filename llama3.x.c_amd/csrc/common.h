@@ -54,16 +54,30 @@ struct Ref {
 // exactly those buffers quantizes in its own prologue (one launch instead of two; block 0 still stores q and s). Any
 // other entry point, llhip_synchronize and the end of a graph capture launch a recorded quantization first, so every
 // observer sees the reference's order. LLAMA_HIP_FUSE_QUANT=0 turns the deferral off.
+// A k_quantize of one device-resident row, recorded so the next GEMV reading (q, s) can quantize in its prologue.
+// norm_w set: x is the input of a k_rmsnorm recorded just before (output norm_out, the quantization's own input).
 struct PendingQuantize {
   int8_t *q;
   float *s;
   const float *x;
   int n, gs;
+  const float *norm_w;
+  float *norm_out;
+  float norm_eps;
 };
+// A k_rmsnorm of one device-resident row, recorded so a k_quantize of its output (and the GEMV after it) can take it.
+struct PendingNorm {
+  float *out;
+  const float *x, *w;
+  int size;
+  float eps;
+};
+void defer_norm(const PendingNorm &job);
 bool quantize_fusion_enabled();
 void defer_quantize(const PendingQuantize &job);
 bool take_pending_quantize(const int8_t *q, const float *s, int n, int gs, PendingQuantize *out);
-bool flush_pending_quantize(); // launches a recorded quantization, if any
+bool flush_pending_quantize(); // launches a recorded norm and quantization, if any
+bool launch_pending_quantize(const PendingQuantize &job, hipStream_t stream); // its norm, then the quantization
 
 class Call {
  public:
@@ -134,6 +148,11 @@ struct GemvJob {
   bool xf_quantize;
   int8_t *xq_out;
   float *xs_out;
+  // With xf_quantize and norm_w: xf is RMSNorm's input, normalized (weights norm_w, norm_eps) before the quantization
+  // and stored to norm_out (the k_rmsnorm that preceded the k_quantize).
+  const float *norm_w;
+  float *norm_out;
+  float norm_eps;
 };
 bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves);
 void set_gemm_splits(int splits); // FP32 / BF16 / INT8 GEMM blocks per tile; 0 = chosen from the grid

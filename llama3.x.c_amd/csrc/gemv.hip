@@ -216,6 +216,9 @@ struct GemvParams {
   const float *xf;
   int8_t *xq_out;   // FUSED: where block 0 stores the quantization it made (the caller's k_quantize outputs)
   float *xs_out;
+  const float *norm_w; // NORM: xf is RMSNorm's input; the kernel normalizes it (weights norm_w) before quantizing
+  float *norm_out;     // and block 0 stores the normalized row there (the caller's k_rmsnorm output)
+  float norm_eps;
   int n, gs, lpg, nchunks;
   long long ld;     // weight row stride in values
   long long sld;    // weight scale row stride (ld / gs)
@@ -281,11 +284,12 @@ __device__ __forceinline__ float dot16f(int4 w, const float4 (&x)[4]) {
 // here from the FP32 input with the k_quantize rule, block 0 also storing them for the caller. load() only issues the
 // global loads into registers; the kernel issues it before the weight loads, so waiting for the input does not wait
 // for the weights (loads complete in issue order for the counter the waits use).
-template <bool FUSED, int BLOCK, int MAXC> struct Input {
+template <bool FUSED, int BLOCK, int MAXC, bool NORM = false> struct Input {
   static constexpr int kFusedPasses = (MAXC * 1024 + BLOCK * 16 - 1) / (BLOCK * 16); // 16 values per thread and pass
   static constexpr int kCopyPasses = (MAXC * 1024 + BLOCK * 16 - 1) / (BLOCK * 16);
   static constexpr int kScalePasses = (MAXC * 64 + BLOCK - 1) / BLOCK; // gs >= 16: at most n / 16 scales
   float4 xf[FUSED ? 4 * kFusedPasses : 1];
+  float4 xw[NORM ? 4 * kFusedPasses : 1]; // NORM: the RMSNorm weights of the same values
   int4 xq[FUSED ? 1 : kCopyPasses];
   float xs[FUSED ? 1 : kScalePasses];
 
@@ -301,6 +305,16 @@ template <bool FUSED, int BLOCK, int MAXC> struct Input {
           const int4 v = load16(r, (i * BLOCK * 16 + tid * 16) * 4 + j * 16, 0);
           xf[4 * i + j] = float4{__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w)};
         }
+      if constexpr (NORM) {
+        const __amdgpu_buffer_rsrc_t rw = buffer(p.norm_w, (unsigned)p.n * 4u);
+#pragma unroll
+        for (int i = 0; i < kFusedPasses; i++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int4 v = load16(rw, (i * BLOCK * 16 + tid * 16) * 4 + j * 16, 0);
+            xw[4 * i + j] = float4{__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w)};
+          }
+      }
     } else {
       const __amdgpu_buffer_rsrc_t rq = buffer(p.xq, (unsigned)p.n), rs = buffer(p.xs, (unsigned)(p.n / p.gs) * 4u);
 #pragma unroll
@@ -310,6 +324,43 @@ template <bool FUSED, int BLOCK, int MAXC> struct Input {
       for (int i = 0; i < kScalePasses; i++)
         xs[i] = load4(rs, (i * BLOCK + tid) * 4);
     }
+  }
+
+  // NORM: RMSNorm of the loaded row in place, src/kernels.c:10-20: the sum of squares reduced over the block (every
+  // block forms the same one), ss /= n, ss += eps, ss = 1 / sqrtf(ss), then w * (ss * x); block 0 stores the result.
+  // `scratch` holds one float per wave.
+  __device__ __forceinline__ void normalize(const GemvParams &p, float *scratch) {
+    const int tid = threadIdx.x;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4 * kFusedPasses; i++) { // values past n were loaded as zeros
+      ss = fmaf(xf[i].x, xf[i].x, ss);
+      ss = fmaf(xf[i].y, xf[i].y, ss);
+      ss = fmaf(xf[i].z, xf[i].z, ss);
+      ss = fmaf(xf[i].w, xf[i].w, ss);
+    }
+    ss = wave_sum(ss);
+    if ((tid & (kWave - 1)) == 0)
+      scratch[tid / kWave] = ss;
+    __syncthreads();
+    ss = 0.0f;
+#pragma unroll
+    for (int w = 0; w < BLOCK / kWave; w++)
+      ss += scratch[w];
+    ss /= p.n;
+    ss += p.norm_eps;
+    ss = 1.0f / sqrtf(ss);
+    const bool keep = blockIdx.x == 0;
+#pragma unroll
+    for (int i = 0; i < kFusedPasses; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float4 v = xf[4 * i + j], w = xw[4 * i + j];
+        xf[4 * i + j] = float4{w.x * (ss * v.x), w.y * (ss * v.y), w.z * (ss * v.z), w.w * (ss * v.w)};
+        const int off = i * BLOCK * 16 + tid * 16 + 4 * j;
+        if (keep && off < p.n)
+          *reinterpret_cast<float4 *>(p.norm_out + off) = xf[4 * i + j];
+      }
   }
 
   __device__ __forceinline__ void stage(const GemvParams &p, int8_t *sxq, float *sxs) const {
@@ -539,7 +590,7 @@ __device__ __forceinline__ void gemv_step(const GemvParams &p, const RowPart<CH,
   parity ^= 1;
 }
 
-template <int WAVES, int CH, int KS, bool SWIGLU, bool FUSED, bool SG>
+template <int WAVES, int CH, int KS, bool SWIGLU, bool FUSED, bool SG, bool NORM = false>
 __global__ __launch_bounds__(WAVES * 64) void q8_gemv(GemvParams p) {
   constexpr int kRows = WAVES / KS; // rows per block step
   extern __shared__ __align__(16) unsigned char smem[];
@@ -554,7 +605,7 @@ __global__ __launch_bounds__(WAVES * 64) void q8_gemv(GemvParams p) {
   const int stride = gridDim.x;
   int step = blockIdx.x; // block-uniform, < steps (the grid never exceeds the step count)
   int parity = 0;
-  Input<FUSED, WAVES * 64, CH * KS> in;
+  Input<FUSED, WAVES * 64, CH * KS, NORM> in;
   in.load(p);
   __builtin_amdgcn_sched_barrier(0);
   // the first two steps' weights are in flight while the block stages its input
@@ -562,6 +613,8 @@ __global__ __launch_bounds__(WAVES * 64) void q8_gemv(GemvParams p) {
   a.load(p, step * kRows + slot, part, lane);
   b.load(p, (step + stride) * kRows + slot, part, lane);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (NORM)
+    in.normalize(p, reinterpret_cast<float *>(red)); // red is free until the first step's partials
   in.stage(p, sxq, sxs);
   __syncthreads();
   while (true) {
@@ -855,7 +908,8 @@ static size_t gemv_lds_bytes(int n, int gs) {
 }
 
 // The input a fast GEMV takes: int8 (xq, xs), FP32 quantized in the prologue, or FP32 as it is (W8A32).
-enum GemvInput { IN_Q8, IN_FUSED, IN_F32 };
+// IN_NORM: FP32 input normalized (RMSNorm) and quantized in the prologue (gs = 64 only).
+enum GemvInput { IN_Q8, IN_FUSED, IN_F32, IN_NORM };
 
 template <int WAVES, int CH, int KS, bool SWIGLU>
 static void launch_shape(const GemvParams &p, GemvInput in, int per_cu, hipStream_t stream) {
@@ -873,7 +927,10 @@ static void launch_shape(const GemvParams &p, GemvInput in, int per_cu, hipStrea
     } else {
       raise("internal: a W8A32 GEMV of more than four chunks per wave");
     }
-  } else if (fused && sg)
+  } else if (in == IN_NORM)
+    hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true, true, true>), dim3(blocks), dim3(WAVES * 64), lds, stream,
+                       p);
+  else if (fused && sg)
     hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true, true>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
   else if (fused)
     hipLaunchKernelGGL((q8_gemv<WAVES, CH, KS, SWIGLU, true, false>), dim3(blocks), dim3(WAVES * 64), lds, stream, p);
@@ -974,6 +1031,14 @@ bool gemv_fast_path(const GemvJob &job) {
   fast = fast && (job.xf_quantize ? aligned16(job.xf) && aligned16(job.xq_out)
                   : f32_input     ? aligned16(job.xf)
                                   : aligned16(job.xq));
+  // RMSNorm in the prologue: gs = 64, aligned weights and output, and the normalized row written by block 0 may not
+  // be the input the other blocks read
+  const bool norm = job.xf_quantize && job.norm_w;
+  if (norm) {
+    const uintptr_t n0 = (uintptr_t)job.norm_out, n1 = n0 + (size_t)job.n * sizeof(float);
+    const uintptr_t x0 = (uintptr_t)job.xf, x1 = x0 + (size_t)job.n * sizeof(float);
+    fast = fast && job.gs == 64 && aligned16(job.norm_w) && aligned16(job.norm_out) && (n1 <= x0 || x1 <= n0);
+  }
   for (int s = 0; s < job.nseg && fast; s++) {
     fast = aligned16(job.seg[s].wq) && (job.epi != EPI_SWIGLU || aligned16(job.seg[s].w3q));
     // With an FP32 input every block reads it while others already write outputs: an output inside the input would
@@ -983,6 +1048,11 @@ bool gemv_fast_path(const GemvJob &job) {
       const uintptr_t o0 = (uintptr_t)job.seg[s].out, o1 = o0 + (size_t)job.seg[s].rows * sizeof(float);
       const uintptr_t x0 = (uintptr_t)job.xf, x1 = x0 + (size_t)job.n * sizeof(float);
       fast = fast && (o1 <= x0 || x1 <= o0);
+      if (norm) { // nor inside the normalized row block 0 writes, nor in the norm weights
+        const uintptr_t n0 = (uintptr_t)job.norm_out, n1 = n0 + (size_t)job.n * sizeof(float);
+        const uintptr_t w0 = (uintptr_t)job.norm_w, w1 = w0 + (size_t)job.n * sizeof(float);
+        fast = fast && (o1 <= n0 || n1 <= o0) && (o1 <= w0 || w1 <= o0);
+      }
     }
   }
   return fast;
@@ -1008,6 +1078,9 @@ bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
     p.xf = job.xf;
     p.xq_out = job.xq_out;
     p.xs_out = job.xs_out;
+    p.norm_w = job.norm_w;
+    p.norm_out = job.norm_out;
+    p.norm_eps = job.norm_eps;
     p.n = job.n;
     p.gs = job.gs;
     p.lpg = lanes_per_group(job.gs);
@@ -1018,7 +1091,7 @@ bool launch_q8_gemv(const GemvJob &job, hipStream_t stream) {
     p.total_rows = rows;
     p.probe = job.probe;
     p.flags = device().error_flags;
-    const GemvInput in = job.xf_quantize ? IN_FUSED : job.xq ? IN_Q8 : IN_F32;
+    const GemvInput in = job.xf_quantize ? (job.norm_w ? IN_NORM : IN_FUSED) : job.xq ? IN_Q8 : IN_F32;
     const bool swiglu = job.epi == EPI_SWIGLU;
     const GemvShape g = gemv_shape(rows, p.nchunks, swiglu, in == IN_F32);
     switch (g.split) {

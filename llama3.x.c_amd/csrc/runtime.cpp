@@ -187,6 +187,8 @@ namespace {
 std::mutex pending_mutex;
 bool pending_active = false;
 PendingQuantize pending_job;
+bool norm_active = false; // a recorded k_rmsnorm (at most one of it and pending_job unconsumed: each flushes the other)
+PendingNorm norm_job;
 } // namespace
 
 bool quantize_fusion_enabled() {
@@ -197,11 +199,40 @@ bool quantize_fusion_enabled() {
   return on;
 }
 
-void defer_quantize(const PendingQuantize &job) {
+void defer_norm(const PendingNorm &job) {
+  flush_pending_quantize(); // what was recorded earlier runs first
+  std::lock_guard<std::mutex> lock(pending_mutex);
+  norm_job = job;
+  norm_active = true;
+}
+
+void defer_quantize(const PendingQuantize &recorded) {
+  PendingQuantize job = recorded;
+  {
+    // the quantization of a recorded norm's whole output takes the norm along: the GEMV normalizes in its prologue
+    std::lock_guard<std::mutex> lock(pending_mutex);
+    if (norm_active && norm_job.out == job.x && norm_job.size == job.n && !job.norm_w) {
+      job.x = norm_job.x;
+      job.norm_w = norm_job.w;
+      job.norm_out = norm_job.out;
+      job.norm_eps = norm_job.eps;
+      norm_active = false;
+    }
+  }
   flush_pending_quantize();
   std::lock_guard<std::mutex> lock(pending_mutex);
   pending_job = job;
   pending_active = true;
+}
+
+bool launch_pending_quantize(const PendingQuantize &job, hipStream_t stream) {
+  const float *x = job.x;
+  if (job.norm_w) {
+    if (!launch_rmsnorm(job.norm_out, job.x, job.norm_w, 1, job.n, job.norm_eps, stream))
+      return false;
+    x = job.norm_out;
+  }
+  return launch_quantize(QuantizeJob{job.q, job.s, x, (size_t)job.n, 1, job.n, job.gs}, stream);
 }
 
 bool take_pending_quantize(const int8_t *q, const float *s, int n, int gs, PendingQuantize *out) {
@@ -215,14 +246,19 @@ bool take_pending_quantize(const int8_t *q, const float *s, int n, int gs, Pendi
 
 bool flush_pending_quantize() {
   PendingQuantize job;
+  PendingNorm norm;
+  bool have_job, have_norm;
   {
     std::lock_guard<std::mutex> lock(pending_mutex);
-    if (!pending_active)
-      return true;
+    have_job = pending_active;
+    have_norm = norm_active;
     job = pending_job;
-    pending_active = false;
+    norm = norm_job;
+    pending_active = norm_active = false;
   }
-  return launch_quantize(QuantizeJob{job.q, job.s, job.x, (size_t)job.n, 1, job.n, job.gs}, the_device.stream);
+  if (have_norm && !launch_rmsnorm(norm.out, norm.x, norm.w, 1, norm.size, norm.eps, the_device.stream))
+    return false;
+  return !have_job || launch_pending_quantize(job, the_device.stream);
 }
 
 Call::Call(const char *name, bool keep_pending) : name_(name) {

@@ -270,3 +270,98 @@ def test_attention_nonfinite_score_fails_and_bookkeeping():
     assert L.k_attention_bytes(32, 8, 128, 8192) == 32 * 128 * 132 * 4  # 130 floats per chunk, rounded to 4
     L.k_attention_free(ctypes.byref(work))
     assert L.kernels_attention_select(b"tiled", b"group") == 1 and L.kernels_attention_select(b"x", None) == 0
+
+
+# ---- RMSNorm recorded into the next GEMV's prologue -----------------------------------------------------------------
+
+
+def synth_q8(rng, d, n, gs=64):
+    return orc.quantize_weights(rng.normal(d * n, 0.0, 0.02).reshape(d, n), gs)
+
+
+@pytest.mark.parametrize("kind", ["store", "swiglu", "qkv", "add_residual"])
+def test_rmsnorm_quantize_gemv_fusion(kind):
+    """k_rmsnorm -> k_quantize -> Q8 GEMV on device memory, the reference's decode order (tp.c:399-401, 419-420): the
+    GEMV normalizes and quantizes in its prologue. The normalized row matches the oracle's within 1e-5, the quantized
+    row is bitwise the quantization of that normalized row, and the GEMV output is within the budget of its float64
+    reference. add_residual adds into the norm's own input, which the fused kernel must not do (it falls back to
+    separate launches): the same checks hold."""
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 1200 + len(kind))
+    n, d, gs = 4096, 1024, 64
+    x = rng.normal(n, 0.0, 2.0)
+    w = rng.normal(n, 1.0, 0.1)
+    wq, ws = synth_q8(rng, d, n)
+    w3q, w3s = synth_q8(rng, d, n)
+    base = rng.normal(n, 0.0, 1.0) if kind == "add_residual" else None
+    dx = hu.dev(x if base is None else x)
+    dw, dxb = hu.dev(w), hu.empty(n, hu.torch().float32)
+    dxq, dxs = hu.empty(n, hu.torch().int8), hu.empty(n // gs, hu.torch().float32)
+    dwq, dws, dw3q, dw3s = hu.dev(wq), hu.dev(ws), hu.dev(w3q), hu.dev(w3s)
+    inp = lh.k8(dxq, dxs)
+    outs = [hu.empty(d if kind != "add_residual" else n, hu.torch().float32) for _ in range(3)]
+    L.k_rmsnorm(lh.ptr(dxb), lh.ptr(dx), lh.ptr(dw), n, 1e-5)
+    L.k_quantize(lh.ptr(dxq), lh.ptr(dxs), lh.ptr(dxb), n, gs)
+    if kind == "store":
+        L.k_matmul_q8(lh.ptr(outs[0]), inp, lh.w8(dwq, dws), n, d, gs)
+    elif kind == "swiglu":
+        L.k_matmul_q8_swiglu(lh.ptr(outs[0]), inp, lh.w8(dwq, dws), lh.w8(dw3q, dw3s), n, d, gs)
+    elif kind == "qkv":
+        L.k_matmul_q8_qkv(lh.ptr(outs[0]), lh.ptr(outs[1]), lh.ptr(outs[2]), inp, lh.w8(dwq, dws), lh.w8(dw3q, dw3s),
+                          lh.w8(dwq, dws), n, d, d, gs)
+    else:  # x += W x_normed with a square W: the output is the norm's input
+        wsq, wss = synth_q8(rng, n, n)
+        dwsq, dwss = hu.dev(wsq), hu.dev(wss)
+        L.k_matmul_q8_add(lh.ptr(dx), inp, lh.w8(dwsq, dwss), n, n, gs)
+    xb = hu.host(dxb)
+    want_xb = orc.rmsnorm(x, w)
+    assert np.all(np.abs(xb - want_xb) <= 1e-5 * np.abs(want_xb) + 1e-7)
+    xq, xs = hu.host(dxq), hu.host(dxs)
+    q2, s2 = orc.quantize(xb, gs)
+    assert np.array_equal(xq, q2) and np.array_equal(hu.bits(xs), hu.bits(s2))
+    if kind == "add_residual":
+        ref, mag = hu.dequant_reference(xq, xs, wsq, wss, gs)
+        hu.assert_within_budget(hu.host(dx), x + ref, mag + np.abs(x), what="residual add")
+        return
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    got = hu.host(outs[0])
+    if kind == "swiglu":
+        ref3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
+        ta, tb = 2e-5 * mag + 1e-6, 2e-5 * mag3 + 1e-6
+        silu = ref / (1.0 + np.exp(-ref))
+        tol = 1.1 * np.abs(ref3) * ta + np.abs(silu) * tb + 1.1 * ta * tb + 1e-6
+        assert np.all(np.abs(got - silu * ref3) <= tol)
+    else:
+        hu.assert_within_budget(got, ref, mag, what=kind)
+    if kind == "qkv":
+        ref3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
+        hu.assert_within_budget(hu.host(outs[1]), ref3, mag3, what="k")
+        hu.assert_within_budget(hu.host(outs[2]), ref, mag, what="v")
+
+
+def test_recorded_rmsnorm_runs_before_any_other_call():
+    """A recorded k_rmsnorm whose output is read by something other than a k_quantize -> GEMV pair still runs first:
+    before a RoPE call on its output, before a quantization of another buffer, and at a synchronization."""
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 1300)
+    n = 256
+    x, w = rng.normal(n, 0.0, 1.0), rng.normal(n, 1.0, 0.1)
+    want = orc.rmsnorm(x, w)
+    dx, dw, dxb = hu.dev(x), hu.dev(w), hu.empty(n, hu.torch().float32)
+    table = np.zeros(2 * 64, np.float32)
+    table[:64] = 1.0  # cos 1, sin 0: the identity rotation
+    dt = hu.dev(table)
+    L.k_rmsnorm(lh.ptr(dxb), lh.ptr(dx), lh.ptr(dw), n, 1e-5)
+    L.k_rope_apply(lh.ptr(dxb), None, lh.ptr(dt), n // 64, 0, 64)  # reads and rewrites the normalized row
+    got = hu.host(dxb)
+    assert np.all(np.abs(got - want) <= 1e-5 * np.abs(want) + 1e-7)
+    other = hu.dev(rng.normal(n, 0.0, 1.0))
+    dxq, dxs = hu.empty(n, hu.torch().int8), hu.empty(n // 64, hu.torch().float32)
+    dxb.zero_()
+    hu.torch().cuda.synchronize()
+    L.k_rmsnorm(lh.ptr(dxb), lh.ptr(dx), lh.ptr(dw), n, 1e-5)
+    L.k_quantize(lh.ptr(dxq), lh.ptr(dxs), lh.ptr(other), n, 64)  # not the norm's output: the norm runs on its own
+    got = hu.host(dxb)
+    assert np.all(np.abs(got - want) <= 1e-5 * np.abs(want) + 1e-7)
+    q2, s2 = orc.quantize(hu.host(other), 64)
+    assert np.array_equal(hu.host(dxq), q2)
