@@ -112,9 +112,18 @@ void rope(const char *name, float *q, size_t q_stride, float *k, size_t k_stride
                        : call.in2d(table, 2 * (size_t)head_dim * f, table_stride * f, (size_t)rows);
   Ref Q = call.out2d(q, (size_t)n_heads * head_dim * f, q_stride * f, (size_t)rows, true);
   Ref K = n_kv_heads > 0 ? call.out2d(k, (size_t)n_kv_heads * head_dim * f, k_stride * f, (size_t)rows, true) : Ref{};
-  if (call.ready() && launch_rope(call.ptr<float>(Q), q_stride, n_kv_heads > 0 ? call.ptr<float>(K) : nullptr,
-                                  k_stride, call.ptr<const float>(T), table_stride, rows, n_heads, n_kv_heads, head_dim,
-                                  call.stream()))
+  if (!call.ready())
+    return;
+  float *qd = call.ptr<float>(Q), *kd = n_kv_heads > 0 ? call.ptr<float>(K) : nullptr;
+  const float *td = call.ptr<const float>(T);
+  const bool aligned = head_dim % 4 == 0 && (((uintptr_t)qd | (uintptr_t)kd) & 15) == 0;
+  if (rows == 1 && !call.staged() && n_kv_heads > 0 && aligned && quantize_fusion_enabled()) {
+    // one device-resident row: recorded, so the cache stores of k and v and the decode attention that follow can
+    // rotate, store and attend in one launch (any other call runs it first)
+    defer_rope(PendingRope{qd, kd, td, n_heads, n_kv_heads, head_dim, 0, {}});
+    return;
+  }
+  if (launch_rope(qd, q_stride, kd, k_stride, td, table_stride, rows, n_heads, n_kv_heads, head_dim, call.stream()))
     call.finish();
 }
 
@@ -151,7 +160,7 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
     raise("%s: null buffer", name);
     return;
   }
-  Call call(name);
+  Call call(name, true); // a recorded RoPE with its cache stores may be taken along
   const size_t f = sizeof(float), row = (size_t)n_heads * head_dim * f;
   const size_t cache = cache_floats(n_kv_heads, head_dim, pos0 + m - 1, pos_stride, head_base) * f;
   Ref Q = call.in(q, row * m), K = call.in(key_cache, cache), V = call.in(value_cache, cache);
@@ -162,7 +171,19 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
   if (!partial)
     return;
   AttentionJob job{call.ptr<float>(O), call.ptr<const float>(Q), call.ptr<const float>(K), call.ptr<const float>(V),
-                   n_heads, n_kv_heads, head_dim, pos0, m, pos_stride, head_base};
+                   n_heads, n_kv_heads, head_dim, pos0, m, pos_stride, head_base, nullptr, nullptr, nullptr};
+  // the fused form reads the caches, q and the new rows as 16-byte vectors
+  const bool aligned = head_dim % 4 == 0 && pos_stride % 4 == 0 && head_base % 4 == 0 &&
+                       (((uintptr_t)job.q | (uintptr_t)job.key | (uintptr_t)job.value) & 15) == 0;
+  PendingRope rope;
+  if (m == 1 && !call.staged() && aligned &&
+      take_pending_rope(job.q, job.key, job.value, pos0, pos_stride, head_base, n_heads, n_kv_heads, head_dim, &rope)) {
+    job.k_new = rope.k;
+    job.v_new = rope.store[1].src;
+    job.table = rope.table;
+  } else if (!flush_pending_quantize()) {
+    return;
+  }
   if (launch_attention(job, partial, call.stream()))
     call.finish();
 }
@@ -274,12 +295,19 @@ void k_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int cou
   size_t pos_stride, head_base;
   strides(n_kv_heads, head_dim, seq_len, kv_head_major(), &pos_stride, &head_base);
   const size_t kv_dim = (size_t)n_kv_heads * head_dim, f = sizeof(float);
-  Call call("k_kv_store");
+  Call call("k_kv_store", true); // may join a recorded RoPE
   Ref S = call.in2d(src, kv_dim * f, src_ld * f, (size_t)count);
   // the whole layer's cache: every position of every KV head (read too, so a staged copy keeps the other positions)
   Ref C = call.out(cache, (size_t)seq_len * kv_dim * f, true);
-  if (call.ready() && launch_kv_store(call.ptr<float>(C), call.ptr<const float>(S), src_ld, pos0, count, n_kv_heads,
-                                      head_dim, pos_stride, head_base, call.stream()))
+  if (!call.ready())
+    return;
+  float *cd = call.ptr<float>(C);
+  const float *sd = call.ptr<const float>(S);
+  if (count == 1 && !call.staged() && attach_kv_store(PendingKvStore{cd, sd, pos0, pos_stride, head_base}, n_kv_heads,
+                                                      head_dim))
+    return; // recorded with the RoPE before it
+  if (flush_pending_quantize() &&
+      launch_kv_store(cd, sd, src_ld, pos0, count, n_kv_heads, head_dim, pos_stride, head_base, call.stream()))
     call.finish();
 }
 

@@ -73,6 +73,27 @@ struct PendingNorm {
   float eps;
 };
 void defer_norm(const PendingNorm &job);
+// A single-row k_rope_apply on device memory and the k_kv_store calls of its rotated k (and of v) that follow it,
+// recorded so the decode attention over the same cache can rotate, store and attend in one launch.
+struct PendingKvStore {
+  float *cache;
+  const float *src;
+  int pos;
+  size_t pos_stride, head_base;
+};
+struct PendingRope {
+  float *q, *k;
+  const float *table;
+  int n_heads, n_kv_heads, head_dim;
+  int stores; // 0, 1 (K) or 2 (K then V)
+  PendingKvStore store[2];
+};
+void defer_rope(const PendingRope &job);
+// Attaches a single-row cache store to the recorded RoPE (K: src is its k; V: after K); false when it does not fit.
+bool attach_kv_store(const PendingKvStore &store, int n_kv_heads, int head_dim);
+// Takes the recorded RoPE with both stores when they are exactly this decode attention's inputs.
+bool take_pending_rope(const float *q, const float *key_cache, const float *value_cache, int position,
+                       size_t pos_stride, size_t head_base, int n_heads, int n_kv_heads, int head_dim, PendingRope *out);
 bool quantize_fusion_enabled();
 void defer_quantize(const PendingQuantize &job);
 bool take_pending_quantize(const int8_t *q, const float *s, int n, int gs, PendingQuantize *out);
@@ -189,6 +210,10 @@ struct AttentionJob {
   const float *q, *key, *value;
   int n_heads, n_kv_heads, head_dim, pos0, rows;
   size_t pos_stride, head_base;
+  // Decode with a recorded RoPE and cache stores (rows == 1): q and k_new are rotated by table in the kernel, q and
+  // k_new written back rotated, and k_new / v_new stored at position pos0 of the caches, which key / value then are.
+  float *k_new;
+  const float *v_new, *table;
 };
 bool attention_shape_ok(int n_heads, int n_kv_heads, int head_dim); // kv_mul <= 16, head_dim <= 256
 size_t attention_partial_floats(int rows, int n_heads, int head_dim, int last_position);

@@ -101,6 +101,14 @@ __device__ __forceinline__ void rotate(float *v, float c, float s) {
   v[1] = a * s + b * c;
 }
 
+// Two pairs (j0, j0 + 1) and (j0 + 2, j0 + 3) of a row, rotated like rotate() (c = table[j], s = table[hd + j + 1]).
+__device__ __forceinline__ float4 rotate4(float4 v, const float *table, int hd, int j0) {
+  float a[2] = {v.x, v.y}, b[2] = {v.z, v.w};
+  rotate(a, table[j0], table[hd + j0 + 1]);
+  rotate(b, table[j0 + 2], table[hd + j0 + 3]);
+  return float4{a[0], a[1], b[0], b[1]};
+}
+
 // Thread i: row i / (n_heads * half), head and pair from the rest; k is rotated for heads below n_kv_heads.
 __global__ __launch_bounds__(kThreads) void rope_rows(float *__restrict__ q, size_t q_stride, float *__restrict__ k,
                                                       size_t k_stride, const float *__restrict__ table,
@@ -145,6 +153,9 @@ struct AttnParams {
   int n_heads, n_kv_heads, head_dim, pos0, chunks; // chunks: per row, for the last row's position
   int rows, tile_rows;                              // query rows, and rows per attn_tile block
   int slot;                                         // floats per partial
+  // fused RoPE and cache store (decode): q (written back rotated), the new k row (likewise) and v row, the table
+  float *rope_q, *k_new;
+  const float *v_new, *table;
   size_t pos_stride, head_base;
   float divisor; // sqrtf(head_dim)
 };
@@ -173,18 +184,35 @@ __global__ __launch_bounds__(kTileThreads) void attn_tile(AttnParams p) {
   const int nqv = nrows * kv_mul;
   float *ks = lds, *vs = ks + kChunk * kst, *qs = vs + kChunk * hd, *es = qs + p.tile_rows * kv_mul * hd;
   const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
+  const bool fresh = p.table != nullptr; // decode with the RoPE and the new cache row folded in
   // every K and V load of the chunk is issued before any is waited for; V lands while the scores are computed
   for (int i = threadIdx.x; i < n * hd4; i += kTileThreads) {
     const int t = i / hd4, d4 = i % hd4;
     const size_t at = (size_t)(t0 + t) * p.pos_stride + 4 * d4;
-    const float4 kv = *reinterpret_cast<const float4 *>(kbase + at), vv = *reinterpret_cast<const float4 *>(vbase + at);
+    float4 kv, vv;
+    if (fresh && t0 + t == p.pos0) {
+      // the new row, from the QKV outputs: k rotated, both stored into the caches and k written back rotated (this
+      // block is the only reader of the position: it lies in the last chunk)
+      const size_t src = (size_t)g * hd + 4 * d4;
+      kv = rotate4(*reinterpret_cast<const float4 *>(p.k_new + src), p.table, hd, 4 * d4);
+      vv = *reinterpret_cast<const float4 *>(p.v_new + src);
+      *reinterpret_cast<float4 *>(p.k_new + src) = kv;
+      *reinterpret_cast<float4 *>(const_cast<float *>(kbase) + at) = kv;
+      *reinterpret_cast<float4 *>(const_cast<float *>(vbase) + at) = vv;
+    } else {
+      kv = *reinterpret_cast<const float4 *>(kbase + at);
+      vv = *reinterpret_cast<const float4 *>(vbase + at);
+    }
     *reinterpret_cast<float4 *>(ks + t * kst + 4 * d4) = kv;
     *reinterpret_cast<float4 *>(vs + t * hd + 4 * d4) = vv;
   }
   for (int i = threadIdx.x; i < nqv * hd4; i += kTileThreads) {
     const int qv = i / hd4, d4 = i % hd4, j = qv / kv_mul, h = qv % kv_mul;
-    *reinterpret_cast<float4 *>(qs + qv * hd + 4 * d4) = *reinterpret_cast<const float4 *>(
-        p.q + ((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * hd + 4 * d4);
+    const size_t at = ((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * hd + 4 * d4;
+    float4 v = *reinterpret_cast<const float4 *>(p.q + at);
+    if (fresh) // every block rotates its own copy; attn_merge writes q back rotated once all blocks have read it
+      v = rotate4(v, p.table, hd, 4 * d4);
+    *reinterpret_cast<float4 *>(qs + qv * hd + 4 * d4) = v;
   }
   __syncthreads();
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
@@ -388,6 +416,12 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
     l += w * part[(size_t)c * p.slot + hd + 1];
   }
   l = block_reduce(l, red, false); // its barriers also publish `weight`
+  if (p.table) { // fused RoPE (decode): q of this head back in place, rotated (every attn_tile block has read it)
+    float *qh = p.rope_q + (size_t)h * hd;
+    for (int d4 = threadIdx.x; d4 < hd / 4; d4 += kThreads)
+      *reinterpret_cast<float4 *>(qh + 4 * d4) =
+          rotate4(*reinterpret_cast<const float4 *>(qh + 4 * d4), p.table, hd, 4 * d4);
+  }
   const int groups = kThreads / hd > 0 ? kThreads / hd : 1;
   const int d = threadIdx.x % hd, grp = threadIdx.x / hd;
   float o = 0.0f;
@@ -474,9 +508,15 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
   p.divisor = sqrtf((float)job.head_dim);
   p.rows = job.rows;
   p.slot = slot_floats(job.head_dim);
+  p.rope_q = const_cast<float *>(job.q);
+  p.k_new = job.k_new;
+  p.v_new = job.v_new;
+  p.table = job.table;
   const int kv_mul = job.n_heads / job.n_kv_heads;
   const bool aligned = job.head_dim % 4 == 0 && job.pos_stride % 4 == 0 && job.head_base % 4 == 0 &&
                        ((uintptr_t)job.q & 15) == 0 && ((uintptr_t)job.key & 15) == 0;
+  if (job.table && !aligned)
+    return raise("internal: a fused RoPE attention on operands the aligned kernel does not take");
   if (aligned) {
     p.tile_rows = attention_tile_rows(job.rows, kv_mul, job.head_dim);
     const size_t lds = attention_tile_lds(p.tile_rows, kv_mul, job.head_dim);

@@ -189,6 +189,21 @@ bool pending_active = false;
 PendingQuantize pending_job;
 bool norm_active = false; // a recorded k_rmsnorm (at most one of it and pending_job unconsumed: each flushes the other)
 PendingNorm norm_job;
+bool rope_active = false; // a recorded k_rope_apply with its cache stores (likewise exclusive of the two above)
+PendingRope rope_job;
+
+bool launch_rope_and_stores(const PendingRope &r, hipStream_t stream) {
+  if (!launch_rope(r.q, (size_t)r.n_heads * r.head_dim, r.k, (size_t)r.n_kv_heads * r.head_dim, r.table,
+                   2 * (size_t)r.head_dim, 1, r.n_heads, r.n_kv_heads, r.head_dim, stream))
+    return false;
+  for (int i = 0; i < r.stores; i++) {
+    const PendingKvStore &st = r.store[i];
+    if (!launch_kv_store(st.cache, st.src, (size_t)r.n_kv_heads * r.head_dim, st.pos, 1, r.n_kv_heads, r.head_dim,
+                         st.pos_stride, st.head_base, stream))
+      return false;
+  }
+  return true;
+}
 } // namespace
 
 bool quantize_fusion_enabled() {
@@ -247,18 +262,59 @@ bool take_pending_quantize(const int8_t *q, const float *s, int n, int gs, Pendi
 bool flush_pending_quantize() {
   PendingQuantize job;
   PendingNorm norm;
-  bool have_job, have_norm;
+  PendingRope rope;
+  bool have_job, have_norm, have_rope;
   {
     std::lock_guard<std::mutex> lock(pending_mutex);
     have_job = pending_active;
     have_norm = norm_active;
+    have_rope = rope_active;
     job = pending_job;
     norm = norm_job;
-    pending_active = norm_active = false;
+    rope = rope_job;
+    pending_active = norm_active = rope_active = false;
   }
+  if (have_rope && !launch_rope_and_stores(rope, the_device.stream))
+    return false;
   if (have_norm && !launch_rmsnorm(norm.out, norm.x, norm.w, 1, norm.size, norm.eps, the_device.stream))
     return false;
   return !have_job || launch_pending_quantize(job, the_device.stream);
+}
+
+void defer_rope(const PendingRope &job) {
+  flush_pending_quantize(); // what was recorded earlier runs first
+  std::lock_guard<std::mutex> lock(pending_mutex);
+  rope_job = job;
+  rope_job.stores = 0;
+  rope_active = true;
+}
+
+bool attach_kv_store(const PendingKvStore &store, int n_kv_heads, int head_dim) {
+  std::lock_guard<std::mutex> lock(pending_mutex);
+  if (!rope_active || rope_job.n_kv_heads != n_kv_heads || rope_job.head_dim != head_dim || rope_job.stores == 2)
+    return false;
+  // the first store must be of the rotated k, the second of another row (v) at the same position and layout
+  if (rope_job.stores == 0 ? store.src != rope_job.k
+                           : (store.src == rope_job.k || store.pos != rope_job.store[0].pos ||
+                              store.pos_stride != rope_job.store[0].pos_stride ||
+                              store.head_base != rope_job.store[0].head_base || store.cache == rope_job.store[0].cache))
+    return false;
+  rope_job.store[rope_job.stores++] = store;
+  return true;
+}
+
+bool take_pending_rope(const float *q, const float *key_cache, const float *value_cache, int position,
+                       size_t pos_stride, size_t head_base, int n_heads, int n_kv_heads, int head_dim, PendingRope *out) {
+  std::lock_guard<std::mutex> lock(pending_mutex);
+  const PendingRope &r = rope_job;
+  if (!rope_active || r.stores != 2 || r.q != q || r.n_heads != n_heads || r.n_kv_heads != n_kv_heads ||
+      r.head_dim != head_dim || r.store[0].cache != key_cache || r.store[1].cache != value_cache ||
+      r.store[0].pos != position || r.store[0].pos_stride != pos_stride || r.store[0].head_base != head_base ||
+      ((uintptr_t)r.store[1].src & 15) != 0) // the fused kernel reads the new v row as 16-byte vectors
+    return false;
+  *out = r;
+  rope_active = false;
+  return true;
 }
 
 Call::Call(const char *name, bool keep_pending) : name_(name) {

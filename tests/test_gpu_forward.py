@@ -365,3 +365,44 @@ def test_recorded_rmsnorm_runs_before_any_other_call():
     assert np.all(np.abs(got - want) <= 1e-5 * np.abs(want) + 1e-7)
     q2, s2 = orc.quantize(hu.host(other), 64)
     assert np.array_equal(hu.host(dxq), q2)
+
+
+# ---- RoPE and the cache stores recorded into the decode attention ----------------------------------------------------
+
+
+@pytest.mark.parametrize("layout,interrupt", [("head", None), ("rows", None), ("head", "sync"), ("head", "position")])
+def test_rope_kv_store_attention_fusion(layout, interrupt):
+    """The reference's decode order (tp.c:409-413): k_rope_apply(q, k), k_kv_store of k and of v at the position,
+    k_attention_kv at that position. Device-resident, the three recorded calls run inside the attention launch: q and k
+    come back rotated bitwise as the oracle rotates them, the cache rows hold the rotated k and v bitwise, and the
+    output is within the attention tolerance of the oracle on the updated cache. A synchronization in between, or an
+    attention at another position, runs the recorded calls on their own first: the same results."""
+    L = hu.lib()
+    assert L.kernels_kv_layout_select(layout.encode()) == 1
+    try:
+        rng = orc.Rng(orc.SEED + 1400 + len(layout) + (0 if interrupt is None else len(interrupt)))
+        nh, nkv, hd, seq, pos = 32, 8, 128, 200, 130
+        kv_dim = nkv * hd
+        ps, hb = orc.kv_strides(nkv, hd, seq, layout == "head")
+        kc0, vc0 = rng.normal(seq * kv_dim, 0, 1), rng.normal(seq * kv_dim, 0, 1)
+        q, k, v = rng.normal(nh * hd, 0, 1), rng.normal(kv_dim, 0, 1), rng.normal(kv_dim, 0, 1)
+        g = golden()
+        table = g["ropetab128_1000/table"]
+        dq, dk, dv, dt = hu.dev(q), hu.dev(k), hu.dev(v), hu.dev(table)
+        dkc, dvc, do = hu.dev(kc0), hu.dev(vc0), hu.empty(nh * hd, hu.torch().float32)
+        L.k_rope_apply(lh.ptr(dq), lh.ptr(dk), lh.ptr(dt), nh, nkv, hd)
+        L.k_kv_store(lh.ptr(dkc), lh.ptr(dk), kv_dim, pos, 1, nkv, hd, seq)
+        if interrupt == "sync":
+            L.llhip_synchronize()
+        L.k_kv_store(lh.ptr(dvc), lh.ptr(dv), kv_dim, pos, 1, nkv, hd, seq)
+        apos = pos if interrupt != "position" else pos + 1
+        L.k_attention_kv(lh.ptr(do), lh.ptr(dq), lh.ptr(dkc), lh.ptr(dvc), None, None, nh, nkv, hd, seq, apos)
+        wq, wk = orc.rope_apply(q, k, table, nh, nkv, hd)
+        kc, vc = kc0.copy(), vc0.copy()
+        orc.lib().orc_kv_store(orc.ptr(kc), orc.ptr(wk), kv_dim, pos, 1, nkv, hd, ps, hb)
+        orc.lib().orc_kv_store(orc.ptr(vc), orc.ptr(v), kv_dim, pos, 1, nkv, hd, ps, hb)
+        assert np.array_equal(hu.bits(hu.host(dq)), hu.bits(wq)) and np.array_equal(hu.bits(hu.host(dk)), hu.bits(wk))
+        assert np.array_equal(hu.bits(hu.host(dkc)), hu.bits(kc)) and np.array_equal(hu.bits(hu.host(dvc)), hu.bits(vc))
+        check_attention(hu.host(do), wq, kc, vc, nh, nkv, hd, seq, apos, ps, hb, f"{layout} {interrupt}")
+    finally:
+        L.kernels_kv_layout_select(b"head")
