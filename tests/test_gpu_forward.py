@@ -219,10 +219,10 @@ def test_attention_decode_shapes(nh, nkv, hd, seq, positions):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,seq,pos0,m", [(8, 2, 64, 48, 20, 6), (32, 8, 128, 300, 0, 130),
-                                                  (32, 8, 128, 300, 100, 64)])
+                                                  (32, 8, 128, 300, 100, 64), (4, 2, 32, 2400, 2300, 40)])
 def test_attention_batch_rows(nh, nkv, hd, seq, pos0, m):
     """k_attention_batch: row i attends to positions 0..pos0 + i, each row as the decode attention at its position; the
-    reference's own batched output on the golden case."""
+    reference's own batched output on the golden case. The last case: 40 rows past position 2300 (37 chunks)."""
     L = hu.lib()
     g = golden()
     rng = orc.Rng(orc.SEED + 700 + m)
