@@ -8,8 +8,8 @@ HIP graph with every input already in HBM; attention, RMSNorm and RoPE are not p
 
 Alongside (`prefill`): the 8B INT8 W8A8 prefill of a 2048-token prompt: per layer quantize the 2048 rows and run the
 int8-MFMA GEMMs (QKV, Wo + residual, W1/W3 SwiGLU, W2 + residual), then the last row's classifier GEMV.
-`forward_decode`: the whole 8B decode token on the device (the matmul set plus RMSNorm, RoPE, the K/V cache store and
-attention over 2048 cached positions), also from a HIP graph.
+`forward_decode`: the whole 8B decode token on the device (the embedding row, the matmul set plus RMSNorm, RoPE, the K/V
+cache store and attention over 2048 cached positions), also from a HIP graph.
 
 Weights ~N(0, 0.02) and activations ~N(0, 1) are drawn on the device (torch, seeded) and quantized by the library's
 own k_quantize rule; the data is synthetic. `roofline` is the dominant kernel of the decode step (the SwiGLU GEMV),
@@ -131,7 +131,8 @@ CONTEXT = 2048  # the position the full decode token is measured at (its attenti
 
 def forward_decode_set(torch, lh, model, seed):
     """One token of the device-resident 8B forward at position CONTEXT - 1, in the reference's decode order
-    (src/tp.c:397-432): per layer RMSNorm, quantize + QKV, RoPE, K/V cache store, attention over the cache, quantize +
+    (src/tp.c:395-432): the token's embedding row (the classifier's Q8_0 table, as a tied model looks it up), per layer
+    RMSNorm, quantize + QKV, RoPE, K/V cache store, attention over the cache, quantize +
     Wo (+ residual), RMSNorm, quantize + W1/W3 SwiGLU, quantize + W2 (+ residual); then the final RMSNorm and the
     classifier. Synthetic cache contents, norm weights and rope table; the matmul weights are the decode set's."""
     import ctypes
@@ -152,6 +153,7 @@ def forward_decode_set(torch, lh, model, seed):
     cfg.head_dim, cfg.rope_theta, cfg.rope_type = HEAD_DIM, 500000.0, 1
     cfg.rope_factor, cfg.rope_low, cfg.rope_high, cfg.rope_original = 8.0, 1.0, 4.0, 8192
     table = torch.empty(2 * HEAD_DIM, **f32)
+    token = torch.tensor([VOCAB // 3], dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()
     pos = CONTEXT - 1
     L.k_rope_table(ctypes.byref(cfg), pos, P(table))
@@ -162,6 +164,7 @@ def forward_decode_set(torch, lh, model, seed):
         return lh.K8Weight(P(pair[0]), P(pair[1]))
 
     def run_step():
+        L.k_embed_q8_rows(P(x), P(model.cls[0]), P(model.cls[1]), P(token), 1, DIM, GS, VOCAB)
         for l, lay in enumerate(model.layers):
             kc, vc = cache[l]
             L.k_rmsnorm(P(xb), P(x), P(norms[2 * l]), DIM, 1e-5)
@@ -541,7 +544,7 @@ def main():
         result["forward_decode"] = {
             "value": round(1.0 / fsec, 2), "unit": "tok/s", "ms_per_token": round(fsec * 1e3, 4),
             "matmul_share": round((seconds / args.steps) / fsec, 3),
-            "workload": f"Llama-3.1-8B Q8_0 decode token on the device at position {CONTEXT - 1}: 32 x (RMSNorm, "
+            "workload": f"Llama-3.1-8B Q8_0 decode token on the device at position {CONTEXT - 1}: embedding row, 32 x (RMSNorm, "
                         "quantize + QKV, RoPE, K/V store, attention over the head-major cache, quantize + Wo +resid, "
                         "RMSNorm, quantize + W1/W3 SwiGLU, quantize + W2 +resid) + RMSNorm + classifier, HIP graph"}
         print(f"# device decode token at position {CONTEXT - 1}: {fsec * 1e3:.3f} ms, {1 / fsec:.1f} tok/s",

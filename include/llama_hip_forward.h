@@ -29,6 +29,14 @@ void k_rope_apply(float *q, float *k, const float *table, int n_heads, int n_kv_
 void k_rope_apply_rows(float *q, size_t q_stride, float *k, size_t k_stride, const float *table, size_t table_stride,
                        int rows, int n_heads, int n_kv_heads, int head_dim);
 
+/* The embedding lookup of a Q8_0 table (vocab x dim int8 values, one float scale per gs consecutive values), inline
+ * in the reference's forward (src/tp.c:395-396 for a token, 444-456 for a batch): out row i = table row ids[i], each
+ * value (float)q * scale, bitwise. ids is read on the device; an id outside [0, vocab) fails with "embedding row id
+ * outside the table" at the next host-visible point and leaves its row unwritten. The table and scales are usually a
+ * registered host range (the tied classifier's weights) or device memory. */
+void k_embed_q8_rows(float *out, const signed char *table, const float *scales, const int *ids, int count, int dim,
+                     int gs, int vocab);
+
 /* kernels.h:127-132: the attention workspace record. The device attention keeps its split-K partials in a library
  * workspace; this record only carries the shapes (partial is never dereferenced). */
 typedef struct {

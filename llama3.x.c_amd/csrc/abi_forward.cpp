@@ -311,6 +311,32 @@ void k_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int cou
     call.finish();
 }
 
+// ---- embedding rows (src/tp.c:395-396, 444-456) -------------------------------------------------------------------
+
+void k_embed_q8_rows(float *out, const int8_t *table, const float *scales, const int *ids, int count, int dim, int gs,
+                     int vocab) {
+  if (count <= 0)
+    return;
+  if (!out || !table || !scales || !ids) {
+    raise("k_embed_q8_rows: null buffer");
+    return;
+  }
+  if (dim <= 0 || vocab <= 0 || gs <= 0 || ((size_t)vocab * dim) % gs != 0) {
+    raise("k_embed_q8_rows: a %d x %d table in groups of %d", vocab, dim, gs);
+    return;
+  }
+  const size_t values = (size_t)vocab * dim;
+  Call call("k_embed_q8_rows");
+  Ref T = call.in(table, values), S = call.in(scales, values / gs * sizeof(float));
+  Ref I = call.in(ids, (size_t)count * sizeof(int));
+  Ref O = call.out(out, (size_t)count * dim * sizeof(float), false);
+  if (!call.ready())
+    return;
+  if (launch_embed_rows(call.ptr<float>(O), call.ptr<const int8_t>(T), call.ptr<const float>(S),
+                        call.ptr<const int>(I), count, dim, gs, vocab, call.stream()))
+    call.finish();
+}
+
 // ---- attention (kernels.h:124-179, src/attention.c:516-596, 1357-1455) -------------------------------------------
 //
 // The device attention keeps its split-K partials in a library workspace, so AttentionWork is the reference's record

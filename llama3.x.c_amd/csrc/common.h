@@ -23,7 +23,8 @@ struct Device {
   bool ready = false;
   int ordinal = 0;
   hipStream_t stream = nullptr;
-  int *error_flags = nullptr; // device: [0] non-finite activation seen by a quantizer, [1] non-finite attention score
+  int *error_flags = nullptr; // device: [0] non-finite activation seen by a quantizer, [1] non-finite attention score,
+                              // [2] an embedding row id outside the table
   int cu_count = 0;
   bool capturing = false;
   void *split_partial = nullptr;  // split-K partial tiles: LLHIP_SPLIT_SLOTS x 256 x 128 floats
@@ -203,6 +204,8 @@ bool launch_rope(float *q, size_t q_stride, float *k, size_t k_stride, const flo
                  int rows, int n_heads, int n_kv_heads, int head_dim, hipStream_t stream);
 bool launch_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,
                      size_t pos_stride, size_t head_base, hipStream_t stream);
+bool launch_embed_rows(float *out, const int8_t *table, const float *scales, const int *ids, int count, int dim,
+                       int gs, int vocab, hipStream_t stream);
 // Causal attention of `rows` query rows at positions pos0 .. pos0 + rows - 1 (q and out: rows x n_heads x head_dim);
 // position t of KV head g at key / value + t * pos_stride + g * head_base.
 struct AttentionJob {

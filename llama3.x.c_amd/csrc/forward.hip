@@ -142,6 +142,26 @@ __global__ __launch_bounds__(kThreads) void kv_store(float *__restrict__ cache, 
   cache[(size_t)(pos0 + r) * pos_stride + (size_t)g * head_base + d] = src[(size_t)r * src_ld + rest];
 }
 
+// ---- embedding rows -------------------------------------------------------------------------------------------------
+
+// out[i][j] = table[ids[i]][j] * scales[(ids[i] * dim + j) / gs]: the int8 value converted exactly and one float
+// product, bitwise the reference's lookup (src/tp.c:395-396, 444-456). An id outside [0, vocab) raises flag 2 and
+// leaves its row untouched. One thread per value; the table row is read once.
+__global__ __launch_bounds__(kThreads) void embed_rows(float *__restrict__ out, const int8_t *__restrict__ table,
+                                                       const float *__restrict__ scales, const int *__restrict__ ids,
+                                                       int count, int dim, int gs, int vocab, int *flags) {
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (long long)count * dim)
+    return;
+  const int r = (int)(i / dim), j = (int)(i % dim), id = ids[r];
+  if (id < 0 || id >= vocab) {
+    flags[2] = 1;
+    return;
+  }
+  const size_t at = (size_t)id * dim + j;
+  out[(size_t)r * dim + j] = (float)table[at] * scales[at / gs];
+}
+
 // ---- attention ------------------------------------------------------------------------------------------------------
 
 struct AttnParams {
@@ -463,6 +483,14 @@ bool launch_kv_store(float *cache, const float *src, size_t src_ld, int pos0, in
   hipLaunchKernelGGL(kv_store, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream, cache,
                      src, src_ld, pos0, count, n_kv_heads, head_dim, pos_stride, head_base);
   return launch_ok("kv_store");
+}
+
+bool launch_embed_rows(float *out, const int8_t *table, const float *scales, const int *ids, int count, int dim,
+                       int gs, int vocab, hipStream_t stream) {
+  const long long threads = (long long)count * dim;
+  hipLaunchKernelGGL(embed_rows, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream, out,
+                     table, scales, ids, count, dim, gs, vocab, device().error_flags);
+  return launch_ok("embed_rows");
 }
 
 int slot_floats(int head_dim) { return (head_dim + 2 + 3) & ~3; }

@@ -118,10 +118,12 @@ bool synchronize_and_check() {
   int flags[16];
   if (!LLHIP_CHECK(hipMemcpy(flags, dev.error_flags, sizeof(flags), hipMemcpyDeviceToHost)))
     return false;
-  if (flags[0] || flags[1]) {
+  if (flags[0] || flags[1] || flags[2]) {
     int zero[16] = {0};
     (void)hipMemcpy(dev.error_flags, zero, sizeof(zero), hipMemcpyHostToDevice);
-    return raise(flags[0] ? "nonfinite activation during INT8 quantization" : "nonfinite value in softmax");
+    return raise(flags[0]   ? "nonfinite activation during INT8 quantization"
+                 : flags[1] ? "nonfinite value in softmax"
+                            : "embedding row id outside the table");
   }
   return true;
 }

@@ -117,6 +117,7 @@ _SIGNATURES = {
     "kernels_kv_layout_select": (I32, [ctypes.c_char_p]),
     "k_kv_strides": (None, [I32, I32, I32, P, P]),
     "k_kv_store": (None, [P, P, SZ, I32, I32, I32, I32, I32]),
+    "k_embed_q8_rows": (None, [P, P, P, P, I32, I32, I32, I32]),
     "k_attention_init": (None, [P, I32, I32, I32, I32]),
     "k_attention_bytes": (SZ, [I32, I32, I32, I32]),
     "k_attention_init_in": (None, [P, I32, I32, I32, I32, P]),

@@ -272,6 +272,42 @@ def test_attention_nonfinite_score_fails_and_bookkeeping():
     assert L.kernels_attention_select(b"tiled", b"group") == 1 and L.kernels_attention_select(b"x", None) == 0
 
 
+# ---- embedding rows ------------------------------------------------------------------------------------------------
+
+
+def test_embed_q8_rows_bitwise_host_device_and_bad_id():
+    """Embedding lookup of a Q8_0 table (src/tp.c:395-396, 444-456): each value is the int8 converted exactly times its
+    group's scale, one float product, so the row is bitwise numpy's float32 product. Groups straddle rows (dim 96,
+    gs 64). Host operands and device operands (ids read on the device) give the same bits."""
+    L = hu.lib()
+    rng = np.random.default_rng(orc.SEED + 909)
+    vocab, dim, gs = 778, 96, 64
+    table = rng.integers(-127, 128, vocab * dim, dtype=np.int8)
+    scales = rng.uniform(1e-4, 2e-2, vocab * dim // gs).astype(np.float32)
+    ids = np.array([0, 777, 5, 5, 400, 1], np.int32)
+    flat = ids[:, None].astype(np.int64) * dim + np.arange(dim)
+    want = table[flat].astype(np.float32) * scales[flat // gs]
+    out = np.full((len(ids), dim), np.nan, np.float32)
+    L.k_embed_q8_rows(lh.ptr(out), lh.ptr(table), lh.ptr(scales), lh.ptr(ids), len(ids), dim, gs, vocab)
+    assert np.array_equal(out.view(np.int32), want.view(np.int32))
+    dt, ds, di = hu.dev(table), hu.dev(scales), hu.dev(ids)
+    do = hu.empty(len(ids) * dim, hu.torch().float32)
+    L.k_embed_q8_rows(lh.ptr(do), lh.ptr(dt), lh.ptr(ds), lh.ptr(di), len(ids), dim, gs, vocab)
+    assert np.array_equal(hu.host(do).reshape(len(ids), dim).view(np.int32), want.view(np.int32))
+    lh.record_failures()
+    try:
+        bad = np.array([3, vocab], np.int32)
+        L.k_embed_q8_rows(lh.ptr(out), lh.ptr(table), lh.ptr(scales), lh.ptr(bad), 2, dim, gs, vocab)
+        assert "embedding row id outside the table" in lh.last_error()
+        L.llhip_clear_error()
+        L.k_embed_q8_rows(lh.ptr(out), lh.ptr(table), lh.ptr(scales), lh.ptr(ids), 1, dim, 7, vocab)
+        assert "groups of 7" in lh.last_error()
+        L.llhip_clear_error()
+    finally:
+        L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+        L.llhip_clear_error()
+
+
 # ---- RMSNorm recorded into the next GEMV's prologue -----------------------------------------------------------------
 
 
