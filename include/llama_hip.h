@@ -48,6 +48,15 @@ int llhip_unregister_host(const void *host);
 /* The device address a host address resolves to (NULL when it is not inside a registered range). */
 void *llhip_resolve(const void *host);
 
+/* The HBM budget (loader.h:46, src/loader.c:28-56): LLAMA_HBM_BUDGET_GIB (a positive number of GiB; anything else
+ * fails with the reference's message), by default the device's whole memory. Every device allocation the library
+ * makes or hands out (registered weights, llhip_malloc buffers such as K/V caches, aligned buffers, its staging and
+ * workspaces) is claimed against it first, and one beyond it fails with "<what> need N bytes of HBM but
+ * LLAMA_HBM_BUDGET_GIB leaves L of B". llhip_hbm_claimed reports the bytes claimed now (no counterpart in the
+ * reference, whose count is private to loader.c). */
+size_t placement_hbm_budget(void);
+size_t llhip_hbm_claimed(void);
+
 /* Device memory owned by the caller, and stream-ordered copies (all on the library stream). */
 void *llhip_malloc(size_t bytes);
 void llhip_free(void *device);

@@ -46,12 +46,16 @@ float *attention_partials(size_t floats) {
   if (attention_workspace) {
     (void)hipStreamSynchronize(dev.stream);
     (void)hipFree(attention_workspace);
+    hbm_release(attention_workspace_floats * sizeof(float));
     attention_workspace = nullptr;
     attention_workspace_floats = 0;
   }
   const size_t want = floats + floats / 4 + 1024;
+  if (!hbm_claim(want * sizeof(float), "the attention workspace"))
+    return nullptr;
   if (hipMalloc((void **)&attention_workspace, want * sizeof(float)) != hipSuccess) {
     (void)hipGetLastError();
+    hbm_release(want * sizeof(float));
     attention_workspace = nullptr;
     raise("allocating %zu bytes of attention workspace failed", want * sizeof(float));
     return nullptr;

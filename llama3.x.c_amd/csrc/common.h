@@ -35,6 +35,10 @@ struct Device {
 #define LLHIP_SPLIT_SLOTS 512
 Device &device();
 bool ensure_device(); // opens the device on first use; false (after raise) when none is usable
+// Claims bytes of HBM against LLAMA_HBM_BUDGET_GIB before an allocation (false after raise when it does not fit), and
+// gives them back after the free.
+bool hbm_claim(size_t bytes, const char *what);
+void hbm_release(size_t bytes);
 // Waits for the stream and turns a device-side error flag into a failure (the reference fails at once; a device
 // kernel can only report at the next host-visible point).
 bool synchronize_and_check();

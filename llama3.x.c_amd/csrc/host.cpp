@@ -196,16 +196,25 @@ void aligned_buffer_alloc(AlignedBuffer *buffer, size_t bytes, MemoryKind kind) 
   buffer->base = buffer->data = nullptr;
   buffer->bytes = 0;
   void *p = nullptr;
-  if (!ensure_device() || !check_hip(hipMalloc(&p, bytes ? bytes : 1), "allocating an aligned buffer") ||
-      !check_hip(hipMemset(p, 0, bytes ? bytes : 1), "clearing an aligned buffer"))
+  const size_t claim = bytes ? bytes : 1;
+  if (!ensure_device() || !hbm_claim(claim, "an aligned buffer"))
     return;
+  if (!check_hip(hipMalloc(&p, claim), "allocating an aligned buffer") ||
+      !check_hip(hipMemset(p, 0, claim), "clearing an aligned buffer")) {
+    if (p)
+      (void)hipFree(p);
+    hbm_release(claim);
+    return;
+  }
   buffer->base = buffer->data = p;
   buffer->bytes = bytes;
 }
 
 void aligned_buffer_free(AlignedBuffer *buffer) {
-  if (buffer->base)
+  if (buffer->base) {
     (void)check_hip(hipFree(buffer->base), "freeing an aligned buffer");
+    hbm_release(buffer->bytes ? buffer->bytes : 1);
+  }
   buffer->base = buffer->data = nullptr;
   buffer->bytes = 0;
 }

@@ -19,6 +19,51 @@ int fail_mode = LLHIP_FAIL_EXIT;
 char last_error[512] = "";
 } // namespace
 
+// ---- HBM budget (src/loader.c:28-56) --------------------------------------------------------------------------------
+//
+// Every device allocation the library makes or hands out (registered weights, llhip_malloc buffers such as the K/V
+// caches, aligned BF16 panels, the staging arena, the attention and split-K workspaces) is claimed against
+// LLAMA_HBM_BUDGET_GIB, by default the device's whole memory; a claim beyond it fails with the reference's message.
+namespace {
+std::mutex budget_mutex;
+size_t hbm_claimed = 0;
+size_t device_total = 0; // the device's memory, known once it is open
+} // namespace
+
+// The budget in bytes, or 0 after raise for a malformed LLAMA_HBM_BUDGET_GIB (parsed on every claim, like the
+// reference, so a bad value never goes unnoticed).
+static size_t budget_bytes() {
+  const char *value = getenv("LLAMA_HBM_BUDGET_GIB");
+  if (!value || !*value)
+    return device_total;
+  char *end;
+  const double gib = strtod(value, &end);
+  if (*end || !(gib > 0) || gib > (double)(1 << 20))
+    return raise("LLAMA_HBM_BUDGET_GIB must be a positive number of GiB"), 0;
+  return (size_t)(gib * (double)(1 << 30));
+}
+
+bool hbm_claim(size_t bytes, const char *what) {
+  const size_t budget = budget_bytes();
+  if (!budget)
+    return false;
+  size_t left;
+  {
+    std::lock_guard<std::mutex> lock(budget_mutex);
+    if (bytes <= budget && hbm_claimed <= budget - bytes) {
+      hbm_claimed += bytes;
+      return true;
+    }
+    left = budget > hbm_claimed ? budget - hbm_claimed : 0;
+  }
+  return raise("%s need %zu bytes of HBM but LLAMA_HBM_BUDGET_GIB leaves %zu of %zu", what, bytes, left, budget);
+}
+
+void hbm_release(size_t bytes) {
+  std::lock_guard<std::mutex> lock(budget_mutex);
+  hbm_claimed -= bytes < hbm_claimed ? bytes : hbm_claimed;
+}
+
 bool raise(const char *format, ...) {
   char message[512];
   va_list args;
@@ -83,6 +128,10 @@ bool ensure_device() {
   hipStream_t stream;
   if (!LLHIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking)))
     return false;
+  device_total = props.totalGlobalMem;
+  if (!hbm_claim((size_t)LLHIP_SPLIT_SLOTS * (256 * 128 * sizeof(float) + sizeof(unsigned)) + 64,
+                 "the split-K workspace"))
+    return false;
   int *flags;
   if (!LLHIP_CHECK(hipMalloc(&flags, 64)))
     return false;
@@ -137,6 +186,7 @@ struct Region {
 };
 std::mutex registry_mutex;
 std::map<uintptr_t, Region> registry;
+std::map<void *, size_t> allocations; // llhip_malloc's buffers and their claimed bytes (under registry_mutex)
 
 // The device copy of p when p lies inside a registered range, else nullptr; *room receives the bytes of the range
 // from p to its end.
@@ -414,11 +464,17 @@ bool Call::ready() {
     if (arena) {
       (void)hipStreamSynchronize(the_device.stream);
       (void)hipFree(arena);
+      hbm_release(arena_bytes);
     }
     arena = nullptr;
     arena_bytes = 0;
     size_t want = arena_used_ + (arena_used_ >> 2) + 4096;
+    if (!hbm_claim(want, "the staging arena")) {
+      failed_ = true;
+      return false;
+    }
     if (!LLHIP_CHECK(hipMalloc(&arena, want))) {
+      hbm_release(want);
       arena = nullptr;
       failed_ = true;
       return false;
@@ -485,10 +541,13 @@ int llhip_register_host(const void *host, size_t bytes) {
         return raise("llhip_register_host: range overlaps a registered range"), -1;
   }
   void *dev;
-  if (!LLHIP_CHECK(hipMalloc(&dev, bytes)))
+  if (!hbm_claim(bytes, "registered weights"))
     return -1;
+  if (!LLHIP_CHECK(hipMalloc(&dev, bytes)))
+    return hbm_release(bytes), -1;
   if (!LLHIP_CHECK(hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice))) {
     (void)hipFree(dev);
+    hbm_release(bytes);
     return -1;
   }
   std::lock_guard<std::mutex> lock(registry_mutex);
@@ -500,16 +559,19 @@ int llhip_unregister_host(const void *host) {
   if (!ensure_device())
     return -1;
   void *dev = nullptr;
+  size_t bytes = 0;
   {
     std::lock_guard<std::mutex> lock(registry_mutex);
     auto it = registry.find((uintptr_t)host);
     if (it == registry.end())
       return raise("llhip_unregister_host: %p is not the start of a registered range", host), -1;
     dev = it->second.device;
+    bytes = it->second.bytes;
     registry.erase(it);
   }
   if (!LLHIP_CHECK(hipStreamSynchronize(the_device.stream)))
     return -1;
+  hbm_release(bytes);
   return LLHIP_CHECK(hipFree(dev)) ? 0 : -1;
 }
 
@@ -518,17 +580,42 @@ void *llhip_resolve(const void *host) { return lookup(host); }
 void *llhip_malloc(size_t bytes) {
   if (!ensure_device())
     return nullptr;
-  void *p = nullptr;
-  if (!LLHIP_CHECK(hipMalloc(&p, bytes ? bytes : 1)))
+  bytes = bytes ? bytes : 1;
+  if (!hbm_claim(bytes, "llhip_malloc"))
     return nullptr;
+  void *p = nullptr;
+  if (!LLHIP_CHECK(hipMalloc(&p, bytes)))
+    return hbm_release(bytes), nullptr;
+  std::lock_guard<std::mutex> lock(registry_mutex);
+  allocations[p] = bytes;
   return p;
 }
 
 void llhip_free(void *p) {
   if (!p || !ensure_device() || !flush_pending_quantize())
     return;
-  if (LLHIP_CHECK(hipStreamSynchronize(the_device.stream)))
-    (void)LLHIP_CHECK(hipFree(p));
+  if (!LLHIP_CHECK(hipStreamSynchronize(the_device.stream)))
+    return;
+  {
+    std::lock_guard<std::mutex> lock(registry_mutex);
+    auto it = allocations.find(p);
+    if (it != allocations.end()) {
+      hbm_release(it->second);
+      allocations.erase(it);
+    }
+  }
+  (void)LLHIP_CHECK(hipFree(p));
+}
+
+size_t placement_hbm_budget(void) {
+  if (!device_total && !getenv("LLAMA_HBM_BUDGET_GIB"))
+    (void)ensure_device(); // the default is the device's memory
+  return budget_bytes();
+}
+
+size_t llhip_hbm_claimed(void) {
+  std::lock_guard<std::mutex> lock(budget_mutex);
+  return hbm_claimed;
 }
 
 void llhip_memcpy_h2d(void *dst, const void *src, size_t bytes) {

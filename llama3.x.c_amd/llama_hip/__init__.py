@@ -118,6 +118,8 @@ _SIGNATURES = {
     "k_kv_strides": (None, [I32, I32, I32, P, P]),
     "k_kv_store": (None, [P, P, SZ, I32, I32, I32, I32, I32]),
     "k_embed_q8_rows": (None, [P, P, P, P, I32, I32, I32, I32]),
+    "placement_hbm_budget": (SZ, []),
+    "llhip_hbm_claimed": (SZ, []),
     "k_attention_init": (None, [P, I32, I32, I32, I32]),
     "k_attention_bytes": (SZ, [I32, I32, I32, I32]),
     "k_attention_init_in": (None, [P, I32, I32, I32, I32, P]),

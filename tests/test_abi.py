@@ -300,3 +300,20 @@ def test_prefill_validate(record):
     toks[2] = 100
     L.prefill_validate(m, lh.ptr(toks), 4, 3, lh.LOGITS_ALL)
     assert lh.last_error() == "forward input out of range: token=100 position=5"
+
+
+def test_hbm_budget_parses_like_the_reference(record, monkeypatch):
+    """placement_hbm_budget (src/loader.c:28-37): LLAMA_HBM_BUDGET_GIB in GiB, fractions allowed; zero, negative,
+    trailing text and more than 2^20 GiB fail with the reference's message. (The default, the device's memory, needs
+    the device and is checked by the GPU tests.)"""
+    L = record
+    monkeypatch.setenv("LLAMA_HBM_BUDGET_GIB", "1.5")
+    assert L.placement_hbm_budget() == 3 << 29
+    monkeypatch.setenv("LLAMA_HBM_BUDGET_GIB", "288")
+    assert L.placement_hbm_budget() == 288 << 30
+    for bad in ("0", "-2", "12GiB", "2000000"):
+        monkeypatch.setenv("LLAMA_HBM_BUDGET_GIB", bad)
+        L.llhip_clear_error()
+        assert L.placement_hbm_budget() == 0
+        assert lh.last_error() == "LLAMA_HBM_BUDGET_GIB must be a positive number of GiB", bad
+    L.llhip_clear_error()
