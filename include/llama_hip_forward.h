@@ -33,7 +33,8 @@ void k_rope_apply_rows(float *q, size_t q_stride, float *k, size_t k_stride, con
  * in the reference's forward (src/tp.c:395-396 for a token, 444-456 for a batch): out row i = table row ids[i], each
  * value (float)q * scale, bitwise. ids is read on the device; an id outside [0, vocab) fails with "embedding row id
  * outside the table" at the next host-visible point and leaves its row unwritten. The table and scales are usually a
- * registered host range (the tied classifier's weights) or device memory. */
+ * registered host range (the tied classifier's weights) or device memory; a plain host table is staged whole on every
+ * call (vocab x dim bytes), so register it once. */
 void k_embed_q8_rows(float *out, const signed char *table, const float *scales, const int *ids, int count, int dim,
                      int gs, int vocab);
 
