@@ -119,6 +119,11 @@ _SIGNATURES = {
     "k_kv_store": (None, [P, P, SZ, I32, I32, I32, I32, I32]),
     "k_embed_q8_rows": (None, [P, P, P, P, I32, I32, I32, I32]),
     "placement_hbm_budget": (SZ, []),
+    "engine_load": (None, [P, ctypes.c_char_p]),
+    "engine_load_context": (None, [P, ctypes.c_char_p, I32]),
+    "engine_forward": (ctypes.POINTER(ctypes.c_float), [P, I32, I32]),
+    "engine_free": (None, [P]),
+    "engine_group_size": (I32, []),
     "llhip_hbm_claimed": (SZ, []),
     "k_attention_init": (None, [P, I32, I32, I32, I32]),
     "k_attention_bytes": (SZ, [I32, I32, I32, I32]),

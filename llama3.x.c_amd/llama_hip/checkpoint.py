@@ -1,0 +1,87 @@
+"""Writer of version-3 INT8 (Q8_0) checkpoints, the format engine_load reads (src/runtime.c:179-260 for the header,
+src/shards.c:77-99 for the tensor order), and a seeded synthetic model for tests and benchmarks.
+
+Header (256 bytes, little-endian): magic 0x616b3432, version 3, the seven Config ints (dim, hidden_dim, n_layers,
+n_heads, n_kv_heads, vocab_size, seq_len), precision (1 = INT8), shared classifier flag, group size, norm_eps,
+rope_theta, rope_type, rope_factor, rope_low, rope_high, rope_original, max_seq_len, head_dim, bos/eos/eot/eom ids,
+a 128-byte NUL-terminated name, 28 zero bytes. Body: FP32 rms_att[L], rms_ffn[L], rms_final; then each INT8 tensor as
+its values followed by its FP32 group scales: the embedding, wq[L], wk[L], wv[L], wo[L], w1[L], w2[L], w3[L], and the
+classifier unless it is tied to the embedding."""
+import struct
+
+import numpy as np
+
+MAGIC = 0x616B3432
+ROLES = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
+
+
+def header(cfg, gs, shared, name="synthetic"):
+    """The 256 header bytes of cfg (a dict with the Config fields)."""
+    h = struct.pack("<II7iiii", MAGIC, 3, cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["n_heads"],
+                    cfg["n_kv_heads"], cfg["vocab_size"], cfg["seq_len"], 1, int(shared), gs)
+    h += struct.pack("<ffifffiiiiiii", cfg.get("norm_eps", 1e-5), cfg.get("rope_theta", 500000.0),
+                     cfg.get("rope_type", 0), cfg.get("rope_factor", 1.0), cfg.get("rope_low", 1.0),
+                     cfg.get("rope_high", 4.0), cfg.get("rope_original", 8192), cfg.get("max_seq_len", cfg["seq_len"]),
+                     cfg["dim"] // cfg["n_heads"], cfg.get("bos_id", 128000), cfg.get("eos_id", 128001),
+                     cfg.get("eot_id", 128009), cfg.get("eom_id", -1))
+    h += name.encode()[:127].ljust(128, b"\0")
+    assert len(h) == 228
+    return h + bytes(28)
+
+
+def quantize_q8(w, gs):
+    """Q8_0 of FP32 rows: per group of gs values scale = max|w| / 127, q = round(w / scale) (half away from zero)."""
+    g = np.asarray(w, np.float32).reshape(-1, gs)
+    scale = (np.abs(g).max(axis=1) / np.float32(127.0)).astype(np.float32)
+    safe = np.where(scale > 0, scale, np.float32(1.0))
+    r = g / safe[:, None]
+    q = (np.sign(r) * np.floor(np.abs(r) + np.float32(0.5))).clip(-127, 127).astype(np.int8)
+    return q.reshape(np.shape(w)), scale
+
+
+def write_q8_v3(path, cfg, gs, norms, tensors, shared=True):
+    """Writes a checkpoint. norms: rms_att (L, dim), rms_ffn (L, dim), rms_final (dim,) float32. tensors: "embed" and
+    each role of ROLES as (q int8 [L][rows][cols] or [rows][cols] for embed/cls, s float32 with one scale per gs
+    values), plus "cls" when not shared."""
+    with open(path, "wb") as f:
+        f.write(header(cfg, gs, shared))
+        for key in ("rms_att", "rms_ffn", "rms_final"):
+            f.write(np.ascontiguousarray(norms[key], np.float32).tobytes())
+
+        def put(q, s):
+            f.write(np.ascontiguousarray(q, np.int8).tobytes())
+            f.write(np.ascontiguousarray(s, np.float32).tobytes())
+
+        put(*tensors["embed"])
+        for role in ROLES:
+            q, s = tensors[role]
+            for layer in range(cfg["n_layers"]):
+                put(q[layer], s[layer])
+        if not shared:
+            put(*tensors["cls"])
+
+
+def synthetic(cfg, gs, seed, scale=0.05):
+    """A seeded random model of cfg: norms near 1, weights ~N(0, scale) quantized to Q8_0. Returns (norms, tensors)."""
+    rng = np.random.default_rng(seed)
+    d, h, L, v = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["vocab_size"]
+    kv = d // cfg["n_heads"] * cfg["n_kv_heads"]
+    norms = {"rms_att": rng.uniform(0.8, 1.2, (L, d)).astype(np.float32),
+             "rms_ffn": rng.uniform(0.8, 1.2, (L, d)).astype(np.float32),
+             "rms_final": rng.uniform(0.8, 1.2, d).astype(np.float32)}
+    shapes = {"wq": (d, d), "wk": (kv, d), "wv": (kv, d), "wo": (d, d), "w1": (h, d), "w2": (d, h), "w3": (h, d)}
+    tensors = {"embed": quantize_q8(rng.normal(0, 1.0, (v, d)).astype(np.float32), gs)}
+    for role, (rows, cols) in shapes.items():
+        q, s = quantize_q8(rng.normal(0, scale, (L, rows, cols)).astype(np.float32), gs)
+        tensors[role] = (q, s.reshape(L, rows * cols // gs))
+    tensors["cls"] = tensors["embed"]
+    return norms, tensors
+
+
+def file_bytes(cfg, gs, shared=True):
+    """The exact size of a version-3 INT8 checkpoint of cfg (src/runtime.c:279-293)."""
+    d, h, L, v = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["vocab_size"]
+    kv = d // cfg["n_heads"] * cfg["n_kv_heads"]
+    t = lambda n: n + n // gs * 4
+    size = 256 + (2 * L + 1) * d * 4 + t(v * d) + L * sum(t(n) for n in (d * d, d * kv, d * kv, d * d, d * h, h * d, d * h))
+    return size + (0 if shared else t(v * d))

@@ -1,0 +1,110 @@
+"""The Q8_0 engine end to end on the device: engine_load of a seeded synthetic version-3 checkpoint and
+engine_forward over a short sequence, against the same forward composed from the oracle's kernels (quantize, the
+W8A8 GEMVs, RMSNorm, RoPE, attention) in the reference's decode order (src/tp.c:387-436).
+
+The device sums in other orders than the oracle (GEMV partials, the RMSNorm and attention reductions), so an
+activation near a rounding boundary of the INT8 quantizer can round the other way; the bar is the reference's own
+W8A8 gate shape (compare_engines.py): the logits within 2% of their range in max norm and 0.5% in L2, and the same
+argmax at every position. A wrong tensor order, head layout, residual or RoPE position breaks all three."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import llama_hip as lh
+from llama_hip import checkpoint as ck
+from oracle import pyoracle as orc
+from tests import hip_util as hu
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(dim=128, hidden_dim=256, n_layers=3, n_heads=8, n_kv_heads=2, vocab_size=200, seq_len=80,
+           rope_theta=10000.0)
+GS = 32
+
+
+def rope_table(cfg, pos):
+    hd = cfg["dim"] // cfg["n_heads"]
+    j = np.arange(0, hd, 2, dtype=np.float32)
+    freq = np.float32(1.0) / np.power(np.float32(cfg["rope_theta"]), j / np.float32(hd)).astype(np.float32)
+    angle = (np.float32(pos) * freq).astype(np.float32)
+    c, s = np.cos(angle).astype(np.float32), np.sin(angle).astype(np.float32)
+    return np.concatenate([np.repeat(c, 2), np.stack([-s, s], 1).reshape(-1)]).astype(np.float32)
+
+
+class OracleForward:
+    """The decode forward from the oracle's kernels, head-major K/V cache as the engine's default layout."""
+
+    def __init__(self, cfg, norms, t):
+        self.c, self.n, self.t = cfg, norms, t
+        d, L, S = cfg["dim"], cfg["n_layers"], cfg["seq_len"]
+        self.hd = d // cfg["n_heads"]
+        self.kv = self.hd * cfg["n_kv_heads"]
+        self.kc = [np.zeros(S * self.kv, np.float32) for _ in range(L)]
+        self.vc = [np.zeros(S * self.kv, np.float32) for _ in range(L)]
+
+    def w(self, role, l):
+        q, s = self.t[role]
+        return q[l], s[l].reshape(q.shape[1], -1)
+
+    def step(self, token, pos):
+        c, d, nh, nkv, hd, S = self.c, self.c["dim"], self.c["n_heads"], self.c["n_kv_heads"], self.hd, self.c["seq_len"]
+        eq, es = self.t["embed"]
+        x = (eq[token].astype(np.float32) * np.repeat(es.reshape(eq.shape[0], -1)[token], GS)).astype(np.float32)
+        table = rope_table(c, pos)
+        ps, hb = orc.kv_strides(nkv, hd, S, True)
+        for l in range(c["n_layers"]):
+            xb = orc.rmsnorm(x, self.n["rms_att"][l])
+            xq, xs = orc.quantize(xb, GS)
+            q = orc.matmul_q8(xq, xs, *self.w("wq", l), GS)
+            k = orc.matmul_q8(xq, xs, *self.w("wk", l), GS)
+            v = orc.matmul_q8(xq, xs, *self.w("wv", l), GS)
+            q, k = orc.rope_apply(q, k, table, nh, nkv, hd)
+            for g in range(nkv):
+                self.kc[l][g * hb + pos * ps: g * hb + pos * ps + hd] = k[g * hd:(g + 1) * hd]
+                self.vc[l][g * hb + pos * ps: g * hb + pos * ps + hd] = v[g * hd:(g + 1) * hd]
+            att = orc.attention(q, self.kc[l], self.vc[l], nh, nkv, hd, S, pos, ps, hb)
+            aq, as_ = orc.quantize(att, GS)
+            orc.matmul_q8(aq, as_, *self.w("wo", l), GS, kind=orc.K_ADD, out=x)
+            xb = orc.rmsnorm(x, self.n["rms_ffn"][l])
+            xq, xs = orc.quantize(xb, GS)
+            w1q, w1s = self.w("w1", l)
+            w3q, w3s = self.w("w3", l)
+            h = orc.matmul_q8(xq, xs, w1q, w1s, GS, kind=orc.K_SWIGLU, w3q=w3q, w3s=w3s)
+            hq, hs = orc.quantize(h, GS)
+            orc.matmul_q8(hq, hs, *self.w("w2", l), GS, kind=orc.K_ADD, out=x)
+        x = orc.rmsnorm(x, self.n["rms_final"])
+        xq, xs = orc.quantize(x, GS)
+        cq, cs = self.t["cls"]
+        return orc.matmul_q8(xq, xs, cq, cs.reshape(cq.shape[0], -1), GS)
+
+
+@pytest.mark.parametrize("layout", ["head", "rows"])
+def test_engine_forward_matches_the_oracle_forward(tmp_path, layout):
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    norms, t = ck.synthetic(CFG, GS, 11)
+    path = os.path.join(tmp_path, "tiny.bin")
+    ck.write_q8_v3(path, CFG, GS, norms, t)
+    assert L.kernels_kv_layout_select(layout.encode()) == 1
+    model = lh.Model()
+    try:
+        claimed = L.llhip_hbm_claimed()
+        L.engine_load(ctypes.byref(model), path.encode())
+        assert model.implementation and model.config.dim == CFG["dim"] and L.engine_group_size() == GS
+        assert L.llhip_hbm_claimed() >= claimed + os.path.getsize(path)  # the checkpoint is resident in HBM
+        ref = OracleForward(CFG, norms, t)
+        rng = np.random.default_rng(3)
+        for pos, token in enumerate(rng.integers(0, CFG["vocab_size"], 70)):  # past the first 64-position chunk
+            out = L.engine_forward(ctypes.byref(model), int(token), pos)
+            assert out, lh.last_error()
+            got = np.ctypeslib.as_array(out, shape=(CFG["vocab_size"],)).copy()
+            want = ref.step(int(token), pos)
+            span = float(want.max() - want.min())
+            assert np.abs(got - want).max() <= 0.02 * span, (layout, pos, np.abs(got - want).max(), span)
+            assert np.linalg.norm(got - want) <= 0.005 * np.linalg.norm(want), (layout, pos)
+            assert got.argmax() == want.argmax(), (layout, pos)
+    finally:
+        L.engine_free(ctypes.byref(model))
+        assert L.kernels_kv_layout_select(b"head") == 1
