@@ -435,6 +435,50 @@ def cpu_baseline(threads, budget_s=30.0):
             "sample": f"oracle scalar Q8 GEMV 4096x4096 x{reps}, {threads} threads, scaled to the 8B token by bytes"}
 
 
+def engine_bench(lh, L, args):
+    """The engine end to end (engine_load + engine_forward, logits to the host every token) on a synthetic untied
+    Llama-3.1-8B version-3 Q8_0 checkpoint written to $TMPDIR: tokens at positions 0 .. warmup + steps - 1, timed on
+    the host clock (engine_forward returns after the logits have arrived). Prints its own JSON line."""
+    import ctypes
+    import tempfile
+
+    import numpy as np
+
+    from llama_hip import checkpoint as ck
+    cfg = dict(dim=DIM, hidden_dim=HIDDEN, n_layers=LAYERS, n_heads=N_HEADS, n_kv_heads=N_KV_HEADS, vocab_size=VOCAB,
+               seq_len=CONTEXT, rope_theta=500000.0, rope_type=1, rope_factor=8.0, rope_low=1.0, rope_high=4.0,
+               rope_original=8192)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "llama8b_q8_synthetic.bin")
+        t0 = time.time()
+        ck.write_random_q8_v3(path, cfg, GS, args.seed, shared=False)
+        print(f"# wrote {os.path.getsize(path) / 1e9:.2f} GB checkpoint in {time.time() - t0:.1f} s", file=sys.stderr,
+              flush=True)
+        model = lh.Model()
+        t0 = time.time()
+        L.engine_load(ctypes.byref(model), path.encode())
+        print(f"# engine_load (map + upload to HBM) {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
+        rng = np.random.default_rng(args.seed)
+        tokens = rng.integers(0, VOCAB, args.warmup + args.steps)
+        for pos in range(args.warmup):
+            assert L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos), lh.last_error()
+        t0 = time.perf_counter()
+        for pos in range(args.warmup, args.warmup + args.steps):
+            out = L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos)
+        sec = (time.perf_counter() - t0) / args.steps
+        assert out, lh.last_error()
+        logits = np.ctypeslib.as_array(out, shape=(VOCAB,))
+        assert np.isfinite(logits).all()
+        L.engine_free(ctypes.byref(model))
+    print(json.dumps({"metric": "8B Q8_0 engine decode tok/s (engine_forward, logits to host)",
+                      "value": round(1.0 / sec, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+                      "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True,
+                      "scaling": "weak", "vs_baseline": None, "dtype": "int8 W8A8", "data": "synthetic",
+                      "config": {"workload": f"Llama-3.1-8B Q8_0 version-3 checkpoint (random int8 weights, untied "
+                                             f"classifier), decode at positions {args.warmup}.."
+                                             f"{args.warmup + args.steps - 1}, cache of {CONTEXT}"}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -449,6 +493,8 @@ def main():
                     help="skip the FP32 / BF16 prefill GEMMs on the Llama-3.2-3B shapes (512 tokens)")
     ap.add_argument("--no-forward", action="store_true",
                     help="skip the full device decode token (matmuls + RMSNorm, RoPE, K/V store, attention)")
+    ap.add_argument("--engine", action="store_true",
+                    help="measure engine_load + engine_forward on a synthetic 8B checkpoint instead")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also launch a plain copy kernel of this many MiB (counter calibration for --pmc runs)")
     args = ap.parse_args()
@@ -463,6 +509,8 @@ def main():
     L = lh.load()
     if L.llhip_init() != 0:
         raise SystemExit(f"no usable MI355X: {lh.last_error()}")
+    if args.engine:
+        return engine_bench(lh, L, args)
     t_setup = time.time()
     model = Model8B(torch, lh, args.seed)
     run_step = decode_set(torch, lh, model, args.seed)

@@ -85,3 +85,26 @@ def file_bytes(cfg, gs, shared=True):
     t = lambda n: n + n // gs * 4
     size = 256 + (2 * L + 1) * d * 4 + t(v * d) + L * sum(t(n) for n in (d * d, d * kv, d * kv, d * d, d * h, h * d, d * h))
     return size + (0 if shared else t(v * d))
+
+
+def write_random_q8_v3(path, cfg, gs, seed, shared=False):
+    """A large synthetic checkpoint written tensor by tensor (for benchmarks): uniform int8 values in [-127, 127],
+    scales uniform in [1e-4, 2e-4] (weights of magnitude about 0.01), norms near 1."""
+    rng = np.random.default_rng(seed)
+    d, h, L, v = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"], cfg["vocab_size"]
+    kv = d // cfg["n_heads"] * cfg["n_kv_heads"]
+    with open(path, "wb") as f:
+        f.write(header(cfg, gs, shared, name="synthetic-8b"))
+        for count in (L * d, L * d, d):
+            f.write(rng.uniform(0.8, 1.2, count).astype(np.float32).tobytes())
+
+        def put(count):
+            f.write(rng.integers(-127, 128, count, dtype=np.int8).tobytes())
+            f.write(rng.uniform(1e-4, 2e-4, count // gs).astype(np.float32).tobytes())
+
+        put(v * d)
+        for count in (d * d, kv * d, kv * d, d * d, h * d, d * h, h * d):
+            for _ in range(L):
+                put(count)
+        if not shared:
+            put(v * d)
