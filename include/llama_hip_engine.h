@@ -20,6 +20,11 @@ void engine_load_context(Model *model, const char *path, int context);
 /* runtime.h:103 (src/tp.c:387-436 with one socket): one decode token at `position`, whose prefix [0, position) was
  * run before; returns vocab_size logits, or NULL when the call failed in record mode. */
 float *engine_forward(Model *model, int token, int position);
+/* runtime.h:104-109 (src/tp.c:528-622 with one socket): count tokens at pos0 (the prefix [0, pos0) run before),
+ * 1 <= count <= engine_max_batch (2048), through the int8 GEMMs and the batched attention. LAST returns vocab_size
+ * logits of the last row, ALL count x vocab_size in row order, NONE returns NULL; the storage belongs to the model and
+ * is invalidated by the next forward. */
+float *engine_forward_batch(Model *model, const int *tokens, int count, int pos0, LogitsWanted want);
 void engine_free(Model *model);   /* runtime.h:114 */
 int engine_group_size(void);      /* runtime.h:116: the loaded checkpoint's group size */
 

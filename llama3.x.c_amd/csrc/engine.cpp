@@ -20,6 +20,7 @@
 #include "common.h"
 #include "llama_hip_engine.h"
 #include "llama_hip_forward.h"
+#include "llama_hip_gemm.h"
 
 namespace llhip {
 namespace {
@@ -49,6 +50,12 @@ struct Engine {
   int8_t *xq = nullptr, *hq = nullptr;
   std::vector<float> host_logits;
   AttentionWork work{};
+  // the batched forward's rows (max_batch of each, allocated on its first call)
+  int batch_rows = 0;
+  float *bx = nullptr, *bxb = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *bhb = nullptr, *bxs = nullptr;
+  float *brope = nullptr, *blogits = nullptr;
+  int8_t *bxq = nullptr;
+  std::vector<float> host_rope, host_batch_logits;
 };
 
 template <typename T> T read_at(const unsigned char *p, int offset) {
@@ -60,7 +67,9 @@ template <typename T> T read_at(const unsigned char *p, int offset) {
 void release(Engine *e) {
   for (void *p : {(void *)e->x, (void *)e->xb, (void *)e->q, (void *)e->k, (void *)e->v, (void *)e->hb,
                   (void *)e->logits, (void *)e->rope, (void *)e->key_cache, (void *)e->value_cache, (void *)e->xs,
-                  (void *)e->hs, (void *)e->xq, (void *)e->hq})
+                  (void *)e->hs, (void *)e->xq, (void *)e->hq, (void *)e->bx, (void *)e->bxb, (void *)e->bq,
+                  (void *)e->bk, (void *)e->bv, (void *)e->bhb, (void *)e->bxs, (void *)e->brope, (void *)e->blogits,
+                  (void *)e->bxq})
     if (p)
       llhip_free(p);
   if (e->map) {
@@ -265,6 +274,95 @@ bool forward(Engine *e, int token, int pos) {
   return llhip_last_error()[0] == 0;
 }
 
+bool allocate_batch(Engine *e, int rows) {
+  const Config &c = e->c;
+  const size_t m = rows, d = c.dim, kv = (size_t)c.head_dim * c.n_kv_heads, h = c.hidden_dim;
+  if (!(device_array(&e->bx, m * d) && device_array(&e->bxb, m * d) && device_array(&e->bq, m * d) &&
+        device_array(&e->bk, m * kv) && device_array(&e->bv, m * kv) && device_array(&e->bhb, m * h) &&
+        device_array(&e->bxq, m * h) && device_array(&e->bxs, m * h / e->gs) &&
+        device_array(&e->brope, m * 2 * c.head_dim)))
+    return false;
+  e->host_rope.resize(m * 2 * c.head_dim);
+  e->batch_rows = rows;
+  return true;
+}
+
+// count tokens at pos0 .. pos0 + count - 1 (src/tp.c:528-622 with one socket, W8A8): the embedding rows and RoPE
+// tables, per layer RMSNorm of the rows, quantize, the QKV GEMM, RoPE, the cache rows, batched causal attention,
+// quantize, Wo + residual, RMSNorm, quantize, W1/W3 SwiGLU, quantize, W2 + residual; then the final RMSNorm,
+// quantize and classifier GEMV of the last row (LAST) or of every row (ALL).
+float *forward_batch(Model *model, Engine *e, const int *tokens, int count, int pos0, LogitsWanted want) {
+  llhip_clear_error();
+  prefill_validate(model, tokens, count, pos0, want);
+  if (llhip_last_error()[0])
+    return nullptr;
+  const Config &c = e->c;
+  const int d = c.dim, hidden = c.hidden_dim, hd = c.head_dim, gs = e->gs, nh = c.n_heads, nkv = c.n_kv_heads;
+  const int kvl = hd * nkv;
+  if (!e->batch_rows && !allocate_batch(e, model->max_batch))
+    return nullptr;
+  for (int i = 0; i < count; i++)
+    k_rope_table(&c, pos0 + i, e->host_rope.data() + (size_t)i * 2 * hd);
+  llhip_memcpy_h2d(e->brope, e->host_rope.data(), (size_t)count * 2 * hd * sizeof(float));
+  k_embed_q8_rows(e->bx, e->embed.q, e->embed.s, tokens, count, d, gs, c.vocab_size);
+  const bool head = kernels_kv_layout_head() != 0;
+  for (int l = 0; l < c.n_layers; l++) {
+    const size_t layer = (size_t)l * c.seq_len * kvl;
+    float *kc = e->key_cache + layer, *vc = e->value_cache + layer;
+    float *kd = head ? e->bk : kc + (size_t)pos0 * kvl, *vd = head ? e->bv : vc + (size_t)pos0 * kvl;
+    k_rmsnorm_rows(e->bxb, e->bx, e->rms_att + (size_t)l * d, count, d, c.norm_eps);
+    k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
+    const GemmQ8Segment qkv[3] = {
+        {e->bq, d, K8Weight{e->wq[l].q, e->wq[l].s}, K8Weight{}, nullptr, nullptr, d, GEMM_STORE},
+        {kd, kvl, K8Weight{e->wk[l].q, e->wk[l].s}, K8Weight{}, nullptr, nullptr, kvl, GEMM_STORE},
+        {vd, kvl, K8Weight{e->wv[l].q, e->wv[l].s}, K8Weight{}, nullptr, nullptr, kvl, GEMM_STORE}};
+    k_gemm_q8(e->bxq, e->bxs, count, d, gs, qkv, 3);
+    k_rope_apply_rows(e->bq, d, kd, kvl, e->brope, 2 * (size_t)hd, count, nh, nkv, hd);
+    if (head) {
+      k_kv_store(kc, kd, kvl, pos0, count, nkv, hd, c.seq_len);
+      k_kv_store(vc, vd, kvl, pos0, count, nkv, hd, c.seq_len);
+    }
+    k_attention_batch_kv(e->bxb, e->bq, kc, vc, nullptr, &e->work, nh, nkv, hd, c.seq_len, pos0, count);
+    k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
+    const GemmQ8Segment wo{e->bx, d, K8Weight{e->wo[l].q, e->wo[l].s}, K8Weight{}, nullptr, nullptr, d, GEMM_ADD};
+    k_gemm_q8(e->bxq, e->bxs, count, d, gs, &wo, 1);
+    k_rmsnorm_rows(e->bxb, e->bx, e->rms_ffn + (size_t)l * d, count, d, c.norm_eps);
+    k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
+    const GemmQ8Segment up{e->bhb,  hidden,  K8Weight{e->w1[l].q, e->w1[l].s}, K8Weight{e->w3[l].q, e->w3[l].s},
+                           nullptr, nullptr, hidden,                          GEMM_SWIGLU};
+    k_gemm_q8(e->bxq, e->bxs, count, d, gs, &up, 1);
+    k_quantize_rows(e->bxq, e->bxs, e->bhb, hidden, count, hidden, gs);
+    const GemmQ8Segment down{e->bx, d, K8Weight{e->w2[l].q, e->w2[l].s}, K8Weight{}, nullptr, nullptr, d, GEMM_ADD};
+    k_gemm_q8(e->bxq, e->bxs, count, hidden, gs, &down, 1);
+  }
+  if (want == LOGITS_NONE) {
+    llhip_synchronize();
+    return nullptr;
+  }
+  const size_t vocab = c.vocab_size;
+  if (want == LOGITS_ALL && !e->blogits && !device_array(&e->blogits, (size_t)e->batch_rows * vocab))
+    return nullptr;
+  const K8Input in{e->xq, e->xs, nullptr};
+  for (int i = want == LOGITS_ALL ? 0 : count - 1; i < count; i++) {
+    float *x = e->bx + (size_t)i * d;
+    k_rmsnorm(x, x, e->rms_final, d, c.norm_eps);
+    k_quantize(e->xq, e->xs, x, d, gs);
+    k_matmul_q8(want == LOGITS_ALL ? e->blogits + (size_t)i * vocab : e->logits, &in, K8Weight{e->cls.q, e->cls.s}, d,
+                c.vocab_size, gs);
+  }
+  float *host;
+  if (want == LOGITS_ALL) {
+    e->host_batch_logits.resize((size_t)count * vocab);
+    host = e->host_batch_logits.data();
+    llhip_memcpy_d2h(host, e->blogits, (size_t)count * vocab * sizeof(float));
+  } else {
+    host = e->host_logits.data();
+    llhip_memcpy_d2h(host, e->logits, vocab * sizeof(float));
+  }
+  llhip_synchronize();
+  return llhip_last_error()[0] ? nullptr : host;
+}
+
 } // namespace
 } // namespace llhip
 
@@ -300,6 +398,15 @@ float *engine_forward(Model *model, int token, int position) {
     return nullptr;
   }
   return forward(e, token, position) ? e->host_logits.data() : nullptr;
+}
+
+float *engine_forward_batch(Model *model, const int *tokens, int count, int pos0, LogitsWanted want) {
+  Engine *e = model ? (Engine *)model->implementation : nullptr;
+  if (!e) {
+    raise("engine_forward_batch: no model loaded");
+    return nullptr;
+  }
+  return forward_batch(model, e, tokens, count, pos0, want);
 }
 
 void engine_free(Model *model) {

@@ -123,6 +123,7 @@ _SIGNATURES = {
     "engine_load_context": (None, [P, ctypes.c_char_p, I32]),
     "engine_forward": (ctypes.POINTER(ctypes.c_float), [P, I32, I32]),
     "engine_free": (None, [P]),
+    "engine_forward_batch": (ctypes.POINTER(ctypes.c_float), [P, P, I32, I32, I32]),
     "engine_group_size": (I32, []),
     "llhip_hbm_claimed": (SZ, []),
     "k_attention_init": (None, [P, I32, I32, I32, I32]),

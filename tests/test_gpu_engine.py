@@ -108,3 +108,53 @@ def test_engine_forward_matches_the_oracle_forward(tmp_path, layout):
     finally:
         L.engine_free(ctypes.byref(model))
         assert L.kernels_kv_layout_select(b"head") == 1
+
+
+def check_logits(got, want, what):
+    span = float(want.max() - want.min())
+    assert np.abs(got - want).max() <= 0.02 * span, (what, np.abs(got - want).max(), span)
+    assert np.linalg.norm(got - want) <= 0.005 * np.linalg.norm(want), what
+    assert got.argmax() == want.argmax(), what
+
+
+@pytest.mark.parametrize("layout", ["head", "rows"])
+def test_engine_forward_batch_matches_the_oracle_forward(tmp_path, layout):
+    """engine_forward_batch (src/tp.c:528-622): 40 prompt tokens from position 0 with every row's logits (ALL), 30
+    more from position 40 with the last row's (LAST), then one decode token, each against the token-by-token oracle
+    forward; bad batches fail with the reference's message."""
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    norms, t = ck.synthetic(CFG, GS, 12)
+    path = os.path.join(tmp_path, "tiny.bin")
+    ck.write_q8_v3(path, CFG, GS, norms, t)
+    assert L.kernels_kv_layout_select(layout.encode()) == 1
+    model = lh.Model()
+    try:
+        L.engine_load(ctypes.byref(model), path.encode())
+        assert model.implementation and L.engine_max_batch(ctypes.byref(model)) == CFG["seq_len"]
+        ref = OracleForward(CFG, norms, t)
+        tokens = np.random.default_rng(4).integers(0, CFG["vocab_size"], 71).astype(np.int32)
+        out = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens[:40]), 40, 0, lh.LOGITS_ALL)
+        assert out, lh.last_error()
+        got = np.ctypeslib.as_array(out, shape=(40, CFG["vocab_size"])).copy()
+        for pos in range(40):
+            check_logits(got[pos], ref.step(int(tokens[pos]), pos), f"{layout} ALL row {pos}")
+        out = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens[40:70]), 30, 40, lh.LOGITS_LAST)
+        assert out, lh.last_error()
+        got = np.ctypeslib.as_array(out, shape=(CFG["vocab_size"],)).copy()
+        for pos in range(40, 70):
+            want = ref.step(int(tokens[pos]), pos)
+        check_logits(got, want, f"{layout} LAST at 69")
+        out = L.engine_forward(ctypes.byref(model), int(tokens[70]), 70)
+        check_logits(np.ctypeslib.as_array(out, shape=(CFG["vocab_size"],)).copy(), ref.step(int(tokens[70]), 70),
+                     f"{layout} decode after the batches")
+        lh.record_failures()
+        try:
+            assert not L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens), 20, 70, lh.LOGITS_LAST)
+            assert "batch input out of range" in lh.last_error()
+        finally:
+            L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+            L.llhip_clear_error()
+    finally:
+        L.engine_free(ctypes.byref(model))
+        assert L.kernels_kv_layout_select(b"head") == 1
