@@ -469,6 +469,17 @@ def engine_bench(lh, L, args):
         assert out, lh.last_error()
         logits = np.ctypeslib.as_array(out, shape=(VOCAB,))
         assert np.isfinite(logits).all()
+        # prefill: a 2048-token prompt from position 0 through engine_forward_batch, the last row's logits
+        prompt = rng.integers(0, VOCAB, CONTEXT).astype(np.int32)
+        pptr = prompt.ctypes.data_as(ctypes.c_void_p)
+        assert L.engine_forward_batch(ctypes.byref(model), pptr, CONTEXT, 0, lh.LOGITS_LAST), lh.last_error()
+        t0 = time.perf_counter()
+        for _ in range(args.prefill_steps):
+            out = L.engine_forward_batch(ctypes.byref(model), pptr, CONTEXT, 0, lh.LOGITS_LAST)
+        psec = (time.perf_counter() - t0) / args.prefill_steps
+        assert out and np.isfinite(np.ctypeslib.as_array(out, shape=(VOCAB,))).all(), lh.last_error()
+        print(f"# engine prefill: {CONTEXT} tokens in {psec * 1e3:.2f} ms, {CONTEXT / psec:.0f} tok/s", file=sys.stderr,
+              flush=True)
         L.engine_free(ctypes.byref(model))
     print(json.dumps({"metric": "8B Q8_0 engine decode tok/s (engine_forward, logits to host)",
                       "value": round(1.0 / sec, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -476,7 +487,10 @@ def engine_bench(lh, L, args):
                       "scaling": "weak", "vs_baseline": None, "dtype": "int8 W8A8", "data": "synthetic",
                       "config": {"workload": f"Llama-3.1-8B Q8_0 version-3 checkpoint (random int8 weights, untied "
                                              f"classifier), decode at positions {args.warmup}.."
-                                             f"{args.warmup + args.steps - 1}, cache of {CONTEXT}"}}), flush=True)
+                                             f"{args.warmup + args.steps - 1}, cache of {CONTEXT}"},
+                      "prefill": {"value": round(CONTEXT / psec, 1), "unit": "tok/s", "ms_per_prompt": round(psec * 1e3, 3),
+                                  "workload": f"engine_forward_batch of a {CONTEXT}-token prompt from position 0, "
+                                              "last row's logits"}}), flush=True)
 
 
 def main():
