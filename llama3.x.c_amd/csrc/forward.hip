@@ -183,6 +183,7 @@ struct AttnParams {
 constexpr int kTileThreads = 512;
 constexpr int kTileWaves = kTileThreads / kWave;
 constexpr int kMaxQv = 64; // query vectors (tile rows x the group's query heads) per attn_tile block
+constexpr int kQvGroup = 4; // query vectors per pass in the batched form
 
 // The aligned form (head_dim % 4 == 0, 16-byte aligned rows): block (chunk c, KV head g, tile of tile_rows query rows).
 // The chunk's K rows and the tile's query vectors are staged in LDS (K rows padded to head_dim + 4 floats, so lane t's
@@ -191,7 +192,10 @@ constexpr int kMaxQv = 64; // query vectors (tile rows x the group's query heads
 // maximum, the exponentials and their sum; then each work item (query vector, four dimensions) sums the
 // exponential-weighted V rows staged beside K. The K and V rows of a chunk are read once, all loads in flight
 // together, for all tile_rows x kv_mul query vectors.
-__global__ __launch_bounds__(kTileThreads) void attn_tile(AttnParams p) {
+// GROUP > 1 (batched rows, every tile's query-vector count a multiple of GROUP): a wave scores GROUP query vectors per
+// pass over its lane's K row and a thread sums GROUP vectors' values per V read, so each K or V value read from LDS
+// serves GROUP products; every dot and sum keeps its order of terms, so the results equal GROUP = 1's.
+template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(AttnParams p) {
   extern __shared__ __align__(16) float lds[];
   const int c = blockIdx.x, g = blockIdx.y, r0 = blockIdx.z * p.tile_rows;
   const int nrows = min(p.tile_rows, p.rows - r0);
@@ -237,21 +241,33 @@ __global__ __launch_bounds__(kTileThreads) void attn_tile(AttnParams p) {
   __syncthreads();
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   bool bad = false;
-  for (int qv = wave; qv < nqv; qv += kTileWaves) {
+  for (int q0 = wave * GROUP; q0 < nqv; q0 += kTileWaves * GROUP) {
+    float dots[GROUP];
+#pragma unroll
+    for (int u = 0; u < GROUP; u++)
+      dots[u] = 0.0f;
+    if (lane < n && t0 + lane <= p.pos0 + r0 + (q0 + GROUP - 1) / kv_mul) { // live for some vector of the group
+      const float *kr = ks + lane * kst, *qr = qs + q0 * hd;
+      for (int i = 0; i < hd; i += 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(kr + i);
+#pragma unroll
+        for (int u = 0; u < GROUP; u++) {
+          const float4 b = *reinterpret_cast<const float4 *>(qr + u * hd + i);
+          dots[u] = fmaf(a.x, b.x, dots[u]);
+          dots[u] = fmaf(a.y, b.y, dots[u]);
+          dots[u] = fmaf(a.z, b.z, dots[u]);
+          dots[u] = fmaf(a.w, b.w, dots[u]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < GROUP; u++) {
+    const int qv = q0 + u;
     const int j = qv / kv_mul, h = qv % kv_mul, pos = p.pos0 + r0 + j;
     const bool live = lane < n && t0 + lane <= pos;
     float s = -FLT_MAX;
     if (live) {
-      const float *kr = ks + lane * kst, *qr = qs + qv * hd;
-      float dot = 0.0f;
-      for (int i = 0; i < hd; i += 4) {
-        const float4 a = *reinterpret_cast<const float4 *>(kr + i), b = *reinterpret_cast<const float4 *>(qr + i);
-        dot = fmaf(a.x, b.x, dot);
-        dot = fmaf(a.y, b.y, dot);
-        dot = fmaf(a.z, b.z, dot);
-        dot = fmaf(a.w, b.w, dot);
-      }
-      s = dot / p.divisor;
+      s = dots[u] / p.divisor;
       bad |= !isfinite(s);
     }
     const float m = wave_max(s);
@@ -263,28 +279,40 @@ __global__ __launch_bounds__(kTileThreads) void attn_tile(AttnParams p) {
       ph[hd] = m;
       ph[hd + 1] = l;
     }
+    }
   }
   if (bad)
     p.flags[1] = 1;
   __syncthreads();
   // value sums: work item (query vector, 4 consecutive dimensions), the exponentials of its row against the V rows
-  for (int it = threadIdx.x; it < nqv * hd4; it += kTileThreads) {
-    const int qv = it / hd4, d4 = it % hd4, j = qv / kv_mul, h = qv % kv_mul;
-    if (t0 > p.pos0 + r0 + j)
-      continue; // this row does not reach the chunk
-    const float *er = es + qv * kChunk, *vr = vs + 4 * d4;
-    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int it = threadIdx.x; it < nqv / GROUP * hd4; it += kTileThreads) {
+    const int q0 = it / hd4 * GROUP, d4 = it % hd4;
+    if (t0 > p.pos0 + r0 + (q0 + GROUP - 1) / kv_mul)
+      continue; // no row of the group reaches the chunk
+    const float *er = es + q0 * kChunk, *vr = vs + 4 * d4;
+    float4 acc[GROUP];
+#pragma unroll
+    for (int u = 0; u < GROUP; u++)
+      acc[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int t = 0; t < n; t++) {
-      const float e = er[t];
       const float4 v = *reinterpret_cast<const float4 *>(vr + t * hd);
-      acc.x = fmaf(e, v.x, acc.x);
-      acc.y = fmaf(e, v.y, acc.y);
-      acc.z = fmaf(e, v.z, acc.z);
-      acc.w = fmaf(e, v.w, acc.w);
+#pragma unroll
+      for (int u = 0; u < GROUP; u++) {
+        const float e = er[u * kChunk + t];
+        acc[u].x = fmaf(e, v.x, acc[u].x);
+        acc[u].y = fmaf(e, v.y, acc[u].y);
+        acc[u].z = fmaf(e, v.z, acc[u].z);
+        acc[u].w = fmaf(e, v.w, acc[u].w);
+      }
     }
-    *reinterpret_cast<float4 *>(p.partial +
-                                (((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * p.chunks + c) * p.slot +
-                                4 * d4) = acc;
+#pragma unroll
+    for (int u = 0; u < GROUP; u++) {
+      const int qv = q0 + u, j = qv / kv_mul, h = qv % kv_mul;
+      if (t0 <= p.pos0 + r0 + j) // rows that reach the chunk
+        *reinterpret_cast<float4 *>(p.partial +
+                                    (((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * p.chunks + c) * p.slot +
+                                    4 * d4) = acc[u];
+    }
   }
 }
 
@@ -548,13 +576,24 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
   if (aligned) {
     p.tile_rows = attention_tile_rows(job.rows, kv_mul, job.head_dim);
     const size_t lds = attention_tile_lds(p.tile_rows, kv_mul, job.head_dim);
-    static const hipError_t allowed =
-        hipFuncSetAttribute((const void *)attn_tile, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static const hipError_t allowed = [] {
+      const hipError_t e1 =
+          hipFuncSetAttribute((const void *)attn_tile<1>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      return e1 != hipSuccess ? e1
+                              : hipFuncSetAttribute((const void *)attn_tile<kQvGroup>,
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    }();
     if (allowed != hipSuccess)
       return raise("allowing the attention kernel its LDS failed: %s", hipGetErrorString(allowed));
     const unsigned tiles = (unsigned)((job.rows + p.tile_rows - 1) / p.tile_rows);
-    hipLaunchKernelGGL(attn_tile, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, tiles), dim3(kTileThreads), lds,
-                       stream, p);
+    // the grouped form needs every tile's query-vector count (rows x kv_mul) to be a multiple of the group
+    const bool grouped = job.rows > 1 && kv_mul % kQvGroup == 0;
+    if (grouped)
+      hipLaunchKernelGGL(attn_tile<kQvGroup>, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, tiles),
+                         dim3(kTileThreads), lds, stream, p);
+    else
+      hipLaunchKernelGGL(attn_tile<1>, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, tiles), dim3(kTileThreads),
+                         lds, stream, p);
     if (!launch_ok("attn_tile"))
       return false;
   } else {
