@@ -158,3 +158,38 @@ def test_engine_forward_batch_matches_the_oracle_forward(tmp_path, layout):
     finally:
         L.engine_free(ctypes.byref(model))
         assert L.kernels_kv_layout_select(b"head") == 1
+
+
+def test_engine_load_context_sizes_the_cache(tmp_path):
+    """engine_load_context (runtime.h:102): a context below the model's seq_len bounds the positions and the batch;
+    the logits at a position inside it equal those of the full-context engine's (same kernels, same inputs)."""
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    norms, t = ck.synthetic(CFG, GS, 13)
+    path = os.path.join(tmp_path, "tiny.bin")
+    ck.write_q8_v3(path, CFG, GS, norms, t)
+    small, full = lh.Model(), lh.Model()
+    try:
+        L.engine_load_context(ctypes.byref(small), path.encode(), 40)
+        L.engine_load(ctypes.byref(full), path.encode())
+        assert small.config.seq_len == 40 and full.config.seq_len == CFG["seq_len"]
+        assert L.engine_max_batch(ctypes.byref(small)) == 40
+        tokens = np.random.default_rng(6).integers(0, CFG["vocab_size"], 40).astype(np.int32)
+        a = L.engine_forward_batch(ctypes.byref(small), lh.ptr(tokens), 40, 0, lh.LOGITS_LAST)
+        got = np.ctypeslib.as_array(a, shape=(CFG["vocab_size"],)).copy()
+        b = L.engine_forward_batch(ctypes.byref(full), lh.ptr(tokens), 40, 0, lh.LOGITS_LAST)
+        want = np.ctypeslib.as_array(b, shape=(CFG["vocab_size"],)).copy()
+        assert np.array_equal(got, want)
+        lh.record_failures()
+        try:
+            assert not L.engine_forward(ctypes.byref(small), 1, 40)
+            assert "position 40 outside the context of 40" in lh.last_error()
+            L.llhip_clear_error()
+            assert not L.engine_forward(ctypes.byref(small), CFG["vocab_size"], 3)
+            assert "outside the vocabulary" in lh.last_error()
+        finally:
+            L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+            L.llhip_clear_error()
+    finally:
+        L.engine_free(ctypes.byref(small))
+        L.engine_free(ctypes.byref(full))
