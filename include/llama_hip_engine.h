@@ -27,6 +27,10 @@ float *engine_forward(Model *model, int token, int position);
 float *engine_forward_batch(Model *model, const int *tokens, int count, int pos0, LogitsWanted want);
 void engine_free(Model *model);   /* runtime.h:114 */
 int engine_group_size(void);      /* runtime.h:116: the loaded checkpoint's group size */
+/* runtime.h:115 (src/engine.c:191-195): "int8_q8_0", or "int8_q8_0_w8a32" when LLAMA_Q8_ACTIVATIONS=fp32 (read by
+ * engine_load: int8 or fp32, anything else fails) makes every GEMV multiply the dequantized weights by the FP32
+ * activations; that mode runs batches of one row, as the reference's does. */
+const char *engine_precision(void);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,7 @@
 #include <unistd.h>
 
 #include <cerrno>
+#include <cstdlib>
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -28,6 +29,7 @@ namespace {
 constexpr uint32_t kMagic = 0x616b3432; // "24ka" read little-endian: the versioned checkpoint tag
 constexpr int kHeaderBytes = 256;
 int loaded_group_size = 0; // the group size of the last checkpoint loaded
+bool fp32_activations = false; // LLAMA_Q8_ACTIVATIONS=fp32: W8A32, dequantized weights times FP32 activations
 
 struct Q8Tensor {
   const int8_t *q;
@@ -242,13 +244,21 @@ bool forward(Engine *e, int token, int pos) {
   k_embed_q8_rows(e->x, e->embed.q, e->embed.s, &token, 1, d, gs, c.vocab_size);
   k_rope_table(&c, pos, e->rope);
   const bool head = kernels_kv_layout_head() != 0;
-  const K8Input in_d{e->xq, e->xs, nullptr}, in_h{e->hq, e->hs, nullptr};
+  // W8A8 quantizes each GEMV input (q8_input, src/tp.c:380-385); W8A32 hands the FP32 rows over instead
+  const bool a32 = fp32_activations;
+  const K8Input in_d = a32 ? K8Input{nullptr, nullptr, e->xb} : K8Input{e->xq, e->xs, nullptr};
+  const K8Input in_h = a32 ? K8Input{nullptr, nullptr, e->hb} : K8Input{e->hq, e->hs, nullptr};
+  const K8Input in_x = a32 ? K8Input{nullptr, nullptr, e->x} : in_d;
+  auto quantize = [&](int8_t *q, float *s, const float *x, int n) {
+    if (!a32)
+      k_quantize(q, s, x, n, gs);
+  };
   for (int l = 0; l < c.n_layers; l++) {
     const size_t layer = (size_t)l * c.seq_len * kvl;
     float *kc = e->key_cache + layer, *vc = e->value_cache + layer;
     float *k = head ? e->k : kc + (size_t)pos * kvl, *v = head ? e->v : vc + (size_t)pos * kvl;
     k_rmsnorm(e->xb, e->x, e->rms_att + (size_t)l * d, d, c.norm_eps);
-    k_quantize(e->xq, e->xs, e->xb, d, gs);
+    quantize(e->xq, e->xs, e->xb, d);
     k_matmul_q8_qkv(e->q, k, v, &in_d, K8Weight{e->wq[l].q, e->wq[l].s}, K8Weight{e->wk[l].q, e->wk[l].s},
                     K8Weight{e->wv[l].q, e->wv[l].s}, d, d, (int)kvl, gs);
     k_rope_apply(e->q, k, e->rope, nh, nkv, hd);
@@ -257,18 +267,18 @@ bool forward(Engine *e, int token, int pos) {
       k_kv_store(vc, v, kvl, pos, 1, nkv, hd, c.seq_len);
     }
     k_attention_kv(e->xb, e->q, kc, vc, nullptr, &e->work, nh, nkv, hd, c.seq_len, pos);
-    k_quantize(e->xq, e->xs, e->xb, d, gs);
+    quantize(e->xq, e->xs, e->xb, d);
     k_matmul_q8_add(e->x, &in_d, K8Weight{e->wo[l].q, e->wo[l].s}, d, d, gs);
     k_rmsnorm(e->xb, e->x, e->rms_ffn + (size_t)l * d, d, c.norm_eps);
-    k_quantize(e->xq, e->xs, e->xb, d, gs);
+    quantize(e->xq, e->xs, e->xb, d);
     k_matmul_q8_swiglu(e->hb, &in_d, K8Weight{e->w1[l].q, e->w1[l].s}, K8Weight{e->w3[l].q, e->w3[l].s}, d, hidden,
                        gs);
-    k_quantize(e->hq, e->hs, e->hb, hidden, gs);
+    quantize(e->hq, e->hs, e->hb, hidden);
     k_matmul_q8_add(e->x, &in_h, K8Weight{e->w2[l].q, e->w2[l].s}, hidden, d, gs);
   }
   k_rmsnorm(e->x, e->x, e->rms_final, d, c.norm_eps);
-  k_quantize(e->xq, e->xs, e->x, d, gs);
-  k_matmul_q8(e->logits, &in_d, K8Weight{e->cls.q, e->cls.s}, d, c.vocab_size, gs);
+  quantize(e->xq, e->xs, e->x, d);
+  k_matmul_q8(e->logits, &in_x, K8Weight{e->cls.q, e->cls.s}, d, c.vocab_size, gs);
   llhip_memcpy_d2h(e->host_logits.data(), e->logits, (size_t)c.vocab_size * sizeof(float));
   llhip_synchronize(); // reports a non-finite activation or score of this token
   return llhip_last_error()[0] == 0;
@@ -299,6 +309,11 @@ float *forward_batch(Model *model, Engine *e, const int *tokens, int count, int 
   const Config &c = e->c;
   const int d = c.dim, hidden = c.hidden_dim, hd = c.head_dim, gs = e->gs, nh = c.n_heads, nkv = c.n_kv_heads;
   const int kvl = hd * nkv;
+  if (fp32_activations) { // W8A32 has no batched GEMM: the batch is one row (src/engine.c:97-104)
+    if (!forward(e, tokens[0], pos0))
+      return nullptr;
+    return want == LOGITS_NONE ? nullptr : e->host_logits.data();
+  }
   if (!e->batch_rows && !allocate_batch(e, model->max_batch))
     return nullptr;
   for (int i = 0; i < count; i++)
@@ -378,6 +393,12 @@ void engine_load_context(Model *model, const char *path, int context) {
     raise("engine_load: null path");
     return;
   }
+  const char *activations = getenv("LLAMA_Q8_ACTIVATIONS"); // src/engine.c:132-135
+  if (activations && *activations && strcmp(activations, "int8") && strcmp(activations, "fp32")) {
+    raise("LLAMA_Q8_ACTIVATIONS must be int8 or fp32");
+    return;
+  }
+  fp32_activations = activations && !strcmp(activations, "fp32");
   Engine *e = open_engine(path, context);
   if (!e)
     return;
@@ -386,7 +407,11 @@ void engine_load_context(Model *model, const char *path, int context) {
   loaded_group_size = e->gs;
   model->file_bytes = e->bytes;
   model->mapped_bytes = e->bytes;
-  prefill_configure_engine(model, LLHIP_PREFILL_BATCH_Q8, 1);
+  prefill_configure_engine(model, fp32_activations ? 1 : LLHIP_PREFILL_BATCH_Q8, 1);
+  if (fp32_activations) {
+    model->prefill_gemm = 0;
+    model->prefill_kernel = nullptr;
+  }
 }
 
 void engine_load(Model *model, const char *path) { engine_load_context(model, path, 0); }
@@ -419,5 +444,7 @@ void engine_free(Model *model) {
 }
 
 int engine_group_size(void) { return loaded_group_size; }
+
+const char *engine_precision(void) { return fp32_activations ? "int8_q8_0_w8a32" : "int8_q8_0"; }
 
 } // extern "C"

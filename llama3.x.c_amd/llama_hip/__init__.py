@@ -125,6 +125,7 @@ _SIGNATURES = {
     "engine_free": (None, [P]),
     "engine_forward_batch": (ctypes.POINTER(ctypes.c_float), [P, P, I32, I32, I32]),
     "engine_group_size": (I32, []),
+    "engine_precision": (ctypes.c_char_p, []),
     "llhip_hbm_claimed": (SZ, []),
     "k_attention_init": (None, [P, I32, I32, I32, I32]),
     "k_attention_bytes": (SZ, [I32, I32, I32, I32]),

@@ -36,13 +36,20 @@ def rope_table(cfg, pos):
 class OracleForward:
     """The decode forward from the oracle's kernels, head-major K/V cache as the engine's default layout."""
 
-    def __init__(self, cfg, norms, t):
-        self.c, self.n, self.t = cfg, norms, t
+    def __init__(self, cfg, norms, t, a32=False):
+        self.c, self.n, self.t, self.a32 = cfg, norms, t, a32
         d, L, S = cfg["dim"], cfg["n_layers"], cfg["seq_len"]
         self.hd = d // cfg["n_heads"]
         self.kv = self.hd * cfg["n_kv_heads"]
         self.kc = [np.zeros(S * self.kv, np.float32) for _ in range(L)]
         self.vc = [np.zeros(S * self.kv, np.float32) for _ in range(L)]
+
+    def mm(self, x, wq, ws, **kw):
+        """A GEMV of x: W8A8 (x quantized per group) or, in W8A32, the FP32 x against the dequantized weights."""
+        if self.a32:
+            return orc.matmul_q8(None, None, wq, ws, GS, xf=np.ascontiguousarray(x, np.float32), **kw)
+        xq, xs = orc.quantize(x, GS)
+        return orc.matmul_q8(xq, xs, wq, ws, GS, **kw)
 
     def w(self, role, l):
         q, s = self.t[role]
@@ -56,28 +63,20 @@ class OracleForward:
         ps, hb = orc.kv_strides(nkv, hd, S, True)
         for l in range(c["n_layers"]):
             xb = orc.rmsnorm(x, self.n["rms_att"][l])
-            xq, xs = orc.quantize(xb, GS)
-            q = orc.matmul_q8(xq, xs, *self.w("wq", l), GS)
-            k = orc.matmul_q8(xq, xs, *self.w("wk", l), GS)
-            v = orc.matmul_q8(xq, xs, *self.w("wv", l), GS)
+            q, k, v = (self.mm(xb, *self.w(r, l)) for r in ("wq", "wk", "wv"))
             q, k = orc.rope_apply(q, k, table, nh, nkv, hd)
             for g in range(nkv):
                 self.kc[l][g * hb + pos * ps: g * hb + pos * ps + hd] = k[g * hd:(g + 1) * hd]
                 self.vc[l][g * hb + pos * ps: g * hb + pos * ps + hd] = v[g * hd:(g + 1) * hd]
             att = orc.attention(q, self.kc[l], self.vc[l], nh, nkv, hd, S, pos, ps, hb)
-            aq, as_ = orc.quantize(att, GS)
-            orc.matmul_q8(aq, as_, *self.w("wo", l), GS, kind=orc.K_ADD, out=x)
+            self.mm(att, *self.w("wo", l), kind=orc.K_ADD, out=x)
             xb = orc.rmsnorm(x, self.n["rms_ffn"][l])
-            xq, xs = orc.quantize(xb, GS)
-            w1q, w1s = self.w("w1", l)
             w3q, w3s = self.w("w3", l)
-            h = orc.matmul_q8(xq, xs, w1q, w1s, GS, kind=orc.K_SWIGLU, w3q=w3q, w3s=w3s)
-            hq, hs = orc.quantize(h, GS)
-            orc.matmul_q8(hq, hs, *self.w("w2", l), GS, kind=orc.K_ADD, out=x)
+            h = self.mm(xb, *self.w("w1", l), kind=orc.K_SWIGLU, w3q=w3q, w3s=w3s)
+            self.mm(h, *self.w("w2", l), kind=orc.K_ADD, out=x)
         x = orc.rmsnorm(x, self.n["rms_final"])
-        xq, xs = orc.quantize(x, GS)
         cq, cs = self.t["cls"]
-        return orc.matmul_q8(xq, xs, cq, cs.reshape(cq.shape[0], -1), GS)
+        return self.mm(x, cq, cs.reshape(cq.shape[0], -1))
 
 
 @pytest.mark.parametrize("layout", ["head", "rows"])
@@ -110,9 +109,9 @@ def test_engine_forward_matches_the_oracle_forward(tmp_path, layout):
         assert L.kernels_kv_layout_select(b"head") == 1
 
 
-def check_logits(got, want, what):
+def check_logits(got, want, what, rel=0.02):
     span = float(want.max() - want.min())
-    assert np.abs(got - want).max() <= 0.02 * span, (what, np.abs(got - want).max(), span)
+    assert np.abs(got - want).max() <= rel * span, (what, np.abs(got - want).max(), span)
     assert np.linalg.norm(got - want) <= 0.005 * np.linalg.norm(want), what
     assert got.argmax() == want.argmax(), what
 
@@ -193,3 +192,45 @@ def test_engine_load_context_sizes_the_cache(tmp_path):
     finally:
         L.engine_free(ctypes.byref(small))
         L.engine_free(ctypes.byref(full))
+
+
+def test_engine_w8a32_mode_matches_the_oracle(tmp_path, monkeypatch):
+    """LLAMA_Q8_ACTIVATIONS=fp32 (src/engine.c:132-135): every GEMV takes the FP32 activations against the dequantized
+    weights, against the oracle's W8A32 GEMV; batches are one row; a bad value fails with the reference's message."""
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    norms, t = ck.synthetic(CFG, GS, 14)
+    path = os.path.join(tmp_path, "tiny.bin")
+    ck.write_q8_v3(path, CFG, GS, norms, t)
+    model = lh.Model()
+    monkeypatch.setenv("LLAMA_Q8_ACTIVATIONS", "fp32")
+    try:
+        L.engine_load(ctypes.byref(model), path.encode())
+        assert L.engine_precision() == b"int8_q8_0_w8a32" and L.engine_max_batch(ctypes.byref(model)) == 1
+        ref = OracleForward(CFG, norms, t, a32=True)
+        tokens = np.random.default_rng(7).integers(0, CFG["vocab_size"], 20).astype(np.int32)
+        for pos in range(20):
+            if pos % 2:
+                out = L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos)
+            else:
+                out = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens[pos:pos + 1]), 1, pos, lh.LOGITS_LAST)
+            assert out, lh.last_error()
+            # no quantizer in the way: only the FP32 summation orders differ, so the bar is 50x tighter than W8A8's
+            # and would reject W8A8 logits (about 5e-4 of the range away here)
+            check_logits(np.ctypeslib.as_array(out, shape=(CFG["vocab_size"],)).copy(),
+                         ref.step(int(tokens[pos]), pos), f"w8a32 pos {pos}", rel=4e-4)
+    finally:
+        L.engine_free(ctypes.byref(model))
+    monkeypatch.setenv("LLAMA_Q8_ACTIVATIONS", "fp16")
+    lh.record_failures()
+    try:
+        other = lh.Model()
+        L.engine_load(ctypes.byref(other), path.encode())
+        assert lh.last_error() == "LLAMA_Q8_ACTIVATIONS must be int8 or fp32" and not other.implementation
+    finally:
+        L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+        L.llhip_clear_error()
+    monkeypatch.delenv("LLAMA_Q8_ACTIVATIONS")
+    L.engine_load(ctypes.byref(other), path.encode())
+    assert L.engine_precision() == b"int8_q8_0"
+    L.engine_free(ctypes.byref(other))
