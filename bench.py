@@ -10,6 +10,8 @@ Alongside (`prefill`): the 8B INT8 W8A8 prefill of a 2048-token prompt: per laye
 int8-MFMA GEMMs (QKV, Wo + residual, W1/W3 SwiGLU, W2 + residual), then the last row's classifier GEMV.
 `forward_decode`: the whole 8B decode token on the device (the embedding row, the matmul set plus RMSNorm, RoPE, the K/V
 cache store and attention over 2048 cached positions), also from a HIP graph.
+`engine`: the Q8_0 engine end to end on a written synthetic 8B version-3 checkpoint: engine_forward per token (logits to
+the host) and engine_forward_batch of a 2048-token prompt (`--no-engine` skips it; `--engine` runs only it).
 
 Weights ~N(0, 0.02) and activations ~N(0, 1) are drawn on the device (torch, seeded) and quantized by the library's
 own k_quantize rule; the data is synthetic. `roofline` is the dominant kernel of the decode step (the SwiGLU GEMV),
@@ -435,10 +437,14 @@ def cpu_baseline(threads, budget_s=30.0):
             "sample": f"oracle scalar Q8 GEMV 4096x4096 x{reps}, {threads} threads, scaled to the 8B token by bytes"}
 
 
-def engine_bench(lh, L, args):
+def engine_bench(lh, L, args, steps=None, warmup=None, prompts=None):
     """The engine end to end (engine_load + engine_forward, logits to the host every token) on a synthetic untied
     Llama-3.1-8B version-3 Q8_0 checkpoint written to $TMPDIR: tokens at positions 0 .. warmup + steps - 1, timed on
-    the host clock (engine_forward returns after the logits have arrived). Prints its own JSON line."""
+    the host clock (engine_forward returns after the logits have arrived), then engine_forward_batch of a 2048-token
+    prompt. Returns the result object."""
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+    prompts = args.prefill_steps if prompts is None else prompts
     import ctypes
     import tempfile
 
@@ -459,13 +465,13 @@ def engine_bench(lh, L, args):
         L.engine_load(ctypes.byref(model), path.encode())
         print(f"# engine_load (map + upload to HBM) {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
         rng = np.random.default_rng(args.seed)
-        tokens = rng.integers(0, VOCAB, args.warmup + args.steps)
-        for pos in range(args.warmup):
+        tokens = rng.integers(0, VOCAB, warmup + steps)
+        for pos in range(warmup):
             assert L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos), lh.last_error()
         t0 = time.perf_counter()
-        for pos in range(args.warmup, args.warmup + args.steps):
+        for pos in range(warmup, warmup + steps):
             out = L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos)
-        sec = (time.perf_counter() - t0) / args.steps
+        sec = (time.perf_counter() - t0) / steps
         assert out, lh.last_error()
         logits = np.ctypeslib.as_array(out, shape=(VOCAB,))
         assert np.isfinite(logits).all()
@@ -474,23 +480,23 @@ def engine_bench(lh, L, args):
         pptr = prompt.ctypes.data_as(ctypes.c_void_p)
         assert L.engine_forward_batch(ctypes.byref(model), pptr, CONTEXT, 0, lh.LOGITS_LAST), lh.last_error()
         t0 = time.perf_counter()
-        for _ in range(args.prefill_steps):
+        for _ in range(prompts):
             out = L.engine_forward_batch(ctypes.byref(model), pptr, CONTEXT, 0, lh.LOGITS_LAST)
-        psec = (time.perf_counter() - t0) / args.prefill_steps
+        psec = (time.perf_counter() - t0) / prompts
         assert out and np.isfinite(np.ctypeslib.as_array(out, shape=(VOCAB,))).all(), lh.last_error()
         print(f"# engine prefill: {CONTEXT} tokens in {psec * 1e3:.2f} ms, {CONTEXT / psec:.0f} tok/s", file=sys.stderr,
               flush=True)
         L.engine_free(ctypes.byref(model))
-    print(json.dumps({"metric": "8B Q8_0 engine decode tok/s (engine_forward, logits to host)",
-                      "value": round(1.0 / sec, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-                      "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True,
+    return {"metric": "8B Q8_0 engine decode tok/s (engine_forward, logits to host)",
+                      "value": round(1.0 / sec, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps,
+                      "warmup": warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True,
                       "scaling": "weak", "vs_baseline": None, "dtype": "int8 W8A8", "data": "synthetic",
                       "config": {"workload": f"Llama-3.1-8B Q8_0 version-3 checkpoint (random int8 weights, untied "
-                                             f"classifier), decode at positions {args.warmup}.."
-                                             f"{args.warmup + args.steps - 1}, cache of {CONTEXT}"},
+                                             f"classifier), decode at positions {warmup}.."
+                                             f"{warmup + steps - 1}, cache of {CONTEXT}"},
                       "prefill": {"value": round(CONTEXT / psec, 1), "unit": "tok/s", "ms_per_prompt": round(psec * 1e3, 3),
                                   "workload": f"engine_forward_batch of a {CONTEXT}-token prompt from position 0, "
-                                              "last row's logits"}}), flush=True)
+                                              "last row's logits"}}
 
 
 def main():
@@ -507,6 +513,7 @@ def main():
                     help="skip the FP32 / BF16 prefill GEMMs on the Llama-3.2-3B shapes (512 tokens)")
     ap.add_argument("--no-forward", action="store_true",
                     help="skip the full device decode token (matmuls + RMSNorm, RoPE, K/V store, attention)")
+    ap.add_argument("--no-engine", action="store_true", help="skip the engine's end-to-end measurement")
     ap.add_argument("--engine", action="store_true",
                     help="measure engine_load + engine_forward on a synthetic 8B checkpoint instead")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -524,7 +531,8 @@ def main():
     if L.llhip_init() != 0:
         raise SystemExit(f"no usable MI355X: {lh.last_error()}")
     if args.engine:
-        return engine_bench(lh, L, args)
+        print(json.dumps(engine_bench(lh, L, args)), flush=True)
+        return
     t_setup = time.time()
     model = Model8B(torch, lh, args.seed)
     run_step = decode_set(torch, lh, model, args.seed)
@@ -643,6 +651,20 @@ def main():
 
     if not args.no_c3:
         result["prefill_3b"] = prefill_3b(torch, lh, args.seed)
+    if not args.no_engine:
+        # the engine end to end (engine_load of a written 8B checkpoint, engine_forward, engine_forward_batch); its
+        # failure (say, no room for the 8.5 GB file) is reported here and leaves the line above intact
+        lh.record_failures()  # a library failure returns with its message instead of ending the process
+        try:
+            eng = engine_bench(lh, L, args, steps=64, warmup=4, prompts=2)
+            result["engine"] = {"decode": {"value": eng["value"], "unit": "tok/s", "ms_per_token": eng["ms_per_step"],
+                                           "workload": eng["config"]["workload"]},
+                                "prefill": eng["prefill"]}
+        except Exception as err:  # noqa: BLE001 - the main metric must still print
+            result["engine"] = {"error": f"{type(err).__name__}: {err}"}
+        finally:
+            L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+            L.llhip_clear_error()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_threads)
     print(json.dumps(result), flush=True)
