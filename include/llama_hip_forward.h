@@ -37,6 +37,9 @@ void k_rope_apply_rows(float *q, size_t q_stride, float *k, size_t k_stride, con
  * call (vocab x dim bytes), so register it once. */
 void k_embed_q8_rows(float *out, const signed char *table, const float *scales, const int *ids, int count, int dim,
                      int gs, int vocab);
+/* The same lookup in an FP32 table (vocab x dim floats; src/tp.c:342 for a token, 449 for a batch, where run copies
+ * the row): out row i = table row ids[i], a copy; the same id check and failure. */
+void k_embed_f32_rows(float *out, const float *table, const int *ids, int count, int dim, int vocab);
 
 /* kernels.h:127-132: the attention workspace record. The device attention keeps its split-K partials in a library
  * workspace; this record only carries the shapes (partial is never dereferenced). */

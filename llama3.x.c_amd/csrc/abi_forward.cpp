@@ -341,6 +341,28 @@ void k_embed_q8_rows(float *out, const int8_t *table, const float *scales, const
     call.finish();
 }
 
+void k_embed_f32_rows(float *out, const float *table, const int *ids, int count, int dim, int vocab) {
+  if (count <= 0)
+    return;
+  if (!out || !table || !ids) {
+    raise("k_embed_f32_rows: null buffer");
+    return;
+  }
+  if (dim <= 0 || vocab <= 0) {
+    raise("k_embed_f32_rows: a %d x %d table", vocab, dim);
+    return;
+  }
+  Call call("k_embed_f32_rows");
+  Ref T = call.in(table, (size_t)vocab * dim * sizeof(float));
+  Ref I = call.in(ids, (size_t)count * sizeof(int));
+  Ref O = call.out(out, (size_t)count * dim * sizeof(float), false);
+  if (!call.ready())
+    return;
+  if (launch_embed_rows_f32(call.ptr<float>(O), call.ptr<const float>(T), call.ptr<const int>(I), count, dim, vocab,
+                            call.stream()))
+    call.finish();
+}
+
 // ---- attention (kernels.h:124-179, src/attention.c:516-596, 1357-1455) -------------------------------------------
 //
 // The device attention keeps its split-K partials in a library workspace, so AttentionWork is the reference's record

@@ -210,6 +210,8 @@ bool launch_kv_store(float *cache, const float *src, size_t src_ld, int pos0, in
                      size_t pos_stride, size_t head_base, hipStream_t stream);
 bool launch_embed_rows(float *out, const int8_t *table, const float *scales, const int *ids, int count, int dim,
                        int gs, int vocab, hipStream_t stream);
+bool launch_embed_rows_f32(float *out, const float *table, const int *ids, int count, int dim, int vocab,
+                           hipStream_t stream);
 // Causal attention of `rows` query rows at positions pos0 .. pos0 + rows - 1 (q and out: rows x n_heads x head_dim);
 // position t of KV head g at key / value + t * pos_stride + g * head_base.
 struct AttentionJob {

@@ -1,20 +1,28 @@
-// The Q8_0 engine's host forward over the device library: engine_load maps a version-3 INT8 checkpoint, uploads it
-// to HBM once (llhip_register_host) and allocates the activations and the K/V cache in device memory; engine_forward
-// runs one decode token in the reference's order (src/tp.c:387-436 with one socket) through the library's entry
-// points, so the recorded forms apply (RMSNorm and quantization inside the GEMV, RoPE and the cache stores inside
-// attention) and only the logits cross PCIe.
+// The engine's host forward over the device library: engine_load maps a checkpoint, checks its header as the
+// reference does, uploads it to HBM once (llhip_register_host) and allocates the activations and the K/V cache in
+// device memory; engine_forward runs one decode token in the reference's order (src/tp.c:337-436 with one socket)
+// through the library's entry points, so the recorded forms apply (RMSNorm and quantization inside the GEMV, RoPE and
+// the cache stores inside attention) and only the logits cross PCIe; engine_forward_batch runs a prompt through the
+// batched GEMMs (src/tp.c:528-622) or, where the reference does (src/engine.c:65-81), one token at a time.
 //
-// The header (src/runtime.c:179-260) and the tensor order (src/shards.c:77-99) are the reference's: FP32 norms first
-// (rms_att[L], rms_ffn[L], rms_final), then each INT8 tensor as its values followed by its group scales, the
-// embedding, then per role the layers back to back (wq, wk, wv, wo, w1, w2, w3), and the classifier unless tied.
+// Formats (src/runtime.c:179-310, tensor order src/shards.c:60-99):
+//   Q8_0, version 3 (256-byte header, precision 1) or version 2 (256-byte header: shared flag byte at 36, group size
+//     at 37): FP32 norms first (rms_att[L], rms_ffn[L], rms_final), then each INT8 tensor as its values followed by
+//     its group scales, the embedding, per role the layers back to back (wq, wk, wv, wo, w1, w2, w3), and the
+//     classifier unless it is tied to the embedding;
+//   FP32, version 3 (precision 0, group size 0) or the legacy 28-byte header (seven ints, a negative vocabulary size
+//     meaning an untied classifier): the embedding, rms_att[L], wq, wk, wv, wo, rms_ffn[L], w1, w2, w3, rms_final,
+//     the legacy file's unused RoPE table (seq_len x head_dim floats), and the classifier unless tied.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
 #include <cerrno>
-#include <cstdlib>
+#include <climits>
+#include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -27,25 +35,42 @@ namespace llhip {
 namespace {
 
 constexpr uint32_t kMagic = 0x616b3432; // "24ka" read little-endian: the versioned checkpoint tag
-constexpr int kHeaderBytes = 256;
-int loaded_group_size = 0; // the group size of the last checkpoint loaded
-bool fp32_activations = false; // LLAMA_Q8_ACTIVATIONS=fp32: W8A32, dequantized weights times FP32 activations
+constexpr size_t kVersionedHeader = 256, kLegacyHeader = 28;
+constexpr int kDefaultContext = 4096;   // src/engine.c:150: the context when none is requested
+constexpr int kPackRoles = 7;           // wq, wk, wv, wo, w1, w2, w3 (src/tp.c:25)
 
-struct Q8Tensor {
-  const int8_t *q;
-  const float *s;
+// The last checkpoint loaded: engine_group_size and engine_precision report it, as the reference's per-process GS and
+// mode do (src/engine.c:17-20, 191-198). Each engine keeps its own mode for its forwards.
+int last_group_size = 0;
+const char *last_precision = "int8_q8_0";
+
+struct Tensor {
+  const void *w = nullptr;   // FP32 values, or the int8 values of a Q8_0 tensor
+  const float *s = nullptr;  // the Q8_0 group scales (nullptr for FP32)
+  const int8_t *q() const { return (const int8_t *)w; }
+  const float *f() const { return (const float *)w; }
+  K8Weight k8() const { return K8Weight{q(), s}; }
 };
 
 struct Engine {
   int fd = -1;
   unsigned char *map = nullptr;
   size_t bytes = 0;
-  int gs = 0;
+  bool q8 = true;    // Q8_0 checkpoint (else FP32)
+  bool a32 = false;  // Q8_0 with LLAMA_Q8_ACTIVATIONS=fp32 (W8A32)
+  bool bf16 = false; // FP32 with LLAMA_PRECISION=bf16: the batched GEMMs on packed BF16 weights
+  int gs = 0;        // Q8_0 group size (0 for FP32)
+  size_t header = 0; // header bytes before the first tensor
   Config c{};
   // inside the registered mapping (the library resolves them to their device copies)
   const float *rms_att = nullptr, *rms_ffn = nullptr, *rms_final = nullptr;
-  Q8Tensor embed{}, cls{};
-  std::vector<Q8Tensor> wq, wk, wv, wo, w1, w2, w3;
+  Tensor embed, cls;
+  std::vector<Tensor> wq, wk, wv, wo, w1, w2, w3;
+  // BF16 mode: the packed copies (device memory), layer-major in the roles' order; the classifier's when all-position
+  // logits are first asked for (src/tp.c:35, 838-860)
+  uint16_t *packed = nullptr, *cls_packed = nullptr;
+  std::vector<const uint16_t *> packed_at;
+  AlignedBuffer panel{};
   // device memory
   float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *logits = nullptr;
   float *rope = nullptr, *key_cache = nullptr, *value_cache = nullptr, *xs = nullptr, *hs = nullptr;
@@ -57,23 +82,35 @@ struct Engine {
   float *bx = nullptr, *bxb = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *bhb = nullptr, *bxs = nullptr;
   float *brope = nullptr, *blogits = nullptr;
   int8_t *bxq = nullptr;
+  int *btokens = nullptr;
   std::vector<float> host_rope, host_batch_logits;
 };
 
-template <typename T> T read_at(const unsigned char *p, int offset) {
+template <typename T> T read_at(const unsigned char *p, size_t offset) {
   T v;
   memcpy(&v, p + offset, sizeof(T));
   return v;
 }
 
+template <typename T> void drop(T *&p) {
+  if (p)
+    llhip_free((void *)p);
+  p = nullptr;
+}
+
+void free_batch(Engine *e) {
+  drop(e->bx), drop(e->bxb), drop(e->bq), drop(e->bk), drop(e->bv), drop(e->bhb), drop(e->bxs), drop(e->brope);
+  drop(e->bxq), drop(e->btokens), drop(e->blogits);
+  if (e->panel.base)
+    aligned_buffer_free(&e->panel);
+  e->batch_rows = 0;
+}
+
 void release(Engine *e) {
-  for (void *p : {(void *)e->x, (void *)e->xb, (void *)e->q, (void *)e->k, (void *)e->v, (void *)e->hb,
-                  (void *)e->logits, (void *)e->rope, (void *)e->key_cache, (void *)e->value_cache, (void *)e->xs,
-                  (void *)e->hs, (void *)e->xq, (void *)e->hq, (void *)e->bx, (void *)e->bxb, (void *)e->bq,
-                  (void *)e->bk, (void *)e->bv, (void *)e->bhb, (void *)e->bxs, (void *)e->brope, (void *)e->blogits,
-                  (void *)e->bxq})
-    if (p)
-      llhip_free(p);
+  free_batch(e);
+  drop(e->x), drop(e->xb), drop(e->q), drop(e->k), drop(e->v), drop(e->hb), drop(e->logits), drop(e->rope);
+  drop(e->key_cache), drop(e->value_cache), drop(e->xs), drop(e->hs), drop(e->xq), drop(e->hq);
+  drop(e->packed), drop(e->cls_packed);
   if (e->map) {
     (void)llhip_unregister_host(e->map);
     munmap(e->map, e->bytes);
@@ -83,93 +120,178 @@ void release(Engine *e) {
   delete e;
 }
 
-// The reference's checks of a version-3 INT8 header (src/runtime.c:213-247, validate_config at :150-167).
-bool parse_header(Engine *e, const char *path) {
-  const unsigned char *h = e->map;
-  if (read_at<uint32_t>(h, 0) != kMagic)
-    return raise("unsupported INT8 checkpoint: expected ak42 version 2 or 3");
-  const int version = read_at<int>(h, 4);
-  if (version != 3)
-    return raise("unsupported checkpoint version %d for this executable", version);
-  const int precision = read_at<int>(h, 36);
-  if (precision < 0 || precision > 1)
-    return raise("unsupported checkpoint precision %d", precision);
-  if (precision != 1)
-    return raise("checkpoint precision requires run executable");
-  Config &c = e->c;
-  memset(&c, 0, sizeof(c));
-  memcpy(&c, h + 8, 28); // dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len
-  c.shared = read_at<int>(h, 40);
-  e->gs = read_at<int>(h, 44);
-  c.norm_eps = read_at<float>(h, 48);
-  c.rope_theta = read_at<float>(h, 52);
-  c.rope_type = read_at<int>(h, 56);
-  c.rope_factor = read_at<float>(h, 60);
-  c.rope_low = read_at<float>(h, 64);
-  c.rope_high = read_at<float>(h, 68);
-  c.rope_original = read_at<int>(h, 72);
-  c.max_seq_len = read_at<int>(h, 76);
-  c.head_dim = read_at<int>(h, 80);
-  c.bos_id = read_at<int>(h, 84);
-  c.eos_id = read_at<int>(h, 88);
-  c.eot_id = read_at<int>(h, 92);
-  c.eom_id = read_at<int>(h, 96);
-  memcpy(c.name, h + 100, 128);
-  if (!memchr(c.name, 0, 128))
-    return raise("unterminated model name");
-  for (int i = 228; i < kHeaderBytes; i++)
-    if (h[i])
-      return raise("unsupported nonzero reserved checkpoint metadata");
-  c.format = version;
-  if (c.shared < 0 || c.shared > 1)
-    return raise("invalid classifier flag in '%s'", path);
-  if (c.dim <= 0 || c.hidden_dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
-      c.vocab_size <= 0 || c.seq_len <= 0 || c.n_heads % c.n_kv_heads || c.head_dim <= 0 ||
-      (long long)c.head_dim * c.n_heads != c.dim)
-    return raise("invalid model config in '%s'", path);
-  if (e->gs <= 0 || e->gs > 131071 || c.dim % e->gs || c.hidden_dim % e->gs)
-    return raise("unsupported INT8 group size %d: must divide dim and hidden_dim and fit int32 accumulation", e->gs);
+// src/runtime.c:147-170: the reference's checks of the hyperparameters, in its order and with its messages.
+bool validate_config(const Config &p, bool quantized, int gs) {
+  if (p.dim <= 0 || p.hidden_dim <= 0 || p.n_layers <= 0 || p.n_heads <= 0 || p.n_kv_heads <= 0 ||
+      p.vocab_size <= 0 || p.seq_len <= 0)
+    return raise("invalid checkpoint dimensions: all seven dimensions must be positive");
+  if (p.dim % p.n_heads || p.n_heads % p.n_kv_heads || (p.dim / p.n_heads) % 2)
+    return raise("unsupported attention dimensions: dim must be divisible by heads, heads must be divisible by KV "
+                 "heads, head size must be even");
+  if (!std::isfinite(p.norm_eps) || p.norm_eps <= 0 || !std::isfinite(p.rope_theta) || p.rope_theta <= 1 ||
+      p.head_dim != p.dim / p.n_heads || p.max_seq_len != p.seq_len)
+    return raise("invalid RMSNorm, RoPE theta, head dimension or context metadata");
+  if (p.rope_type != 0 && p.rope_type != 1)
+    return raise("unsupported RoPE scaling type %d", p.rope_type);
+  if (!std::isfinite(p.rope_factor) || !std::isfinite(p.rope_low) || !std::isfinite(p.rope_high) ||
+      p.rope_factor < 1 || p.rope_low <= 0 || p.rope_high <= p.rope_low || p.rope_original <= 0)
+    return raise("invalid RoPE scaling metadata");
+  if (p.format == 3 && (p.bos_id < 0 || p.bos_id >= p.vocab_size || p.eos_id < 0 || p.eos_id >= p.vocab_size ||
+                        p.eot_id < -1 || p.eot_id >= p.vocab_size || p.eom_id < -1 || p.eom_id >= p.vocab_size))
+    return raise("invalid special token metadata");
+  if (quantized && (gs <= 0 || gs > 131071 || p.dim % gs || p.hidden_dim % gs))
+    return raise("unsupported INT8 group size %d: must divide dim and hidden_dim and fit int32 accumulation", gs);
   return true;
 }
 
-// Walks the tensors in file order; false (after raise) when the file is not exactly their size.
+// src/runtime.c:179-270: the header of any of the four formats into e->c, e->q8, e->gs and e->header.
+bool parse_header(Engine *e, const char *path) {
+  const unsigned char *h = e->map;
+  Config &c = e->c;
+  memset(&c, 0, sizeof(c));
+  // the defaults of files without the metadata (src/runtime.c:198-207)
+  c.norm_eps = 1e-5f;
+  c.rope_theta = 500000.0f;
+  c.rope_factor = 1;
+  c.rope_low = 1;
+  c.rope_high = 4;
+  c.rope_original = 8192;
+  c.bos_id = 128000;
+  c.eos_id = 128001;
+  c.eot_id = 128009;
+  c.eom_id = -1;
+  int shared = 0;
+  if (read_at<uint32_t>(h, 0) == kMagic) {
+    if (e->bytes < kVersionedHeader)
+      return raise("truncated versioned checkpoint header");
+    e->header = kVersionedHeader;
+    const int version = read_at<int>(h, 4);
+    if (version == 3) {
+      const int precision = read_at<int>(h, 36);
+      if (precision < 0 || precision > 1)
+        return raise("unsupported checkpoint precision %d", precision);
+      e->q8 = precision == 1;
+      memcpy(&c, h + 8, 28); // dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len
+      shared = read_at<int>(h, 40);
+      e->gs = read_at<int>(h, 44);
+      c.norm_eps = read_at<float>(h, 48);
+      c.rope_theta = read_at<float>(h, 52);
+      c.rope_type = read_at<int>(h, 56);
+      c.rope_factor = read_at<float>(h, 60);
+      c.rope_low = read_at<float>(h, 64);
+      c.rope_high = read_at<float>(h, 68);
+      c.rope_original = read_at<int>(h, 72);
+      c.max_seq_len = read_at<int>(h, 76);
+      c.head_dim = read_at<int>(h, 80);
+      c.bos_id = read_at<int>(h, 84);
+      c.eos_id = read_at<int>(h, 88);
+      c.eot_id = read_at<int>(h, 92);
+      c.eom_id = read_at<int>(h, 96);
+      memcpy(c.name, h + 100, 128);
+      if (!memchr(c.name, 0, 128))
+        return raise("unterminated model name");
+      for (size_t i = 228; i < kVersionedHeader; i++)
+        if (h[i])
+          return raise("unsupported nonzero reserved checkpoint metadata");
+      if (!e->q8 && e->gs != 0)
+        return raise("FP32 checkpoint must have group size zero");
+    } else if (version == 2) { // an INT8 format only
+      e->q8 = true;
+      memcpy(&c, h + 8, 28);
+      shared = h[36];
+      e->gs = read_at<int>(h, 37);
+    } else {
+      return raise("unsupported checkpoint version %d for this executable", version);
+    }
+    c.format = version;
+    if (shared < 0 || shared > 1)
+      return raise("invalid classifier flag in '%s'", path);
+  } else { // the legacy FP32 header: seven ints, the sign of the vocabulary size tells the classifier apart
+    e->q8 = false;
+    e->gs = 0;
+    e->header = kLegacyHeader;
+    memcpy(&c, h, 28);
+    if (c.vocab_size == INT_MIN)
+      return raise("invalid vocabulary size in '%s'", path);
+    shared = c.vocab_size > 0;
+    c.vocab_size = std::abs(c.vocab_size);
+  }
+  c.shared = shared;
+  if (c.format != 3) {
+    c.max_seq_len = c.seq_len;
+    c.head_dim = c.n_heads > 0 ? c.dim / c.n_heads : 0;
+  }
+  return validate_config(c, e->q8, e->gs);
+}
+
+// Walks the tensors in file order (src/runtime.c:271-296 sizes them); false (after raise) when the file is not their
+// size. The tensor sizes are bounded by the validated dimensions (each below 2^31), so the products fit size_t.
 bool place_tensors(Engine *e, const char *path) {
   const Config &c = e->c;
   const size_t d = c.dim, hd = c.hidden_dim, kv = (size_t)c.head_dim * c.n_kv_heads, L = c.n_layers;
-  size_t at = kHeaderBytes;
+  const size_t vocab = c.vocab_size;
+  size_t at = e->header;
+  bool aligned = true;
   auto floats = [&](size_t count) {
     const float *p = (const float *)(e->map + (at <= e->bytes ? at : 0));
     at += count * sizeof(float);
     return p;
   };
-  auto q8 = [&](size_t count) {
-    Q8Tensor t{(const int8_t *)(e->map + (at <= e->bytes ? at : 0)), nullptr};
+  auto tensor = [&](size_t count) {
+    Tensor t;
+    if (!e->q8) {
+      t.w = floats(count);
+      return t;
+    }
+    if (count % (size_t)e->gs || count % sizeof(float)) // src/runtime.c:172-177
+      aligned = false;
+    t.w = e->map + (at <= e->bytes ? at : 0);
     at += count;
     t.s = (const float *)(e->map + (at <= e->bytes ? at : 0));
     at += count / e->gs * sizeof(float);
     return t;
   };
-  auto layers = [&](std::vector<Q8Tensor> &v, size_t count) {
+  auto layers = [&](std::vector<Tensor> &v, size_t count) {
     v.resize(L);
     for (size_t l = 0; l < L; l++)
-      v[l] = q8(count);
+      v[l] = tensor(count);
   };
-  e->rms_att = floats(L * d);
-  e->rms_ffn = floats(L * d);
-  e->rms_final = floats(d);
-  e->embed = q8((size_t)c.vocab_size * d);
-  layers(e->wq, d * d);
-  layers(e->wk, kv * d);
-  layers(e->wv, kv * d);
-  layers(e->wo, d * d);
-  layers(e->w1, hd * d);
-  layers(e->w2, d * hd);
-  layers(e->w3, hd * d);
-  e->cls = c.shared ? e->embed : q8((size_t)c.vocab_size * d);
+  if (e->q8) {
+    e->rms_att = floats(L * d);
+    e->rms_ffn = floats(L * d);
+    e->rms_final = floats(d);
+    e->embed = tensor(vocab * d);
+    layers(e->wq, d * d);
+    layers(e->wk, kv * d);
+    layers(e->wv, kv * d);
+    layers(e->wo, d * d);
+    layers(e->w1, hd * d);
+    layers(e->w2, d * hd);
+    layers(e->w3, hd * d);
+  } else {
+    e->embed = tensor(vocab * d);
+    e->rms_att = floats(L * d);
+    layers(e->wq, d * d);
+    layers(e->wk, kv * d);
+    layers(e->wv, kv * d);
+    layers(e->wo, d * d);
+    e->rms_ffn = floats(L * d);
+    layers(e->w1, hd * d);
+    layers(e->w2, d * hd);
+    layers(e->w3, hd * d);
+    e->rms_final = floats(d);
+    if (c.format == 0)
+      (void)floats((size_t)c.seq_len * c.head_dim); // the legacy RoPE table, unused
+  }
+  e->cls = c.shared ? e->embed : tensor(vocab * d);
+  if (!aligned)
+    return raise("unsupported INT8 tensor alignment/group size: the tensors of a %dx%d model in groups of %d", c.dim,
+                 c.hidden_dim, e->gs);
   if (at > e->bytes)
     return raise("truncated checkpoint '%s': need %zu bytes, found %zu", path, at, e->bytes);
-  if (at != e->bytes)
+  if (c.format == 3 && at != e->bytes)
     return raise("version 3 checkpoint has unexpected trailing bytes");
+  // an older format may carry trailing bytes (the reference logs a warning and reads on)
   return true;
 }
 
@@ -180,17 +302,43 @@ template <typename T> bool device_array(T **p, size_t count) {
 
 bool allocate(Engine *e) {
   const Config &c = e->c;
-  const size_t d = c.dim, kv = (size_t)c.head_dim * c.n_kv_heads;
+  const size_t d = c.dim, kv = (size_t)c.head_dim * c.n_kv_heads, h = c.hidden_dim;
   const size_t cache = (size_t)c.n_layers * c.seq_len * kv;
+  const size_t groups = e->q8 ? (size_t)e->gs : 1;
   return device_array(&e->x, d) && device_array(&e->xb, d) && device_array(&e->q, d) && device_array(&e->k, kv) &&
-         device_array(&e->v, kv) && device_array(&e->hb, (size_t)c.hidden_dim) &&
-         device_array(&e->logits, (size_t)c.vocab_size) && device_array(&e->rope, 2 * (size_t)c.head_dim) &&
-         device_array(&e->key_cache, cache) && device_array(&e->value_cache, cache) &&
-         device_array(&e->xq, d) && device_array(&e->xs, d / e->gs) && device_array(&e->hq, (size_t)c.hidden_dim) &&
-         device_array(&e->hs, (size_t)c.hidden_dim / e->gs);
+         device_array(&e->v, kv) && device_array(&e->hb, h) && device_array(&e->logits, (size_t)c.vocab_size) &&
+         device_array(&e->rope, 2 * (size_t)c.head_dim) && device_array(&e->key_cache, cache) &&
+         device_array(&e->value_cache, cache) && device_array(&e->xq, d) && device_array(&e->xs, d / groups) &&
+         device_array(&e->hq, h) && device_array(&e->hs, h / groups);
 }
 
-Engine *open_engine(const char *path, int context) {
+// BF16 mode (src/tp.c:805-830): every layer's seven matrices packed once into the BF16 layout the GEMM reads
+// (pack_bf16_vnni, host side), uploaded to one device allocation.
+bool pack_weights(Engine *e) {
+  const Config &c = e->c;
+  const int d = c.dim, h = c.hidden_dim, kv = c.head_dim * c.n_kv_heads;
+  const int rows[kPackRoles] = {d, kv, kv, d, h, d, h}, cols[kPackRoles] = {d, d, d, d, d, h, d};
+  const std::vector<Tensor> *roles[kPackRoles] = {&e->wq, &e->wk, &e->wv, &e->wo, &e->w1, &e->w2, &e->w3};
+  size_t per_layer = 0;
+  for (int i = 0; i < kPackRoles; i++)
+    per_layer += bf16_vnni_elements(rows[i], cols[i]);
+  if (!device_array(&e->packed, per_layer * c.n_layers))
+    return false;
+  std::vector<uint16_t> host(per_layer);
+  e->packed_at.resize((size_t)c.n_layers * kPackRoles);
+  for (int l = 0; l < c.n_layers; l++) {
+    size_t at = 0;
+    for (int i = 0; i < kPackRoles; i++) {
+      pack_bf16_vnni(host.data() + at, (*roles[i])[l].f(), rows[i], cols[i], (size_t)cols[i]);
+      e->packed_at[(size_t)l * kPackRoles + i] = e->packed + (size_t)l * per_layer + at;
+      at += bf16_vnni_elements(rows[i], cols[i]);
+    }
+    llhip_memcpy_h2d(e->packed + (size_t)l * per_layer, host.data(), per_layer * sizeof(uint16_t));
+  }
+  return llhip_last_error()[0] == 0;
+}
+
+Engine *open_engine(Model *model, const char *path, int context, bool a32) {
   Engine *e = new Engine();
   e->fd = open(path, O_RDONLY);
   if (e->fd < 0) {
@@ -198,7 +346,7 @@ Engine *open_engine(const char *path, int context) {
     return release(e), nullptr;
   }
   struct stat st;
-  if (fstat(e->fd, &st) || !S_ISREG(st.st_mode) || st.st_size < kHeaderBytes) {
+  if (fstat(e->fd, &st) || !S_ISREG(st.st_mode) || st.st_size < (off_t)kLegacyHeader) {
     raise("invalid/truncated checkpoint '%s': expected a regular file with complete header", path);
     return release(e), nullptr;
   }
@@ -214,43 +362,72 @@ Engine *open_engine(const char *path, int context) {
     e->map = nullptr;
     return release(e), nullptr;
   }
-  if (context > 0 && context < e->c.seq_len)
-    e->c.seq_len = context; // the K/V cache covers the requested context only
-  if (llhip_register_host(e->map, e->bytes) != 0) {
+  e->a32 = e->q8 && a32;
+  // src/engine.c:145-150: the context requested, else the checkpoint's up to 4096 positions
+  if (context < 0 || context > e->c.seq_len) {
+    raise("requested context exceeds checkpoint context");
     munmap(e->map, e->bytes);
     e->map = nullptr;
     return release(e), nullptr;
   }
-  if (!allocate(e))
+  e->c.seq_len = context ? context : (e->c.seq_len < kDefaultContext ? e->c.seq_len : kDefaultContext);
+  model->config = e->c;
+  // src/engine.c:83-118: the prefill policy of each format
+  if (e->q8) {
+    prefill_precision(1); // LLAMA_PRECISION=bf16 is an error for Q8_0
+    if (llhip_last_error()[0])
+      return munmap(e->map, e->bytes), e->map = nullptr, release(e), nullptr;
+    prefill_configure_engine(model, e->a32 ? 1 : LLHIP_PREFILL_BATCH_Q8, 1);
+    if (e->a32) {
+      model->prefill_gemm = 0;
+      model->prefill_kernel = nullptr;
+    }
+  } else {
+    model->prefill_bf16 = prefill_precision(0);
+    if (!llhip_last_error()[0])
+      prefill_configure_engine(model, model->prefill_bf16 ? LLHIP_PREFILL_BATCH_BF16 : LLHIP_PREFILL_BATCH_F32, 0);
+    e->bf16 = model->prefill_bf16 != 0;
+  }
+  if (llhip_last_error()[0]) {
+    munmap(e->map, e->bytes);
+    e->map = nullptr;
+    return release(e), nullptr;
+  }
+  kernels_init(); // src/engine.c:127-128 (LLAMA_KERNELS, and the device opens), once the file has passed its checks
+  if (llhip_last_error()[0] || llhip_register_host(e->map, e->bytes) != 0) {
+    munmap(e->map, e->bytes);
+    e->map = nullptr;
+    return release(e), nullptr;
+  }
+  if (!allocate(e) || (e->bf16 && !pack_weights(e)))
     return release(e), nullptr;
   k_attention_init(&e->work, e->c.n_heads, e->c.n_kv_heads, e->c.head_dim, e->c.seq_len);
   e->host_logits.resize((size_t)e->c.vocab_size);
   return e;
 }
 
-// One decode token (src/tp.c:387-436, one socket, W8A8): the embedding row, per layer RMSNorm, quantize, QKV, RoPE,
-// the K/V cache (head-major: staged rows then k_kv_store; rows layout: written in place), attention, quantize,
+// One decode token (src/tp.c:337-436 with one socket). Q8_0: the embedding row, per layer RMSNorm, quantize, QKV,
+// RoPE, the K/V cache (head-major: staged rows then k_kv_store; rows layout: written in place), attention, quantize,
 // Wo + residual, RMSNorm, quantize, W1/W3 SwiGLU, quantize, W2 + residual; then the final RMSNorm in place, quantize
-// and the classifier.
-bool forward(Engine *e, int token, int pos) {
+// and the classifier. W8A32 hands the FP32 rows to the GEMVs instead of quantizing; FP32 runs the FP32 GEMVs. The
+// classifier runs only when the logits are wanted (src/engine.c:75-77); they land in e->host_logits.
+bool forward(Engine *e, int token, int pos, bool want_logits) {
   const Config &c = e->c;
   const int d = c.dim, hidden = c.hidden_dim, hd = c.head_dim, gs = e->gs, nh = c.n_heads, nkv = c.n_kv_heads;
   const size_t kvl = (size_t)hd * nkv;
-  llhip_clear_error(); // the result below reports this token's failures only
-  if (token < 0 || token >= c.vocab_size)
-    return raise("token %d outside the vocabulary of %d", token, c.vocab_size);
-  if (pos < 0 || pos >= c.seq_len)
-    return raise("position %d outside the context of %d", pos, c.seq_len);
-  k_embed_q8_rows(e->x, e->embed.q, e->embed.s, &token, 1, d, gs, c.vocab_size);
+  if (e->q8)
+    k_embed_q8_rows(e->x, e->embed.q(), e->embed.s, &token, 1, d, gs, c.vocab_size);
+  else
+    k_embed_f32_rows(e->x, e->embed.f(), &token, 1, d, c.vocab_size);
   k_rope_table(&c, pos, e->rope);
   const bool head = kernels_kv_layout_head() != 0;
   // W8A8 quantizes each GEMV input (q8_input, src/tp.c:380-385); W8A32 hands the FP32 rows over instead
-  const bool a32 = fp32_activations;
+  const bool a32 = e->a32;
   const K8Input in_d = a32 ? K8Input{nullptr, nullptr, e->xb} : K8Input{e->xq, e->xs, nullptr};
   const K8Input in_h = a32 ? K8Input{nullptr, nullptr, e->hb} : K8Input{e->hq, e->hs, nullptr};
   const K8Input in_x = a32 ? K8Input{nullptr, nullptr, e->x} : in_d;
   auto quantize = [&](int8_t *q, float *s, const float *x, int n) {
-    if (!a32)
+    if (e->q8 && !a32)
       k_quantize(q, s, x, n, gs);
   };
   for (int l = 0; l < c.n_layers; l++) {
@@ -259,8 +436,10 @@ bool forward(Engine *e, int token, int pos) {
     float *k = head ? e->k : kc + (size_t)pos * kvl, *v = head ? e->v : vc + (size_t)pos * kvl;
     k_rmsnorm(e->xb, e->x, e->rms_att + (size_t)l * d, d, c.norm_eps);
     quantize(e->xq, e->xs, e->xb, d);
-    k_matmul_q8_qkv(e->q, k, v, &in_d, K8Weight{e->wq[l].q, e->wq[l].s}, K8Weight{e->wk[l].q, e->wk[l].s},
-                    K8Weight{e->wv[l].q, e->wv[l].s}, d, d, (int)kvl, gs);
+    if (e->q8)
+      k_matmul_q8_qkv(e->q, k, v, &in_d, e->wq[l].k8(), e->wk[l].k8(), e->wv[l].k8(), d, d, (int)kvl, gs);
+    else
+      k_matmul_qkv(e->q, k, v, e->xb, e->wq[l].f(), e->wk[l].f(), e->wv[l].f(), d, d, (int)kvl);
     k_rope_apply(e->q, k, e->rope, nh, nkv, hd);
     if (head) {
       k_kv_store(kc, k, kvl, pos, 1, nkv, hd, c.seq_len);
@@ -268,87 +447,144 @@ bool forward(Engine *e, int token, int pos) {
     }
     k_attention_kv(e->xb, e->q, kc, vc, nullptr, &e->work, nh, nkv, hd, c.seq_len, pos);
     quantize(e->xq, e->xs, e->xb, d);
-    k_matmul_q8_add(e->x, &in_d, K8Weight{e->wo[l].q, e->wo[l].s}, d, d, gs);
+    if (e->q8)
+      k_matmul_q8_add(e->x, &in_d, e->wo[l].k8(), d, d, gs);
+    else
+      k_matmul_add(e->x, e->xb, e->wo[l].f(), d, d);
     k_rmsnorm(e->xb, e->x, e->rms_ffn + (size_t)l * d, d, c.norm_eps);
     quantize(e->xq, e->xs, e->xb, d);
-    k_matmul_q8_swiglu(e->hb, &in_d, K8Weight{e->w1[l].q, e->w1[l].s}, K8Weight{e->w3[l].q, e->w3[l].s}, d, hidden,
-                       gs);
+    if (e->q8)
+      k_matmul_q8_swiglu(e->hb, &in_d, e->w1[l].k8(), e->w3[l].k8(), d, hidden, gs);
+    else
+      k_matmul_swiglu(e->hb, e->xb, e->w1[l].f(), e->w3[l].f(), d, hidden);
     quantize(e->hq, e->hs, e->hb, hidden);
-    k_matmul_q8_add(e->x, &in_h, K8Weight{e->w2[l].q, e->w2[l].s}, hidden, d, gs);
+    if (e->q8)
+      k_matmul_q8_add(e->x, &in_h, e->w2[l].k8(), hidden, d, gs);
+    else
+      k_matmul_add(e->x, e->hb, e->w2[l].f(), hidden, d);
   }
-  k_rmsnorm(e->x, e->x, e->rms_final, d, c.norm_eps);
-  quantize(e->xq, e->xs, e->x, d);
-  k_matmul_q8(e->logits, &in_x, K8Weight{e->cls.q, e->cls.s}, d, c.vocab_size, gs);
-  llhip_memcpy_d2h(e->host_logits.data(), e->logits, (size_t)c.vocab_size * sizeof(float));
+  if (want_logits) {
+    k_rmsnorm(e->x, e->x, e->rms_final, d, c.norm_eps);
+    quantize(e->xq, e->xs, e->x, d);
+    if (e->q8)
+      k_matmul_q8(e->logits, &in_x, e->cls.k8(), d, c.vocab_size, gs);
+    else
+      k_matmul(e->logits, e->x, e->cls.f(), d, c.vocab_size);
+    llhip_memcpy_d2h(e->host_logits.data(), e->logits, (size_t)c.vocab_size * sizeof(float));
+  }
   llhip_synchronize(); // reports a non-finite activation or score of this token
   return llhip_last_error()[0] == 0;
 }
 
+// The batched forward's rows, max_batch of each, on its first call; all or nothing.
 bool allocate_batch(Engine *e, int rows) {
   const Config &c = e->c;
   const size_t m = rows, d = c.dim, kv = (size_t)c.head_dim * c.n_kv_heads, h = c.hidden_dim;
-  if (!(device_array(&e->bx, m * d) && device_array(&e->bxb, m * d) && device_array(&e->bq, m * d) &&
-        device_array(&e->bk, m * kv) && device_array(&e->bv, m * kv) && device_array(&e->bhb, m * h) &&
-        device_array(&e->bxq, m * h) && device_array(&e->bxs, m * h / e->gs) &&
-        device_array(&e->brope, m * 2 * c.head_dim)))
+  const size_t groups = e->q8 ? (size_t)e->gs : 1;
+  const bool ok = device_array(&e->bx, m * d) && device_array(&e->bxb, m * d) && device_array(&e->bq, m * d) &&
+                  device_array(&e->bk, m * kv) && device_array(&e->bv, m * kv) && device_array(&e->bhb, m * h) &&
+                  device_array(&e->bxq, e->q8 ? m * h : 1) && device_array(&e->bxs, e->q8 ? m * h / groups : 1) &&
+                  device_array(&e->brope, m * 2 * c.head_dim) && device_array(&e->btokens, m);
+  if (ok && e->bf16) {
+    aligned_buffer_alloc(&e->panel, k_gemm_bf16_panel_bytes(rows, c.dim > c.hidden_dim ? c.dim : c.hidden_dim),
+                         MEM_ACTIVATION);
+    if (!e->panel.base) {
+      free_batch(e);
+      return false;
+    }
+  }
+  if (!ok) {
+    free_batch(e); // nothing stays claimed, and the next call tries again
     return false;
+  }
   e->host_rope.resize(m * 2 * c.head_dim);
   e->batch_rows = rows;
   return true;
 }
 
-// count tokens at pos0 .. pos0 + count - 1 (src/tp.c:528-622 with one socket, W8A8): the embedding rows and RoPE
-// tables, per layer RMSNorm of the rows, quantize, the QKV GEMM, RoPE, the cache rows, batched causal attention,
-// quantize, Wo + residual, RMSNorm, quantize, W1/W3 SwiGLU, quantize, W2 + residual; then the final RMSNorm,
-// quantize and classifier GEMV of the last row (LAST) or of every row (ALL).
-float *forward_batch(Model *model, Engine *e, const int *tokens, int count, int pos0, LogitsWanted want) {
-  llhip_clear_error();
-  prefill_validate(model, tokens, count, pos0, want);
-  if (llhip_last_error()[0])
-    return nullptr;
+// One product on FP32 activations (src/tp.c:475-490): the FP32 GEMM, or in BF16 mode the same segments on the packed
+// copies of layer l's matrices `index` (and `index3` for the SwiGLU pair).
+void gemm_f32_or_bf16(Engine *e, const float *a, int lda, int m, int k, const GemmSegment *seg, int count, int l,
+                      const int *index, int index3) {
+  if (!e->bf16) {
+    k_gemm_f32(a, lda, m, k, seg, count);
+    return;
+  }
+  GemmBf16Segment b[GEMM_MAX_SEGMENTS];
+  for (int i = 0; i < count; i++)
+    b[i] = GemmBf16Segment{seg[i].c, seg[i].ldc, e->packed_at[(size_t)l * kPackRoles + index[i]],
+                           index3 >= 0 ? e->packed_at[(size_t)l * kPackRoles + index3] : nullptr, seg[i].n,
+                           seg[i].kind};
+  k_gemm_bf16(a, lda, m, k, b, count, &e->panel);
+}
+
+// count tokens at pos0 .. pos0 + count - 1 through the GEMMs (src/tp.c:528-622 with one socket): the embedding rows
+// and RoPE tables, per layer RMSNorm of the rows, (quantize,) the QKV GEMM, RoPE, the cache rows, batched causal
+// attention, (quantize,) Wo + residual, RMSNorm, (quantize,) W1/W3 SwiGLU, (quantize,) W2 + residual; then the final
+// RMSNorm and classifier of the last row (LAST) or of every row (ALL; in BF16 mode one BF16 GEMM on the packed
+// classifier).
+float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int pos0, LogitsWanted want) {
   const Config &c = e->c;
   const int d = c.dim, hidden = c.hidden_dim, hd = c.head_dim, gs = e->gs, nh = c.n_heads, nkv = c.n_kv_heads;
   const int kvl = hd * nkv;
-  if (fp32_activations) { // W8A32 has no batched GEMM: the batch is one row (src/engine.c:97-104)
-    if (!forward(e, tokens[0], pos0))
-      return nullptr;
-    return want == LOGITS_NONE ? nullptr : e->host_logits.data();
-  }
   if (!e->batch_rows && !allocate_batch(e, model->max_batch))
     return nullptr;
   for (int i = 0; i < count; i++)
     k_rope_table(&c, pos0 + i, e->host_rope.data() + (size_t)i * 2 * hd);
   llhip_memcpy_h2d(e->brope, e->host_rope.data(), (size_t)count * 2 * hd * sizeof(float));
-  k_embed_q8_rows(e->bx, e->embed.q, e->embed.s, tokens, count, d, gs, c.vocab_size);
+  llhip_memcpy_h2d(e->btokens, tokens, (size_t)count * sizeof(int));
+  if (e->q8)
+    k_embed_q8_rows(e->bx, e->embed.q(), e->embed.s, e->btokens, count, d, gs, c.vocab_size);
+  else
+    k_embed_f32_rows(e->bx, e->embed.f(), e->btokens, count, d, c.vocab_size);
   const bool head = kernels_kv_layout_head() != 0;
+  static const int kQkv[3] = {0, 1, 2}, kWo[1] = {3}, kW1[1] = {4}, kW2[1] = {5};
   for (int l = 0; l < c.n_layers; l++) {
     const size_t layer = (size_t)l * c.seq_len * kvl;
     float *kc = e->key_cache + layer, *vc = e->value_cache + layer;
     float *kd = head ? e->bk : kc + (size_t)pos0 * kvl, *vd = head ? e->bv : vc + (size_t)pos0 * kvl;
     k_rmsnorm_rows(e->bxb, e->bx, e->rms_att + (size_t)l * d, count, d, c.norm_eps);
-    k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
-    const GemmQ8Segment qkv[3] = {
-        {e->bq, d, K8Weight{e->wq[l].q, e->wq[l].s}, K8Weight{}, nullptr, nullptr, d, GEMM_STORE},
-        {kd, kvl, K8Weight{e->wk[l].q, e->wk[l].s}, K8Weight{}, nullptr, nullptr, kvl, GEMM_STORE},
-        {vd, kvl, K8Weight{e->wv[l].q, e->wv[l].s}, K8Weight{}, nullptr, nullptr, kvl, GEMM_STORE}};
-    k_gemm_q8(e->bxq, e->bxs, count, d, gs, qkv, 3);
+    if (e->q8) {
+      k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
+      const GemmQ8Segment qkv[3] = {
+          {e->bq, d, e->wq[l].k8(), K8Weight{}, nullptr, nullptr, d, GEMM_STORE},
+          {kd, kvl, e->wk[l].k8(), K8Weight{}, nullptr, nullptr, kvl, GEMM_STORE},
+          {vd, kvl, e->wv[l].k8(), K8Weight{}, nullptr, nullptr, kvl, GEMM_STORE}};
+      k_gemm_q8(e->bxq, e->bxs, count, d, gs, qkv, 3);
+    } else {
+      const GemmSegment qkv[3] = {{e->bq, d, e->wq[l].f(), nullptr, (size_t)d, d, GEMM_STORE},
+                                  {kd, kvl, e->wk[l].f(), nullptr, (size_t)d, kvl, GEMM_STORE},
+                                  {vd, kvl, e->wv[l].f(), nullptr, (size_t)d, kvl, GEMM_STORE}};
+      gemm_f32_or_bf16(e, e->bxb, d, count, d, qkv, 3, l, kQkv, -1);
+    }
     k_rope_apply_rows(e->bq, d, kd, kvl, e->brope, 2 * (size_t)hd, count, nh, nkv, hd);
     if (head) {
       k_kv_store(kc, kd, kvl, pos0, count, nkv, hd, c.seq_len);
       k_kv_store(vc, vd, kvl, pos0, count, nkv, hd, c.seq_len);
     }
     k_attention_batch_kv(e->bxb, e->bq, kc, vc, nullptr, &e->work, nh, nkv, hd, c.seq_len, pos0, count);
-    k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
-    const GemmQ8Segment wo{e->bx, d, K8Weight{e->wo[l].q, e->wo[l].s}, K8Weight{}, nullptr, nullptr, d, GEMM_ADD};
-    k_gemm_q8(e->bxq, e->bxs, count, d, gs, &wo, 1);
+    if (e->q8) {
+      k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
+      const GemmQ8Segment wo{e->bx, d, e->wo[l].k8(), K8Weight{}, nullptr, nullptr, d, GEMM_ADD};
+      k_gemm_q8(e->bxq, e->bxs, count, d, gs, &wo, 1);
+    } else {
+      const GemmSegment wo{e->bx, d, e->wo[l].f(), nullptr, (size_t)d, d, GEMM_ADD};
+      gemm_f32_or_bf16(e, e->bxb, d, count, d, &wo, 1, l, kWo, -1);
+    }
     k_rmsnorm_rows(e->bxb, e->bx, e->rms_ffn + (size_t)l * d, count, d, c.norm_eps);
-    k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
-    const GemmQ8Segment up{e->bhb,  hidden,  K8Weight{e->w1[l].q, e->w1[l].s}, K8Weight{e->w3[l].q, e->w3[l].s},
-                           nullptr, nullptr, hidden,                          GEMM_SWIGLU};
-    k_gemm_q8(e->bxq, e->bxs, count, d, gs, &up, 1);
-    k_quantize_rows(e->bxq, e->bxs, e->bhb, hidden, count, hidden, gs);
-    const GemmQ8Segment down{e->bx, d, K8Weight{e->w2[l].q, e->w2[l].s}, K8Weight{}, nullptr, nullptr, d, GEMM_ADD};
-    k_gemm_q8(e->bxq, e->bxs, count, hidden, gs, &down, 1);
+    if (e->q8) {
+      k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
+      const GemmQ8Segment up{e->bhb, hidden, e->w1[l].k8(), e->w3[l].k8(), nullptr, nullptr, hidden, GEMM_SWIGLU};
+      k_gemm_q8(e->bxq, e->bxs, count, d, gs, &up, 1);
+      k_quantize_rows(e->bxq, e->bxs, e->bhb, hidden, count, hidden, gs);
+      const GemmQ8Segment down{e->bx, d, e->w2[l].k8(), K8Weight{}, nullptr, nullptr, d, GEMM_ADD};
+      k_gemm_q8(e->bxq, e->bxs, count, hidden, gs, &down, 1);
+    } else {
+      const GemmSegment up{e->bhb, hidden, e->w1[l].f(), e->w3[l].f(), (size_t)d, hidden, GEMM_SWIGLU};
+      gemm_f32_or_bf16(e, e->bxb, d, count, d, &up, 1, l, kW1, 6);
+      const GemmSegment down{e->bx, d, e->w2[l].f(), nullptr, (size_t)hidden, d, GEMM_ADD};
+      gemm_f32_or_bf16(e, e->bhb, hidden, count, hidden, &down, 1, l, kW2, -1);
+    }
   }
   if (want == LOGITS_NONE) {
     llhip_synchronize();
@@ -357,13 +593,30 @@ float *forward_batch(Model *model, Engine *e, const int *tokens, int count, int 
   const size_t vocab = c.vocab_size;
   if (want == LOGITS_ALL && !e->blogits && !device_array(&e->blogits, (size_t)e->batch_rows * vocab))
     return nullptr;
-  const K8Input in{e->xq, e->xs, nullptr};
-  for (int i = want == LOGITS_ALL ? 0 : count - 1; i < count; i++) {
-    float *x = e->bx + (size_t)i * d;
-    k_rmsnorm(x, x, e->rms_final, d, c.norm_eps);
-    k_quantize(e->xq, e->xs, x, d, gs);
-    k_matmul_q8(want == LOGITS_ALL ? e->blogits + (size_t)i * vocab : e->logits, &in, K8Weight{e->cls.q, e->cls.s}, d,
-                c.vocab_size, gs);
+  if (want == LOGITS_ALL && e->bf16) { // src/tp.c:601-609: a BF16 GEMM on the packed classifier
+    if (!e->cls_packed) {
+      std::vector<uint16_t> host(bf16_vnni_elements(c.vocab_size, d));
+      pack_bf16_vnni(host.data(), e->cls.f(), c.vocab_size, d, (size_t)d);
+      if (!device_array(&e->cls_packed, host.size()))
+        return nullptr;
+      llhip_memcpy_h2d(e->cls_packed, host.data(), host.size() * sizeof(uint16_t));
+    }
+    k_rmsnorm_rows(e->bx, e->bx, e->rms_final, count, d, c.norm_eps);
+    const GemmBf16Segment seg{e->blogits, c.vocab_size, e->cls_packed, nullptr, c.vocab_size, GEMM_STORE};
+    k_gemm_bf16(e->bx, d, count, d, &seg, 1, &e->panel);
+  } else {
+    const K8Input in{e->xq, e->xs, nullptr};
+    for (int i = want == LOGITS_ALL ? 0 : count - 1; i < count; i++) {
+      float *x = e->bx + (size_t)i * d;
+      float *out = want == LOGITS_ALL ? e->blogits + (size_t)i * vocab : e->logits;
+      k_rmsnorm(x, x, e->rms_final, d, c.norm_eps);
+      if (e->q8) {
+        k_quantize(e->xq, e->xs, x, d, gs);
+        k_matmul_q8(out, &in, e->cls.k8(), d, c.vocab_size, gs);
+      } else {
+        k_matmul(out, x, e->cls.f(), d, c.vocab_size);
+      }
+    }
   }
   float *host;
   if (want == LOGITS_ALL) {
@@ -378,6 +631,27 @@ float *forward_batch(Model *model, Engine *e, const int *tokens, int count, int 
   return llhip_last_error()[0] ? nullptr : host;
 }
 
+// src/engine.c:65-81: with the batched GEMM on, more than one row (in BF16 mode any row) runs through the GEMMs;
+// otherwise the rows run one token at a time, the classifier only for the rows whose logits are asked for.
+float *forward_batch(Model *model, Engine *e, const int *tokens, int count, int pos0, LogitsWanted want) {
+  prefill_validate(model, tokens, count, pos0, want);
+  if (llhip_last_error()[0])
+    return nullptr;
+  if (model->prefill_gemm && (count > 1 || e->bf16))
+    return forward_rows(model, e, tokens, count, pos0, want);
+  const size_t vocab = e->c.vocab_size;
+  if (want == LOGITS_ALL)
+    e->host_batch_logits.resize((size_t)count * vocab);
+  for (int i = 0; i < count; i++) {
+    const bool wanted = want == LOGITS_ALL || (want == LOGITS_LAST && i == count - 1);
+    if (!forward(e, tokens[i], pos0 + i, wanted))
+      return nullptr;
+    if (want == LOGITS_ALL)
+      memcpy(e->host_batch_logits.data() + (size_t)i * vocab, e->host_logits.data(), vocab * sizeof(float));
+  }
+  return want == LOGITS_NONE ? nullptr : want == LOGITS_ALL ? e->host_batch_logits.data() : e->host_logits.data();
+}
+
 } // namespace
 } // namespace llhip
 
@@ -388,30 +662,33 @@ extern "C" {
 const int engine_q8 = 1;
 
 void engine_load_context(Model *model, const char *path, int context) {
+  if (!model) {
+    raise("engine_load: null model");
+    return;
+  }
   memset(model, 0, sizeof(*model));
   if (!path) {
     raise("engine_load: null path");
     return;
   }
+  llhip_clear_error();
   const char *activations = getenv("LLAMA_Q8_ACTIVATIONS"); // src/engine.c:132-135
   if (activations && *activations && strcmp(activations, "int8") && strcmp(activations, "fp32")) {
     raise("LLAMA_Q8_ACTIVATIONS must be int8 or fp32");
     return;
   }
-  fp32_activations = activations && !strcmp(activations, "fp32");
-  Engine *e = open_engine(path, context);
-  if (!e)
+  const bool a32 = activations && !strcmp(activations, "fp32");
+  Engine *e = open_engine(model, path, context, a32);
+  if (!e) {
+    memset(model, 0, sizeof(*model));
     return;
+  }
   model->config = e->c;
   model->implementation = e;
-  loaded_group_size = e->gs;
   model->file_bytes = e->bytes;
   model->mapped_bytes = e->bytes;
-  prefill_configure_engine(model, fp32_activations ? 1 : LLHIP_PREFILL_BATCH_Q8, 1);
-  if (fp32_activations) {
-    model->prefill_gemm = 0;
-    model->prefill_kernel = nullptr;
-  }
+  last_group_size = e->gs;
+  last_precision = e->q8 ? (e->a32 ? "int8_q8_0_w8a32" : "int8_q8_0") : (e->bf16 ? "bf16_from_fp32" : "fp32");
 }
 
 void engine_load(Model *model, const char *path) { engine_load_context(model, path, 0); }
@@ -422,7 +699,12 @@ float *engine_forward(Model *model, int token, int position) {
     raise("engine_forward: no model loaded");
     return nullptr;
   }
-  return forward(e, token, position) ? e->host_logits.data() : nullptr;
+  llhip_clear_error(); // the result reports this token's failures only
+  if (token < 0 || token >= model->config.vocab_size || position < 0 || position >= model->config.seq_len) {
+    raise("forward input out of range: token=%d position=%d", token, position); // src/engine.c:171-172
+    return nullptr;
+  }
+  return forward(e, token, position, true) ? e->host_logits.data() : nullptr;
 }
 
 float *engine_forward_batch(Model *model, const int *tokens, int count, int pos0, LogitsWanted want) {
@@ -431,7 +713,22 @@ float *engine_forward_batch(Model *model, const int *tokens, int count, int pos0
     raise("engine_forward_batch: no model loaded");
     return nullptr;
   }
+  llhip_clear_error();
   return forward_batch(model, e, tokens, count, pos0, want);
+}
+
+void engine_kv_stats(Model *model, int position, int verify, KvStats *out) {
+  (void)verify;
+  Engine *e = model ? (Engine *)model->implementation : nullptr;
+  if (!e || !out) {
+    raise("engine_kv_stats: no model loaded");
+    return;
+  }
+  const size_t row = (size_t)e->c.head_dim * e->c.n_kv_heads * sizeof(float);
+  memset(out, 0, sizeof(*out));
+  out->reserved_bytes = 2 * (size_t)e->c.n_layers * (size_t)e->c.seq_len * row;
+  out->active_bytes = 2 * (size_t)e->c.n_layers * (size_t)(position > 0 ? position : 0) * row;
+  out->node = -1;
 }
 
 void engine_free(Model *model) {
@@ -443,8 +740,8 @@ void engine_free(Model *model) {
   model->implementation = nullptr;
 }
 
-int engine_group_size(void) { return loaded_group_size; }
+int engine_group_size(void) { return last_group_size; }
 
-const char *engine_precision(void) { return fp32_activations ? "int8_q8_0_w8a32" : "int8_q8_0"; }
+const char *engine_precision(void) { return last_precision; }
 
 } // extern "C"

@@ -12,6 +12,7 @@
 //                  attn_merge rescales the chunks by exp(m_c - M) and normalizes (src/attention.c:664-682).
 //                  HBM-bound on the K/V cache: 8 * kv_dim bytes per position and query row.
 #include <cfloat>
+#include <type_traits>
 
 #include "common.h"
 
@@ -160,6 +161,26 @@ __global__ __launch_bounds__(kThreads) void embed_rows(float *__restrict__ out, 
   }
   const size_t at = (size_t)id * dim + j;
   out[(size_t)r * dim + j] = (float)table[at] * scales[at / gs];
+}
+
+// The FP32 table's lookup (src/tp.c:342 for a token, 449 for a batch): a copy of row ids[i], 16 bytes per thread when
+// dim is a multiple of 4 (the table's rows are then 16-byte aligned), else one value per thread. An id outside
+// [0, vocab) raises flag 2 and leaves its row untouched.
+template <int V>
+__global__ __launch_bounds__(kThreads) void embed_rows_f32(float *__restrict__ out, const float *__restrict__ table,
+                                                           const int *__restrict__ ids, int count, int dim, int vocab,
+                                                           int *flags) {
+  using Vec = typename std::conditional<V == 4, float4, float>::type;
+  const int per_row = dim / V;
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (long long)count * per_row)
+    return;
+  const int r = (int)(i / per_row), j = (int)(i % per_row), id = ids[r];
+  if (id < 0 || id >= vocab) {
+    flags[2] = 1;
+    return;
+  }
+  reinterpret_cast<Vec *>(out + (size_t)r * dim)[j] = reinterpret_cast<const Vec *>(table + (size_t)id * dim)[j];
 }
 
 // ---- attention ------------------------------------------------------------------------------------------------------
@@ -519,6 +540,20 @@ bool launch_embed_rows(float *out, const int8_t *table, const float *scales, con
   hipLaunchKernelGGL(embed_rows, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream, out,
                      table, scales, ids, count, dim, gs, vocab, device().error_flags);
   return launch_ok("embed_rows");
+}
+
+bool launch_embed_rows_f32(float *out, const float *table, const int *ids, int count, int dim, int vocab,
+                           hipStream_t stream) {
+  const bool vec = dim % 4 == 0 && ((uintptr_t)out | (uintptr_t)table) % 16 == 0;
+  const long long threads = (long long)count * (vec ? dim / 4 : dim);
+  const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads));
+  if (vec)
+    hipLaunchKernelGGL(embed_rows_f32<4>, grid, dim3(kThreads), 0, stream, out, table, ids, count, dim, vocab,
+                       device().error_flags);
+  else
+    hipLaunchKernelGGL(embed_rows_f32<1>, grid, dim3(kThreads), 0, stream, out, table, ids, count, dim, vocab,
+                       device().error_flags);
+  return launch_ok("embed_rows_f32");
 }
 
 int slot_floats(int head_dim) { return (head_dim + 2 + 3) & ~3; }

@@ -90,6 +90,12 @@ class Config(ctypes.Structure):
                [("name", ctypes.c_char * 128)]
 
 
+class KvStats(ctypes.Structure):  # include/llama_hip_engine.h (runtime.h:80-86)
+    _fields_ = [("reserved_bytes", SZ), ("active_bytes", SZ), ("resident_bytes", SZ), ("node", I32),
+                ("verified", I32), ("full", I32), ("pages_queried", SZ), ("pages_wrong_node", SZ),
+                ("pages_missing", SZ)]
+
+
 class Model(ctypes.Structure):
     _fields_ = [("config", Config), ("implementation", P), ("file_bytes", SZ), ("mapped_bytes", SZ),
                 ("max_batch", I32), ("prefill_logits", I32), ("prefill_gemm", I32), ("prefill_kernel", ctypes.c_char_p),
@@ -118,6 +124,7 @@ _SIGNATURES = {
     "k_kv_strides": (None, [I32, I32, I32, P, P]),
     "k_kv_store": (None, [P, P, SZ, I32, I32, I32, I32, I32]),
     "k_embed_q8_rows": (None, [P, P, P, P, I32, I32, I32, I32]),
+    "k_embed_f32_rows": (None, [P, P, P, I32, I32, I32]),
     "placement_hbm_budget": (SZ, []),
     "engine_load": (None, [P, ctypes.c_char_p]),
     "engine_load_context": (None, [P, ctypes.c_char_p, I32]),
@@ -126,6 +133,7 @@ _SIGNATURES = {
     "engine_forward_batch": (ctypes.POINTER(ctypes.c_float), [P, P, I32, I32, I32]),
     "engine_group_size": (I32, []),
     "engine_precision": (ctypes.c_char_p, []),
+    "engine_kv_stats": (None, [P, I32, I32, P]),
     "llhip_hbm_claimed": (SZ, []),
     "k_attention_init": (None, [P, I32, I32, I32, I32]),
     "k_attention_bytes": (SZ, [I32, I32, I32, I32]),

@@ -182,10 +182,10 @@ def test_engine_load_context_sizes_the_cache(tmp_path):
         lh.record_failures()
         try:
             assert not L.engine_forward(ctypes.byref(small), 1, 40)
-            assert "position 40 outside the context of 40" in lh.last_error()
+            assert lh.last_error() == "forward input out of range: token=1 position=40"
             L.llhip_clear_error()
             assert not L.engine_forward(ctypes.byref(small), CFG["vocab_size"], 3)
-            assert "outside the vocabulary" in lh.last_error()
+            assert lh.last_error() == f"forward input out of range: token={CFG['vocab_size']} position=3"
         finally:
             L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
             L.llhip_clear_error()
