@@ -1,0 +1,134 @@
+"""End to end at Llama-3.1-8B size: a Q8_0 checkpoint of random-init weights (~N(0, 0.02), RMSNorm weights 1.0,
+32 layers, 32 query / 8 KV heads of 128, vocabulary 128256, RoPE theta 500000 with Llama 3.1 scaling, gs 64), 2048
+random token ids prefilled in one engine_forward_batch with every row's logits, then 256 greedy engine_forward steps,
+against runq's engine on the CPU (the reference built from its sources: probe-int8).
+
+W8A8 requantizes every activation, so any change of FP32 order flips some roundings, and 32 layers of random weights
+carry those flips into the logits. The reference's own gate for such comparisons is statistical (rms 0.2, argmax
+0.9, max 16; docs/architecture.md:274, written for real checkpoints). On this random model the reference does not
+meet its own argmax bar against itself: its batched prefill against its per-token path gives rms 0.086 and argmax
+0.79 over the last 256 prompt positions (measured on the GPU box). So the test measures that floor on the same file
+and requires the engine to stay at it: every comparison within the rms and max bars of the gate, and within 1.25x the
+floor's rms and 0.08 (0.15 for the 64 decode rows) of its argmax agreement.
+
+Compared: our batched rows and our token-by-token replay of the prompt (last 256 positions) with each other and
+with the reference's batched and per-token rows; our first 64 greedy decode steps with the reference's per-token
+forwards of the same tokens (probe tail mode, tools/compare_engines.py --tail)."""
+import ctypes
+import os
+import shutil
+import sys
+import time
+
+import numpy as np
+import pytest
+
+import llama_hip as lh
+from llama_hip import checkpoint as ck
+from tests import hip_util as hu
+from tests import ref_probe as rp
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(dim=4096, hidden_dim=14336, n_layers=32, n_heads=32, n_kv_heads=8, vocab_size=128256, seq_len=8192,
+           rope_theta=500000.0, rope_type=1, rope_factor=8.0, rope_low=1.0, rope_high=4.0, rope_original=8192)
+PROMPT, DECODE, LAST, COMPARED = 2048, 256, 256, 64
+
+
+def say(*a):
+    print("[c5]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def scratch_dir(tmp_path):
+    """/dev/shm when it can hold the 8.5 GB file with room to spare (it is memory on the GPU box), else tmp_path."""
+    shm = "/dev/shm"
+    if os.path.isdir(shm) and shutil.disk_usage(shm).free > 40 << 30:
+        d = os.path.join(shm, f"llhip-c5-{os.getpid()}")
+        os.makedirs(d, exist_ok=True)
+        return d
+    return str(tmp_path)
+
+
+def at_floor(ref, got, floor, what, argmax_slack):
+    s = rp.gate_statistical(ref, got, what=what, rms_max=0.2, argmax_min=0.0, max_abs=16.0)
+    say(f"{what}: rms {s['rms']:.4f} argmax {s['argmax']:.3f} max {s['max_abs']:.3f}")
+    assert s["rms"] <= 1.25 * floor["rms"], (what, s, floor)
+    assert s["argmax"] >= floor["argmax"] - argmax_slack, (what, s, floor)
+
+
+def test_c5_8b_prefill_2048_then_256_greedy_steps(tmp_path):
+    if not rp.have("probe-int8"):
+        pytest.skip("oracle/_ref/probe-int8 not built (make -C oracle ref)")
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    d = scratch_dir(tmp_path)
+    path = os.path.join(d, "c5-8b-q8.bin")
+    model = lh.Model()
+    try:
+        t = time.time()
+        size = ck.write_q8_v3_normal(path, CFG, 64, seed=88172645463325252)
+        assert os.path.getsize(path) == size
+        say(f"wrote {size / 1e9:.2f} GB in {time.time() - t:.1f} s")
+        V = CFG["vocab_size"]
+        tokens = np.random.default_rng(2048).integers(0, V, PROMPT).astype(np.int32)
+        L.engine_load(ctypes.byref(model), path.encode())
+        assert model.implementation, lh.last_error()
+        assert model.config.seq_len == 4096 and L.engine_max_batch(ctypes.byref(model)) == PROMPT
+        t = time.time()
+        p = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens), PROMPT, 0, lh.LOGITS_ALL)
+        assert p, lh.last_error()
+        rows = np.ctypeslib.as_array(p, shape=(PROMPT, V))
+        assert np.isfinite(rows).all()
+        ours_batch, last_row = rows[-LAST:].copy(), rows[-1].copy()
+        say(f"prefill of {PROMPT} tokens with every row's logits in {time.time() - t:.2f} s")
+        # greedy decode from the prefill's last row
+        greedy, decode = [], []
+        logits = last_row
+        t = time.time()
+        for step in range(DECODE):
+            tok = int(np.argmax(logits))
+            greedy.append(tok)
+            p = L.engine_forward(ctypes.byref(model), tok, PROMPT + step)
+            assert p, (step, lh.last_error())
+            logits = np.ctypeslib.as_array(p, shape=(V,)).copy()
+            assert np.isfinite(logits).all(), step
+            if step < COMPARED:
+                decode.append(logits)
+        say(f"{DECODE} greedy steps in {time.time() - t:.2f} s; first tokens {greedy[:8]}")
+        assert all(0 <= g < V for g in greedy)
+        # LAST of the same batch is its ALL row
+        p = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens), PROMPT, 0, lh.LOGITS_LAST)
+        assert p and np.array_equal(np.ctypeslib.as_array(p, shape=(V,)), last_row)
+        # the prompt token by token (rewrites the cache rows in order)
+        t = time.time()
+        ours_tokens = np.empty((LAST, V), np.float32)
+        for pos in range(PROMPT):
+            p = L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos)
+            assert p, (pos, lh.last_error())
+            if pos >= PROMPT - LAST:
+                ours_tokens[pos - PROMPT + LAST] = np.ctypeslib.as_array(p, shape=(V,))
+        say(f"token-by-token replay in {time.time() - t:.2f} s")
+        L.engine_free(ctypes.byref(model))
+        # the reference on the CPU: its batched rows, and its per-token forwards of the last 256 prompt positions and
+        # of our first 64 greedy tokens after them
+        t = time.time()
+        ref_batch = rp.run("probe-int8", path, list(tokens), V, mode="batch", batch=256, timeout=900)[-LAST:].copy()
+        ref_tail = rp.run("probe-int8", path, list(tokens) + greedy[:COMPARED], V, mode="tail",
+                          tail=LAST + COMPARED, batch=256, timeout=900)
+        say(f"reference (CPU, {rp.threads()} threads): two 2048-token prefills and {LAST + COMPARED} per-token "
+            f"forwards in {time.time() - t:.1f} s")
+        ref_tokens, ref_decode = ref_tail[:LAST], ref_tail[LAST:]
+        floor = rp.compare(ref_tokens, ref_batch)[1]
+        say(f"reference batched against its per-token (the floor): rms {floor['rms']:.4f} argmax {floor['argmax']:.3f}")
+        at_floor(ours_tokens, ours_batch, floor, "our batched against our per-token", 0.08)
+        at_floor(ref_batch, ours_batch, floor, "our batched against the reference's batched", 0.08)
+        at_floor(ref_tokens, ours_tokens, floor, "our per-token against the reference's per-token", 0.08)
+        at_floor(ref_decode, np.stack(decode), floor, "our 64 greedy steps against the reference's", 0.15)
+    finally:
+        if model.implementation:
+            L.engine_free(ctypes.byref(model))
+        if os.path.exists(path):
+            os.unlink(path)
+        if d.startswith("/dev/shm/"):
+            shutil.rmtree(d, ignore_errors=True)
