@@ -76,6 +76,19 @@ void k_attention_batch(float *out, const float *q, const float *key_cache, const
 void k_attention_batch_layout(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
                               AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int pos0,
                               int m, size_t pos_stride, size_t head_base);
+/* No counterpart in the reference: k_attention_batch_layout for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It allocates nothing: its split-K partials live in
+ * a fixed per-device array of 4 Mi floats (16 MiB, located when llhip_init opens the device), not in the workspace the
+ * other forms grow on first use. Every buffer must be device memory or inside a registered range (host buffers would
+ * need the staging arena), the library must be initialized (llhip_init), and m rows of n_heads heads up to position
+ * pos0 + m - 1 must fit: m * n_heads * ((pos0 + m - 1) / 64 + 1) * ((head_dim + 5) & ~3) floats, at most 4 Mi
+ * (decode with 32 heads of 128 reaches position 63487). Anything else fails with a message. The results equal
+ * k_attention_batch_layout's bit for bit. Every call on a device shares its array, which keeps the last call's
+ * contents (every slot a call reads it writes first); calls ordered on the library's stream are safe, two that may
+ * run concurrently on one GPU (graphs replayed on other streams) race. */
+void k_attention_batch_layout_noalloc(float *out, const float *q, const float *key_cache, const float *value_cache,
+                                      float *att, AttentionWork *work, int n_heads, int n_kv_heads, int head_dim,
+                                      int seq_len, int pos0, int m, size_t pos_stride, size_t head_base);
 
 /* kernels.h:52-53, 168-179: the engine-facing K/V cache of one layer in the active layout (LLAMA_KV_LAYOUT=rows|head,
  * head-major by default), and k_attention / k_attention_batch on it. */

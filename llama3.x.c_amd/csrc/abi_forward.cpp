@@ -141,9 +141,11 @@ size_t cache_floats(int n_kv_heads, int head_dim, int last, size_t pos_stride, s
   return (size_t)last * pos_stride + (size_t)(n_kv_heads - 1) * head_base + (size_t)head_dim;
 }
 
+// noalloc: the partials go to the per-device scratch array instead of the grown workspace, and nothing may allocate
+// (no staging of host buffers, no device init).
 void attention(const char *name, float *out, const float *q, const float *key_cache, const float *value_cache,
                int n_heads, int n_kv_heads, int head_dim, int seq_len, int pos0, int m, size_t pos_stride,
-               size_t head_base) {
+               size_t head_base, bool noalloc = false) {
   if (m <= 0 || n_heads <= 0)
     return;
   if (!attention_shape_ok(n_heads, n_kv_heads, head_dim)) {
@@ -164,16 +166,36 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
     raise("%s: null buffer", name);
     return;
   }
+  const size_t partial_floats = attention_partial_floats(m, n_heads, head_dim, pos0 + m - 1);
+  if (noalloc) {
+    if (!device().ready) {
+      raise("%s: the library is not initialized on this device (call llhip_init first: opening the device "
+            "allocates)", name);
+      return;
+    }
+    if (partial_floats > kAttentionScratchFloats) {
+      raise("%s: %d rows of %d heads up to position %d need %zu floats of scratch; it holds %zu", name, m, n_heads,
+            pos0 + m - 1, partial_floats, kAttentionScratchFloats);
+      return;
+    }
+  }
   Call call(name, true); // a recorded RoPE with its cache stores may be taken along
   const size_t f = sizeof(float), row = (size_t)n_heads * head_dim * f;
   const size_t cache = cache_floats(n_kv_heads, head_dim, pos0 + m - 1, pos_stride, head_base) * f;
   Ref Q = call.in(q, row * m), K = call.in(key_cache, cache), V = call.in(value_cache, cache);
   Ref O = call.out(out, row * m, false);
+  if (noalloc && call.staged()) { // staging would allocate the arena
+    raise("%s: every buffer must be device memory or inside a registered range", name);
+    return;
+  }
   if (!call.ready())
     return;
-  float *partial = attention_partials(attention_partial_floats(m, n_heads, head_dim, pos0 + m - 1));
-  if (!partial)
+  float *partial = noalloc ? attention_scratch(device().ordinal) : attention_partials(partial_floats);
+  if (!partial) {
+    if (noalloc)
+      raise("%s: the attention scratch has no device address", name);
     return;
+  }
   AttentionJob job{call.ptr<float>(O), call.ptr<const float>(Q), call.ptr<const float>(K), call.ptr<const float>(V),
                    n_heads, n_kv_heads, head_dim, pos0, m, pos_stride, head_base, nullptr, nullptr, nullptr};
   // the fused form reads the caches, q and the new rows as 16-byte vectors
@@ -446,6 +468,14 @@ void k_attention_batch_layout(float *out, const float *q, const float *key_cache
   (void)att, (void)work;
   attention("k_attention_batch_layout", out, q, key_cache, value_cache, n_heads, n_kv_heads, head_dim, seq_len, pos0,
             m, pos_stride, head_base);
+}
+
+void k_attention_batch_layout_noalloc(float *out, const float *q, const float *key_cache, const float *value_cache,
+                                      float *att, AttentionWork *work, int n_heads, int n_kv_heads, int head_dim,
+                                      int seq_len, int pos0, int m, size_t pos_stride, size_t head_base) {
+  (void)att, (void)work;
+  attention("k_attention_batch_layout_noalloc", out, q, key_cache, value_cache, n_heads, n_kv_heads, head_dim, seq_len,
+            pos0, m, pos_stride, head_base, true);
 }
 
 void k_attention_kv(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,

@@ -212,6 +212,12 @@ bool launch_embed_rows(float *out, const int8_t *table, const float *scales, con
                        int gs, int vocab, hipStream_t stream);
 bool launch_embed_rows_f32(float *out, const float *table, const int *ids, int count, int dim, int vocab,
                            hipStream_t stream);
+// The allocation-free attention's partials (forward.hip): a file-scope device array of kAttentionScratchFloats floats
+// per device. attention_scratch_setup finds its device address on `ordinal` (current) once, at device init;
+// attention_scratch returns it (nullptr before).
+constexpr size_t kAttentionScratchFloats = size_t(4) << 20;
+bool attention_scratch_setup(int ordinal);
+float *attention_scratch(int ordinal);
 // Causal attention of `rows` query rows at positions pos0 .. pos0 + rows - 1 (q and out: rows x n_heads x head_dim);
 // position t of KV head g at key / value + t * pos_stride + g * head_base.
 struct AttentionJob {

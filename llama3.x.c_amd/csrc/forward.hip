@@ -556,6 +556,37 @@ bool launch_embed_rows_f32(float *out, const float *table, const int *ids, int c
   return launch_ok("embed_rows_f32");
 }
 
+// ---- the allocation-free attention's scratch --------------------------------------------------------------------
+//
+// k_attention_batch_layout_noalloc keeps its split-K partials here instead of in the grown workspace: 4 Mi floats
+// (16 MiB), one copy per device, held until the process ends. In host code `scratch` names a host-side stand-in, not
+// the device memory: the device address comes from hipGetSymbolAddress, once per device with that device current
+// (attention_scratch_setup, called when the library opens the device), and only that address reaches kernels.
+static __device__ __align__(256) float scratch[kAttentionScratchFloats];
+namespace {
+constexpr int kMaxOrdinals = 64;
+float *scratch_address[kMaxOrdinals] = {};
+} // namespace
+
+bool attention_scratch_setup(int ordinal) {
+  if (ordinal < 0 || ordinal >= kMaxOrdinals)
+    return raise("device ordinal %d: the attention scratch table holds %d devices", ordinal, kMaxOrdinals);
+  if (scratch_address[ordinal])
+    return true;
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return raise("locating the attention scratch on device %d failed: %s", ordinal, hipGetErrorString(e));
+  }
+  scratch_address[ordinal] = (float *)p;
+  return true;
+}
+
+float *attention_scratch(int ordinal) {
+  return ordinal >= 0 && ordinal < kMaxOrdinals ? scratch_address[ordinal] : nullptr;
+}
+
 int slot_floats(int head_dim) { return (head_dim + 2 + 3) & ~3; }
 
 size_t attention_partial_floats(int rows, int n_heads, int head_dim, int last_position) {

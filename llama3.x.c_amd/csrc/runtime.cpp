@@ -144,6 +144,8 @@ bool ensure_device() {
       !LLHIP_CHECK(hipMalloc((void **)&arrivals, LLHIP_SPLIT_SLOTS * sizeof(unsigned))) ||
       !LLHIP_CHECK(hipMemset(arrivals, 0, LLHIP_SPLIT_SLOTS * sizeof(unsigned))))
     return false;
+  if (!attention_scratch_setup(ordinal)) // the allocation-free attention's array: its address on this device
+    return false;
   the_device.split_partial = partial;
   the_device.split_count = arrivals;
   the_device.ordinal = ordinal;

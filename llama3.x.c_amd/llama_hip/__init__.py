@@ -146,6 +146,7 @@ _SIGNATURES = {
     "k_attention_layout": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, SZ, SZ]),
     "k_attention_batch": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, I32]),
     "k_attention_batch_layout": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, SZ, SZ]),
+    "k_attention_batch_layout_noalloc": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, SZ, SZ]),
     "k_attention_kv": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32]),
     "k_attention_batch_kv": (None, [P, P, P, P, P, P, I32, I32, I32, I32, I32, I32]),
     "kernels_attention_name": (ctypes.c_char_p, []),

@@ -1,0 +1,137 @@
+"""k_attention_batch_layout_noalloc, the attention entry point that allocates nothing (its split-K partials live in a
+fixed per-device array): equal bit for bit to k_attention_batch_layout on two calls in a row, the second smaller; no
+HBM claimed by the calls; replayable from a HIP graph captured around it; host buffers, an oversized call and an
+uninitialized library refused with a message."""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import llama_hip as lh
+from tests import hip_util as hu
+
+pytestmark = pytest.mark.gpu
+
+NH, NKV, HD, SEQ = 32, 8, 128, 4096  # Llama-3.1-8B heads
+SCRATCH_FLOATS = 4 << 20
+
+
+def head_major(rng, seq):
+    """Random K and V caches in the head-major layout ([kv_head][position][head_dim]) and their strides."""
+    k = rng.standard_normal((NKV, seq, HD), dtype=np.float32)
+    v = rng.standard_normal((NKV, seq, HD), dtype=np.float32)
+    return k, v, HD, seq * HD
+
+
+def run(L, name, out, q, k, v, pos0, m, ps, hb, seq=SEQ):
+    getattr(L, name)(lh.ptr(out), lh.ptr(q), lh.ptr(k), lh.ptr(v), None, None, NH, NKV, HD, seq, pos0, m, ps, hb)
+
+
+def test_noalloc_attention_equals_the_workspace_form():
+    L = hu.lib()
+    T = hu.torch()
+    assert L.llhip_init() == 0, lh.last_error()
+    rng = np.random.default_rng(31)
+    k, v, ps, hb = head_major(rng, SEQ)
+    kd, vd = hu.dev(k), hu.dev(v)
+    cases = [(1000, 16), (300, 1)]  # a 16-row batch, then a smaller call: one decode row
+    for pos0, m in cases:
+        assert m * NH * ((pos0 + m - 1) // 64 + 1) * 132 <= SCRATCH_FLOATS
+    outs = []
+    claimed = L.llhip_hbm_claimed()
+    for pos0, m in cases:
+        q = hu.dev(rng.standard_normal((m, NH * HD), dtype=np.float32))
+        out = hu.empty((m, NH * HD), T.float32)
+        run(L, "k_attention_batch_layout_noalloc", out, q, kd, vd, pos0, m, ps, hb)
+        L.llhip_synchronize()
+        assert not lh.last_error()
+        outs.append((q, hu.host(out)))
+    assert L.llhip_hbm_claimed() == claimed  # nothing allocated through the library
+    for (pos0, m), (q, got) in zip(cases, outs):
+        want = hu.empty((m, NH * HD), T.float32)
+        run(L, "k_attention_batch_layout", want, q, kd, vd, pos0, m, ps, hb)
+        assert np.array_equal(got, hu.host(want)), (pos0, m)
+        assert np.isfinite(got).all()
+
+
+def test_noalloc_attention_replays_from_a_graph():
+    """Captured once, replayed three times with eager work and synchronizations in between; every replay equals the
+    eager result."""
+    L = hu.lib()
+    T = hu.torch()
+    assert L.llhip_init() == 0, lh.last_error()
+    rng = np.random.default_rng(32)
+    k, v, ps, hb = head_major(rng, 2048)
+    kd, vd = hu.dev(k), hu.dev(v)
+    q = hu.dev(rng.standard_normal((1, NH * HD), dtype=np.float32))
+    eager = hu.empty((1, NH * HD), T.float32)
+    run(L, "k_attention_batch_layout_noalloc", eager, q, kd, vd, 2047, 1, ps, hb, seq=2048)
+    L.llhip_synchronize()
+    want = hu.host(eager)
+    out = hu.empty((1, NH * HD), T.float32)
+    assert L.llhip_graph_begin() == 0, lh.last_error()
+    run(L, "k_attention_batch_layout_noalloc", out, q, kd, vd, 2047, 1, ps, hb, seq=2048)
+    graph = L.llhip_graph_end()
+    assert graph, lh.last_error()
+    try:
+        for i in range(3):
+            out.zero_()
+            T.cuda.synchronize()
+            other = hu.empty((4, NH * HD), T.float32)  # eager work on the same array between replays
+            run(L, "k_attention_batch_layout_noalloc", other, hu.dev(rng.standard_normal((4, NH * HD),
+                                                                                          dtype=np.float32)),
+                kd, vd, 100, 4, ps, hb, seq=2048)
+            L.llhip_synchronize()
+            assert L.llhip_graph_launch(graph) == 0, lh.last_error()
+            L.llhip_synchronize()
+            assert np.array_equal(hu.host(out), want), i
+    finally:
+        L.llhip_graph_destroy(graph)
+
+
+def test_noalloc_attention_refusals():
+    L = hu.lib()
+    T = hu.torch()
+    assert L.llhip_init() == 0, lh.last_error()
+    rng = np.random.default_rng(33)
+    k, v, ps, hb = head_major(rng, 256)
+    kd, vd = hu.dev(k), hu.dev(v)
+    lh.record_failures()
+    try:
+        big = 2048
+        q = hu.empty((big, NH * HD), T.float32)
+        out = hu.empty((big, NH * HD), T.float32)
+        kb, vb = hu.empty((NKV, big, HD), T.float32), hu.empty((NKV, big, HD), T.float32)
+        run(L, "k_attention_batch_layout_noalloc", out, q, kb, vb, 0, big, HD, big * HD, seq=big)
+        assert "floats of scratch; it holds 4194304" in lh.last_error(), lh.last_error()
+        L.llhip_clear_error()
+        qh = rng.standard_normal((1, NH * HD), dtype=np.float32)  # host memory: staging would allocate
+        outh = np.zeros((1, NH * HD), np.float32)
+        run(L, "k_attention_batch_layout_noalloc", outh, qh, kd, vd, 10, 1, ps, hb, seq=256)
+        assert "every buffer must be device memory" in lh.last_error(), lh.last_error()
+        assert not outh.any()
+    finally:
+        L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+        L.llhip_clear_error()
+
+
+def test_noalloc_attention_needs_an_initialized_library():
+    """In a process whose library has not opened the device (torch has), the call refuses rather than open it."""
+    code = """
+import sys
+sys.path.insert(0, {pkg!r})
+import torch
+import llama_hip as lh
+L = lh.load()
+lh.record_failures()
+b = torch.zeros(8 * 64 * 128, device="cuda")
+torch.cuda.synchronize()
+p = b.data_ptr()
+L.k_attention_batch_layout_noalloc(p, p, p, p, None, None, 8, 8, 128, 64, 0, 1, 128, 64 * 128)
+print(lh.last_error())
+""".format(pkg=os.path.dirname(lh.LIB_PATH))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "the library is not initialized on this device" in r.stdout, r.stdout
