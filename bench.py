@@ -10,13 +10,15 @@ Alongside (`prefill`): the 8B INT8 W8A8 prefill of a 2048-token prompt: per laye
 int8-MFMA GEMMs (QKV, Wo + residual, W1/W3 SwiGLU, W2 + residual), then the last row's classifier GEMV.
 `forward_decode`: the whole 8B decode token on the device (the embedding row, the matmul set plus RMSNorm, RoPE, the K/V
 cache store and attention over 2048 cached positions), also from a HIP graph.
-`engine`: the Q8_0 engine end to end on a written synthetic 8B version-3 checkpoint: engine_forward per token (logits to
-the host) and engine_forward_batch of a 2048-token prompt (`--no-engine` skips it; `--engine` runs only it).
+`engine`: the engine end to end at the configuration of a Llama-3.1-8B Q8_0 forward (a version-3 checkpoint of
+random-init weights written to /dev/shm): a 2048-token prompt through engine_forward_batch, then 256 greedy
+engine_forward steps (`--no-engine` skips it; `--engine` runs only it).
 
 Weights ~N(0, 0.02) and activations ~N(0, 1) are drawn on the device (torch, seeded) and quantized by the library's
 own k_quantize rule; the data is synthetic. `roofline` is the dominant kernel of the decode step (the SwiGLU GEMV),
-its 32 launches captured into one graph and timed with HIP events on the library stream. `cpu_baseline` runs the reference's own gemm-bench
-(oracle/_ref, built from the reference's sources) on the same shapes on this host's cores.
+its 32 launches captured into one graph and timed with HIP events on the library stream. `cpu_baseline` runs the
+reference's own gemm-bench (oracle/_ref, built from the reference's sources) on this host's cores (one socket's
+physical cores, read with lscpu): its W8A8 GEMV on the decode shapes and its Q8 GEMM on the 2048-row prefill shapes.
 """
 import argparse
 import json
@@ -385,36 +387,89 @@ def prefill_3b(torch, lh, seed, steps=3):
     return out
 
 
-def cpu_baseline(threads, budget_s=30.0):
-    """The reference's own instrument, gemm-bench --gemv (tests/gemm_bench.c), on the five 8B decode shapes with cold
-    weights, scaled to one token (32 x the layer set + the classifier). Falls back to the oracle's threaded scalar GEMV
-    when the reference was not built here."""
+def host_topology():
+    """Sockets, physical cores per socket and logical CPUs of this host (lscpu), and the CPUs this process may use."""
+    topo = {"sockets": 1, "cores_per_socket": os.cpu_count() or 1, "threads_per_core": 1,
+            "logical_cpus": os.cpu_count() or 1, "model": "?"}
+    try:
+        out = subprocess.run(["lscpu", "-J"], capture_output=True, text=True, timeout=30).stdout
+        fields = {e["field"].rstrip(":"): e["data"] for e in json.loads(out)["lscpu"]}
+        topo.update(sockets=int(fields.get("Socket(s)", 1)), cores_per_socket=int(fields.get("Core(s) per socket", 1)),
+                    threads_per_core=int(fields.get("Thread(s) per core", 1)),
+                    logical_cpus=int(fields.get("CPU(s)", os.cpu_count() or 1)), model=fields.get("Model name", "?"))
+    except (OSError, ValueError, KeyError, subprocess.SubprocessError):
+        pass
+    try:
+        topo["usable_cpus"] = len(os.sched_getaffinity(0))
+    except AttributeError:
+        topo["usable_cpus"] = topo["logical_cpus"]
+    return topo
+
+
+def gemm_bench(exe, threads, args, timeout=600):
+    env = dict(os.environ, LLAMA_THREADS=str(threads), LLAMA_BACKEND="teams", LLAMA_KERNELS="auto")
+    r = subprocess.run([exe] + args, env=env, capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError(f"gemm-bench failed ({r.returncode}): {r.stderr[-500:]}")
+    return [json.loads(line) for line in r.stdout.splitlines() if line.startswith("{")]
+
+
+def cpu_baseline(threads=None, budget_s=30.0):
+    """The reference's own instrument, gemm-bench (tests/gemm_bench.c, built from its sources into oracle/_ref), on
+    this host's cores, as BASELINE.md plans it: the W8A8 GEMV on the five 8B decode shapes with cold weights, scaled
+    to one token (32 x the layer set + the classifier), and the W8A8 Q8 GEMM at m = 2048 on the four 8B prefill
+    shapes, scaled to a 2048-token prompt (32 x the layer; the activation quantization it reports is added). Threads:
+    one socket's physical cores (the reference's single-socket configuration), capped by the CPUs this process may
+    use. Falls back to the oracle's threaded scalar GEMV when the reference was not built here."""
+    topo = host_topology()
+    if threads is None:
+        threads = max(1, min(topo["cores_per_socket"], topo["usable_cpus"]))
+    host = {k: topo[k] for k in ("model", "sockets", "cores_per_socket", "threads_per_core", "logical_cpus",
+                                 "usable_cpus")}
     exe = os.path.join(ROOT, "oracle", "_ref", "gemm-bench")
     shapes = [(DIM, DIM), (KV_DIM, DIM), (HIDDEN, DIM), (DIM, HIDDEN), (VOCAB, DIM)]
     per_token = {(DIM, DIM): 2 * LAYERS, (KV_DIM, DIM): 2 * LAYERS, (HIDDEN, DIM): 2 * LAYERS, (DIM, HIDDEN): LAYERS,
                  (VOCAB, DIM): 1}
     if os.path.exists(exe):
-        env = dict(os.environ, LLAMA_THREADS=str(threads), LLAMA_KERNELS="auto")
         reps = 100  # about 10 s of wall time on 16 host threads
-        cmd = [exe, "--kernel", "q8", "--gemv", "--m", "1", "--reps", str(reps), "--cold-mib", "1200", "--shapes",
-               ",".join(f"{n}x{k}" for n, k in shapes)]
         t0 = time.time()
-        r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
-        if r.returncode == 0:
-            med = {}
-            isa = "?"
-            for line in r.stdout.splitlines():
-                rec = json.loads(line)
-                if rec["kernel"] == "gemv_rows_q8":
-                    med[(rec["n"], rec["k"])] = rec["median_s"]
-                    isa = rec["isa"]
-            token_s = sum(med[s] * c for s, c in per_token.items())
-            return {"value": round(1.0 / token_s, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-                    "sample": f"reference gemm-bench --kernel q8 --gemv (isa {isa}, {threads} threads, {reps} reps, cold "
-                              f"copies over 1200 MiB) on the 8B shapes 4096x4096, 1024x4096, 14336x4096, 4096x14336, "
-                              f"128256x4096; per-token time = 32 x (2 wq/wo + 2 wk/wv + 2 w1/w3 + w2) + classifier "
-                              f"= {token_s * 1e3:.2f} ms; wall {time.time() - t0:.1f} s",
-                    "weight_gbs": round(7973699584 / token_s / 1e9, 1)}
+        med, isa = {}, "?"
+        for rec in gemm_bench(exe, threads, ["--kernel", "q8", "--gemv", "--m", "1", "--reps", str(reps),
+                                             "--cold-mib", "1200", "--shapes", ",".join(f"{n}x{k}" for n, k in shapes)]):
+            if rec["kernel"] == "gemv_rows_q8":
+                med[(rec["n"], rec["k"])] = rec["median_s"]
+                isa = rec["isa"]
+        token_s = sum(med[sh] * c for sh, c in per_token.items())
+        decode_wall = time.time() - t0
+        # prefill: the Q8 GEMM of a 2048-row batch on QKV (6144 x 4096), Wo, W1 and W3 (14336 x 4096 each), W2
+        t0 = time.time()
+        pre_shapes = [(DIM + 2 * KV_DIM, DIM), (DIM, DIM), (HIDDEN, DIM), (DIM, HIDDEN)]
+        per_layer = {(DIM + 2 * KV_DIM, DIM): 1, (DIM, DIM): 1, (HIDDEN, DIM): 2, (DIM, HIDDEN): 1}
+        gmed, quant = {}, {}
+        for rec in gemm_bench(exe, threads, ["--kernel", "q8", "--m", str(PROMPT), "--reps", "3", "--shapes",
+                                             ",".join(f"{n}x{k}" for n, k in pre_shapes)]):
+            if rec["kernel"] == "gemm_q8":
+                gmed[(rec["n"], rec["k"])] = rec["median_s"]
+                quant[(rec["n"], rec["k"])] = rec.get("quant_median_s", 0.0)
+                impl = rec.get("impl", "?")
+        # per layer the rows are quantized before QKV, Wo, W1/W3 (once for both) and W2
+        layer_s = sum(gmed[sh] * c for sh, c in per_layer.items()) + sum(quant[sh] for sh in pre_shapes)
+        prompt_s = LAYERS * layer_s + med[(VOCAB, DIM)]  # plus the last row's classifier GEMV
+        ops = 2 * PROMPT * LAYERS * sum(n * k * c for (n, k), c in per_layer.items())
+        return {"value": round(1.0 / token_s, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+                "sample": f"reference gemm-bench --kernel q8 --gemv (isa {isa}, {threads} threads, {reps} reps, cold "
+                          f"copies over 1200 MiB) on the 8B shapes 4096x4096, 1024x4096, 14336x4096, 4096x14336, "
+                          f"128256x4096; per-token time = 32 x (2 wq/wo + 2 wk/wv + 2 w1/w3 + w2) + classifier "
+                          f"= {token_s * 1e3:.2f} ms; wall {decode_wall:.1f} s",
+                "weight_gbs": round(7973699584 / token_s / 1e9, 1),
+                "prefill": {"value": round(PROMPT / prompt_s, 2), "unit": "tok/s", "tops": round(ops / prompt_s / 1e12, 3),
+                            "sample": f"reference gemm-bench --kernel q8 --m {PROMPT} ({impl}, {threads} threads, 3 "
+                                      f"reps) on 6144x4096, 4096x4096, 14336x4096, 4096x14336; per prompt 32 x "
+                                      f"(QKV + Wo + 2 x W1/W3 + W2 + the row quantizations) + the last row's "
+                                      f"classifier = {prompt_s:.2f} s; wall {time.time() - t0:.1f} s"},
+                "host": host,
+                "cores_note": "one socket's physical cores" + (" = all host cores" if threads == topo["logical_cpus"]
+                                                               else f" of {topo['logical_cpus']} host CPUs")}
     # fallback: the oracle's scalar GEMV on one 4096x4096 matrix, threaded, scaled to a token by bytes
     import numpy as np
 
@@ -433,70 +488,83 @@ def cpu_baseline(threads, budget_s=30.0):
         reps += 1
     per_call = (time.time() - t0) / reps
     token_s = per_call * 7973699584 / weight_bytes(DIM, DIM)
-    return {"value": round(1.0 / token_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+    return {"value": round(1.0 / token_s, 3), "unit": "tok/s", "cores": threads, "kind": "port", "host": host,
             "sample": f"oracle scalar Q8 GEMV 4096x4096 x{reps}, {threads} threads, scaled to the 8B token by bytes"}
 
 
-def engine_bench(lh, L, args, steps=None, warmup=None, prompts=None):
-    """The engine end to end (engine_load + engine_forward, logits to the host every token) on a synthetic untied
-    Llama-3.1-8B version-3 Q8_0 checkpoint written to $TMPDIR: tokens at positions 0 .. warmup + steps - 1, timed on
-    the host clock (engine_forward returns after the logits have arrived), then engine_forward_batch of a 2048-token
-    prompt. Returns the result object."""
-    steps = args.steps if steps is None else steps
-    warmup = args.warmup if warmup is None else warmup
+def engine_bench(lh, L, args, prompts=None):
+    """The engine end to end at the configuration of a Llama-3.1-8B Q8_0 forward: a version-3 checkpoint of random-init
+    weights (~N(0, 0.02), RMSNorm weights 1.0, untied classifier, RoPE theta 500000 with Llama 3.1 scaling) written to
+    /dev/shm (or $TMPDIR), a 2048-token prompt of random ids through engine_forward_batch (the last row's logits),
+    then 256 greedy engine_forward steps from position 2048 (logits to the host and their argmax every step), timed on
+    the host clock. Returns the result object; a failure names its stage."""
     prompts = args.prefill_steps if prompts is None else prompts
+    decode_steps = 256
     import ctypes
+    import shutil
     import tempfile
 
     import numpy as np
 
     from llama_hip import checkpoint as ck
     cfg = dict(dim=DIM, hidden_dim=HIDDEN, n_layers=LAYERS, n_heads=N_HEADS, n_kv_heads=N_KV_HEADS, vocab_size=VOCAB,
-               seq_len=CONTEXT, rope_theta=500000.0, rope_type=1, rope_factor=8.0, rope_low=1.0, rope_high=4.0,
+               seq_len=8192, rope_theta=500000.0, rope_type=1, rope_factor=8.0, rope_low=1.0, rope_high=4.0,
                rope_original=8192)
-    with tempfile.TemporaryDirectory() as tmp:
-        path = os.path.join(tmp, "llama8b_q8_synthetic.bin")
-        t0 = time.time()
-        ck.write_random_q8_v3(path, cfg, GS, args.seed, shared=False)
-        print(f"# wrote {os.path.getsize(path) / 1e9:.2f} GB checkpoint in {time.time() - t0:.1f} s", file=sys.stderr,
-              flush=True)
+    base = "/dev/shm" if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > 40 << 30 else None
+    stage = "write"
+    with tempfile.TemporaryDirectory(dir=base) as tmp:
+        path = os.path.join(tmp, "llama8b_q8_normal.bin")
         model = lh.Model()
-        t0 = time.time()
-        L.engine_load(ctypes.byref(model), path.encode())
-        print(f"# engine_load (map + upload to HBM) {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
-        rng = np.random.default_rng(args.seed)
-        tokens = rng.integers(0, VOCAB, warmup + steps)
-        for pos in range(warmup):
-            assert L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos), lh.last_error()
-        t0 = time.perf_counter()
-        for pos in range(warmup, warmup + steps):
-            out = L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos)
-        sec = (time.perf_counter() - t0) / steps
-        assert out, lh.last_error()
-        logits = np.ctypeslib.as_array(out, shape=(VOCAB,))
-        assert np.isfinite(logits).all()
-        # prefill: a 2048-token prompt from position 0 through engine_forward_batch, the last row's logits
-        prompt = rng.integers(0, VOCAB, CONTEXT).astype(np.int32)
-        pptr = prompt.ctypes.data_as(ctypes.c_void_p)
-        assert L.engine_forward_batch(ctypes.byref(model), pptr, CONTEXT, 0, lh.LOGITS_LAST), lh.last_error()
-        t0 = time.perf_counter()
-        for _ in range(prompts):
-            out = L.engine_forward_batch(ctypes.byref(model), pptr, CONTEXT, 0, lh.LOGITS_LAST)
-        psec = (time.perf_counter() - t0) / prompts
-        assert out and np.isfinite(np.ctypeslib.as_array(out, shape=(VOCAB,))).all(), lh.last_error()
-        print(f"# engine prefill: {CONTEXT} tokens in {psec * 1e3:.2f} ms, {CONTEXT / psec:.0f} tok/s", file=sys.stderr,
-              flush=True)
-        L.engine_free(ctypes.byref(model))
+        try:
+            t0 = time.time()
+            ck.write_q8_v3_normal(path, cfg, GS, args.seed)
+            print(f"# wrote {os.path.getsize(path) / 1e9:.2f} GB checkpoint in {time.time() - t0:.1f} s",
+                  file=sys.stderr, flush=True)
+            stage = "load"
+            t0 = time.time()
+            L.engine_load(ctypes.byref(model), path.encode())
+            assert model.implementation, lh.last_error()
+            print(f"# engine_load (map + upload to HBM) {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
+            stage = "prefill"
+            rng = np.random.default_rng(args.seed)
+            prompt = rng.integers(0, VOCAB, PROMPT).astype(np.int32)
+            pptr = prompt.ctypes.data_as(ctypes.c_void_p)
+            out = L.engine_forward_batch(ctypes.byref(model), pptr, PROMPT, 0, lh.LOGITS_LAST)  # warm-up
+            assert out, lh.last_error()
+            t0 = time.perf_counter()
+            for _ in range(prompts):
+                out = L.engine_forward_batch(ctypes.byref(model), pptr, PROMPT, 0, lh.LOGITS_LAST)
+            psec = (time.perf_counter() - t0) / prompts
+            assert out, lh.last_error()
+            logits = np.ctypeslib.as_array(out, shape=(VOCAB,)).copy()
+            assert np.isfinite(logits).all()
+            print(f"# engine prefill: {PROMPT} tokens in {psec * 1e3:.2f} ms, {PROMPT / psec:.0f} tok/s",
+                  file=sys.stderr, flush=True)
+            stage = "decode"
+            t0 = time.perf_counter()
+            for step in range(decode_steps):
+                out = L.engine_forward(ctypes.byref(model), int(np.argmax(logits)), PROMPT + step)
+                assert out, lh.last_error()
+                logits = np.ctypeslib.as_array(out, shape=(VOCAB,))
+            sec = (time.perf_counter() - t0) / decode_steps
+            assert np.isfinite(logits).all()
+            print(f"# engine decode: {decode_steps} greedy steps at positions {PROMPT}..{PROMPT + decode_steps - 1}, "
+                  f"{sec * 1e3:.3f} ms/token, {1.0 / sec:.1f} tok/s", file=sys.stderr, flush=True)
+        except Exception as e:
+            raise RuntimeError(f"engine {stage}: {e}") from e
+        finally:
+            if model.implementation:
+                L.engine_free(ctypes.byref(model))
     return {"metric": "8B Q8_0 engine decode tok/s (engine_forward, logits to host)",
-                      "value": round(1.0 / sec, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps,
-                      "warmup": warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True,
-                      "scaling": "weak", "vs_baseline": None, "dtype": "int8 W8A8", "data": "synthetic",
-                      "config": {"workload": f"Llama-3.1-8B Q8_0 version-3 checkpoint (random int8 weights, untied "
-                                             f"classifier), decode at positions {warmup}.."
-                                             f"{warmup + steps - 1}, cache of {CONTEXT}"},
-                      "prefill": {"value": round(CONTEXT / psec, 1), "unit": "tok/s", "ms_per_prompt": round(psec * 1e3, 3),
-                                  "workload": f"engine_forward_batch of a {CONTEXT}-token prompt from position 0, "
-                                              "last row's logits"}}
+            "value": round(1.0 / sec, 2), "unit": "tok/s", "n_gpus": 1, "steps": decode_steps, "warmup": 0,
+            "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8 W8A8", "data": "synthetic",
+            "config": {"workload": f"Llama-3.1-8B Q8_0 version-3 checkpoint of random-init weights (~N(0, 0.02), "
+                                   f"norms 1, untied), {decode_steps} greedy engine_forward steps at positions "
+                                   f"{PROMPT}..{PROMPT + decode_steps - 1} after the prompt, logits to the host"},
+            "prefill": {"value": round(PROMPT / psec, 1), "unit": "tok/s", "ms_per_prompt": round(psec * 1e3, 3),
+                        "workload": f"engine_forward_batch of a {PROMPT}-token prompt of random ids from position 0, "
+                                    f"the last row's logits"}}
 
 
 def main():
@@ -507,7 +575,8 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=None,
+                    help="threads of the CPU baseline (default: one socket's physical cores, as lscpu reports them)")
     ap.add_argument("--seed", type=int, default=88172645463325252 % (1 << 31))
     ap.add_argument("--no-c3", action="store_true",
                     help="skip the FP32 / BF16 prefill GEMMs on the Llama-3.2-3B shapes (512 tokens)")
@@ -652,11 +721,11 @@ def main():
     if not args.no_c3:
         result["prefill_3b"] = prefill_3b(torch, lh, args.seed)
     if not args.no_engine:
-        # the engine end to end (engine_load of a written 8B checkpoint, engine_forward, engine_forward_batch); its
-        # failure (say, no room for the 8.5 GB file) is reported here and leaves the line above intact
+        # the engine end to end (engine_load of a written 8B checkpoint, engine_forward_batch, engine_forward); its
+        # failure (say, no room for the 8.5 GB file) is reported here with its stage and leaves the line above intact
         lh.record_failures()  # a library failure returns with its message instead of ending the process
         try:
-            eng = engine_bench(lh, L, args, steps=64, warmup=4, prompts=2)
+            eng = engine_bench(lh, L, args, prompts=2)
             result["engine"] = {"decode": {"value": eng["value"], "unit": "tok/s", "ms_per_token": eng["ms_per_step"],
                                            "workload": eng["config"]["workload"]},
                                 "prefill": eng["prefill"]}
