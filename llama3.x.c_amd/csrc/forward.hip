@@ -16,6 +16,8 @@
 
 #include "common.h"
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 namespace llhip {
 namespace {
 
@@ -337,6 +339,146 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
   }
 }
 
+// Batched attention on the FP32 matrix cores (flash form): block (tile of 128 / kv_mul query rows, KV head g), the
+// tile's 128 query vectors (row j, query head h of the group: vector j * kv_mul + h) in 8 waves of 16. The block walks
+// the 64-position chunks its rows reach; per chunk it stages the K and V rows in LDS (row stride HD + 4 floats, zero
+// past the last position), and each wave
+//   - scores its 16 vectors against the 64 positions on v_mfma_f32_16x16x4_f32, as S^T = K Q^T: four 16-position
+//     tiles, HD / 4 MFMAs each; the dot's terms go in a permuted order (MFMA step kk, lane group q takes dimension
+//     q * HD / 4 + kk), so a lane's share of its query vector is HD / 4 consecutive floats held in registers and its
+//     K reads are 16-byte runs;
+//   - masks the positions past each row's own (causal), takes the chunk maximum and the running maximum, rescales
+//     its running sum and value sums by exp(m_old - m_new), and forms p = exp(s - m_new);
+//   - adds P V to its value sums as O^T = V^T P^T: the score accumulators are the B operand as they stand (MFMA step
+//     (tile t, element e) takes positions 16 t + 4 q + e from lane group q), and V^T is read from LDS.
+// At the end each vector's value sum is divided by its running sum and stored. Every product is FP32 on the matrix
+// cores; the sums run in other orders than the split form's, within FP32 rounding of the same softmax.
+template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(AttnParams p) {
+  constexpr int kSt = HD + 4;      // LDS row stride of a staged K or V row
+  constexpr int kQ = HD / 4;       // dimensions per lane group in the score MFMAs
+  constexpr int kDt = HD / 16;     // 16-dimension tiles of the value sums
+  constexpr int kQv = 128;         // query vectors per block
+  extern __shared__ __align__(16) float lds[];
+  float *ks = lds, *vs = lds + kChunk * kSt;
+  const int kv_mul = p.n_heads / p.n_kv_heads, tile_rows = kQv / kv_mul;
+  const int ntiles = (p.rows + tile_rows - 1) / tile_rows;
+  const int tile = ntiles - 1 - (int)blockIdx.x; // the longest (latest) tiles first
+  const int g = blockIdx.y, r0 = tile * tile_rows;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int lq = lane >> 4, lc = lane & 15;
+  const int qv = wave * 16 + lc, j = qv / kv_mul, h = qv % kv_mul, row = r0 + j;
+  const bool active = row < p.rows;
+  const int pos = p.pos0 + (active ? row : 0);            // this lane's query row's position
+  const int wave_last = p.pos0 + min(r0 + (wave * 16 + 15) / kv_mul, p.rows - 1);
+  const int last = p.pos0 + min(r0 + tile_rows, p.rows) - 1; // the tile's last position
+  const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
+  // this lane's dimensions lq * HD / 4 .. + HD / 4 of its query vector
+  float qr[kQ];
+  {
+    const float *src = p.q + ((size_t)(active ? row : 0) * p.n_heads + (size_t)g * kv_mul + h) * HD + lq * kQ;
+#pragma unroll
+    for (int i = 0; i < kQ; i += 4) {
+      const float4 v = active ? *reinterpret_cast<const float4 *>(src + i) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      qr[i] = v.x, qr[i + 1] = v.y, qr[i + 2] = v.z, qr[i + 3] = v.w;
+    }
+  }
+  v4f o[kDt];
+#pragma unroll
+  for (int d = 0; d < kDt; d++)
+    o[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = -FLT_MAX, l_run = 0.0f;
+  bool bad = false;
+  const int chunks = last / kChunk + 1;
+  for (int c = 0; c < chunks; c++) {
+    const int t0 = c * kChunk;
+    __syncthreads(); // the previous chunk's rows are read
+    for (int i = threadIdx.x; i < kChunk * (HD / 4); i += kTileThreads) {
+      const int t = i / (HD / 4), d4 = i % (HD / 4);
+      float4 kv = float4{0.0f, 0.0f, 0.0f, 0.0f}, vv = kv;
+      if (t0 + t <= last) {
+        const size_t at = (size_t)(t0 + t) * p.pos_stride + 4 * d4;
+        kv = *reinterpret_cast<const float4 *>(kbase + at);
+        vv = *reinterpret_cast<const float4 *>(vbase + at);
+      }
+      *reinterpret_cast<float4 *>(ks + t * kSt + 4 * d4) = kv;
+      *reinterpret_cast<float4 *>(vs + t * kSt + 4 * d4) = vv;
+    }
+    __syncthreads();
+    if (t0 > wave_last)
+      continue; // no row of this wave reaches the chunk (wave-uniform)
+    // S^T: position 16 t + 4 lq + e (t = 0..3, e = 0..3) against this lane's query vector
+    v4f sc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      sc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const float *kr = ks + (16 * t + lc) * kSt + lq * kQ;
+#pragma unroll
+      for (int i = 0; i < kQ; i += 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(kr + i);
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qr[i], sc[t], 0, 0, 0);
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qr[i + 1], sc[t], 0, 0, 0);
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qr[i + 2], sc[t], 0, 0, 0);
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qr[i + 3], sc[t], 0, 0, 0);
+      }
+    }
+    // causal mask, the chunk maximum over the vector's 64 positions (16 here, the rest in lanes lc + 16, 32, 48)
+    float cmax = -FLT_MAX;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int at = t0 + 16 * t + 4 * lq + e;
+        const bool live = active && at <= pos;
+        float s = -FLT_MAX;
+        if (live) {
+          s = sc[t][e] / p.divisor;
+          bad |= !isfinite(s);
+        }
+        sc[t][e] = s;
+        cmax = fmaxf(cmax, s);
+      }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+    const float m_new = fmaxf(m_run, cmax);
+    const float alpha = expf(m_run - m_new); // 0 before the first live position, 1 when the maximum stays
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float pe = sc[t][e] > -FLT_MAX ? expf(sc[t][e] - m_new) : 0.0f;
+        sc[t][e] = pe;
+        psum += pe;
+      }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    // O^T += V^T P^T: dimension 16 d + lc, positions 16 t + 4 lq + e
+#pragma unroll
+    for (int d = 0; d < kDt; d++) {
+      o[d] *= alpha;
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vs[(16 * t + 4 * lq + e) * kSt + 16 * d + lc], sc[t][e], o[d],
+                                                      0, 0, 0);
+    }
+  }
+  if (bad)
+    p.flags[1] = 1;
+  if (!active)
+    return;
+  // lane (lq, lc) holds dimensions 16 d + 4 lq + e of vector lc
+  const float inv = 1.0f / l_run;
+  float *dst = p.out + ((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * HD;
+#pragma unroll
+  for (int d = 0; d < kDt; d++)
+    *reinterpret_cast<float4 *>(dst + 16 * d + 4 * lq) =
+        float4{o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv};
+}
+
 // Block (chunk c, KV head g, query row r). Waves take positions t0 + w, t0 + w + 4, ...: lane l holds dimensions
 // l, l + 64, ... of the K row, dots it with each query head of the group held the same way, and the wave sum over the
 // lanes gives the score, (dot) / sqrtf(head_dim) like the reference. Then per head the chunk maximum, the
@@ -639,6 +781,28 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
                        ((uintptr_t)job.q & 15) == 0 && ((uintptr_t)job.key & 15) == 0;
   if (job.table && !aligned)
     return raise("internal: a fused RoPE attention on operands the aligned kernel does not take");
+  // batches of at least 16 rows with 64 or 128 dimensions per head: the flash kernel on the matrix cores, no merge
+  const bool flash = !job.table && aligned && job.rows >= 16 && (job.head_dim == 64 || job.head_dim == 128) &&
+                     128 % kv_mul == 0 && ((uintptr_t)job.out & 15) == 0 && ((uintptr_t)job.value & 15) == 0;
+  if (flash) {
+    static const hipError_t flash_allowed = [] {
+      const hipError_t e = hipFuncSetAttribute((const void *)attn_flash<128>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kChunk * 132 * 4);
+      return e != hipSuccess ? e
+                             : hipFuncSetAttribute((const void *)attn_flash<64>,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kChunk * 68 * 4);
+    }();
+    if (flash_allowed != hipSuccess)
+      return raise("allowing the attention kernel its LDS failed: %s", hipGetErrorString(flash_allowed));
+    const int tile_rows = 128 / kv_mul;
+    const dim3 grid((unsigned)((job.rows + tile_rows - 1) / tile_rows), (unsigned)job.n_kv_heads);
+    const size_t lds = 2 * (size_t)kChunk * (job.head_dim + 4) * sizeof(float);
+    if (job.head_dim == 128)
+      hipLaunchKernelGGL(attn_flash<128>, grid, dim3(kTileThreads), lds, stream, p);
+    else
+      hipLaunchKernelGGL(attn_flash<64>, grid, dim3(kTileThreads), lds, stream, p);
+    return launch_ok("attn_flash");
+  }
   if (aligned) {
     p.tile_rows = attention_tile_rows(job.rows, kv_mul, job.head_dim);
     const size_t lds = attention_tile_lds(p.tile_rows, kv_mul, job.head_dim);

@@ -240,6 +240,56 @@ def test_attention_batch_rows(nh, nkv, hd, seq, pos0, m):
         assert np.all(np.abs(got.reshape(-1) - g["attbatch/out"]) <= 2e-5 * np.abs(vc).max() + 1e-6)
 
 
+@pytest.mark.parametrize("nh,nkv,hd,seq,pos0,m,layout", [
+    (32, 8, 128, 2100, 0, 2048, "head"),   # the 8B prompt (rows sampled below)
+    (16, 16, 64, 300, 7, 200, "rows"),     # kv_mul 1: 128-row tiles
+    (16, 8, 128, 400, 130, 77, "head"),    # kv_mul 2, a ragged last tile
+    (32, 4, 64, 260, 64, 96, "rows"),      # kv_mul 8: 16-row tiles, starting on a chunk boundary
+    (64, 4, 128, 200, 33, 50, "head"),     # kv_mul 16: 8-row tiles
+    (8, 2, 128, 1500, 1400, 16, "rows"),   # 16 rows, 23 chunks each
+])
+def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout):
+    """Batches of at least 16 rows with 64 or 128 dimensions per head run the flash kernel on the FP32 matrix cores:
+    every checked row within the float64 budget of the decode attention at its position and within twice it of the
+    oracle, for GQA ratios 1-16, both layouts, ragged tiles and long contexts."""
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 900 + m + hd)
+    kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(m * nh * hd, 0, 1)
+    ps, hb = orc.kv_strides(nkv, hd, seq, layout == "head")
+    dq, dk, dv, do = hu.dev(q), hu.dev(kc), hu.dev(vc), hu.empty(m * nh * hd, hu.torch().float32)
+    L.k_attention_batch_layout(lh.ptr(do), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), None, None, nh, nkv, hd, seq, pos0, m,
+                               ps, hb)
+    got = hu.host(do).reshape(m, -1)
+    assert not lh.last_error()
+    rows = range(m) if m <= 200 else sorted({0, 1, 63, 64, 127, 128, 1000, m - 2, m - 1})
+    for i in rows:
+        check_attention(got[i], q.reshape(m, -1)[i], kc, vc, nh, nkv, hd, seq, pos0 + i, ps, hb, f"row {i}")
+
+
+def test_attention_flash_nonfinite_score_fails():
+    L = hu.lib()
+    lh.record_failures()
+    try:
+        nh, nkv, hd, seq, m = 8, 2, 64, 40, 20
+        rng = orc.Rng(orc.SEED + 909)
+        kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(m * nh * hd, 0, 1)
+        kc[15 * nkv * hd + 70] = np.inf  # position 15, KV head 1
+        dq, dk, dv, do = hu.dev(q), hu.dev(kc), hu.dev(vc), hu.empty(m * nh * hd, hu.torch().float32)
+        L.k_attention_batch(lh.ptr(do), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), None, None, nh, nkv, hd, seq, 10, m)
+        L.llhip_synchronize()
+        assert "nonfinite value in softmax" in lh.last_error()
+        L.llhip_clear_error()
+        L.k_attention_batch(lh.ptr(do), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), None, None, nh, nkv, hd, seq, 0, 15)
+        L.llhip_synchronize()  # rows 0..14 stop before position 15: the split kernel (15 rows), no failure
+        assert lh.last_error() == ""
+        L.k_attention_batch(lh.ptr(do), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), None, None, nh, nkv, hd, seq, 0, 16)
+        L.llhip_synchronize()  # row 15 reaches it: the flash kernel's failure
+        assert "nonfinite value in softmax" in lh.last_error()
+    finally:
+        L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+        L.llhip_clear_error()
+
+
 def test_attention_nonfinite_score_fails_and_bookkeeping():
     L = hu.lib()
     lh.record_failures()
