@@ -339,10 +339,12 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
   }
 }
 
-// Batched attention on the FP32 matrix cores (flash form): block (tile of 128 / kv_mul query rows, KV head g), the
-// tile's 128 query vectors (row j, query head h of the group: vector j * kv_mul + h) in 8 waves of 16. The block walks
-// the 64-position chunks its rows reach; per chunk it stages the K and V rows in LDS (row stride HD + 4 floats, zero
-// past the last position), and each wave
+// Batched attention on the FP32 matrix cores (flash form): query rows in tiles of 128 / kv_mul (the tile's 128 query
+// vectors: row j, query head h of the group as vector j * kv_mul + h, in 8 waves of 16). Block (p, KV head g) takes
+// tile T - 1 - p and then tile p, so every block has about the same number of causal chunks (one block per CU). Per
+// tile it walks the 64-position chunks the tile's rows reach, the K and V rows of a chunk staged in LDS (row stride
+// HD + 4 floats, zero past the last position), double-buffered: the next chunk's loads are in flight while the
+// current one is computed, one barrier per chunk. Each wave
 //   - scores its 16 vectors against the 64 positions on v_mfma_f32_16x16x4_f32, as S^T = K Q^T: four 16-position
 //     tiles, HD / 4 MFMAs each; the dot's terms go in a permuted order (MFMA step kk, lane group q takes dimension
 //     q * HD / 4 + kk), so a lane's share of its query vector is HD / 4 consecutive floats held in registers and its
@@ -350,133 +352,181 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
 //   - masks the positions past each row's own (causal), takes the chunk maximum and the running maximum, rescales
 //     its running sum and value sums by exp(m_old - m_new), and forms p = exp(s - m_new);
 //   - adds P V to its value sums as O^T = V^T P^T: the score accumulators are the B operand as they stand (MFMA step
-//     (tile t, element e) takes positions 16 t + 4 q + e from lane group q), and V^T is read from LDS.
+//     (tile t, element e) takes positions 16 t + 4 q + e from lane group q), and V^T is read from LDS, value tile d
+//     holding dimensions HD / 16 * m + d (m = 0..15), so a lane's values of a position are consecutive.
 // At the end each vector's value sum is divided by its running sum and stored. Every product is FP32 on the matrix
 // cores; the sums run in other orders than the split form's, within FP32 rounding of the same softmax.
+template <int HD> struct FlashStage {
+  static constexpr int kPer = kChunk * (HD / 4) / kTileThreads; // float4 of K (and of V) per thread and chunk
+  float4 k[kPer], v[kPer];
+  // the chunk at t0 of KV head rows kbase / vbase, zero past `last`
+  __device__ __forceinline__ void load(const AttnParams &p, const float *kbase, const float *vbase, int t0, int last) {
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+      const int i = threadIdx.x + u * kTileThreads, t = i / (HD / 4), d4 = i % (HD / 4);
+      k[u] = v[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t0 + t <= last) {
+        const size_t at = (size_t)(t0 + t) * p.pos_stride + 4 * d4;
+        k[u] = *reinterpret_cast<const float4 *>(kbase + at);
+        v[u] = *reinterpret_cast<const float4 *>(vbase + at);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float *ks, float *vs) const {
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+      const int i = threadIdx.x + u * kTileThreads, t = i / (HD / 4), d4 = i % (HD / 4);
+      *reinterpret_cast<float4 *>(ks + t * (HD + 4) + 4 * d4) = k[u];
+      *reinterpret_cast<float4 *>(vs + t * (HD + 4) + 4 * d4) = v[u];
+    }
+  }
+};
+
 template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(AttnParams p) {
   constexpr int kSt = HD + 4;      // LDS row stride of a staged K or V row
   constexpr int kQ = HD / 4;       // dimensions per lane group in the score MFMAs
   constexpr int kDt = HD / 16;     // 16-dimension tiles of the value sums
-  constexpr int kQv = 128;         // query vectors per block
+  constexpr int kQv = 128;         // query vectors per tile
+  constexpr int kBuf = 2 * kChunk * kSt; // floats of one staged chunk (K and V)
   extern __shared__ __align__(16) float lds[];
-  float *ks = lds, *vs = lds + kChunk * kSt;
   const int kv_mul = p.n_heads / p.n_kv_heads, tile_rows = kQv / kv_mul;
   const int ntiles = (p.rows + tile_rows - 1) / tile_rows;
-  const int tile = ntiles - 1 - (int)blockIdx.x; // the longest (latest) tiles first
-  const int g = blockIdx.y, r0 = tile * tile_rows;
+  const int g = blockIdx.y;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int lq = lane >> 4, lc = lane & 15;
-  const int qv = wave * 16 + lc, j = qv / kv_mul, h = qv % kv_mul, row = r0 + j;
-  const bool active = row < p.rows;
-  const int pos = p.pos0 + (active ? row : 0);            // this lane's query row's position
-  const int wave_last = p.pos0 + min(r0 + (wave * 16 + 15) / kv_mul, p.rows - 1);
-  const int last = p.pos0 + min(r0 + tile_rows, p.rows) - 1; // the tile's last position
+  const int qv = wave * 16 + lc, j = qv / kv_mul, h = qv % kv_mul;
   const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
-  // this lane's dimensions lq * HD / 4 .. + HD / 4 of its query vector
-  float qr[kQ];
-  {
-    const float *src = p.q + ((size_t)(active ? row : 0) * p.n_heads + (size_t)g * kv_mul + h) * HD + lq * kQ;
-#pragma unroll
-    for (int i = 0; i < kQ; i += 4) {
-      const float4 v = active ? *reinterpret_cast<const float4 *>(src + i) : float4{0.0f, 0.0f, 0.0f, 0.0f};
-      qr[i] = v.x, qr[i + 1] = v.y, qr[i + 2] = v.z, qr[i + 3] = v.w;
-    }
-  }
-  v4f o[kDt];
-#pragma unroll
-  for (int d = 0; d < kDt; d++)
-    o[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = -FLT_MAX, l_run = 0.0f;
   bool bad = false;
-  const int chunks = last / kChunk + 1;
-  for (int c = 0; c < chunks; c++) {
-    const int t0 = c * kChunk;
-    __syncthreads(); // the previous chunk's rows are read
-    for (int i = threadIdx.x; i < kChunk * (HD / 4); i += kTileThreads) {
-      const int t = i / (HD / 4), d4 = i % (HD / 4);
-      float4 kv = float4{0.0f, 0.0f, 0.0f, 0.0f}, vv = kv;
-      if (t0 + t <= last) {
-        const size_t at = (size_t)(t0 + t) * p.pos_stride + 4 * d4;
-        kv = *reinterpret_cast<const float4 *>(kbase + at);
-        vv = *reinterpret_cast<const float4 *>(vbase + at);
-      }
-      *reinterpret_cast<float4 *>(ks + t * kSt + 4 * d4) = kv;
-      *reinterpret_cast<float4 *>(vs + t * kSt + 4 * d4) = vv;
-    }
-    __syncthreads();
-    if (t0 > wave_last)
-      continue; // no row of this wave reaches the chunk (wave-uniform)
-    // S^T: position 16 t + 4 lq + e (t = 0..3, e = 0..3) against this lane's query vector
-    v4f sc[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      sc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-      const float *kr = ks + (16 * t + lc) * kSt + lq * kQ;
+  for (int pass = 0; pass < 2; pass++) {
+    const int tile = pass == 0 ? ntiles - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    if (pass == 1 && tile >= ntiles - 1 - (int)blockIdx.x)
+      break; // the middle tile of an odd count is taken once
+    const int r0 = tile * tile_rows, row = r0 + j;
+    const bool active = row < p.rows;
+    const int pos = p.pos0 + (active ? row : 0);              // this lane's query row's position
+    const int wave_last = p.pos0 + min(r0 + (wave * 16 + 15) / kv_mul, p.rows - 1);
+    const int last = p.pos0 + min(r0 + tile_rows, p.rows) - 1; // the tile's last position
+    // this lane's dimensions lq * HD / 4 .. + HD / 4 of its query vector
+    float qr[kQ];
+    {
+      const float *src = p.q + ((size_t)(active ? row : 0) * p.n_heads + (size_t)g * kv_mul + h) * HD + lq * kQ;
 #pragma unroll
       for (int i = 0; i < kQ; i += 4) {
-        const float4 a = *reinterpret_cast<const float4 *>(kr + i);
-        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qr[i], sc[t], 0, 0, 0);
-        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qr[i + 1], sc[t], 0, 0, 0);
-        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qr[i + 2], sc[t], 0, 0, 0);
-        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qr[i + 3], sc[t], 0, 0, 0);
+        const float4 v = active ? *reinterpret_cast<const float4 *>(src + i) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        qr[i] = v.x, qr[i + 1] = v.y, qr[i + 2] = v.z, qr[i + 3] = v.w;
       }
     }
-    // causal mask, the chunk maximum over the vector's 64 positions (16 here, the rest in lanes lc + 16, 32, 48)
-    float cmax = -FLT_MAX;
+    v4f o[kDt];
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int d = 0; d < kDt; d++)
+      o[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -FLT_MAX, l_run = 0.0f;
+    const int chunks = last / kChunk + 1;
+    FlashStage<HD> st;
+    st.load(p, kbase, vbase, 0, last);
+    for (int c = 0; c < chunks; c++) {
+      const int t0 = c * kChunk;
+      float *ks = lds + (c & 1) * kBuf, *vs = ks + kChunk * kSt;
+      // buffer c % 2 was last read for chunk c - 2, before the barrier of chunk c - 1
+      st.store(ks, vs);
+      __syncthreads();
+      if (c + 1 < chunks)
+        st.load(p, kbase, vbase, t0 + kChunk, last); // in flight while this chunk is computed
+      if (t0 > wave_last)
+        continue; // no row of this wave reaches the chunk (wave-uniform)
+      // S^T: position 16 t + 4 lq + e (t = 0..3, e = 0..3) against this lane's query vector; the four position tiles'
+      // accumulators take turns, so consecutive MFMAs never wait on each other
+      v4f sc[4];
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int at = t0 + 16 * t + 4 * lq + e;
-        const bool live = active && at <= pos;
-        float s = -FLT_MAX;
-        if (live) {
-          s = sc[t][e] / p.divisor;
-          bad |= !isfinite(s);
-        }
-        sc[t][e] = s;
-        cmax = fmaxf(cmax, s);
+      for (int t = 0; t < 4; t++)
+        sc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < kQ; i += 4) {
+        float4 a[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          a[t] = *reinterpret_cast<const float4 *>(ks + (16 * t + lc) * kSt + lq * kQ + i);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].x, qr[i], sc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].y, qr[i + 1], sc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].z, qr[i + 2], sc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].w, qr[i + 3], sc[t], 0, 0, 0);
       }
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-    const float m_new = fmaxf(m_run, cmax);
-    const float alpha = expf(m_run - m_new); // 0 before the first live position, 1 when the maximum stays
-    float psum = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float pe = sc[t][e] > -FLT_MAX ? expf(sc[t][e] - m_new) : 0.0f;
-        sc[t][e] = pe;
-        psum += pe;
-      }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    // O^T += V^T P^T: dimension 16 d + lc, positions 16 t + 4 lq + e
-#pragma unroll
-    for (int d = 0; d < kDt; d++) {
-      o[d] *= alpha;
+      // causal mask, the chunk maximum over the vector's 64 positions (16 here, the rest in lanes lc + 16, 32, 48)
+      float cmax = -FLT_MAX;
 #pragma unroll
       for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-          o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vs[(16 * t + 4 * lq + e) * kSt + 16 * d + lc], sc[t][e], o[d],
-                                                      0, 0, 0);
+        for (int e = 0; e < 4; e++) {
+          const int at = t0 + 16 * t + 4 * lq + e;
+          const bool live = active && at <= pos;
+          float s = -FLT_MAX;
+          if (live) {
+            s = sc[t][e] / p.divisor;
+            bad |= !isfinite(s);
+          }
+          sc[t][e] = s;
+          cmax = fmaxf(cmax, s);
+        }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+      const float m_new = fmaxf(m_run, cmax);
+      const float alpha = expf(m_run - m_new); // 0 before the first live position, 1 when the maximum stays
+      float psum = 0.0f;
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float pe = sc[t][e] > -FLT_MAX ? expf(sc[t][e] - m_new) : 0.0f;
+          sc[t][e] = pe;
+          psum += pe;
+        }
+      psum += __shfl_xor(psum, 16);
+      psum += __shfl_xor(psum, 32);
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int d = 0; d < kDt; d++)
+        o[d] *= alpha;
+      // O^T += V^T P^T; the dimension tiles' accumulators take turns
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float *vr = vs + (16 * t + 4 * lq + e) * kSt + kDt * lc;
+          float va[kDt];
+#pragma unroll
+          for (int d = 0; d < kDt; d += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(vr + d);
+            va[d] = v.x, va[d + 1] = v.y, va[d + 2] = v.z, va[d + 3] = v.w;
+          }
+#pragma unroll
+          for (int d = 0; d < kDt; d++)
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[d], sc[t][e], o[d], 0, 0, 0);
+        }
     }
+    __syncthreads(); // the next tile's first chunk reuses buffer 0
+    if (!active)
+      continue;
+    // lane (lq, lc) holds dimensions kDt * (4 lq + e) + d of vector lc: for each e, kDt consecutive floats
+    const float inv = 1.0f / l_run;
+    float *dst = p.out + ((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * HD;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+#pragma unroll
+      for (int d = 0; d < kDt; d += 4)
+        *reinterpret_cast<float4 *>(dst + kDt * (4 * lq + e) + d) =
+            float4{o[d][e] * inv, o[d + 1][e] * inv, o[d + 2][e] * inv, o[d + 3][e] * inv};
   }
   if (bad)
     p.flags[1] = 1;
-  if (!active)
-    return;
-  // lane (lq, lc) holds dimensions 16 d + 4 lq + e of vector lc
-  const float inv = 1.0f / l_run;
-  float *dst = p.out + ((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * HD;
-#pragma unroll
-  for (int d = 0; d < kDt; d++)
-    *reinterpret_cast<float4 *>(dst + 16 * d + 4 * lq) =
-        float4{o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv};
 }
 
 // Block (chunk c, KV head g, query row r). Waves take positions t0 + w, t0 + w + 4, ...: lane l holds dimensions
@@ -785,18 +835,19 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
   const bool flash = !job.table && aligned && job.rows >= 16 && (job.head_dim == 64 || job.head_dim == 128) &&
                      128 % kv_mul == 0 && ((uintptr_t)job.out & 15) == 0 && ((uintptr_t)job.value & 15) == 0;
   if (flash) {
+    // two staged chunks of K and V rows: 4 x 64 x (HD + 4) floats (135 KB at HD = 128)
     static const hipError_t flash_allowed = [] {
       const hipError_t e = hipFuncSetAttribute((const void *)attn_flash<128>,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kChunk * 132 * 4);
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 4 * kChunk * 132 * 4);
       return e != hipSuccess ? e
                              : hipFuncSetAttribute((const void *)attn_flash<64>,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kChunk * 68 * 4);
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 4 * kChunk * 68 * 4);
     }();
     if (flash_allowed != hipSuccess)
       return raise("allowing the attention kernel its LDS failed: %s", hipGetErrorString(flash_allowed));
-    const int tile_rows = 128 / kv_mul;
-    const dim3 grid((unsigned)((job.rows + tile_rows - 1) / tile_rows), (unsigned)job.n_kv_heads);
-    const size_t lds = 2 * (size_t)kChunk * (job.head_dim + 4) * sizeof(float);
+    const int tile_rows = 128 / kv_mul, tiles = (job.rows + tile_rows - 1) / tile_rows;
+    const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)job.n_kv_heads); // a block per pair of tiles
+    const size_t lds = 4 * (size_t)kChunk * (job.head_dim + 4) * sizeof(float);
     if (job.head_dim == 128)
       hipLaunchKernelGGL(attn_flash<128>, grid, dim3(kTileThreads), lds, stream, p);
     else
