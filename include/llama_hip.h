@@ -101,6 +101,12 @@ void llhip_set_gemm_splits(int splits);
  * on it beyond FP32 summation order. For tuning and tests. */
 void llhip_set_bf16_tile(int tile);
 
+/* Output tile of the INT8 prefill GEMM with gs = 64: 1 = 256 x 128, 2 = 256 x 256, 0 = by grid (256 x 256 when the
+ * grid has at least four 256 x 128 tiles per CU; LLAMA_HIP_Q8_TILE=narrow|wide sets the same at start-up). Other group
+ * sizes and the group-dot probe always take 256 x 128. Results do not depend on it beyond FP32 summation order; the
+ * int32 group dots are exact either way. For tuning and tests. */
+void llhip_set_q8_tile(int tile);
+
 /* The int32 probe of the decode GEMV: dots[g * d + r] = the exact int32 dot of group g of input row xq and weight
  * row r, as the streaming GEMV kernel itself forms it before the FP32 rescale (gs % 16 == 0 takes the fast kernel). */
 void llhip_q8_gemv_group_dots(int32_t *dots, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws,

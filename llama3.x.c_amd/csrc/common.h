@@ -183,6 +183,7 @@ struct GemvJob {
 bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves);
 void set_gemm_splits(int splits); // FP32 / BF16 / INT8 GEMM blocks per tile; 0 = chosen from the grid
 void set_bf16_tile(int tile);     // BF16 GEMM tile: 0 by grid, 1 256 x 128, 2 256 x 256
+void set_q8_tile(int tile);       // INT8 GEMM tile (gs = 64): 0 by grid, 1 256 x 128, 2 256 x 256
 bool gemv_fast_path(const GemvJob &job);
 bool launch_q8_gemv(const GemvJob &job, hipStream_t stream);
 

@@ -927,6 +927,226 @@ template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void bf16_gemm
 }
 
 
+// ---- W8A8 Q8_0, wide tiles ----------------------------------------------------------------------------------------
+//
+// q8_gemm_lds waits on its operands as much as on its rescale. On the 8B W1/W3 launch (2048 x 2 * 14336 x 4096) it
+// takes 538 us. Copies of it measured: without the rescale, 450 us; without the operand loads, 402; without both,
+// 202. The weight tile's loads, half the bytes, cost more than the activations': the weights come from HBM and the
+// activations from L2, so what limits is the misses a CU keeps in flight, not bandwidth.
+//
+// This kernel owns a 256 x 256 tile (the wide BF16 kernel's shape). That is a third fewer operand bytes per output, and
+// A is read half as often. Eight waves in 4 x 2 each own 64 x 128 as 4 x 8 MFMA tiles. Their FP32 sums take 128
+// registers, so the int32 results cannot all wait for the next step as in q8_gemm_lds. Instead:
+// - a step's MFMAs run column tile by column tile (j = 0..7, rows i = 0..3);
+// - each tile's results are rescaled one column tile later, just before tile (j, i)'s MFMA overwrites those of
+//   (j - 1, i): converted, then added with that step's scales;
+// - only column tile 7 crosses into the next step, where its rescale keeps the VALU busy while the next operands
+//   arrive behind the barrier.
+// Four stages of 34 KB (the A and B tiles, and the xs / ws of the step's group) keep three steps in flight. gs = 64
+// only (one group per step). Under SWIGLU the tile holds 128 columns of W1 and the same 128 of W3 (b_row_wide).
+constexpr int kQWStages = 4, kQWLoadsPerStep = 5; // per wave: two A blocks, two B blocks, one scale load
+constexpr int kQWBOff = 16 * kQWStages * 1024;     // 16 A blocks per stage, then 16 B blocks
+constexpr int kQWSOff = kQWBOff + 16 * kQWStages * 1024;
+constexpr int kQWSStride = 512 * 4; // xs of the 256 rows, then ws of the 256 B-tile rows
+constexpr size_t kQWLds = (size_t)kQWSOff + (size_t)kQWStages * kQWSStride; // 136 KB
+static_assert(kQWLds <= 160 * 1024, "one wide int8 block fits a CU's LDS");
+
+template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_wide(Q8Params p) {
+  extern __shared__ __align__(16) unsigned char q8_smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int logical = xcd_logical(blockIdx.x, p.grid.total * (SPLIT ? p.sk.splits : 1));
+  const int tile = SPLIT ? __builtin_amdgcn_readfirstlane(logical / p.sk.splits) : logical;
+  const int split = SPLIT ? __builtin_amdgcn_readfirstlane(logical % p.sk.splits) : 0;
+  const TilePos t = q8_tile_of(p.grid, tile, kWTileM, kWTileN);
+  const TileSeg seg = q8_seg_of(p.grid, t.s);
+  const int groups = p.k / 64, steps = groups;
+  const int s0 = SPLIT ? split * p.sk.per : 0, s1 = SPLIT ? min(steps, s0 + p.sk.per) : steps;
+  const long long k = p.k;
+
+  // Loads: lane l places its 16 bytes at l * 16 of a 1 KB block (row l / 4, chunk l % 4 XOR-swizzled by the row).
+  const int lrow4 = lane >> 2, chunk = lane & 3;
+  const int ra = 32 * wave + lrow4; // A rows ra (block 2 wave) and ra + 16 (block 2 wave + 1)
+  const __amdgpu_buffer_rsrc_t rA = q8_buffer(p.xq + (long long)t.m0 * k, (long long)min(kWTileM, p.m - t.m0) * k);
+  const int offA0 = (int)(ra * k) + ((chunk ^ q8_swizzle(ra)) << 4);
+  const int offA1 = (int)((ra + 16) * k) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
+  // B-tile blocks 2 wave and 2 wave + 1 (rows 16 blk ..), each of one matrix
+  auto b_resource = [&](int blk) {
+    const int rb = 16 * blk;
+    const int colB = t.swiglu ? t.n0 + (rb & 127) : t.n0 + rb;
+    const int8_t *wmat = (const int8_t *)((t.swiglu && rb >= 128) ? seg.w3 : seg.w);
+    return q8_buffer(wmat + (long long)colB * k, (long long)min(16, seg.n - colB) * k);
+  };
+  const __amdgpu_buffer_rsrc_t rB0 = b_resource(2 * wave), rB1 = b_resource(2 * wave + 1);
+  const int offB = (int)(lrow4 * k) + ((chunk ^ q8_swizzle(lrow4)) << 4);
+  // scale loads: waves 0..3 the xs of rows 64 wave .., waves 4..7 the ws of B-tile rows 64 (wave - 4) ..
+  __amdgpu_buffer_rsrc_t rS;
+  int scale_dst;
+  if (wave < 4) {
+    const int r0 = t.m0 + 64 * wave;
+    rS = q8_buffer(p.xs + (long long)r0 * groups, (long long)min(64, p.m - r0) * groups * 4);
+    scale_dst = 64 * wave * 4;
+  } else {
+    const int h = wave - 4;
+    const float *src = (t.swiglu && h >= 2) ? seg.w3s : seg.ws;
+    const int c0 = t.swiglu ? t.n0 + 64 * (h & 1) : t.n0 + 64 * h;
+    rS = q8_buffer(src + (long long)c0 * groups, (long long)min(64, seg.n - c0) * groups * 4);
+    scale_dst = (kWTileM + 64 * h) * 4;
+  }
+  const int offS = lane * groups * 4;
+  const __amdgpu_buffer_rsrc_t none = q8_buffer(p.xq, 0);
+
+  // The loads of K step `step` into stage ST; a step past the end loads nothing (zero-length resources).
+  auto issue = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value;
+    const bool live = step < s1;
+    const int k0 = step * 64;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
+                                             (void *)(q8_smem + ((2 * wave) * kQWStages + st) * 1024), 16, offA0, k0,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
+                                             (void *)(q8_smem + ((2 * wave + 1) * kQWStages + st) * 1024), 16, offA1,
+                                             k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB0 : none,
+                                             (void *)(q8_smem + kQWBOff + ((2 * wave) * kQWStages + st) * 1024), 16,
+                                             offB, k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB1 : none,
+                                             (void *)(q8_smem + kQWBOff + ((2 * wave + 1) * kQWStages + st) * 1024),
+                                             16, offB, k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rS : none,
+                                             (void *)(q8_smem + kQWSOff + st * kQWSStride + scale_dst), 4, offS,
+                                             step * 4, 0, 0);
+  };
+
+  // Per-lane LDS read bases; the stage, the row tile and the column tile within a half add immediates.
+  const int lrow = lane & 15, lr4 = (lane >> 4) * 4;
+  const int lane_part = lrow * 64 + (((lane >> 4) ^ q8_swizzle(lrow)) << 4);
+  const unsigned char *abase = q8_smem + (4 * wm) * kQWStages * 1024 + lane_part;
+  const unsigned char *blo = q8_smem + kQWBOff + (b_row_wide(t.swiglu, wn, 0) / 16) * kQWStages * 1024 + lane_part;
+  const unsigned char *bhi = q8_smem + kQWBOff + (b_row_wide(t.swiglu, wn, 4) / 16) * kQWStages * 1024 + lane_part;
+  const unsigned char *xsbase = q8_smem + kQWSOff + (64 * wm + lr4) * 4;
+  const unsigned char *wslo = q8_smem + kQWSOff + (kWTileM + b_row_wide(t.swiglu, wn, 0) + lrow) * 4;
+  const unsigned char *wshi = q8_smem + kQWSOff + (kWTileM + b_row_wide(t.swiglu, wn, 4) + lrow) * 4;
+
+  v4f acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // The int32 results of two column tiles: round j of a step writes set j % 2 while the VALU rescales the other,
+  // written one round earlier (column tile j - 1, or tile 7 of the previous step), so no VALU waits on a running MFMA.
+  v4i dot[2][4] = {};
+
+  auto rescale = [&](const v4i &d, float ws, const v4f &xs, v4f &c) {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      c[e] = fmaf((float)d[e] * ws, xs[e], c[e]);
+  };
+  // One step's MFMAs from stage ST. CARRY: tile 7 of the previous step (stage ST - 1, whose scales are still in
+  // place) waits in dot[1], rescaled in round 0.
+  auto mma_step = [&](auto ST, auto CARRY) {
+    constexpr int st = decltype(ST)::value, pst = (st + kQWStages - 1) % kQWStages;
+    constexpr bool carry = decltype(CARRY)::value;
+    auto b_op = [&](int j) {
+      return *reinterpret_cast<const v4i *>((j < 4 ? blo : bhi) + ((j & 3) * kQWStages + st) * 1024);
+    };
+    auto xs_op = [&](int stage, int i) {
+      return *reinterpret_cast<const v4f *>(xsbase + stage * kQWSStride + i * 64);
+    };
+    auto ws_op = [&](int stage, int j) {
+      return *reinterpret_cast<const float *>((j < 4 ? wslo : wshi) + stage * kQWSStride + (j & 3) * 64);
+    };
+    v4i a[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      a[i] = *reinterpret_cast<const v4i *>(abase + (i * kQWStages + st) * 1024);
+    v4i b = b_op(0);
+    v4f xs[4];
+    float ws = 0.f;
+    if (carry) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        xs[i] = xs_op(pst, i);
+      ws = ws_op(pst, 7);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Round j: first the reads the next round needs (its B operand and ws, and in round 0 this step's xs), then four
+    // MFMAs into set j % 2, each followed by the 12 VALU instructions of one tile of the other set. The rounds are
+    // fenced from each other, so the next round's MFMAs are not hoisted over these rescales.
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const v4i bn = j < 7 ? b_op(j + 1) : b;
+      const float wsn = j < 7 ? ws_op(st, j) : ws;
+      v4f xsn[4];
+      if (j == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          xsn[i] = xs_op(st, i);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        dot[j & 1][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b, v4i{0, 0, 0, 0}, 0, 0, 0);
+        if (j > 0 || carry)
+          rescale(dot[(j & 1) ^ 1][i], ws, xs[i], acc[i][j > 0 ? j - 1 : 7]);
+      }
+      if (j == 0) // DS reads
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+      else
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // one MFMA
+        if (j > 0 || carry)
+          __builtin_amdgcn_sched_group_barrier(0x002, 12, 0); // one tile's convert, multiply, FMA
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      b = bn;
+      ws = wsn;
+      if (j == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          xs[i] = xsn[i];
+      }
+    }
+  };
+  // Step `step` is in stage ST: wait until step + 1 has landed for every wave (the stage of step - 1 is then free for
+  // step + 3), then step + 1's MFMAs, after the rescale of step's column tile 7.
+  auto advance = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value, nst = (st + 1) % kQWStages, fill = (st + kQWStages - 1) % kQWStages;
+    wait_vmcnt<(kQWStages - 3) * kQWLoadsPerStep>();
+    __builtin_amdgcn_s_barrier();
+    issue(step + kQWStages - 1, std::integral_constant<int, fill>{});
+    mma_step(std::integral_constant<int, nst>{}, std::true_type{});
+  };
+
+  issue_first<0, kQWStages - 1>(issue, s0);
+  wait_vmcnt<(kQWStages - 2) * kQWLoadsPerStep>(); // step s0 has landed for this wave
+  __builtin_amdgcn_s_barrier();                      // ... and for every wave
+  mma_step(std::integral_constant<int, 0>{}, std::false_type{});
+  // Whole rounds of four steps: the stages of steps past the end hold zeros (zero-length loads), so their MFMAs and
+  // rescales add nothing, and advance(s1 - 1), which every round count reaches, rescales the last step's tile 7.
+  for (int step = s0; step < s1; step += kQWStages) {
+    advance(step, std::integral_constant<int, 0>{});
+    advance(step + 1, std::integral_constant<int, 1>{});
+    advance(step + 2, std::integral_constant<int, 2>{});
+    advance(step + 3, std::integral_constant<int, 3>{});
+  }
+  // the loads issued for steps past the end still target this block's LDS: let them land before the block exits
+  __builtin_amdgcn_s_waitcnt(0);
+  if (SPLIT) {
+    v4f *slot = p.sk.partial + (size_t)(tile * p.sk.splits + split) * kWSlotV4 + threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        slot[(i * 8 + j) * kQ8Threads] = acc[i][j];
+    return;
+  }
+  store_tile_wide(seg, t, acc, wm, wn, lane, p.m);
+}
+
 // Any group size (gs % 64 != 0): one thread per output, the per-group int32 dot in plain integer arithmetic.
 __global__ __launch_bounds__(kBlock) void q8_gemm_generic(TileGrid g, const int8_t *xq, const float *xs, int m, int k,
                                                           int gs) {
@@ -1157,8 +1377,65 @@ int q8_tile_m() {
   return tile;
 }
 
+std::atomic<int> forced_q8_tile{0}; // llhip_set_q8_tile: 0 unset, 1 narrow, 2 wide
+
+// The wide kernel (256 x 256 tiles) for gs = 64, when it is picked: LLAMA_HIP_Q8_TILE = wide / narrow (read once) or
+// llhip_set_q8_tile force it; otherwise by grid. A wide tile takes about 1.7 times a 256 x 128 tile (measured on the
+// 8B shapes at 1024 to 4096 rows: 15% less time per output), so the wide grid wins when its rounds of one tile per CU,
+// weighted 1.7, are fewer than the narrow grid's. Grids of fewer narrow tiles than CUs keep the narrow kernel, whose
+// split K fills the CUs. Measured (us, narrow / wide): W1/W3 of 2048 rows 507 / 492 (7 rounds against 3.5), QKV 137 /
+// 120 (2 against 1); Wo and W2 87 / 101 and 243 / 252 (one round each); at 4096 rows Wo 170 / 156, W2 483 / 443.
+bool q8_use_wide(const Q8Params &p, const SegList &segs) {
+  if (p.gs != 64)
+    return false;
+  static const int env_tile = [] {
+    const char *env = getenv("LLAMA_HIP_Q8_TILE");
+    return env && !strcmp(env, "wide") ? 2 : env && !strcmp(env, "narrow") ? 1 : 0;
+  }();
+  const int forced = forced_q8_tile.load() ? forced_q8_tile.load() : env_tile;
+  if (forced)
+    return forced == 2;
+  const int cus = device().cu_count > 0 ? device().cu_count : 256;
+  const int narrow = make_q8_grid(segs.seg, segs.nseg, p.m).total;
+  if (narrow < cus)
+    return false;
+  const int wide = make_q8_grid(segs.seg, segs.nseg, p.m, kWTileM, kWTileN).total;
+  return 17LL * ((wide + cus - 1) / cus) < 10LL * ((narrow + cus - 1) / cus);
+}
+
+// The wide int8 kernel; its partial tiles are twice the size, so half as many fit the workspace.
+bool q8_wide_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
+  constexpr int kWideSlots = kSplitSlots / 2;
+  p.grid = make_q8_grid(segs.seg, segs.nseg, p.m, kWTileM, kWTileN);
+  if (p.grid.total <= 0)
+    return true;
+  const int steps = p.k / 64;
+  p.sk.splits = p.grid.total > kWideSlots ? 1 : choose_splits(p.grid.total, steps, &p.sk.per, 1, kWideSlots);
+  if (p.sk.splits == 1)
+    p.sk.per = steps;
+  p.sk.partial = (v4f *)device().split_partial;
+  p.sk.count = device().split_count;
+  static const hipError_t a0 =
+      hipFuncSetAttribute((const void *)q8_gemm_wide<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds);
+  static const hipError_t a1 =
+      hipFuncSetAttribute((const void *)q8_gemm_wide<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds);
+  if (!check_hip(a0, "allowing the Q8 GEMM its LDS") || !check_hip(a1, "allowing the Q8 GEMM its LDS"))
+    return false;
+  if (p.sk.splits == 1) {
+    hipLaunchKernelGGL(q8_gemm_wide<false>, dim3((unsigned)p.grid.total), dim3(kQ8Threads), kQWLds, stream, p);
+    return launch_ok("q8_gemm_wide");
+  }
+  hipLaunchKernelGGL(q8_gemm_wide<true>, dim3((unsigned)(p.grid.total * p.sk.splits)), dim3(kQ8Threads), kQWLds,
+                     stream, p);
+  if (!launch_ok("q8_gemm_wide"))
+    return false;
+  return launch_split_reduce<8, kQ8Threads>(p.grid, p.sk, p.m, kWTileM, kWTileN, stream);
+}
+
 template <bool PROBE> bool launch_q8_lds(Q8Params p, const GemmSegmentDev *segs, int nseg, hipStream_t stream) {
   const SegList list{segs, nseg};
+  if (!PROBE && q8_use_wide(p, list))
+    return q8_wide_launch(p, list, stream);
   if (q8_tile_m() == 256)
     return p.gs == 64 ? q8_launch<Q8Wide, PROBE, true>(p, list, stream) : q8_launch<Q8Wide, PROBE, false>(p, list, stream);
   return p.gs == 64 ? q8_launch<Q8Pair, PROBE, true>(p, list, stream) : q8_launch<Q8Pair, PROBE, false>(p, list, stream);
@@ -1332,6 +1609,8 @@ bool f32_fast_path(const GemmF32Job &job) {
 void set_gemm_splits(int splits) { forced_splits.store(splits > 0 ? splits : 0); }
 
 void set_bf16_tile(int tile) { forced_bf16_tile.store(tile == 1 || tile == 2 ? tile : 0); }
+
+void set_q8_tile(int tile) { forced_q8_tile.store(tile == 1 || tile == 2 ? tile : 0); }
 
 bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream) {
   if (job.m <= 0 || job.k <= 0)

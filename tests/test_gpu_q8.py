@@ -470,6 +470,63 @@ def test_gemm_q8_split_k(m, n, k, gs):
         L.llhip_set_gemm_splits(0)
 
 
+@pytest.mark.parametrize("m,n,k", [(33, 20, 128), (40, 33, 192), (130, 257, 1024), (256, 384, 4096), (129, 129, 640),
+                                   (600, 200, 1024), (300, 136, 14336), (513, 65, 320), (257, 513, 2048),
+                                   (1, 64, 64)])
+def test_gemm_q8_wide_tiles(m, n, k):
+    """The 256 x 256 int8 kernel (gs = 64), forced: every kind within the budget, and bit for bit the 256 x 128
+    kernel's result at every forced split count (both add each group's ((float)dot * ws) * xs in group order, and
+    split partials in split order), so the two tilings differ in nothing but speed. Also a three-segment call."""
+    L = hu.lib()
+    gs = 64
+    xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 4242 + m + n)
+    ldc = n + 3
+    base = rng.uniform(m * ldc, 3.0).reshape(m, ldc)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    r3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
+    dx = [hu.dev(a) for a in (xq, xs, wq, ws, w3q, w3s)]
+
+    def run(kind, tile, splits):
+        L.llhip_set_q8_tile(tile)
+        L.llhip_set_gemm_splits(splits)
+        c = hu.dev(base)
+        seg = lh.GemmQ8Segment(lh.ptr(c), ldc, lh.w8(dx[2], dx[3]), lh.w8(dx[4], dx[5]), None, None, n, kind)
+        L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+        got = hu.host(c)
+        assert lh.last_error() == "", lh.last_error()
+        assert np.array_equal(hu.bits(got[:, n:]), hu.bits(base[:, n:])), "row padding was written"
+        return got[:, :n]
+
+    try:
+        for splits in (1, 2, 3, 0):
+            for kind in (lh.GEMM_STORE, lh.GEMM_ADD, lh.GEMM_SWIGLU, lh.GEMM_PARTIAL):
+                what = f"wide {m}x{n}x{k} kind {kind} splits {splits}"
+                got = run(kind, 2, splits)
+                if kind == lh.GEMM_ADD:
+                    hu.assert_within_budget(got, base[:, :n] + ref, mag + np.abs(base[:, :n]), what=what)
+                elif kind == lh.GEMM_SWIGLU:
+                    want = ref / (1 + np.exp(-ref)) * r3
+                    tol = 2e-5 * (mag * (np.abs(r3) + 1) + mag3 * (np.abs(ref) + 1)) + 1e-6  # tests/q8.c:130
+                    assert np.all(np.abs(got - want) <= tol), what
+                else:
+                    hu.assert_within_budget(got, ref, mag, what=what)
+                if splits:  # the automatic count differs between the tilings (a wide grid has half the tiles)
+                    assert np.array_equal(hu.bits(got), hu.bits(run(kind, 1, splits))), what + " vs 256 x 128"
+        L.llhip_set_q8_tile(2)
+        L.llhip_set_gemm_splits(1)
+        widths = (n, max(16, n // 4), max(16, n // 4))
+        outs = [hu.dev(np.zeros((m, nn), np.float32)) for nn in widths]
+        mats = [(hu.dev(wq[:nn]), hu.dev(ws[:nn])) for nn in widths]  # kept alive across the call
+        segs = (lh.GemmQ8Segment * 3)(*[lh.GemmQ8Segment(lh.ptr(o), nn, lh.w8(*w), lh.K8Weight(), None, None, nn,
+                                                         lh.GEMM_STORE) for o, w, nn in zip(outs, mats, widths)])
+        L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, segs, 3)
+        for o, nn in zip(outs, widths):
+            hu.assert_within_budget(hu.host(o), ref[:, :nn], mag[:, :nn], what=f"wide segment of {nn}")
+    finally:
+        L.llhip_set_q8_tile(0)
+        L.llhip_set_gemm_splits(0)
+
+
 def test_gemm_q8_qkv_segments_and_gemv_agreement():
     """Three segments sharing the activations (QKV), and each GEMM row against the GEMV of that row."""
     L = hu.lib()
