@@ -8,6 +8,7 @@ HIP graph with every input already in HBM; attention, RMSNorm and RoPE are not p
 
 Alongside (`prefill`): the 8B INT8 W8A8 prefill of a 2048-token prompt: per layer quantize the 2048 rows and run the
 int8-MFMA GEMMs (QKV, Wo + residual, W1/W3 SwiGLU, W2 + residual), then the last row's classifier GEMV.
+`decode_1b` and `gemv_2048`: the Llama-3.2-1B decode matmul set and one cold 2048 x 2048 GEMV, launch-amortized.
 `forward_decode`: the whole 8B decode token on the device (the embedding row, the matmul set plus RMSNorm, RoPE, the K/V
 cache store and attention over 2048 cached positions), also from a HIP graph.
 `engine`: the engine end to end at the configuration of a Llama-3.1-8B Q8_0 forward (a version-3 checkpoint of
@@ -387,6 +388,95 @@ def prefill_3b(torch, lh, seed, steps=3):
     return out
 
 
+def decode_1b(torch, lh, seed, steps=50):
+    """C2, the Llama-3.2-1B decode-step matmul set (dim 2048, kv_dim 512, hidden 8192, 16 layers, classifier 128256 x
+    2048, gs 64: per layer quantize, QKV, Wo +resid, W1/W3 SwiGLU, W2 +resid), replayed from one HIP graph; and C1, one
+    2048 x 2048 GEMV (the 1B wq), launch-amortized (64 launches in one graph) and cold: the 64 launches read 64 copies
+    of the weights, 286 MB, more than the 256 MB last-level cache. Weights ~N(0, 0.02) quantized by k_quantize_rows,
+    activations ~N(0, 1)."""
+    L = lh.load()
+    D, KVD, H, NL, V = 2048, 512, 8192, 16, 128256
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 5)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    P = lh.ptr
+
+    def q8(rows, k):
+        w = torch.empty(rows, k, **f32)
+        w.normal_(0.0, 0.02, generator=gen)
+        q = torch.empty(rows, k, dtype=torch.int8, device="cuda")
+        s = torch.empty(rows, k // GS, **f32)
+        torch.cuda.synchronize()
+        L.k_quantize_rows(P(q), P(s), P(w), k, rows, k, GS)
+        L.llhip_synchronize()
+        return q, s
+
+    shapes = [("wq", D, D), ("wk", KVD, D), ("wv", KVD, D), ("wo", D, D), ("w1", H, D), ("w3", H, D), ("w2", D, H)]
+    layers = [{name: q8(r, k) for name, r, k in shapes} for _ in range(NL)]
+    cls = q8(V, D)
+    acts = [{n: torch.randn(size, generator=gen, **f32) for n, size in (("att", D), ("o", D), ("ffn", D), ("h", H))}
+            for _ in range(NL)]
+    x_cls = torch.randn(D, generator=gen, **f32)
+    xq_d, xs_d = torch.empty(D, dtype=torch.int8, device="cuda"), torch.empty(D // GS, **f32)
+    xq_h, xs_h = torch.empty(H, dtype=torch.int8, device="cuda"), torch.empty(H // GS, **f32)
+    q, k, v = torch.empty(D, **f32), torch.empty(KVD, **f32), torch.empty(KVD, **f32)
+    resid, hb, logits = torch.zeros(D, **f32), torch.empty(H, **f32), torch.empty(V, **f32)
+    torch.cuda.synchronize()
+
+    def w8(pair):
+        return lh.K8Weight(P(pair[0]), P(pair[1]))
+
+    ind, inh = lh.K8Input(P(xq_d), P(xs_d), None), lh.K8Input(P(xq_h), P(xs_h), None)
+
+    def step():
+        for lay, a in zip(layers, acts):
+            L.k_quantize(P(xq_d), P(xs_d), P(a["att"]), D, GS)
+            L.k_matmul_q8_qkv(P(q), P(k), P(v), ind, w8(lay["wq"]), w8(lay["wk"]), w8(lay["wv"]), D, D, KVD, GS)
+            L.k_quantize(P(xq_d), P(xs_d), P(a["o"]), D, GS)
+            L.k_matmul_q8_add(P(resid), ind, w8(lay["wo"]), D, D, GS)
+            L.k_quantize(P(xq_d), P(xs_d), P(a["ffn"]), D, GS)
+            L.k_matmul_q8_swiglu(P(hb), ind, w8(lay["w1"]), w8(lay["w3"]), D, H, GS)
+            L.k_quantize(P(xq_h), P(xs_h), P(a["h"]), H, GS)
+            L.k_matmul_q8_add(P(resid), inh, w8(lay["w2"]), H, D, GS)
+        L.k_quantize(P(xq_d), P(xs_d), P(x_cls), D, GS)
+        L.k_matmul_q8(P(logits), ind, w8(cls), D, V, GS)
+
+    step()
+    L.llhip_synchronize()
+    assert L.llhip_graph_begin() == 0
+    step()
+    graph = L.llhip_graph_end()
+    sec = time_graph(torch, L, graph, steps, 3) / steps
+    L.llhip_graph_destroy(graph)
+    # the 8B step's accounting (main): QKV as one GEMV of 3072 rows, W1/W3 as two weight streams sharing one input
+    per_step = NL * (q8_bytes(D + 2 * KVD, D) + q8_bytes(D, D) + 2 * weight_bytes(H, D) + D + D // GS * 4 + H * 4
+                     + q8_bytes(D, H)) + q8_bytes(V, D)
+    c2 = {"value": round(1.0 / sec, 1), "unit": "tok/s", "ms_per_token": round(sec * 1e3, 4),
+          "bytes_per_step": per_step, "hbm_frac": round(per_step / sec / 1e9 / HBM_PEAK_GBS, 4),
+          "workload": "C2: Llama-3.2-1B decode-step matmul set (16 layers of quantize + QKV, Wo +resid, W1/W3 "
+                      "SwiGLU, W2 +resid; classifier 128256 x 2048), gs 64, one HIP graph per token"}
+    print(f"# 1B decode matmul set: {sec * 1e3:.3f} ms/token, {1 / sec:.0f} tok/s, "
+          f"{per_step / sec / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
+    del layers, cls
+    torch.cuda.empty_cache()
+    # C1: the 2048 x 2048 GEMV from cold weights, 64 launches per graph
+    copies = [q8(D, D) for _ in range(64)]
+    x = torch.randn(D, generator=gen, **f32)
+    xq, xs, out = torch.empty(D, dtype=torch.int8, device="cuda"), torch.empty(D // GS, **f32), torch.empty(D, **f32)
+    L.k_quantize(P(xq), P(xs), P(x), D, GS)
+    L.llhip_synchronize()
+    inp = lh.K8Input(P(xq), P(xs), None)
+    avg = time_per_launch(torch, L, [lambda c=c: L.k_matmul_q8(P(out), inp, w8(c), D, D, GS) for c in copies], reps=5)
+    c1_bytes = q8_bytes(D, D)
+    c1 = {"us_per_gemv": round(avg * 1e6, 3), "bytes": c1_bytes, "hbm_frac": round(c1_bytes / avg / 1e9 / HBM_PEAK_GBS, 4),
+          "workload": "C1: one 2048 x 2048 Q8_0 GEMV (gs 64, pre-quantized input), 64 launches in one HIP graph over "
+                      "64 weight copies (286 MB, beyond the last-level cache)"}
+    print(f"# C1 GEMV 2048x2048 cold: {avg * 1e6:.2f} us, {c1_bytes / avg / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
+    del copies
+    torch.cuda.empty_cache()
+    return c2, c1
+
+
 def host_topology():
     """Sockets, physical cores per socket and logical CPUs of this host (lscpu), and the CPUs this process may use."""
     topo = {"sockets": 1, "cores_per_socket": os.cpu_count() or 1, "threads_per_core": 1,
@@ -578,6 +668,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=None,
                     help="threads of the CPU baseline (default: one socket's physical cores, as lscpu reports them)")
     ap.add_argument("--seed", type=int, default=88172645463325252 % (1 << 31))
+    ap.add_argument("--no-1b", action="store_true",
+                    help="skip the Llama-3.2-1B decode matmul set and the cold 2048 x 2048 GEMV (C2, C1)")
     ap.add_argument("--no-c3", action="store_true",
                     help="skip the FP32 / BF16 prefill GEMMs on the Llama-3.2-3B shapes (512 tokens)")
     ap.add_argument("--no-forward", action="store_true",
@@ -718,6 +810,8 @@ def main():
               f"{ach:.0f} TOP/s in the W1/W3 GEMM", file=sys.stderr, flush=True)
     L.llhip_graph_destroy(graph)
 
+    if not args.no_1b:
+        result["decode_1b"], result["gemv_2048"] = decode_1b(torch, lh, args.seed)
     if not args.no_c3:
         result["prefill_3b"] = prefill_3b(torch, lh, args.seed)
     if not args.no_engine:

@@ -958,7 +958,9 @@ static GemvShape gemv_shape(int total_rows, int nchunks, bool swiglu, bool f32_i
   static const int env_split = env_shape("LLAMA_HIP_GEMV_KSPLIT", 1, 8);
   static const int env_per_cu = env_shape("LLAMA_HIP_GEMV_BLOCKS_PER_CU", 1, 64);
   static const int env_waves = env_shape("LLAMA_HIP_GEMV_BLOCK_WAVES", 8, 16);
-  GemvShape g{nchunks <= 8 ? 2 : 4, 2, 16};
+  // waves per row by row length, measured: one for k <= 2048 (Llama-3.2-1B: QKV 5.0 -> 4.35 us, W1/W3 9.9 -> 9.1 us
+  // against two), two for k <= 4096 (the 8B shapes), four beyond (1B W2, k = 8192: 7.5 -> 6.6 us; 8B W2, k = 14336)
+  GemvShape g{nchunks <= 2 ? 1 : nchunks <= 4 ? 2 : 4, 2, 16};
   if (swiglu) {
     g.per_cu = 2;
     g.waves = 8;
