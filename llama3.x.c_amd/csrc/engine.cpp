@@ -73,17 +73,22 @@ struct Engine {
   AlignedBuffer panel{};
   // device memory
   float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *logits = nullptr;
-  float *rope = nullptr, *key_cache = nullptr, *value_cache = nullptr, *xs = nullptr, *hs = nullptr;
+  float *key_cache = nullptr, *value_cache = nullptr, *xs = nullptr, *hs = nullptr;
+  // the RoPE table of every position (2 * head_dim floats each), computed at load with the reference's expressions
+  float *rope_all = nullptr;
   int8_t *xq = nullptr, *hq = nullptr;
-  std::vector<float> host_logits;
+  int *token_dev = nullptr;
+  // pinned host memory: a decode token's id on its way in and its logits on the way out, so neither copy waits
+  int *token_host = nullptr;
+  float *host_logits = nullptr;
   AttentionWork work{};
   // the batched forward's rows (max_batch of each, allocated on its first call)
   int batch_rows = 0;
   float *bx = nullptr, *bxb = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *bhb = nullptr, *bxs = nullptr;
-  float *brope = nullptr, *blogits = nullptr;
+  float *blogits = nullptr;
   int8_t *bxq = nullptr;
   int *btokens = nullptr;
-  std::vector<float> host_rope, host_batch_logits;
+  std::vector<float> host_batch_logits;
 };
 
 template <typename T> T read_at(const unsigned char *p, size_t offset) {
@@ -99,7 +104,7 @@ template <typename T> void drop(T *&p) {
 }
 
 void free_batch(Engine *e) {
-  drop(e->bx), drop(e->bxb), drop(e->bq), drop(e->bk), drop(e->bv), drop(e->bhb), drop(e->bxs), drop(e->brope);
+  drop(e->bx), drop(e->bxb), drop(e->bq), drop(e->bk), drop(e->bv), drop(e->bhb), drop(e->bxs);
   drop(e->bxq), drop(e->btokens), drop(e->blogits);
   if (e->panel.base)
     aligned_buffer_free(&e->panel);
@@ -108,8 +113,12 @@ void free_batch(Engine *e) {
 
 void release(Engine *e) {
   free_batch(e);
-  drop(e->x), drop(e->xb), drop(e->q), drop(e->k), drop(e->v), drop(e->hb), drop(e->logits), drop(e->rope);
-  drop(e->key_cache), drop(e->value_cache), drop(e->xs), drop(e->hs), drop(e->xq), drop(e->hq);
+  drop(e->x), drop(e->xb), drop(e->q), drop(e->k), drop(e->v), drop(e->hb), drop(e->logits), drop(e->rope_all);
+  drop(e->key_cache), drop(e->value_cache), drop(e->xs), drop(e->hs), drop(e->xq), drop(e->hq), drop(e->token_dev);
+  if (e->token_host)
+    (void)hipHostFree(e->token_host);
+  if (e->host_logits)
+    (void)hipHostFree(e->host_logits);
   drop(e->packed), drop(e->cls_packed);
   if (e->map) {
     (void)llhip_unregister_host(e->map);
@@ -300,6 +309,26 @@ template <typename T> bool device_array(T **p, size_t count) {
   return *p != nullptr;
 }
 
+template <typename T> bool pinned(T **p, size_t count) {
+  if (hipHostMalloc((void **)p, count * sizeof(T), hipHostMallocDefault) == hipSuccess)
+    return true;
+  (void)hipGetLastError();
+  *p = nullptr;
+  return raise("engine: %zu bytes of pinned host memory could not be allocated", count * sizeof(T));
+}
+
+// The RoPE table rows of positions 0 .. seq_len - 1 (k_rope_table on the host: the reference's expressions and C
+// library, so each row is bitwise the one it makes per token), uploaded once; a token or a batch takes its rows in
+// place.
+bool rope_tables(Engine *e) {
+  const size_t row = 2 * (size_t)e->c.head_dim;
+  std::vector<float> host(row * e->c.seq_len);
+  for (int pos = 0; pos < e->c.seq_len; pos++)
+    k_rope_table(&e->c, pos, host.data() + (size_t)pos * row);
+  llhip_memcpy_h2d(e->rope_all, host.data(), host.size() * sizeof(float));
+  return llhip_last_error()[0] == 0;
+}
+
 bool allocate(Engine *e) {
   const Config &c = e->c;
   const size_t d = c.dim, kv = (size_t)c.head_dim * c.n_kv_heads, h = c.hidden_dim;
@@ -307,9 +336,10 @@ bool allocate(Engine *e) {
   const size_t groups = e->q8 ? (size_t)e->gs : 1;
   return device_array(&e->x, d) && device_array(&e->xb, d) && device_array(&e->q, d) && device_array(&e->k, kv) &&
          device_array(&e->v, kv) && device_array(&e->hb, h) && device_array(&e->logits, (size_t)c.vocab_size) &&
-         device_array(&e->rope, 2 * (size_t)c.head_dim) && device_array(&e->key_cache, cache) &&
+         device_array(&e->rope_all, 2 * (size_t)c.head_dim * c.seq_len) && device_array(&e->key_cache, cache) &&
          device_array(&e->value_cache, cache) && device_array(&e->xq, d) && device_array(&e->xs, d / groups) &&
-         device_array(&e->hq, h) && device_array(&e->hs, h / groups);
+         device_array(&e->hq, h) && device_array(&e->hs, h / groups) && device_array(&e->token_dev, 1) &&
+         pinned(&e->token_host, 1) && pinned(&e->host_logits, (size_t)c.vocab_size) && rope_tables(e);
 }
 
 // BF16 mode (src/tp.c:805-830): every layer's seven matrices packed once into the BF16 layout the GEMM reads
@@ -402,7 +432,6 @@ Engine *open_engine(Model *model, const char *path, int context, bool a32) {
   if (!allocate(e) || (e->bf16 && !pack_weights(e)))
     return release(e), nullptr;
   k_attention_init(&e->work, e->c.n_heads, e->c.n_kv_heads, e->c.head_dim, e->c.seq_len);
-  e->host_logits.resize((size_t)e->c.vocab_size);
   return e;
 }
 
@@ -415,11 +444,19 @@ bool forward(Engine *e, int token, int pos, bool want_logits) {
   const Config &c = e->c;
   const int d = c.dim, hidden = c.hidden_dim, hd = c.head_dim, gs = e->gs, nh = c.n_heads, nkv = c.n_kv_heads;
   const size_t kvl = (size_t)hd * nkv;
+  // the id goes in through pinned memory on the library's stream, behind the previous token's work (which ended
+  // with a synchronization, so the pinned word is free again)
+  *e->token_host = token;
+  if (!flush_pending_quantize() ||
+      hipMemcpyAsync(e->token_dev, e->token_host, sizeof(int), hipMemcpyHostToDevice, device().stream) != hipSuccess) {
+    (void)hipGetLastError();
+    return raise("engine_forward: copying the token id to the device failed");
+  }
   if (e->q8)
-    k_embed_q8_rows(e->x, e->embed.q(), e->embed.s, &token, 1, d, gs, c.vocab_size);
+    k_embed_q8_rows(e->x, e->embed.q(), e->embed.s, e->token_dev, 1, d, gs, c.vocab_size);
   else
-    k_embed_f32_rows(e->x, e->embed.f(), &token, 1, d, c.vocab_size);
-  k_rope_table(&c, pos, e->rope);
+    k_embed_f32_rows(e->x, e->embed.f(), e->token_dev, 1, d, c.vocab_size);
+  const float *rope = e->rope_all + (size_t)pos * 2 * hd;
   const bool head = kernels_kv_layout_head() != 0;
   // W8A8 quantizes each GEMV input (q8_input, src/tp.c:380-385); W8A32 hands the FP32 rows over instead
   const bool a32 = e->a32;
@@ -440,7 +477,7 @@ bool forward(Engine *e, int token, int pos, bool want_logits) {
       k_matmul_q8_qkv(e->q, k, v, &in_d, e->wq[l].k8(), e->wk[l].k8(), e->wv[l].k8(), d, d, (int)kvl, gs);
     else
       k_matmul_qkv(e->q, k, v, e->xb, e->wq[l].f(), e->wk[l].f(), e->wv[l].f(), d, d, (int)kvl);
-    k_rope_apply(e->q, k, e->rope, nh, nkv, hd);
+    k_rope_apply(e->q, k, rope, nh, nkv, hd);
     if (head) {
       k_kv_store(kc, k, kvl, pos, 1, nkv, hd, c.seq_len);
       k_kv_store(vc, v, kvl, pos, 1, nkv, hd, c.seq_len);
@@ -470,9 +507,14 @@ bool forward(Engine *e, int token, int pos, bool want_logits) {
       k_matmul_q8(e->logits, &in_x, e->cls.k8(), d, c.vocab_size, gs);
     else
       k_matmul(e->logits, e->x, e->cls.f(), d, c.vocab_size);
-    llhip_memcpy_d2h(e->host_logits.data(), e->logits, (size_t)c.vocab_size * sizeof(float));
+    if (!flush_pending_quantize() ||
+        hipMemcpyAsync(e->host_logits, e->logits, (size_t)c.vocab_size * sizeof(float), hipMemcpyDeviceToHost,
+                       device().stream) != hipSuccess) {
+      (void)hipGetLastError();
+      return raise("engine_forward: copying the logits to the host failed");
+    }
   }
-  llhip_synchronize(); // reports a non-finite activation or score of this token
+  llhip_synchronize(); // the logits have landed; reports a non-finite activation or score of this token
   return llhip_last_error()[0] == 0;
 }
 
@@ -484,7 +526,7 @@ bool allocate_batch(Engine *e, int rows) {
   const bool ok = device_array(&e->bx, m * d) && device_array(&e->bxb, m * d) && device_array(&e->bq, m * d) &&
                   device_array(&e->bk, m * kv) && device_array(&e->bv, m * kv) && device_array(&e->bhb, m * h) &&
                   device_array(&e->bxq, e->q8 ? m * h : 1) && device_array(&e->bxs, e->q8 ? m * h / groups : 1) &&
-                  device_array(&e->brope, m * 2 * c.head_dim) && device_array(&e->btokens, m);
+                  device_array(&e->btokens, m);
   if (ok && e->bf16) {
     aligned_buffer_alloc(&e->panel, k_gemm_bf16_panel_bytes(rows, c.dim > c.hidden_dim ? c.dim : c.hidden_dim),
                          MEM_ACTIVATION);
@@ -497,7 +539,6 @@ bool allocate_batch(Engine *e, int rows) {
     free_batch(e); // nothing stays claimed, and the next call tries again
     return false;
   }
-  e->host_rope.resize(m * 2 * c.head_dim);
   e->batch_rows = rows;
   return true;
 }
@@ -529,9 +570,7 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
   const int kvl = hd * nkv;
   if (!e->batch_rows && !allocate_batch(e, model->max_batch))
     return nullptr;
-  for (int i = 0; i < count; i++)
-    k_rope_table(&c, pos0 + i, e->host_rope.data() + (size_t)i * 2 * hd);
-  llhip_memcpy_h2d(e->brope, e->host_rope.data(), (size_t)count * 2 * hd * sizeof(float));
+  const float *brope = e->rope_all + (size_t)pos0 * 2 * hd; // rows pos0 .. pos0 + count - 1
   llhip_memcpy_h2d(e->btokens, tokens, (size_t)count * sizeof(int));
   if (e->q8)
     k_embed_q8_rows(e->bx, e->embed.q(), e->embed.s, e->btokens, count, d, gs, c.vocab_size);
@@ -557,7 +596,7 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
                                   {vd, kvl, e->wv[l].f(), nullptr, (size_t)d, kvl, GEMM_STORE}};
       gemm_f32_or_bf16(e, e->bxb, d, count, d, qkv, 3, l, kQkv, -1);
     }
-    k_rope_apply_rows(e->bq, d, kd, kvl, e->brope, 2 * (size_t)hd, count, nh, nkv, hd);
+    k_rope_apply_rows(e->bq, d, kd, kvl, brope, 2 * (size_t)hd, count, nh, nkv, hd);
     if (head) {
       k_kv_store(kc, kd, kvl, pos0, count, nkv, hd, c.seq_len);
       k_kv_store(vc, vd, kvl, pos0, count, nkv, hd, c.seq_len);
@@ -624,7 +663,7 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
     host = e->host_batch_logits.data();
     llhip_memcpy_d2h(host, e->blogits, (size_t)count * vocab * sizeof(float));
   } else {
-    host = e->host_logits.data();
+    host = e->host_logits;
     llhip_memcpy_d2h(host, e->logits, vocab * sizeof(float));
   }
   llhip_synchronize();
@@ -647,9 +686,9 @@ float *forward_batch(Model *model, Engine *e, const int *tokens, int count, int 
     if (!forward(e, tokens[i], pos0 + i, wanted))
       return nullptr;
     if (want == LOGITS_ALL)
-      memcpy(e->host_batch_logits.data() + (size_t)i * vocab, e->host_logits.data(), vocab * sizeof(float));
+      memcpy(e->host_batch_logits.data() + (size_t)i * vocab, e->host_logits, vocab * sizeof(float));
   }
-  return want == LOGITS_NONE ? nullptr : want == LOGITS_ALL ? e->host_batch_logits.data() : e->host_logits.data();
+  return want == LOGITS_NONE ? nullptr : want == LOGITS_ALL ? e->host_batch_logits.data() : e->host_logits;
 }
 
 } // namespace
@@ -704,7 +743,7 @@ float *engine_forward(Model *model, int token, int position) {
     raise("forward input out of range: token=%d position=%d", token, position); // src/engine.c:171-172
     return nullptr;
   }
-  return forward(e, token, position, true) ? e->host_logits.data() : nullptr;
+  return forward(e, token, position, true) ? e->host_logits : nullptr;
 }
 
 float *engine_forward_batch(Model *model, const int *tokens, int count, int pos0, LogitsWanted want) {
