@@ -350,12 +350,14 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
 //     q * HD / 4 + kk), so a lane's share of its query vector is HD / 4 consecutive floats held in registers and its
 //     K reads are 16-byte runs;
 //   - masks the positions past each row's own (causal), takes the chunk maximum and the running maximum, rescales
-//     its running sum and value sums by exp(m_old - m_new), and forms p = exp(s - m_new);
+//     its running sum and value sums by exp(m_old - m_new), and forms p = exp(s - m_new); the scores are kept in base
+//     2 (s * log2(e) / divisor, one multiply where the split form divides), so each exponential is the native exp2;
 //   - adds P V to its value sums as O^T = V^T P^T: the score accumulators are the B operand as they stand (MFMA step
 //     (tile t, element e) takes positions 16 t + 4 q + e from lane group q), and V^T is read from LDS, value tile d
 //     holding dimensions HD / 16 * m + d (m = 0..15), so a lane's values of a position are consecutive.
 // At the end each vector's value sum is divided by its running sum and stored. Every product is FP32 on the matrix
-// cores; the sums run in other orders than the split form's, within FP32 rounding of the same softmax.
+// cores; the sums run in other orders than the split form's and the scores are rounded once more, within FP32
+// rounding of the same softmax.
 template <int HD> struct FlashStage {
   static constexpr int kPer = kChunk * (HD / 4) / kTileThreads; // float4 of K (and of V) per thread and chunk
   float4 k[kPer], v[kPer];
@@ -396,6 +398,8 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
   const int lq = lane >> 4, lc = lane & 15;
   const int qv = wave * 16 + lc, j = qv / kv_mul, h = qv % kv_mul;
   const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
+  // scores in base 2: s * log2(e) / divisor, so that exp(s / divisor - m) is the native exp2 of (s2 - m2)
+  const float scale2 = 1.4426950408889634f / p.divisor;
   bool bad = false;
   for (int pass = 0; pass < 2; pass++) {
     const int tile = pass == 0 ? ntiles - 1 - (int)blockIdx.x : (int)blockIdx.x;
@@ -469,7 +473,7 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
           const bool live = active && at <= pos;
           float s = -FLT_MAX;
           if (live) {
-            s = sc[t][e] / p.divisor;
+            s = sc[t][e] * scale2;
             bad |= !isfinite(s);
           }
           sc[t][e] = s;
@@ -478,13 +482,13 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
       cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
       const float m_new = fmaxf(m_run, cmax);
-      const float alpha = expf(m_run - m_new); // 0 before the first live position, 1 when the maximum stays
+      const float alpha = exp2f(m_run - m_new); // 0 before the first live position, 1 when the maximum stays
       float psum = 0.0f;
 #pragma unroll
       for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const float pe = sc[t][e] > -FLT_MAX ? expf(sc[t][e] - m_new) : 0.0f;
+          const float pe = sc[t][e] > -FLT_MAX ? exp2f(sc[t][e] - m_new) : 0.0f;
           sc[t][e] = pe;
           psum += pe;
         }
