@@ -15,6 +15,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "lanes.h"
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
@@ -30,20 +31,6 @@ constexpr int kMaxGroup = 16;   // query heads per KV head
 bool launch_ok(const char *what) {
   const hipError_t e = hipGetLastError();
   return e == hipSuccess || raise("launching %s failed: %s", what, hipGetErrorString(e));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1)
-    v += __shfl_xor(v, o);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1)
-    v = fmaxf(v, __shfl_xor(v, o));
-  return v;
 }
 
 // ---- RMSNorm -----------------------------------------------------------------------------------------------------
@@ -104,12 +91,23 @@ __device__ __forceinline__ void rotate(float *v, float c, float s) {
   v[1] = a * s + b * c;
 }
 
-// Two pairs (j0, j0 + 1) and (j0 + 2, j0 + 3) of a row, rotated like rotate() (c = table[j], s = table[hd + j + 1]).
-__device__ __forceinline__ float4 rotate4(float4 v, const float *table, int hd, int j0) {
+// The cosines and sines of the pairs (j0, j0 + 1) and (j0 + 2, j0 + 3) of a row: c = table[j], s = table[hd + j + 1].
+struct Rot4 {
+  float c0, s0, c1, s1;
+};
+__device__ __forceinline__ Rot4 rot4_of(const float *table, int hd, int j0) {
+  return Rot4{table[j0], table[hd + j0 + 1], table[j0 + 2], table[hd + j0 + 3]};
+}
+
+// Two pairs of a row rotated like rotate(), by the cosines and sines of rot4_of.
+__device__ __forceinline__ float4 rotate4(float4 v, const Rot4 &r) {
   float a[2] = {v.x, v.y}, b[2] = {v.z, v.w};
-  rotate(a, table[j0], table[hd + j0 + 1]);
-  rotate(b, table[j0 + 2], table[hd + j0 + 3]);
+  rotate(a, r.c0, r.s0);
+  rotate(b, r.c1, r.s1);
   return float4{a[0], a[1], b[0], b[1]};
+}
+__device__ __forceinline__ float4 rotate4(float4 v, const float *table, int hd, int j0) {
+  return rotate4(v, rot4_of(table, hd, j0));
 }
 
 // Thread i: row i / (n_heads * half), head and pair from the rest; k is rotated for heads below n_kv_heads.
@@ -207,6 +205,7 @@ constexpr int kTileThreads = 512;
 constexpr int kTileWaves = kTileThreads / kWave;
 constexpr int kMaxQv = 64; // query vectors (tile rows x the group's query heads) per attn_tile block
 constexpr int kQvGroup = 4; // query vectors per pass in the batched form
+constexpr int kTileLoads = 4; // K, V and query items per thread loaded together (64 positions x 128 dimensions)
 
 // The aligned form (head_dim % 4 == 0, 16-byte aligned rows): block (chunk c, KV head g, tile of tile_rows query rows).
 // The chunk's K rows and the tile's query vectors are staged in LDS (K rows padded to head_dim + 4 floats, so lane t's
@@ -218,7 +217,9 @@ constexpr int kQvGroup = 4; // query vectors per pass in the batched form
 // GROUP > 1 (batched rows, every tile's query-vector count a multiple of GROUP): a wave scores GROUP query vectors per
 // pass over its lane's K row and a thread sums GROUP vectors' values per V read, so each K or V value read from LDS
 // serves GROUP products; every dot and sum keeps its order of terms, so the results equal GROUP = 1's.
-template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(AttnParams p) {
+// HD: the head dimension when it is known at compile time (64 or 128; 0 takes p.head_dim), so the dot and the value
+// sums unroll and their LDS reads are issued ahead of the products instead of one latency per step.
+template <int GROUP, int HD> __global__ __launch_bounds__(kTileThreads) void attn_tile(AttnParams p) {
   extern __shared__ __align__(16) float lds[];
   const int c = blockIdx.x, g = blockIdx.y, r0 = blockIdx.z * p.tile_rows;
   const int nrows = min(p.tile_rows, p.rows - r0);
@@ -227,19 +228,70 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
   if (t0 > last)
     return; // no row of the tile reaches this chunk; the merge reads only each row's own chunks
   const int n = min(kChunk, last + 1 - t0);
-  const int kv_mul = p.n_heads / p.n_kv_heads, hd = p.head_dim, hd4 = hd / 4, kst = hd + 4;
+  const int kv_mul = p.n_heads / p.n_kv_heads, hd = HD ? HD : p.head_dim, hd4 = hd / 4, kst = hd + 4;
   const int nqv = nrows * kv_mul;
   float *ks = lds, *vs = ks + kChunk * kst, *qs = vs + kChunk * hd, *es = qs + p.tile_rows * kv_mul * hd;
   const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
   const bool fresh = p.table != nullptr; // decode with the RoPE and the new cache row folded in
-  // every K and V load of the chunk is issued before any is waited for; V lands while the scores are computed
-  for (int i = threadIdx.x; i < n * hd4; i += kTileThreads) {
+  // Loads: work item i is 4 dimensions (d4) of K row t (and of V row t) and of query vector qv, i = t * hd4 + d4 =
+  // qv * hd4 + d4. The first kTileLoads items of each thread are loaded together, K, the query vectors (and the RoPE
+  // factors) first and V last, and nothing waits for V before the scores are computed. Row and query indices past
+  // the chunk's or tile's last clamp to it, so every one of those loads reads a valid address; only items in range
+  // are stored. The new row (fresh: it lies in this chunk, which no other block reads) comes from the QKV outputs.
+  const int kv_items = n * hd4, q_items = nqv * hd4;
+  float4 kr[kTileLoads], qr[kTileLoads];
+  Rot4 rot[kTileLoads];
+#pragma unroll
+  for (int u = 0; u < kTileLoads; u++) {
+    const int i = threadIdx.x + u * kTileThreads, d4 = i % hd4;
+    const int t = min(i / hd4, n - 1), qv = min(i / hd4, nqv - 1), j = qv / kv_mul, h = qv % kv_mul;
+    const bool novel = fresh && t0 + t == p.pos0;
+    const size_t at = (size_t)(t0 + t) * p.pos_stride + 4 * d4, src = (size_t)g * hd + 4 * d4;
+    kr[u] = *reinterpret_cast<const float4 *>(novel ? p.k_new + src : kbase + at);
+    qr[u] = *reinterpret_cast<const float4 *>(p.q + ((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * hd +
+                                              4 * d4);
+    if (fresh)
+      rot[u] = rot4_of(p.table, hd, 4 * d4);
+  }
+  // V stays in four named registers through the scores (an array indexed after the score loop went to scratch)
+  auto v_load = [&](int u) {
+    const int i = threadIdx.x + u * kTileThreads, d4 = i % hd4, t = min(i / hd4, n - 1);
+    const bool novel = fresh && t0 + t == p.pos0;
+    return *reinterpret_cast<const float4 *>(novel ? p.v_new + (size_t)g * hd + 4 * d4
+                                                   : vbase + (size_t)(t0 + t) * p.pos_stride + 4 * d4);
+  };
+  auto v_store = [&](int u, const float4 &v) {
+    const int i = threadIdx.x + u * kTileThreads, t = i / hd4, d4 = i % hd4;
+    if (i < kv_items) {
+      if (fresh && t0 + t == p.pos0)
+        *reinterpret_cast<float4 *>(const_cast<float *>(vbase) + (size_t)(t0 + t) * p.pos_stride + 4 * d4) = v;
+      *reinterpret_cast<float4 *>(vs + t * hd + 4 * d4) = v;
+    }
+  };
+  static_assert(kTileLoads == 4, "four V registers");
+  const float4 vr0 = v_load(0), vr1 = v_load(1), vr2 = v_load(2), vr3 = v_load(3);
+#pragma unroll
+  for (int u = 0; u < kTileLoads; u++) {
+    const int i = threadIdx.x + u * kTileThreads, t = i / hd4, d4 = i % hd4;
+    if (i < kv_items) {
+      float4 kv = kr[u];
+      if (fresh && t0 + t == p.pos0) { // k rotated, stored into the cache and written back rotated
+        kv = rotate4(kv, rot[u]);
+        const size_t src = (size_t)g * hd + 4 * d4, at = (size_t)(t0 + t) * p.pos_stride + 4 * d4;
+        *reinterpret_cast<float4 *>(p.k_new + src) = kv;
+        *reinterpret_cast<float4 *>(const_cast<float *>(kbase) + at) = kv;
+      }
+      *reinterpret_cast<float4 *>(ks + t * kst + 4 * d4) = kv;
+    }
+    if (i < q_items) // every block rotates its own copy; attn_merge writes q back rotated once all blocks have read it
+      *reinterpret_cast<float4 *>(qs + i / hd4 * hd + 4 * d4) = fresh ? rotate4(qr[u], rot[u]) : qr[u];
+  }
+  // items past the first kTileLoads per thread (head_dim above 128, or more than 2048 query values)
+  for (int i = threadIdx.x + kTileLoads * kTileThreads; i < kv_items; i += kTileThreads) {
     const int t = i / hd4, d4 = i % hd4;
     const size_t at = (size_t)(t0 + t) * p.pos_stride + 4 * d4;
     float4 kv, vv;
     if (fresh && t0 + t == p.pos0) {
-      // the new row, from the QKV outputs: k rotated, both stored into the caches and k written back rotated (this
-      // block is the only reader of the position: it lies in the last chunk)
       const size_t src = (size_t)g * hd + 4 * d4;
       kv = rotate4(*reinterpret_cast<const float4 *>(p.k_new + src), p.table, hd, 4 * d4);
       vv = *reinterpret_cast<const float4 *>(p.v_new + src);
@@ -253,11 +305,11 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
     *reinterpret_cast<float4 *>(ks + t * kst + 4 * d4) = kv;
     *reinterpret_cast<float4 *>(vs + t * hd + 4 * d4) = vv;
   }
-  for (int i = threadIdx.x; i < nqv * hd4; i += kTileThreads) {
+  for (int i = threadIdx.x + kTileLoads * kTileThreads; i < q_items; i += kTileThreads) {
     const int qv = i / hd4, d4 = i % hd4, j = qv / kv_mul, h = qv % kv_mul;
     const size_t at = ((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * hd + 4 * d4;
     float4 v = *reinterpret_cast<const float4 *>(p.q + at);
-    if (fresh) // every block rotates its own copy; attn_merge writes q back rotated once all blocks have read it
+    if (fresh)
       v = rotate4(v, p.table, hd, 4 * d4);
     *reinterpret_cast<float4 *>(qs + qv * hd + 4 * d4) = v;
   }
@@ -271,15 +323,46 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
       dots[u] = 0.0f;
     if (lane < n && t0 + lane <= p.pos0 + r0 + (q0 + GROUP - 1) / kv_mul) { // live for some vector of the group
       const float *kr = ks + lane * kst, *qr = qs + q0 * hd;
-      for (int i = 0; i < hd; i += 4) {
-        const float4 a = *reinterpret_cast<const float4 *>(kr + i);
+      auto add4 = [&](const float4 &a, const float4 &b, float &dot) {
+        dot = fmaf(a.x, b.x, dot);
+        dot = fmaf(a.y, b.y, dot);
+        dot = fmaf(a.z, b.z, dot);
+        dot = fmaf(a.w, b.w, dot);
+      };
+      if constexpr (HD > 0) {
+        // batches of B float4 of K (and of each query vector), the next batch's reads issued before this batch's
+        // products, so one LDS latency is exposed per dot rather than one per step; same order of terms
+        constexpr int B = GROUP >= 4 ? 1 : 4 / GROUP, NB = HD / (4 * B);
+        static_assert(HD % (4 * B) == 0, "whole batches");
+        float4 kb[2][B], qb[2][B][GROUP];
+        auto load = [&](int slot, int i0) {
 #pragma unroll
-        for (int u = 0; u < GROUP; u++) {
-          const float4 b = *reinterpret_cast<const float4 *>(qr + u * hd + i);
-          dots[u] = fmaf(a.x, b.x, dots[u]);
-          dots[u] = fmaf(a.y, b.y, dots[u]);
-          dots[u] = fmaf(a.z, b.z, dots[u]);
-          dots[u] = fmaf(a.w, b.w, dots[u]);
+          for (int b = 0; b < B; b++) {
+            kb[slot][b] = *reinterpret_cast<const float4 *>(kr + i0 + 4 * b);
+#pragma unroll
+            for (int u = 0; u < GROUP; u++)
+              qb[slot][b][u] = *reinterpret_cast<const float4 *>(qr + u * HD + i0 + 4 * b);
+          }
+        };
+        load(0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+          if (nb + 1 < NB)
+            load((nb + 1) & 1, 4 * B * (nb + 1));
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int b = 0; b < B; b++)
+#pragma unroll
+            for (int u = 0; u < GROUP; u++)
+              add4(kb[nb & 1][b], qb[nb & 1][b][u], dots[u]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        for (int i = 0; i < hd; i += 4) {
+          const float4 a = *reinterpret_cast<const float4 *>(kr + i);
+#pragma unroll
+          for (int u = 0; u < GROUP; u++)
+            add4(a, *reinterpret_cast<const float4 *>(qr + u * hd + i), dots[u]);
         }
       }
     }
@@ -306,6 +389,10 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
   }
   if (bad)
     p.flags[1] = 1;
+  v_store(0, vr0);
+  v_store(1, vr1);
+  v_store(2, vr2);
+  v_store(3, vr3);
   __syncthreads();
   // value sums: work item (query vector, 4 consecutive dimensions), the exponentials of its row against the V rows
   for (int it = threadIdx.x; it < nqv / GROUP * hd4; it += kTileThreads) {
@@ -317,7 +404,7 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
 #pragma unroll
     for (int u = 0; u < GROUP; u++)
       acc[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int t = 0; t < n; t++) {
+    auto add_row = [&](int t) {
       const float4 v = *reinterpret_cast<const float4 *>(vr + t * hd);
 #pragma unroll
       for (int u = 0; u < GROUP; u++) {
@@ -327,6 +414,14 @@ template <int GROUP> __global__ __launch_bounds__(kTileThreads) void attn_tile(A
         acc[u].z = fmaf(e, v.z, acc[u].z);
         acc[u].w = fmaf(e, v.w, acc[u].w);
       }
+    };
+    if (n == kChunk) { // a whole chunk: unrolled, the reads of later rows in flight while earlier rows are summed
+#pragma unroll 16
+      for (int t = 0; t < kChunk; t++)
+        add_row(t);
+    } else {
+      for (int t = 0; t < n; t++)
+        add_row(t);
     }
 #pragma unroll
     for (int u = 0; u < GROUP; u++) {
@@ -647,10 +742,12 @@ __global__ __launch_bounds__(kThreads) void attn_chunks(AttnParams p) {
 }
 
 // Block (head h, query row r): M = max over the row's chunks of m_c, weight_c = expf(m_c - M), L = sum of
-// weight_c * l_c, out = (sum of weight_c * o_c) / L. The chunks are spread over the threads (every load in flight at
-// once, not one chunk after another): the maxima and weights by chunk, the value sums by (dimension, chunk group), the
-// groups meeting in LDS.
+// weight_c * l_c, out = (sum of weight_c * o_c) / L. The chunks are spread over the threads: the maxima and weights
+// by chunk, the value sums by (dimension, chunk group), the groups meeting in LDS. Thread c holds chunk c's m_c and
+// l_c, and each (dimension, group) thread its first kMergeHeld values o_c, all loaded together before the first
+// reduction, so the block waits for the partials once (twice past 256 chunks or kMergeHeld chunks per group).
 constexpr int kMaxMergeChunks = 4096; // 262144 positions
+constexpr int kMergeHeld = 32;
 
 __device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_max) {
   v = is_max ? wave_max(v) : wave_sum(v);
@@ -670,12 +767,29 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
   const int h = blockIdx.x, r = blockIdx.y;
   const int hd = p.head_dim, chunks = (p.pos0 + r) / kChunk + 1;
   const float *part = p.partial + ((size_t)(r * p.n_heads + h) * p.chunks) * p.slot;
-  float m = -FLT_MAX;
-  for (int c = threadIdx.x; c < chunks; c += kThreads)
+  const int groups = kThreads / hd > 0 ? kThreads / hd : 1;
+  const int d = threadIdx.x % hd, grp = threadIdx.x / hd;
+  const bool summer = grp < groups;
+  float held[kMergeHeld];
+#pragma unroll
+  for (int k = 0; k < kMergeHeld; k++) {
+    const int c = grp + k * groups;
+    held[k] = summer && c < chunks ? part[(size_t)c * p.slot + d] : 0.0f;
+  }
+  const bool mine = threadIdx.x < chunks;
+  const float m0 = mine ? part[(size_t)threadIdx.x * p.slot + hd] : -FLT_MAX;
+  const float l0 = mine ? part[(size_t)threadIdx.x * p.slot + hd + 1] : 0.0f;
+  float m = m0;
+  for (int c = threadIdx.x + kThreads; c < chunks; c += kThreads)
     m = fmaxf(m, part[(size_t)c * p.slot + hd]);
   m = block_reduce(m, red, true);
   float l = 0.0f;
-  for (int c = threadIdx.x; c < chunks; c += kThreads) {
+  if (mine) {
+    const float w = expf(m0 - m);
+    weight[threadIdx.x] = w;
+    l = w * l0;
+  }
+  for (int c = threadIdx.x + kThreads; c < chunks; c += kThreads) {
     const float w = expf(part[(size_t)c * p.slot + hd] - m);
     weight[c] = w;
     l += w * part[(size_t)c * p.slot + hd + 1];
@@ -687,12 +801,15 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
       *reinterpret_cast<float4 *>(qh + 4 * d4) =
           rotate4(*reinterpret_cast<const float4 *>(qh + 4 * d4), p.table, hd, 4 * d4);
   }
-  const int groups = kThreads / hd > 0 ? kThreads / hd : 1;
-  const int d = threadIdx.x % hd, grp = threadIdx.x / hd;
   float o = 0.0f;
-  if (grp < groups && d < hd) {
+  if (summer) {
+    // branch-free, so every weight read is in flight at once: past the last chunk the held value is zero and the
+    // weight read is clamped to the last chunk's (the product adds an exact zero)
+#pragma unroll
+    for (int k = 0; k < kMergeHeld; k++)
+      o = fmaf(weight[min(grp + k * groups, chunks - 1)], held[k], o);
 #pragma unroll 8
-    for (int c = grp; c < chunks; c += groups)
+    for (int c = grp + kMergeHeld * groups; c < chunks; c += groups)
       o = fmaf(weight[c], part[(size_t)c * p.slot + d], o);
   }
   red[threadIdx.x] = o;
@@ -861,24 +978,28 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
   if (aligned) {
     p.tile_rows = attention_tile_rows(job.rows, kv_mul, job.head_dim);
     const size_t lds = attention_tile_lds(p.tile_rows, kv_mul, job.head_dim);
+    typedef void (*TileKernel)(AttnParams);
+    // [grouped][head_dim 128, 64, other]
+    static const TileKernel kernels[2][3] = {{attn_tile<1, 128>, attn_tile<1, 64>, attn_tile<1, 0>},
+                                             {attn_tile<kQvGroup, 128>, attn_tile<kQvGroup, 64>, attn_tile<kQvGroup, 0>}};
     static const hipError_t allowed = [] {
-      const hipError_t e1 =
-          hipFuncSetAttribute((const void *)attn_tile<1>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      return e1 != hipSuccess ? e1
-                              : hipFuncSetAttribute((const void *)attn_tile<kQvGroup>,
-                                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      for (const auto &row : kernels)
+        for (TileKernel k : row) {
+          const hipError_t e =
+              hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+          if (e != hipSuccess)
+            return e;
+        }
+      return hipSuccess;
     }();
     if (allowed != hipSuccess)
       return raise("allowing the attention kernel its LDS failed: %s", hipGetErrorString(allowed));
     const unsigned tiles = (unsigned)((job.rows + p.tile_rows - 1) / p.tile_rows);
     // the grouped form needs every tile's query-vector count (rows x kv_mul) to be a multiple of the group
     const bool grouped = job.rows > 1 && kv_mul % kQvGroup == 0;
-    if (grouped)
-      hipLaunchKernelGGL(attn_tile<kQvGroup>, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, tiles),
-                         dim3(kTileThreads), lds, stream, p);
-    else
-      hipLaunchKernelGGL(attn_tile<1>, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, tiles), dim3(kTileThreads),
-                         lds, stream, p);
+    const TileKernel kernel = kernels[grouped][job.head_dim == 128 ? 0 : job.head_dim == 64 ? 1 : 2];
+    hipLaunchKernelGGL(kernel, dim3((unsigned)p.chunks, (unsigned)job.n_kv_heads, tiles), dim3(kTileThreads), lds,
+                       stream, p);
     if (!launch_ok("attn_tile"))
       return false;
   } else {
