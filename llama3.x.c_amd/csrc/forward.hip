@@ -250,7 +250,7 @@ template <int GROUP, int HD> __global__ __launch_bounds__(kTileThreads) void att
     kr[u] = *reinterpret_cast<const float4 *>(novel ? p.k_new + src : kbase + at);
     qr[u] = *reinterpret_cast<const float4 *>(p.q + ((size_t)(r0 + j) * p.n_heads + (size_t)g * kv_mul + h) * hd +
                                               4 * d4);
-    if (fresh)
+    if (fresh && (i < q_items || novel)) // the RoPE factors only where a query value or the new K row needs them
       rot[u] = rot4_of(p.table, hd, 4 * d4);
   }
   // V stays in four named registers through the scores (an array indexed after the score loop went to scratch)
