@@ -434,6 +434,179 @@ template <int GROUP, int HD> __global__ __launch_bounds__(kTileThreads) void att
   }
 }
 
+// Decode (one query row; the kv_mul query vectors of KV head g share every K and V row). Block (chunk c, KV head g),
+// 512 threads, HD dimensions known at compile time (64 or 128), kv_mul <= 8:
+//   - K rows go from global memory straight into registers, read once for all the vectors (no LDS copy): wave w holds
+//     rows 8 w .. 8 w + 7, eight lanes a row, lane ds of a row its float4 ds, ds + 8, ... (each load instruction reads
+//     128 contiguous bytes of eight rows). A lane forms its partial dot with every query vector (read from LDS), and
+//     the row's eight lanes add theirs by DPP, so every dot is whole in registers;
+//   - wave v then masks vector v's 64 scores, takes the chunk maximum, the exponentials and their sum as attn_tile
+//     does, while the other waves store the V rows (whose loads land meanwhile) into LDS;
+//   - the value sums run over all 512 threads: item (vector, four dimensions) and a slice of the chunk's positions,
+//     the position slices added in order in LDS.
+// Each dot and value sum is attn_tile's sum in another association (within FP32 rounding). With the fused RoPE (table
+// set), the new row's lanes rotate their K values and store them into the cache and back into k_new, and the V item
+// threads of that row store it into the cache, as attn_tile does.
+constexpr int kDecodeMaxQv = 8;
+template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_decode(AttnParams p) {
+  extern __shared__ __align__(16) float lds[];
+  constexpr int HD4 = HD / 4, KPER = HD4 / 8, VPER = kChunk * HD4 / kTileThreads;
+  static_assert(KPER >= 1 && kChunk == 8 * kTileWaves && kChunk * HD4 % kTileThreads == 0, "rows and V items");
+  const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const int t0 = c * kChunk;
+  if (t0 > p.pos0)
+    return; // past the row's position; the merge reads only its own chunks
+  const int n = min(kChunk, p.pos0 + 1 - t0);
+  const int nqv = p.n_heads / p.n_kv_heads; // query vectors of the KV head (<= kDecodeMaxQv)
+  float *vs = lds, *qs = vs + kChunk * HD, *dots = qs + nqv * HD, *es = dots + nqv * kChunk;
+  float4 *po = reinterpret_cast<float4 *>(es + nqv * kChunk);
+  const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
+  const bool fresh = p.table != nullptr;
+  const int lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int row = 8 * wave + lane / 8, ds = lane % 8; // this lane's K row and its place in the row
+  const int t = min(row, n - 1);                      // clamped: rows past the chunk's end are masked
+  const bool novel_k = fresh && t0 + t == p.pos0;
+  const float4 zero4 = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  // RoPE factors as two float4 of the table: cosines at j0 .. j0 + 3, sines at HD + j0 .. HD + j0 + 3
+  auto factors = [&](const float4 &cs, const float4 &sn) { return Rot4{cs.x, sn.y, cs.z, sn.w}; };
+
+  // Loads, all issued before the first wait: this lane's K values, one query item, the V items.
+  float4 kreg[KPER], kcos[KPER], ksin[KPER];
+#pragma unroll
+  for (int s = 0; s < KPER; s++) {
+    const int d4 = 8 * s + ds;
+    kreg[s] = *reinterpret_cast<const float4 *>(novel_k ? p.k_new + (size_t)g * HD + 4 * d4
+                                                        : kbase + (size_t)(t0 + t) * p.pos_stride + 4 * d4);
+    kcos[s] = ksin[s] = zero4;
+    if (novel_k) {
+      kcos[s] = *reinterpret_cast<const float4 *>(p.table + 4 * d4);
+      ksin[s] = *reinterpret_cast<const float4 *>(p.table + HD + 4 * d4);
+    }
+  }
+  const bool has_q = tid < nqv * HD4;
+  const int qv = has_q ? tid / HD4 : 0, qd4 = tid % HD4;
+  float4 qreg = zero4, qcos = zero4, qsin = zero4;
+  if (has_q) {
+    qreg = *reinterpret_cast<const float4 *>(p.q + ((size_t)g * nqv + qv) * HD + 4 * qd4);
+    if (fresh) {
+      qcos = *reinterpret_cast<const float4 *>(p.table + 4 * qd4);
+      qsin = *reinterpret_cast<const float4 *>(p.table + HD + 4 * qd4);
+    }
+  }
+  // V items in named registers (an array indexed across the dot phase was placed in scratch)
+  auto v_load = [&](int u) {
+    const int i = tid + u * kTileThreads, tv = min(i / HD4, n - 1), d4 = i % HD4;
+    const bool novel_v = fresh && t0 + tv == p.pos0;
+    return *reinterpret_cast<const float4 *>(novel_v ? p.v_new + (size_t)g * HD + 4 * d4
+                                                     : vbase + (size_t)(t0 + tv) * p.pos_stride + 4 * d4);
+  };
+  auto v_store = [&](int u, const float4 &x) {
+    const int i = tid + u * kTileThreads, tv = i / HD4, d4 = i % HD4;
+    *reinterpret_cast<float4 *>(vs + tv * HD + 4 * d4) = x;
+    if (fresh && tv < n && t0 + tv == p.pos0)
+      *reinterpret_cast<float4 *>(const_cast<float *>(vbase) + (size_t)(t0 + tv) * p.pos_stride + 4 * d4) = x;
+  };
+  static_assert(VPER == 2 || VPER == 4, "two or four V items per thread");
+  const float4 v0 = v_load(0), v1 = v_load(1), v2 = VPER == 4 ? v_load(2) : zero4, v3 = VPER == 4 ? v_load(3) : zero4;
+  if (novel_k) { // the new row's K: rotated; the lanes of the real row store it into the cache and back into k_new
+#pragma unroll
+    for (int s = 0; s < KPER; s++) {
+      kreg[s] = rotate4(kreg[s], factors(kcos[s], ksin[s]));
+      if (row == t) {
+        const int d4 = 8 * s + ds;
+        *reinterpret_cast<float4 *>(p.k_new + (size_t)g * HD + 4 * d4) = kreg[s];
+        *reinterpret_cast<float4 *>(const_cast<float *>(kbase) + (size_t)(t0 + t) * p.pos_stride + 4 * d4) = kreg[s];
+      }
+    }
+  }
+  if (has_q) // every block rotates its own copy; attn_merge writes q back rotated once all blocks have read it
+    *reinterpret_cast<float4 *>(qs + qv * HD + 4 * qd4) = fresh ? rotate4(qreg, factors(qcos, qsin)) : qreg;
+  __syncthreads();
+  // every vector's dot with this lane's row: the lane's values in order, then the row's eight lanes by DPP
+  for (int v = 0; v < nqv; v++) {
+    float dot = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KPER; s++) {
+      const float4 a = kreg[s], b = *reinterpret_cast<const float4 *>(qs + v * HD + 4 * (8 * s + ds));
+      dot = fmaf(a.x, b.x, dot);
+      dot = fmaf(a.y, b.y, dot);
+      dot = fmaf(a.z, b.z, dot);
+      dot = fmaf(a.w, b.w, dot);
+    }
+    dot = group_reduce_add(dot, 8);
+    if (ds == 0)
+      dots[v * kChunk + row] = dot;
+  }
+  __syncthreads();
+  if (wave < nqv) { // wave v scores vector v
+    const int v = wave;
+    const bool live = lane < n;
+    float sc = -FLT_MAX;
+    bool bad = false;
+    if (live) {
+      sc = dots[v * kChunk + lane] / p.divisor;
+      bad = !isfinite(sc);
+    }
+    const float m = wave_max(sc);
+    const float e = live ? expf(sc - m) : 0.0f;
+    es[v * kChunk + lane] = e;
+    const float l = wave_sum(e);
+    if (lane == 0) {
+      float *ph = p.partial + (((size_t)g * nqv + v) * p.chunks + c) * p.slot;
+      ph[HD] = m;
+      ph[HD + 1] = l;
+    }
+    if (bad)
+      p.flags[1] = 1;
+  }
+  v_store(0, v0);
+  v_store(1, v1);
+  if constexpr (VPER == 4) {
+    v_store(2, v2);
+    v_store(3, v3);
+  }
+  __syncthreads();
+  // value sums: item (vector, four dimensions) over position slice `slice` of the chunk, sixteen positions at a time
+  const int items = nqv * HD4, slices = kTileThreads / items, span = (kChunk + slices - 1) / slices;
+  const int slice = tid / items, item = tid % items, v = item / HD4, d4 = item % HD4;
+  if (slice < slices) {
+    const int ta = slice * span, tb = min(n, ta + span);
+    const float *er = es + v * kChunk, *vr = vs + 4 * d4;
+    float4 acc = zero4;
+    for (int t1 = ta; t1 < tb; t1 += 16) {
+      // branch-free (each position's reads in flight together): a position past the slice adds 0 times a staged row
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        const int tt = min(t1 + k, kChunk - 1);
+        const float e = t1 + k < tb ? er[tt] : 0.0f;
+        const float4 x = *reinterpret_cast<const float4 *>(vr + tt * HD);
+        acc.x = fmaf(e, x.x, acc.x);
+        acc.y = fmaf(e, x.y, acc.y);
+        acc.z = fmaf(e, x.z, acc.z);
+        acc.w = fmaf(e, x.w, acc.w);
+      }
+    }
+    po[slice * items + item] = acc;
+  }
+  __syncthreads();
+  if (tid < items) {
+    float4 total = po[item];
+    for (int sl = 1; sl < slices; sl++) {
+      const float4 x = po[sl * items + item];
+      total.x += x.x;
+      total.y += x.y;
+      total.z += x.z;
+      total.w += x.w;
+    }
+    *reinterpret_cast<float4 *>(p.partial + (((size_t)g * nqv + v) * p.chunks + c) * p.slot + 4 * d4) = total;
+  }
+}
+
+size_t attention_decode_lds(int kv_mul, int head_dim) {
+  return ((size_t)kChunk * head_dim + (size_t)kv_mul * head_dim + 2 * (size_t)kv_mul * kChunk) * sizeof(float) +
+         (size_t)kTileThreads * 16;
+}
+
 // Batched attention on the FP32 matrix cores (flash form): query rows in tiles of 128 / kv_mul (the tile's 128 query
 // vectors: row j, query head h of the group as vector j * kv_mul + h, in 8 waves of 16). Block (p, KV head g) takes
 // tile T - 1 - p and then tile p, so every block has about the same number of causal chunks (one block per CU). Per
@@ -975,7 +1148,19 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
       hipLaunchKernelGGL(attn_flash<64>, grid, dim3(kTileThreads), lds, stream, p);
     return launch_ok("attn_flash");
   }
-  if (aligned) {
+  // decode: the slice-parallel kernel for 64 or 128 dimensions and up to eight query vectors per KV head
+  if (aligned && job.rows == 1 && (job.head_dim == 64 || job.head_dim == 128) && kv_mul <= kDecodeMaxQv &&
+      kv_mul * job.head_dim / 4 <= kTileThreads) {
+    p.tile_rows = 1;
+    const dim3 grid((unsigned)p.chunks, (unsigned)job.n_kv_heads);
+    const size_t lds = attention_decode_lds(kv_mul, job.head_dim);
+    if (job.head_dim == 128)
+      hipLaunchKernelGGL(attn_decode<128>, grid, dim3(kTileThreads), lds, stream, p);
+    else
+      hipLaunchKernelGGL(attn_decode<64>, grid, dim3(kTileThreads), lds, stream, p);
+    if (!launch_ok("attn_decode"))
+      return false;
+  } else if (aligned) {
     p.tile_rows = attention_tile_rows(job.rows, kv_mul, job.head_dim);
     const size_t lds = attention_tile_lds(p.tile_rows, kv_mul, job.head_dim);
     typedef void (*TileKernel)(AttnParams);
