@@ -203,9 +203,14 @@ def test_attention_golden_cases_both_layouts():
 
 @pytest.mark.parametrize("nh,nkv,hd,seq,positions", [(32, 8, 128, 600, (0, 63, 64, 65, 599)),
                                                      (8, 8, 64, 200, (1, 127, 199)), (12, 4, 96, 130, (129,)),
-                                                     (16, 1, 256, 70, (69,)), (4, 2, 32, 40, (39,))])
+                                                     (16, 1, 256, 70, (69,)), (4, 2, 32, 40, (39,)),
+                                                     (24, 8, 128, 300, (0, 127, 130, 299)),
+                                                     (64, 8, 128, 150, (1, 64, 149)), (32, 8, 64, 200, (5, 127, 199)),
+                                                     (16, 2, 64, 100, (63, 99))])
 def test_attention_decode_shapes(nh, nkv, hd, seq, positions):
-    """Decode attention at chunk boundaries (63, 64, 65) and GQA ratios 1-16, head_dim 32-256, head-major layout."""
+    """Decode attention at chunk boundaries (63, 64, 65) and GQA ratios 1-16, head_dim 32-256, head-major layout.
+    head_dim 64 or 128 with up to 8 query heads per KV head take the decode kernel (the 3B model's 3, the 1B and 8B
+    models' 4, and 8); the others the general one."""
     L = hu.lib()
     rng = orc.Rng(orc.SEED + nh * 31 + hd + seq)
     kc, vc = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1)
@@ -456,8 +461,14 @@ def test_recorded_rmsnorm_runs_before_any_other_call():
 # ---- RoPE and the cache stores recorded into the decode attention ----------------------------------------------------
 
 
-@pytest.mark.parametrize("layout,interrupt", [("head", None), ("rows", None), ("head", "sync"), ("head", "position")])
-def test_rope_kv_store_attention_fusion(layout, interrupt):
+@pytest.mark.parametrize("layout,interrupt,shape", [("head", None, (32, 8, 128, 200, 130)),
+                                                    ("rows", None, (32, 8, 128, 200, 130)),
+                                                    ("head", "sync", (32, 8, 128, 200, 130)),
+                                                    ("head", "position", (32, 8, 128, 200, 130)),
+                                                    ("head", None, (24, 8, 128, 300, 127)),
+                                                    ("head", None, (32, 8, 64, 200, 128)),
+                                                    ("rows", None, (64, 8, 128, 150, 63))])
+def test_rope_kv_store_attention_fusion(layout, interrupt, shape):
     """The reference's decode order (tp.c:409-413): k_rope_apply(q, k), k_kv_store of k and of v at the position,
     k_attention_kv at that position. Device-resident, the three recorded calls run inside the attention launch: q and k
     come back rotated bitwise as the oracle rotates them, the cache rows hold the rotated k and v bitwise, and the
@@ -466,14 +477,15 @@ def test_rope_kv_store_attention_fusion(layout, interrupt):
     L = hu.lib()
     assert L.kernels_kv_layout_select(layout.encode()) == 1
     try:
-        rng = orc.Rng(orc.SEED + 1400 + len(layout) + (0 if interrupt is None else len(interrupt)))
-        nh, nkv, hd, seq, pos = 32, 8, 128, 200, 130
+        rng = orc.Rng(orc.SEED + 1400 + len(layout) + (0 if interrupt is None else len(interrupt)) + sum(shape))
+        nh, nkv, hd, seq, pos = shape
         kv_dim = nkv * hd
         ps, hb = orc.kv_strides(nkv, hd, seq, layout == "head")
         kc0, vc0 = rng.normal(seq * kv_dim, 0, 1), rng.normal(seq * kv_dim, 0, 1)
         q, k, v = rng.normal(nh * hd, 0, 1), rng.normal(kv_dim, 0, 1), rng.normal(kv_dim, 0, 1)
         g = golden()
-        table = g["ropetab128_1000/table"]
+        # the reference's table row for 128 dimensions; any 2 * hd values otherwise (the rotation only reads them)
+        table = g["ropetab128_1000/table"] if hd == 128 else rng.uniform(2 * hd, 1.0).astype(np.float32)
         dq, dk, dv, dt = hu.dev(q), hu.dev(k), hu.dev(v), hu.dev(table)
         dkc, dvc, do = hu.dev(kc0), hu.dev(vc0), hu.empty(nh * hd, hu.torch().float32)
         L.k_rope_apply(lh.ptr(dq), lh.ptr(dk), lh.ptr(dt), nh, nkv, hd)
