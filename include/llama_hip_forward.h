@@ -9,6 +9,7 @@
 #define LLAMA_HIP_FORWARD_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #include "llama_hip_prefill.h" /* Config (include/runtime.h:9-16): k_rope_table reads head_dim and the rope fields */
 
@@ -20,6 +21,12 @@ extern "C" {
  * products are the reference's; the sum of squares is reduced in another order (within 1e-6 relative of it). */
 void k_rmsnorm(float *out, const float *x, const float *weight, int size, float epsilon);
 void k_rmsnorm_rows(float *out, const float *x, const float *weight, int rows, int size, float epsilon);
+/* No counterpart in the reference: k_rmsnorm_rows then k_quantize_rows of the same rows in one launch, bitwise the two
+ * calls, without the normalized rows in memory (for the engine's batched forward, src/tp.c:546-547, 576-577). Rows of
+ * at most 8192 values in whole groups of gs, a power of two from 4 to 256; x and weight 16-byte aligned, q 4-byte
+ * aligned. A non-finite normalized value fails at the next synchronization, as k_quantize_rows does. */
+void llhip_rmsnorm_quantize_rows(int8_t *q, float *s, const float *x, const float *weight, int rows, int size,
+                                 float epsilon, int gs);
 
 /* kernels.h:61-68: one position's table (2 * head_dim floats: cosines duplicated per pair, then -sin, +sin), computed
  * on the host with the C library as the reference computes it (src/kernels.c:49-61); and the rotation of q's n_heads and

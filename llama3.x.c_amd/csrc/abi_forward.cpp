@@ -230,6 +230,36 @@ void k_rmsnorm_rows(float *out, const float *x, const float *weight, int rows, i
   rmsnorm("k_rmsnorm_rows", out, x, weight, rows, size, epsilon);
 }
 
+// No counterpart in the reference: k_rmsnorm_rows then k_quantize_rows of the same rows in one launch, without the
+// normalized rows in memory (the engine's batched forward, src/tp.c:546-547 and 576-577); bitwise the two calls.
+void llhip_rmsnorm_quantize_rows(int8_t *q, float *s, const float *x, const float *weight, int rows, int size,
+                                 float epsilon, int gs) {
+  const char *name = "llhip_rmsnorm_quantize_rows";
+  if (rows <= 0 || size <= 0)
+    return;
+  if (!q || !s || !x || !weight) {
+    raise("%s: null buffer", name);
+    return;
+  }
+  if (!rmsnorm_quantize_fits(size, gs)) {
+    raise("%s: %d values per row in groups of %d: at most 8192, a whole number of groups of a power of two from 4 to "
+          "256", name, size, gs);
+    return;
+  }
+  if (((uintptr_t)x | (uintptr_t)weight) & 15 || (uintptr_t)q & 3) {
+    raise("%s: x and weight must be 16-byte aligned and q 4-byte aligned", name);
+    return;
+  }
+  Call call(name);
+  Ref X = call.in(x, (size_t)rows * size * sizeof(float)), W = call.in(weight, (size_t)size * sizeof(float));
+  Ref Q = call.out(q, (size_t)rows * size, false), S = call.out(s, (size_t)rows * (size / gs) * sizeof(float), false);
+  if (!call.ready())
+    return;
+  if (launch_rmsnorm_quantize(call.ptr<int8_t>(Q), call.ptr<float>(S), call.ptr<const float>(X),
+                              call.ptr<const float>(W), rows, size, epsilon, gs, call.stream()))
+    call.finish();
+}
+
 // ---- RoPE (kernels.h:61-68, src/kernels_simd.c:194-225, src/kernels.c:49-61) ----------------------------------
 
 // The table is computed on the host with the C library's powf / cosf / sinf, the reference's own expressions, so it is

@@ -151,6 +151,12 @@ struct QuantizeJob {
   int m, n, gs;
 };
 bool launch_quantize(const QuantizeJob &job, hipStream_t stream);
+// RMSNorm then k_quantize of rows of n values in one launch (bitwise k_rmsnorm_rows then k_quantize_rows), for the
+// shapes rmsnorm_quantize_fits takes: n <= 8192, n % gs == 0, gs a power of two from 4 to 256; 16-byte aligned x and
+// weight, 4-byte aligned q.
+bool rmsnorm_quantize_fits(int n, int gs);
+bool launch_rmsnorm_quantize(int8_t *q, float *s, const float *x, const float *weight, int rows, int n, float epsilon,
+                             int gs, hipStream_t stream);
 
 struct GemvSegment {
   float *out;

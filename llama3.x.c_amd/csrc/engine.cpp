@@ -578,13 +578,24 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
     k_embed_f32_rows(e->bx, e->embed.f(), e->btokens, count, d, c.vocab_size);
   const bool head = kernels_kv_layout_head() != 0;
   static const int kQkv[3] = {0, 1, 2}, kWo[1] = {3}, kW1[1] = {4}, kW2[1] = {5};
+  // RMSNorm of the rows into the GEMM's input: for Q8_0 the normalized rows quantized in the same launch where the
+  // shape allows (bitwise k_rmsnorm_rows then k_quantize_rows), the FP32 rows otherwise
+  const bool fused_norm = e->q8 && rmsnorm_quantize_fits(d, gs);
+  auto norm_rows = [&](const float *w) {
+    if (fused_norm) {
+      llhip_rmsnorm_quantize_rows(e->bxq, e->bxs, e->bx, w, count, d, c.norm_eps, gs);
+      return;
+    }
+    k_rmsnorm_rows(e->bxb, e->bx, w, count, d, c.norm_eps);
+    if (e->q8)
+      k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
+  };
   for (int l = 0; l < c.n_layers; l++) {
     const size_t layer = (size_t)l * c.seq_len * kvl;
     float *kc = e->key_cache + layer, *vc = e->value_cache + layer;
     float *kd = head ? e->bk : kc + (size_t)pos0 * kvl, *vd = head ? e->bv : vc + (size_t)pos0 * kvl;
-    k_rmsnorm_rows(e->bxb, e->bx, e->rms_att + (size_t)l * d, count, d, c.norm_eps);
+    norm_rows(e->rms_att + (size_t)l * d);
     if (e->q8) {
-      k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
       const GemmQ8Segment qkv[3] = {
           {e->bq, d, e->wq[l].k8(), K8Weight{}, nullptr, nullptr, d, GEMM_STORE},
           {kd, kvl, e->wk[l].k8(), K8Weight{}, nullptr, nullptr, kvl, GEMM_STORE},
@@ -610,9 +621,8 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
       const GemmSegment wo{e->bx, d, e->wo[l].f(), nullptr, (size_t)d, d, GEMM_ADD};
       gemm_f32_or_bf16(e, e->bxb, d, count, d, &wo, 1, l, kWo, -1);
     }
-    k_rmsnorm_rows(e->bxb, e->bx, e->rms_ffn + (size_t)l * d, count, d, c.norm_eps);
+    norm_rows(e->rms_ffn + (size_t)l * d);
     if (e->q8) {
-      k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
       const GemmQ8Segment up{e->bhb, hidden, e->w1[l].k8(), e->w3[l].k8(), nullptr, nullptr, hidden, GEMM_SWIGLU};
       k_gemm_q8(e->bxq, e->bxs, count, d, gs, &up, 1);
       k_quantize_rows(e->bxq, e->bxs, e->bhb, hidden, count, hidden, gs);

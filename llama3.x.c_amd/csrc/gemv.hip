@@ -118,6 +118,76 @@ __global__ __launch_bounds__(kBlock) void quantize_lanes(int8_t *__restrict__ q,
     s[(size_t)row * (n / gs) + off / gs] = scale;
 }
 
+// RMSNorm of each row, then k_quantize of the normalized values, without the normalized row in memory: one 1024-thread
+// block per row, thread t holding values 4 t + 4096 p. The sum of squares runs in rmsnorm_rows' order (each thread's
+// values by fmaf, the wave's by the DPP sum, the waves' in order) and w * (ss * x) rounds as there, so the values
+// quantized are rmsnorm_rows' bit for bit; a group of gs values is gs / 4 consecutive lanes (the group maximum a lane
+// reduction) quantized by the k_quantize rule as quantize_lanes applies it. Bitwise k_rmsnorm_rows then
+// k_quantize_rows. n <= kNormQPasses * 4096, n % gs == 0, gs a power of two from 4 to 256.
+constexpr int kNormQThreads = 1024, kNormQPasses = 2;
+__global__ __launch_bounds__(kNormQThreads) void rmsnorm_quantize_rows(int8_t *__restrict__ q, float *__restrict__ s,
+                                                                       const float *__restrict__ x,
+                                                                       const float *__restrict__ weight, int n,
+                                                                       float epsilon, int gs, int *__restrict__ flags) {
+  __shared__ float part[kNormQThreads / kWave];
+  const int tid = threadIdx.x;
+  const float *row = x + (size_t)blockIdx.x * n;
+  float4 v[kNormQPasses], w[kNormQPasses];
+  float ss = 0.0f;
+#pragma unroll
+  for (int p = 0; p < kNormQPasses; p++) {
+    const int j = 4 * tid + p * 4 * kNormQThreads;
+    v[p] = w[p] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (j < n) {
+      v[p] = *reinterpret_cast<const float4 *>(row + j);
+      w[p] = *reinterpret_cast<const float4 *>(weight + j);
+      ss = fmaf(v[p].x, v[p].x, ss);
+      ss = fmaf(v[p].y, v[p].y, ss);
+      ss = fmaf(v[p].z, v[p].z, ss);
+      ss = fmaf(v[p].w, v[p].w, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & (kWave - 1)) == 0)
+    part[tid / kWave] = ss;
+  __syncthreads();
+  ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormQThreads / kWave; i++)
+    ss += part[i];
+  // src/kernels.c:15-17, the same three roundings
+  ss /= n;
+  ss += epsilon;
+  ss = 1.0f / sqrtf(ss);
+  const int lpg = gs / 4, groups = n / gs;
+  bool bad = false;
+#pragma unroll
+  for (int p = 0; p < kNormQPasses; p++) {
+    const int base = p * 4 * kNormQThreads, j = 4 * tid + base;
+    if (base + 4 * (tid & ~(kWave - 1)) >= n)
+      continue; // the whole wave is past the row (groups never straddle it: n % gs == 0)
+    const float e[4] = {w[p].x * (ss * v[p].x), w[p].y * (ss * v[p].y), w[p].z * (ss * v[p].z),
+                        w[p].w * (ss * v[p].w)};
+    float peak = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      peak = fmaxf(peak, fabsf(e[i])); // a NaN is skipped here and caught by quantize_fast
+    peak = group_reduce_max(peak, lpg);
+    const float scale = peak / 127.0f;
+    bool ok;
+    const float inv = group_reciprocal(scale, ok);
+    int qv[4];
+    quantize_fast(e, scale, inv, ok, qv, bad);
+    if (j < n) {
+      *reinterpret_cast<int *>(q + (size_t)blockIdx.x * n + j) = pack_bytes(qv[0], qv[1], qv[2], qv[3]);
+      if ((tid & (lpg - 1)) == 0)
+        s[(size_t)blockIdx.x * groups + j / gs] = scale;
+    }
+  }
+  if (bad)
+    flags[0] = 1;
+}
+
 // Any group size: one thread per group, the reference's loop order (src/gemv.c:599-623).
 __global__ __launch_bounds__(kBlock) void quantize_groups(int8_t *__restrict__ q, float *__restrict__ s,
                                                           const float *__restrict__ x, size_t ldx, int n, int gs,
@@ -810,6 +880,20 @@ bool launch_ok(const char *what) {
 }
 
 } // namespace
+
+bool rmsnorm_quantize_fits(int n, int gs) {
+  return n > 0 && n <= kNormQPasses * 4 * kNormQThreads && gs >= 4 && gs <= 256 && (gs & (gs - 1)) == 0 &&
+         n % gs == 0;
+}
+
+bool launch_rmsnorm_quantize(int8_t *q, float *s, const float *x, const float *weight, int rows, int n, float epsilon,
+                             int gs, hipStream_t stream) {
+  if (rows <= 0)
+    return true;
+  hipLaunchKernelGGL(rmsnorm_quantize_rows, dim3((unsigned)rows), dim3(kNormQThreads), 0, stream, q, s, x, weight, n,
+                     epsilon, gs, device().error_flags);
+  return launch_ok("rmsnorm_quantize_rows");
+}
 
 bool launch_quantize(const QuantizeJob &job, hipStream_t stream) {
   if (job.m <= 0 || job.n / job.gs <= 0)

@@ -64,6 +64,45 @@ def test_rmsnorm_rows_against_oracle(rows, size):
     assert np.all(np.abs(hu.host(do) - want) <= 1e-5 * np.abs(want) + 1e-7)
 
 
+@pytest.mark.parametrize("rows,size,gs", [(1, 4096, 64), (37, 4096, 64), (5, 2048, 64), (9, 3072, 32), (3, 8192, 64),
+                                          (4, 640, 128), (6, 96, 4), (2, 1024, 256), (130, 4096, 64)])
+def test_rmsnorm_quantize_rows_fused(rows, size, gs):
+    """llhip_rmsnorm_quantize_rows: bitwise k_rmsnorm_rows then k_quantize_rows (the same normalized values, the same
+    quantization), over rows up to 8192 values and group sizes 4-256, with values at rounding ties of the quantizer;
+    and a non-finite value fails as k_quantize_rows does."""
+    L = hu.lib()
+    rng = orc.Rng(orc.SEED + 3100 + rows * 7 + size + gs)
+    x = rng.normal(rows * size, 0.0, 2.0).reshape(rows, size)
+    x[0, :8] = [0.0, -0.0, 1e-30, 3.5, -3.5, 127.0, -127.0, 0.5]
+    w = rng.normal(size, 1.0, 0.2)
+    dx, dw = hu.dev(x), hu.dev(w)
+    groups = size // gs
+    t = hu.torch()
+    q1, s1 = hu.empty((rows, size), t.int8), hu.empty((rows, groups), t.float32)
+    q2, s2, xb = hu.empty((rows, size), t.int8), hu.empty((rows, groups), t.float32), hu.empty((rows, size), t.float32)
+    L.llhip_rmsnorm_quantize_rows(lh.ptr(q1), lh.ptr(s1), lh.ptr(dx), lh.ptr(dw), rows, size, 1e-5, gs)
+    L.k_rmsnorm_rows(lh.ptr(xb), lh.ptr(dx), lh.ptr(dw), rows, size, 1e-5)
+    L.k_quantize_rows(lh.ptr(q2), lh.ptr(s2), lh.ptr(xb), size, rows, size, gs)
+    assert lh.last_error() == "", lh.last_error()
+    assert np.array_equal(hu.host(q1), hu.host(q2)), "quantized values"
+    assert np.array_equal(hu.bits(hu.host(s1)), hu.bits(hu.host(s2))), "scales"
+    # against the oracle: its RMSNorm then quantization, within one step of the grid where the normalized value's
+    # reduction order moves it across a rounding boundary
+    want_q, want_s = orc.quantize(orc.rmsnorm(x, w, 1e-5), gs)
+    assert np.allclose(hu.host(s1), want_s, rtol=1e-5, atol=0)
+    assert np.max(np.abs(hu.host(q1).astype(int) - want_q.astype(int))) <= 1
+    if rows == 1:
+        lh.record_failures()
+        try:
+            x[0, 5] = np.inf
+            L.llhip_rmsnorm_quantize_rows(lh.ptr(q1), lh.ptr(s1), lh.ptr(hu.dev(x)), lh.ptr(dw), rows, size, 1e-5, gs)
+            L.llhip_synchronize()
+            assert "nonfinite activation during INT8 quantization" in lh.last_error(), lh.last_error()
+        finally:
+            L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+            L.llhip_clear_error()
+
+
 # ---- RoPE --------------------------------------------------------------------------------------------------------------
 
 
