@@ -127,6 +127,13 @@ void k_quantize_rows(int8_t *q, float *s, const float *x, size_t ldx, int m, int
  * int8 MFMA (v_mfma_i32_16x16x64_i8, one 64-wide group per instruction) and an FP32 rescale-accumulate. */
 void k_gemm_q8(const int8_t *xq, const float *xs, int m, int k, int gs, const GemmQ8Segment *segments, int count);
 Q8GemmBackend k_gemm_q8_pick(int gs, const GemmQ8Segment *segments, int count); /* gemm.h:135 */
+/* No counterpart in the reference: hb = silu(W1 x) * (W3 x) as k_gemm_q8's GEMM_SWIGLU forms it, quantized in the
+ * GEMM's epilogue (groups of 64: hq int8 [m][n], hs [m][n / 64]) instead of written out in FP32; bitwise k_gemm_q8
+ * GEMM_SWIGLU then k_quantize_rows of its output (the engine's batched forward, src/tp.c:580-584). Returns 1 when it
+ * ran, 0 with nothing launched when the shape does not take the wide int8 kernel unsplit (gs 64, n % 64 == 0, the
+ * launcher's choice for m, n, k); a non-finite value fails at the next synchronization, as k_quantize_rows does. */
+int llhip_gemm_q8_swiglu_quantize(const int8_t *xq, const float *xs, int m, int k, int gs, const K8Weight *w1,
+                                  const K8Weight *w3, int n, int8_t *hq, float *hs);
 
 /* gemm.h:138-144 */
 typedef struct {

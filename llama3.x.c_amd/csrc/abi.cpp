@@ -474,6 +474,44 @@ void k_gemm_q8(const int8_t *xq, const float *xs, int m, int k, int gs, const Ge
   gemm_q8("k_gemm_q8", true, xq, xs, m, k, gs, segments, count);
 }
 
+// No counterpart in the reference: hb = silu(W1 x) * (W3 x) as k_gemm_q8's GEMM_SWIGLU computes it, quantized in the
+// GEMM's epilogue by the k_quantize rule (groups of 64) instead of written out in FP32 (the engine's batched forward:
+// the SwiGLU GEMM then k_quantize_rows of hb, src/tp.c:580-584); bitwise those two calls. 1 when it ran, 0 (nothing
+// launched) when the shape does not take the wide int8 kernel unsplit.
+int llhip_gemm_q8_swiglu_quantize(const int8_t *xq, const float *xs, int m, int k, int gs, const K8Weight *w1,
+                                  const K8Weight *w3, int n, int8_t *hq, float *hs) {
+  const char *name = "llhip_gemm_q8_swiglu_quantize";
+  if (!w1 || !w3 || !w1->q || !w1->s || !w3->q || !w3->s || !xq || !xs || !hq || !hs) {
+    raise("%s: null buffer", name);
+    return 0;
+  }
+  if (gs != 64 || k % gs || n % 64 || m <= 0 || n <= 0 || k <= 0)
+    return 0;
+  const int groups = k / gs;
+  Call call(name);
+  Ref XQ = call.in(xq, (size_t)m * k), XS = call.in(xs, (size_t)m * groups * sizeof(float));
+  Ref W = call.in(w1->q, (size_t)n * k), WS = call.in(w1->s, (size_t)n * groups * sizeof(float));
+  Ref W3 = call.in(w3->q, (size_t)n * k), W3S = call.in(w3->s, (size_t)n * groups * sizeof(float));
+  Ref HQ = call.out(hq, (size_t)m * n, false), HS = call.out(hs, (size_t)m * (n / 64) * sizeof(float), false);
+  if (!call.ready())
+    return 0;
+  GemmQ8Job job{};
+  job.seg[0] = GemmSegmentDev{nullptr, n, call.ptr<const void>(W), call.ptr<const void>(W3), call.ptr<const float>(WS),
+                              call.ptr<const float>(W3S), (size_t)k, n, EPI_SWIGLU};
+  job.seg[0].cq = call.ptr<int8_t>(HQ);
+  job.seg[0].cs = call.ptr<float>(HS);
+  job.nseg = 1;
+  job.xq = call.ptr<const int8_t>(XQ);
+  job.xs = call.ptr<const float>(XS);
+  job.m = m;
+  job.k = k;
+  job.gs = gs;
+  if (((uintptr_t)job.xq | (uintptr_t)job.seg[0].w | (uintptr_t)job.seg[0].w3) & 15 ||
+      !launch_q8_gemm_swiglu_quantized(job, call.stream()))
+    return 0;
+  return call.finish() ? 1 : 0;
+}
+
 Q8GemmBackend k_gemm_q8_pick(int gs, const GemmQ8Segment *segments, int count) {
   (void)segments, (void)count;
   return gs > 0 && gs % 64 == 0 ? Q8_GEMM_HIP_MFMA : Q8_GEMM_PORTABLE;

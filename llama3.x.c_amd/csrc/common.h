@@ -249,6 +249,10 @@ struct GemmSegmentDev {
   size_t ldw;            // F32 only: weight row stride in floats
   int n;
   Epilogue epi;
+  // Q8 SWIGLU through q8_gemm_swiglu_quantized only: the output quantized by the k_quantize rule in groups of 64
+  // (cq [m][n] int8, cs [m][n / 64]) instead of written to c
+  int8_t *cq = nullptr;
+  float *cs = nullptr;
 };
 struct GemmQ8Job {
   const int8_t *xq;
@@ -259,6 +263,10 @@ struct GemmQ8Job {
 };
 bool q8_gemm_fast_path(const int8_t *xq, int m, int k, int gs); // the pipelined int8-MFMA kernel takes the shape
 bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream);
+// One SWIGLU segment whose output goes out quantized (seg[0].cq / cs, groups of 64): launched, and true, when the
+// launcher's choice for the shape is the wide int8 kernel without split K (the epilogue holds whole output groups);
+// false, with nothing launched, otherwise (the caller runs the GEMM and k_quantize_rows).
+bool launch_q8_gemm_swiglu_quantized(const GemmQ8Job &job, hipStream_t stream);
 bool q8_gemm_skinny_path(const int8_t *xq, int m, int k, int gs); // at most 32 rows: stream the weights once
 bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream);
 bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream);

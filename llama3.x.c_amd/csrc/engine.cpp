@@ -85,8 +85,8 @@ struct Engine {
   // the batched forward's rows (max_batch of each, allocated on its first call)
   int batch_rows = 0;
   float *bx = nullptr, *bxb = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *bhb = nullptr, *bxs = nullptr;
-  float *blogits = nullptr;
-  int8_t *bxq = nullptr;
+  float *bhs = nullptr, *blogits = nullptr;
+  int8_t *bxq = nullptr, *bhq = nullptr; // quantized rows of dim (xb) and of hidden_dim (hb) values
   int *btokens = nullptr;
   std::vector<float> host_batch_logits;
 };
@@ -105,7 +105,7 @@ template <typename T> void drop(T *&p) {
 
 void free_batch(Engine *e) {
   drop(e->bx), drop(e->bxb), drop(e->bq), drop(e->bk), drop(e->bv), drop(e->bhb), drop(e->bxs);
-  drop(e->bxq), drop(e->btokens), drop(e->blogits);
+  drop(e->bxq), drop(e->bhq), drop(e->bhs), drop(e->btokens), drop(e->blogits);
   if (e->panel.base)
     aligned_buffer_free(&e->panel);
   e->batch_rows = 0;
@@ -525,7 +525,8 @@ bool allocate_batch(Engine *e, int rows) {
   const size_t groups = e->q8 ? (size_t)e->gs : 1;
   const bool ok = device_array(&e->bx, m * d) && device_array(&e->bxb, m * d) && device_array(&e->bq, m * d) &&
                   device_array(&e->bk, m * kv) && device_array(&e->bv, m * kv) && device_array(&e->bhb, m * h) &&
-                  device_array(&e->bxq, e->q8 ? m * h : 1) && device_array(&e->bxs, e->q8 ? m * h / groups : 1) &&
+                  device_array(&e->bxq, e->q8 ? m * d : 1) && device_array(&e->bxs, e->q8 ? m * d / groups : 1) &&
+                  device_array(&e->bhq, e->q8 ? m * h : 1) && device_array(&e->bhs, e->q8 ? m * h / groups : 1) &&
                   device_array(&e->btokens, m);
   if (ok && e->bf16) {
     aligned_buffer_alloc(&e->panel, k_gemm_bf16_panel_bytes(rows, c.dim > c.hidden_dim ? c.dim : c.hidden_dim),
@@ -623,11 +624,17 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
     }
     norm_rows(e->rms_ffn + (size_t)l * d);
     if (e->q8) {
-      const GemmQ8Segment up{e->bhb, hidden, e->w1[l].k8(), e->w3[l].k8(), nullptr, nullptr, hidden, GEMM_SWIGLU};
-      k_gemm_q8(e->bxq, e->bxs, count, d, gs, &up, 1);
-      k_quantize_rows(e->bxq, e->bxs, e->bhb, hidden, count, hidden, gs);
+      // hb quantized in the SwiGLU GEMM's epilogue where the shape allows (bitwise the GEMM then k_quantize_rows)
+      const K8Weight w1 = e->w1[l].k8(), w3 = e->w3[l].k8();
+      if (!llhip_gemm_q8_swiglu_quantize(e->bxq, e->bxs, count, d, gs, &w1, &w3, hidden, e->bhq, e->bhs)) {
+        const GemmQ8Segment up{e->bhb, hidden, w1, w3, nullptr, nullptr, hidden, GEMM_SWIGLU};
+        k_gemm_q8(e->bxq, e->bxs, count, d, gs, &up, 1);
+        k_quantize_rows(e->bhq, e->bhs, e->bhb, hidden, count, hidden, gs);
+      }
+      if (llhip_last_error()[0])
+        return nullptr;
       const GemmQ8Segment down{e->bx, d, e->w2[l].k8(), K8Weight{}, nullptr, nullptr, d, GEMM_ADD};
-      k_gemm_q8(e->bxq, e->bxs, count, hidden, gs, &down, 1);
+      k_gemm_q8(e->bhq, e->bhs, count, hidden, gs, &down, 1);
     } else {
       const GemmSegment up{e->bhb, hidden, e->w1[l].f(), e->w3[l].f(), (size_t)d, hidden, GEMM_SWIGLU};
       gemm_f32_or_bf16(e, e->bxb, d, count, d, &up, 1, l, kW1, 6);

@@ -21,6 +21,8 @@
 #include <vector>
 
 #include "common.h"
+#include "lanes.h"
+#include "quant.h"
 
 namespace llhip {
 namespace {
@@ -46,6 +48,8 @@ struct TileSeg {
   int epi;
   int first_tile; // first logical tile of this segment
   int ntiles;     // its column tiles
+  int8_t *cq;     // SWIGLU output quantized in groups of 64 (the wide int8 kernel only), else null
+  float *cs;
 };
 
 struct TileGrid {
@@ -124,10 +128,48 @@ __device__ __forceinline__ void store_tile(const TileSeg &seg, const TilePos &t,
 }
 
 // The wide BF16 tile's epilogue: rows 64 wm + 16 i + 4 (l / 16) + e, columns 128 wn + 16 j + l % 16, or under SWIGLU
-// silu(W1 column 64 wn + 16 j + l % 16) * (the same W3 column) from tiles j and j + 4.
+// silu(W1 column 64 wn + 16 j + l % 16) * (the same W3 column) from tiles j and j + 4. With seg.cq set (SWIGLU, the
+// int8 kernel) a wave's 64 columns of a row are one quantization group, held by the 16 lanes of the row's lane group:
+// their maximum is a DPP row reduction, and the values go out by the k_quantize rule as int8 with the group's scale
+// (bitwise the FP32 output then k_quantize_rows); a non-finite value sets flags[0].
 __device__ __forceinline__ void store_tile_wide(const TileSeg &seg, const TilePos &t, const v4f (&acc)[4][8], int wm,
-                                                int wn, int lane, int m) {
+                                                int wn, int lane, int m, int *flags = nullptr) {
   const int lc = lane & 15, lr = (lane >> 4) * 4;
+  if (t.swiglu && seg.cq) {
+    const int c0 = t.n0 + 64 * wn; // the wave's group (seg.n % 64 == 0)
+    const int groups = seg.n / 64;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int row = t.m0 + wm * 64 + 16 * i + lr + e;
+        float v[4];
+        float peak = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          v[j] = silu_gate(acc[i][j][e], acc[i][j + 4][e]);
+          peak = fmaxf(peak, fabsf(v[j])); // a NaN is skipped here and caught by quantize_fast
+        }
+        peak = group_reduce_max(peak, 16);
+        const float scale = peak / 127.0f;
+        bool ok;
+        const float inv = group_reciprocal(scale, ok);
+        int q[4];
+        quantize_fast(v, scale, inv, ok, q, bad);
+        if (row < m && c0 < seg.n) {
+          int8_t *qrow = seg.cq + (long long)row * seg.n;
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            qrow[c0 + 16 * j + lc] = (int8_t)q[j];
+          if (lc == 0)
+            seg.cs[(long long)row * groups + c0 / 64] = scale;
+        }
+      }
+    if (bad && flags)
+      flags[0] = 1;
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -228,6 +270,7 @@ struct Q8Params {
   int m, k, gs;
   int32_t *probe; // optional (one segment, no SWIGLU): probe[(g * m + r) * n + c]
   SplitK sk;
+  int *flags; // [0]: a non-finite value met by a quantizing epilogue
 };
 
 __device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical, int tile_m = kQ8TileM,
@@ -1144,7 +1187,7 @@ template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_w
         slot[(i * 8 + j) * kQ8Threads] = acc[i][j];
     return;
   }
-  store_tile_wide(seg, t, acc, wm, wn, lane, p.m);
+  store_tile_wide(seg, t, acc, wm, wn, lane, p.m, p.flags);
 }
 
 // Any group size (gs % 64 != 0): one thread per output, the per-group int32 dot in plain integer arithmetic.
@@ -1290,7 +1333,8 @@ TileGrid make_grid(const GemmSegmentDev *segs, int nseg, int m) {
   for (int s = 0; s < nseg; s++) {
     const GemmSegmentDev &d = segs[s];
     const int width = d.epi == EPI_SWIGLU ? kTile / 2 : kTile;
-    g.seg[s] = TileSeg{d.c, d.ldc, d.w, d.w3, d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width};
+    g.seg[s] = TileSeg{d.c,   d.ldc, d.w,   d.w3,  d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width,
+                       d.cq, d.cs};
     tiles += g.seg[s].ntiles * g.mtiles;
   }
   g.total = tiles;
@@ -1305,7 +1349,8 @@ Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m, int tile_m = kQ
   for (int s = 0; s < nseg; s++) {
     const GemmSegmentDev &d = segs[s];
     const int width = d.epi == EPI_SWIGLU ? tile_n / 2 : tile_n;
-    g.seg[s] = TileSeg{d.c, d.ldc, d.w, d.w3, d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width};
+    g.seg[s] = TileSeg{d.c,   d.ldc, d.w,   d.w3,  d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width,
+                       d.cq, d.cs};
     tiles += g.seg[s].ntiles * g.mtiles;
   }
   g.total = tiles;
@@ -1403,18 +1448,22 @@ bool q8_use_wide(const Q8Params &p, const SegList &segs) {
   return 17LL * ((wide + cus - 1) / cus) < 10LL * ((narrow + cus - 1) / cus);
 }
 
-// The wide int8 kernel; its partial tiles are twice the size, so half as many fit the workspace.
-bool q8_wide_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
+// The wide int8 kernel's grid and split count; its partial tiles are twice the size, so half as many fit the workspace.
+void q8_wide_grid(Q8Params &p, const SegList &segs) {
   constexpr int kWideSlots = kSplitSlots / 2;
   p.grid = make_q8_grid(segs.seg, segs.nseg, p.m, kWTileM, kWTileN);
-  if (p.grid.total <= 0)
-    return true;
   const int steps = p.k / 64;
   p.sk.splits = p.grid.total > kWideSlots ? 1 : choose_splits(p.grid.total, steps, &p.sk.per, 1, kWideSlots);
   if (p.sk.splits == 1)
     p.sk.per = steps;
   p.sk.partial = (v4f *)device().split_partial;
   p.sk.count = device().split_count;
+}
+
+bool q8_wide_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
+  q8_wide_grid(p, segs);
+  if (p.grid.total <= 0)
+    return true;
   static const hipError_t a0 =
       hipFuncSetAttribute((const void *)q8_gemm_wide<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds);
   static const hipError_t a1 =
@@ -1460,7 +1509,35 @@ bool launch_q8_gemm(const GemmQ8Job &job, hipStream_t stream) {
   p.m = job.m;
   p.k = job.k;
   p.gs = job.gs;
+  p.flags = device().error_flags;
   return launch_q8_lds<false>(p, job.seg, job.nseg, stream);
+}
+
+bool launch_q8_gemm_swiglu_quantized(const GemmQ8Job &job, hipStream_t stream) {
+  const GemmSegmentDev &seg = job.seg[0];
+  if (job.nseg != 1 || seg.epi != EPI_SWIGLU || !seg.cq || !seg.cs || seg.n % 64 || job.gs != 64 || job.m <= 0 ||
+      !q8_gemm_fast_path(job.xq, job.m, job.k, job.gs) ||
+      (q8_gemm_skinny_path(job.xq, job.m, job.k, job.gs) && !forced_splits.load()))
+    return false;
+  Q8Params p{};
+  p.xq = job.xq;
+  p.xs = job.xs;
+  p.m = job.m;
+  p.k = job.k;
+  p.gs = job.gs;
+  p.flags = device().error_flags;
+  const SegList list{job.seg, 1};
+  if (!q8_use_wide(p, list))
+    return false;
+  q8_wide_grid(p, list);
+  if (p.sk.splits != 1 || p.grid.total <= 0)
+    return false;
+  static const hipError_t a0 =
+      hipFuncSetAttribute((const void *)q8_gemm_wide<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds);
+  if (!check_hip(a0, "allowing the Q8 GEMM its LDS"))
+    return false;
+  hipLaunchKernelGGL(q8_gemm_wide<false>, dim3((unsigned)p.grid.total), dim3(kQ8Threads), kQWLds, stream, p);
+  return launch_ok("q8_gemm_wide");
 }
 
 bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream) {

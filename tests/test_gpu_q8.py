@@ -6,6 +6,7 @@ scales and the int32 group dots are bitwise the oracle's; FP32 outputs lie withi
 the reference's own scalar results; the floored relative error d / (|ref| + 1e-3) (tests/q8_engine.c:71) is checked
 against the north-star tolerance 1e-4.
 """
+import ctypes
 import os
 
 import numpy as np
@@ -522,6 +523,61 @@ def test_gemm_q8_wide_tiles(m, n, k):
         L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, segs, 3)
         for o, nn in zip(outs, widths):
             hu.assert_within_budget(hu.host(o), ref[:, :nn], mag[:, :nn], what=f"wide segment of {nn}")
+    finally:
+        L.llhip_set_q8_tile(0)
+        L.llhip_set_gemm_splits(0)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 256, 1024), (513, 640, 320), (257, 128, 4096), (1024, 384, 2048)])
+def test_gemm_q8_swiglu_quantized(m, n, k):
+    """llhip_gemm_q8_swiglu_quantize: hb quantized in the wide int8 kernel's epilogue, bitwise k_gemm_q8 GEMM_SWIGLU then
+    k_quantize_rows of its output; it declines (returns 0, writes nothing) where the launcher would not run the wide
+    kernel unsplit, and a non-finite hb value fails as k_quantize_rows does."""
+    L = hu.lib()
+    gs = 64
+    xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 6161 + m + n)
+    t = hu.torch()
+    dx = [hu.dev(a) for a in (xq, xs, wq, ws, w3q, w3s)]
+    w1, w3 = lh.w8(dx[2], dx[3]), lh.w8(dx[4], dx[5])
+    try:
+        L.llhip_set_q8_tile(2)
+        L.llhip_set_gemm_splits(1)
+        hq, hs = hu.empty((m, n), t.int8), hu.empty((m, n // 64), t.float32)
+        assert L.llhip_gemm_q8_swiglu_quantize(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, ctypes.byref(w1), ctypes.byref(w3),
+                                               n, lh.ptr(hq), lh.ptr(hs)) == 1
+        hb = hu.dev(np.zeros((m, n), np.float32))
+        seg = lh.GemmQ8Segment(lh.ptr(hb), n, w1, w3, None, None, n, lh.GEMM_SWIGLU)
+        L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+        q2, s2 = hu.empty((m, n), t.int8), hu.empty((m, n // 64), t.float32)
+        L.k_quantize_rows(lh.ptr(q2), lh.ptr(s2), lh.ptr(hb), n, m, n, gs)
+        assert lh.last_error() == "", lh.last_error()
+        assert np.array_equal(hu.host(hq), hu.host(q2)), "quantized values"
+        assert np.array_equal(hu.bits(hu.host(hs)), hu.bits(hu.host(s2))), "scales"
+        # declined: the 256 x 128 kernel forced, or split K, or another group size; nothing is written
+        for tile, splits in ((1, 1), (2, 2)):
+            L.llhip_set_q8_tile(tile)
+            L.llhip_set_gemm_splits(splits)
+            hq0 = hu.dev(np.full((m, n), 7, np.int8))
+            assert L.llhip_gemm_q8_swiglu_quantize(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, ctypes.byref(w1),
+                                                   ctypes.byref(w3), n, lh.ptr(hq0), lh.ptr(hs)) == 0
+            assert np.all(hu.host(hq0) == 7)
+        L.llhip_set_q8_tile(2)
+        L.llhip_set_gemm_splits(1)
+        assert L.llhip_gemm_q8_swiglu_quantize(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, 32, ctypes.byref(w1),
+                                               ctypes.byref(w3), n, lh.ptr(hq), lh.ptr(hs)) == 0
+        if m == 300:
+            lh.record_failures()
+            try:
+                xs_bad = xs.copy()
+                xs_bad[5, 0] = np.inf  # row 5's dots become infinite, its SwiGLU values non-finite
+                assert L.llhip_gemm_q8_swiglu_quantize(lh.ptr(dx[0]), lh.ptr(hu.dev(xs_bad)), m, k, gs,
+                                                       ctypes.byref(w1), ctypes.byref(w3), n, lh.ptr(hq),
+                                                       lh.ptr(hs)) == 1
+                L.llhip_synchronize()
+                assert "nonfinite activation during INT8 quantization" in lh.last_error(), lh.last_error()
+            finally:
+                L.llhip_set_fail_mode(lh.LLHIP_FAIL_EXIT)
+                L.llhip_clear_error()
     finally:
         L.llhip_set_q8_tile(0)
         L.llhip_set_gemm_splits(0)
