@@ -35,6 +35,13 @@ void k_rope_table(const Config *p, int position, float *table);
 void k_rope_apply(float *q, float *k, const float *table, int n_heads, int n_kv_heads, int head_dim);
 void k_rope_apply_rows(float *q, size_t q_stride, float *k, size_t k_stride, const float *table, size_t table_stride,
                        int rows, int n_heads, int n_kv_heads, int head_dim);
+/* No counterpart in the reference: k_rope_apply_rows of q and k, then k_kv_store of k and of v at positions pos0 ..
+ * pos0 + rows - 1 of the caches (the selected layout), in one launch and bitwise those three calls (k is also left
+ * rotated in place); for the engine's batched forward (src/tp.c:550-557). head_dim and the strides multiples of 4, one
+ * table row of 2 * head_dim values per row (table_stride >= 2 * head_dim), 16-byte aligned q, k, v and table. */
+void llhip_rope_kv_store_rows(float *q, size_t q_stride, float *k, const float *v, size_t kv_stride, const float *table,
+                              size_t table_stride, int rows, int n_heads, int n_kv_heads, int head_dim,
+                              float *key_cache, float *value_cache, int pos0, int seq_len);
 
 /* The embedding lookup of a Q8_0 table (vocab x dim int8 values, one float scale per gs consecutive values), inline
  * in the reference's forward (src/tp.c:395-396 for a token, 444-456 for a batch): out row i = table row ids[i], each

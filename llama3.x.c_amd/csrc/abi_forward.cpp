@@ -367,6 +367,45 @@ void k_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int cou
     call.finish();
 }
 
+// No counterpart in the reference: k_rope_apply_rows of q and k, then k_kv_store of k and of v at pos0.. (the engine's
+// batched forward, src/tp.c:550-557), in one launch and bitwise those calls; rows of q, k and v 16-byte aligned.
+void llhip_rope_kv_store_rows(float *q, size_t q_stride, float *k, const float *v, size_t kv_stride, const float *table,
+                              size_t table_stride, int rows, int n_heads, int n_kv_heads, int head_dim,
+                              float *key_cache, float *value_cache, int pos0, int seq_len) {
+  const char *name = "llhip_rope_kv_store_rows";
+  if (rows <= 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0)
+    return;
+  if (!q || !k || !v || !table || !key_cache || !value_cache) {
+    raise("%s: null buffer", name);
+    return;
+  }
+  if (head_dim % 4 || n_kv_heads > n_heads || q_stride % 4 || kv_stride % 4 || table_stride % 4 ||
+      table_stride < 2 * (size_t)head_dim ||
+      ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)table) & 15) {
+    raise("%s: needs head_dim and the row strides multiples of 4, a table row per row and 16-byte aligned rows", name);
+    return;
+  }
+  if (pos0 < 0 || pos0 + rows > seq_len) {
+    raise("%s: positions %d..%d are outside the cache of %d", name, pos0, pos0 + rows - 1, seq_len);
+    return;
+  }
+  size_t pos_stride, head_base;
+  strides(n_kv_heads, head_dim, seq_len, kv_head_major(), &pos_stride, &head_base);
+  const size_t f = sizeof(float), kv_dim = (size_t)n_kv_heads * head_dim;
+  Call call(name);
+  Ref Q = call.out2d(q, (size_t)n_heads * head_dim * f, q_stride * f, (size_t)rows, true);
+  Ref K = call.out2d(k, kv_dim * f, kv_stride * f, (size_t)rows, true);
+  Ref V = call.in2d(v, kv_dim * f, kv_stride * f, (size_t)rows);
+  Ref T = call.in2d(table, 2 * (size_t)head_dim * f, table_stride * f, (size_t)rows);
+  Ref KC = call.out(key_cache, (size_t)seq_len * kv_dim * f, true), VC = call.out(value_cache, (size_t)seq_len * kv_dim * f, true);
+  if (!call.ready())
+    return;
+  if (launch_rope_kv_rows(call.ptr<float>(Q), q_stride, call.ptr<float>(K), call.ptr<const float>(V), kv_stride,
+                          call.ptr<const float>(T), table_stride, rows, n_heads, n_kv_heads, head_dim,
+                          call.ptr<float>(KC), call.ptr<float>(VC), pos0, pos_stride, head_base, call.stream()))
+    call.finish();
+}
+
 // ---- embedding rows (src/tp.c:395-396, 444-456) -------------------------------------------------------------------
 
 void k_embed_q8_rows(float *out, const int8_t *table, const float *scales, const int *ids, int count, int dim, int gs,

@@ -215,6 +215,10 @@ bool launch_rope(float *q, size_t q_stride, float *k, size_t k_stride, const flo
                  int rows, int n_heads, int n_kv_heads, int head_dim, hipStream_t stream);
 bool launch_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,
                      size_t pos_stride, size_t head_base, hipStream_t stream);
+// rope_rows of q and k, then k and v stored into the caches at pos0.. (and k written back rotated), in one launch
+bool launch_rope_kv_rows(float *q, size_t q_stride, float *k, const float *v, size_t kv_stride, const float *table,
+                         size_t table_stride, int rows, int n_heads, int n_kv_heads, int head_dim, float *key_cache,
+                         float *value_cache, int pos0, size_t pos_stride, size_t head_base, hipStream_t stream);
 bool launch_embed_rows(float *out, const int8_t *table, const float *scales, const int *ids, int count, int dim,
                        int gs, int vocab, hipStream_t stream);
 bool launch_embed_rows_f32(float *out, const float *table, const int *ids, int count, int dim, int vocab,

@@ -608,10 +608,15 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
                                   {vd, kvl, e->wv[l].f(), nullptr, (size_t)d, kvl, GEMM_STORE}};
       gemm_f32_or_bf16(e, e->bxb, d, count, d, qkv, 3, l, kQkv, -1);
     }
-    k_rope_apply_rows(e->bq, d, kd, kvl, brope, 2 * (size_t)hd, count, nh, nkv, hd);
-    if (head) {
-      k_kv_store(kc, kd, kvl, pos0, count, nkv, hd, c.seq_len);
-      k_kv_store(vc, vd, kvl, pos0, count, nkv, hd, c.seq_len);
+    if (head && hd % 4 == 0) { // RoPE and both cache stores in one launch (bitwise the three calls below)
+      llhip_rope_kv_store_rows(e->bq, d, kd, vd, kvl, brope, 2 * (size_t)hd, count, nh, nkv, hd, kc, vc, pos0,
+                               c.seq_len);
+    } else { // in the rows layout the QKV GEMM wrote k and v into the cache rows themselves
+      k_rope_apply_rows(e->bq, d, kd, kvl, brope, 2 * (size_t)hd, count, nh, nkv, hd);
+      if (head) {
+        k_kv_store(kc, kd, kvl, pos0, count, nkv, hd, c.seq_len);
+        k_kv_store(vc, vd, kvl, pos0, count, nkv, hd, c.seq_len);
+      }
     }
     k_attention_batch_kv(e->bxb, e->bq, kc, vc, nullptr, &e->work, nh, nkv, hd, c.seq_len, pos0, count);
     if (e->q8) {

@@ -143,6 +143,43 @@ __global__ __launch_bounds__(kThreads) void kv_store(float *__restrict__ cache, 
   cache[(size_t)(pos0 + r) * pos_stride + (size_t)g * head_base + d] = src[(size_t)r * src_ld + rest];
 }
 
+// RoPE of a batch of rows and their K/V cache stores in one launch: thread i takes four dimensions (one float4) of row
+// r's q heads, then of its k heads, then of its v heads. q and k are rotated as rope_rows rotates them (the same
+// products, rounded the same way), k and v go into the cache at position pos0 + r, and k is also written back rotated:
+// bitwise rope_rows then the two kv_store calls. 16-byte aligned rows, head_dim % 4 == 0.
+__global__ __launch_bounds__(kThreads) void rope_kv_rows(float *__restrict__ q, size_t q_stride, float *__restrict__ k,
+                                                         const float *__restrict__ v, size_t kv_stride,
+                                                         const float *__restrict__ table, size_t table_stride, int rows,
+                                                         int n_heads, int n_kv_heads, int head_dim,
+                                                         float *__restrict__ key_cache, float *__restrict__ value_cache,
+                                                         int pos0, size_t pos_stride, size_t head_base) {
+  const int hd4 = head_dim / 4, qu = n_heads * hd4, ku = n_kv_heads * hd4;
+  const long long per_row = qu + 2LL * ku;
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= per_row * rows)
+    return;
+  const int r = (int)(i / per_row), u = (int)(i % per_row);
+  const float *t = table + (size_t)r * table_stride;
+  if (u < qu) {
+    const int h = u / hd4, d = 4 * (u % hd4);
+    float4 *p = reinterpret_cast<float4 *>(q + (size_t)r * q_stride + (size_t)h * head_dim + d);
+    *p = rotate4(*p, t, head_dim, d);
+    return;
+  }
+  const bool is_k = u < qu + ku;
+  const int w = is_k ? u - qu : u - qu - ku, g = w / hd4, d = 4 * (w % hd4);
+  const size_t at = (size_t)r * kv_stride + (size_t)g * head_dim + d;
+  const size_t slot = (size_t)(pos0 + r) * pos_stride + (size_t)g * head_base + d;
+  if (is_k) {
+    float4 *p = reinterpret_cast<float4 *>(k + at);
+    const float4 x = rotate4(*p, t, head_dim, d);
+    *p = x;
+    *reinterpret_cast<float4 *>(key_cache + slot) = x;
+  } else {
+    *reinterpret_cast<float4 *>(value_cache + slot) = *reinterpret_cast<const float4 *>(v + at);
+  }
+}
+
 // ---- embedding rows -------------------------------------------------------------------------------------------------
 
 // out[i][j] = table[ids[i]][j] * scales[(ids[i] * dim + j) / gs]: the int8 value converted exactly and one float
@@ -1010,6 +1047,16 @@ bool launch_rope(float *q, size_t q_stride, float *k, size_t k_stride, const flo
   hipLaunchKernelGGL(rope_rows, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream, q,
                      q_stride, k, k_stride, table, table_stride, rows, n_heads, n_kv_heads, head_dim);
   return launch_ok("rope_rows");
+}
+
+bool launch_rope_kv_rows(float *q, size_t q_stride, float *k, const float *v, size_t kv_stride, const float *table,
+                         size_t table_stride, int rows, int n_heads, int n_kv_heads, int head_dim, float *key_cache,
+                         float *value_cache, int pos0, size_t pos_stride, size_t head_base, hipStream_t stream) {
+  const long long threads = (long long)rows * (n_heads + 2LL * n_kv_heads) * (head_dim / 4);
+  hipLaunchKernelGGL(rope_kv_rows, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream, q,
+                     q_stride, k, v, kv_stride, table, table_stride, rows, n_heads, n_kv_heads, head_dim, key_cache,
+                     value_cache, pos0, pos_stride, head_base);
+  return launch_ok("rope_kv_rows");
 }
 
 bool launch_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int count, int n_kv_heads, int head_dim,

@@ -497,6 +497,40 @@ def test_recorded_rmsnorm_runs_before_any_other_call():
     assert np.array_equal(hu.host(dxq), q2)
 
 
+@pytest.mark.parametrize("rows,nh,nkv,hd,seq,pos0,layout", [(5, 32, 8, 128, 64, 3, "head"), (37, 8, 2, 64, 100, 60, "head"),
+                                                             (3, 4, 4, 32, 10, 7, "rows"), (130, 24, 8, 128, 300, 0, "head")])
+def test_rope_kv_store_rows_fused(rows, nh, nkv, hd, seq, pos0, layout):
+    """llhip_rope_kv_store_rows: bitwise k_rope_apply_rows of q and k then k_kv_store of k and v (the caches, q and the
+    rotated k), in either cache layout."""
+    L = hu.lib()
+    assert L.kernels_kv_layout_select(layout.encode()) == 1
+    try:
+        rng = orc.Rng(orc.SEED + 4100 + rows + nh + hd + pos0)
+        d, kvl = nh * hd, nkv * hd
+        q, k, v = (rng.normal(rows * n, 0, 1).reshape(rows, n) for n in (d, kvl, kvl))
+        table = rng.uniform(rows * 2 * hd, 1.0).reshape(rows, 2 * hd)
+        kc0, vc0 = rng.normal(seq * kvl, 0, 1), rng.normal(seq * kvl, 0, 1)
+        out = []
+        for fused in (True, False):
+            dq, dk, dv, dt = hu.dev(q), hu.dev(k), hu.dev(v), hu.dev(table)
+            dkc, dvc = hu.dev(kc0), hu.dev(vc0)
+            if fused:
+                L.llhip_rope_kv_store_rows(lh.ptr(dq), d, lh.ptr(dk), lh.ptr(dv), kvl, lh.ptr(dt), 2 * hd, rows, nh, nkv,
+                                           hd, lh.ptr(dkc), lh.ptr(dvc), pos0, seq)
+            else:
+                L.k_rope_apply_rows(lh.ptr(dq), d, lh.ptr(dk), kvl, lh.ptr(dt), 2 * hd, rows, nh, nkv, hd)
+                L.k_kv_store(lh.ptr(dkc), lh.ptr(dk), kvl, pos0, rows, nkv, hd, seq)
+                L.k_kv_store(lh.ptr(dvc), lh.ptr(dv), kvl, pos0, rows, nkv, hd, seq)
+            assert lh.last_error() == "", lh.last_error()
+            out.append([hu.bits(hu.host(a)) for a in (dq, dk, dkc, dvc)])
+        for what, a, b in zip(("q", "k", "key cache", "value cache"), *out):
+            assert np.array_equal(a, b), what
+        wq, wk = orc.rope_apply(q[0], k[0], table[0], nh, nkv, hd)  # the oracle on the first row
+        assert np.array_equal(out[0][0][0], hu.bits(wq)) and np.array_equal(out[0][1][0], hu.bits(wk))
+    finally:
+        L.kernels_kv_layout_select(b"head")
+
+
 # ---- RoPE and the cache stores recorded into the decode attention ----------------------------------------------------
 
 
