@@ -4,9 +4,11 @@
 // The tiled kernel (gemm.hip) computes 256 activation rows per tile whatever m is, so below a few dozen rows its time
 // is that of m = 256, about three times the time to stream the weights. Here the weights are streamed once, as in the
 // decode GEMV: a block owns 16 weight rows (16 output columns, and the same 16 of W3 under SWIGLU) and its waves (four
-// or eight) split K into consecutive ranges. Per 64-value K step a wave loads its 1 KB of weights (16 bytes per lane)
-// straight into the B operand of v_mfma_i32_16x16x64_i8 and the activations (16 rows per MFMA tile, MT = 1 or 2
-// tiles) into the A operand, four steps ahead. At a group's last step the exact int32 dots are rescaled,
+// or eight) split K into consecutive ranges. A wave loads the weights of two 64-value K steps at once, as two loads of
+// 1 KB that each take 128 contiguous bytes of eight rows (a load of one step's operand would take 64 bytes of each of
+// 16 rows, half a cache line, and took up to 19% longer on the 8B shapes), and forms the B operand of v_mfma_i32_16x16x64_i8 for each
+// step with one DPP row shift per register. The activations (16 rows per MFMA tile, MT = 1 or 2 tiles) load straight
+// into the A operand; two pairs of steps are in flight. At a group's last step the exact int32 dots are rescaled,
 // acc += ((float)dot * ws) * xs, from scales staged in LDS. The waves' partial sums of an output meet in LDS and are
 // added in wave order; the epilogue (STORE, ADD, SWIGLU) follows.
 #include <atomic>
@@ -19,7 +21,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kSkDepth = 4; // K steps in flight per wave
+constexpr int kSkPairs = 2; // pairs of K steps in flight per wave
 
 struct SkSeg {
   float *c;
@@ -92,20 +94,33 @@ template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_ge
   const __amdgpu_buffer_rsrc_t rA = sk_buffer(p.xq, (long long)p.m * k);
   const __amdgpu_buffer_rsrc_t none = sk_buffer(p.xq, 0);
   const int off = (int)((lane & 15) * k) + (lane >> 4) * 16; // MFMA operand: row lane % 16, K bytes 16 (lane / 16) ..
+  // Weights two K steps at a time: load X takes rows 0-7 and Y rows 8-15, each row's 128 bytes whole (lane l: row
+  // l % 8, 16-byte chunk l / 16 + 4 ((l % 16) / 8), so lanes 0-7 of each 16-lane row hold the first step's chunk and
+  // lanes 8-15 the second's). A pair may reach past the wave's range or the row's end: the activations of such a step
+  // read zero, so whatever weight bytes it holds add nothing.
+  const int chunk = (lane >> 4) + 4 * ((lane >> 3) & 1);
+  const int offX = (int)((lane & 7) * k) + 16 * chunk, offY = offX + (int)(8 * k);
 
-  v4i b[kSkDepth], b3[kSkDepth], a[kSkDepth][MT];
-  auto issue = [&](int step, v4i &bb, v4i &bb3, v4i (&aa)[MT]) {
-    const bool live = step < s1;
-    const int k0 = step * 64;
-    bb = __builtin_amdgcn_raw_buffer_load_b128(live ? rB : none, off, k0, kStream);
-    bb3 = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3 : none, off, k0, kStream);
+  v4i x[kSkPairs], y[kSkPairs], x3[kSkPairs], y3[kSkPairs], a[kSkPairs][2][MT];
+  auto issue = [&](int st, int d) { // steps st and st + 1
+    const bool live = st < s1;
+    const int k0 = st * 64;
+    x[d] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB : none, offX, k0, kStream);
+    y[d] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB : none, offY, k0, kStream);
+    if (swiglu) {
+      x3[d] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3 : none, offX, k0, kStream);
+      y3[d] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3 : none, offY, k0, kStream);
+    }
 #pragma unroll
-    for (int t = 0; t < MT; t++)
-      aa[t] = __builtin_amdgcn_raw_buffer_load_b128(live ? rA : none, off + (int)(16 * t * k), k0, 0);
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int t = 0; t < MT; t++)
+        a[d][h][t] =
+            __builtin_amdgcn_raw_buffer_load_b128(st + h < s1 ? rA : none, off + (int)(16 * t * k), k0 + 64 * h, 0);
   };
 #pragma unroll
-  for (int d = 0; d < kSkDepth; d++)
-    issue(s0 + d, b[d], b3[d], a[d]);
+  for (int d = 0; d < kSkPairs; d++)
+    issue(s0 + 2 * d, d);
   __syncthreads(); // the scales are staged
 
   v4f acc[MT], acc3[MT];
@@ -115,32 +130,51 @@ template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_ge
     acc[t] = acc3[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     dot[t] = dot3[t] = v4i{0, 0, 0, 0};
   }
+  // The operand of step h of a pair (row lane % 16, chunk lane / 16): X with lanes 8-15 of each 16-lane row taken from
+  // Y's lanes 0-7 (h = 0, DPP row_shr:8 into banks 2-3), or Y with lanes 0-7 taken from X's lanes 8-15 (h = 1,
+  // row_shl:8 into banks 0-1).
+  auto operand = [&](const v4i &lo, const v4i &hi, int h) {
+    v4i r;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      r[e] = h == 0 ? __builtin_amdgcn_update_dpp(lo[e], hi[e], 0x118, 0xF, 0xC, false)
+                    : __builtin_amdgcn_update_dpp(hi[e], lo[e], 0x108, 0xF, 0x3, false);
+    return r;
+  };
   const int lr = (lane >> 4) * 4, lc = lane & 15;
-  // whole rounds of kSkDepth steps (the ring's slots are constants); steps past s1 add zero dots
-  for (int step = s0; step < s1; step += kSkDepth) {
+  // whole rounds of kSkPairs pairs (the ring's slots are constants); steps past s1 multiply zero activations
+  for (int step = s0; step < s1; step += 2 * kSkPairs) {
 #pragma unroll
-    for (int d = 0; d < kSkDepth; d++) {
-      const int st = step + d;
-      const bool first = st % spg == 0, last = st % spg == spg - 1;
+    for (int d = 0; d < kSkPairs; d++) {
 #pragma unroll
-      for (int t = 0; t < MT; t++) {
-        dot[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][t], b[d], first ? v4i{0, 0, 0, 0} : dot[t], 0, 0, 0);
+      for (int h = 0; h < 2; h++) {
+        const int st = step + 2 * d + h;
+        const bool first = st % spg == 0, last = st % spg == spg - 1;
+        const v4i b = operand(x[d], y[d], h);
+        v4i b3 = b;
         if (swiglu)
-          dot3[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][t], b3[d], first ? v4i{0, 0, 0, 0} : dot3[t], 0, 0, 0);
-      }
-      issue(st + kSkDepth, b[d], b3[d], a[d]);
-      if (last) {
-        const int g = min(st / spg, G - 1); // past the end the dots are zero; any group's scales will do
-        const float wsc = sws[lc * G + g], w3sc = sw3s[lc * G + g];
+          b3 = operand(x3[d], y3[d], h);
 #pragma unroll
-        for (int t = 0; t < MT; t++)
+        for (int t = 0; t < MT; t++) {
+          dot[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b, first ? v4i{0, 0, 0, 0} : dot[t], 0, 0, 0);
+          if (swiglu)
+            dot3[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b3, first ? v4i{0, 0, 0, 0} : dot3[t], 0, 0, 0);
+        }
+        if (h == 1)
+          issue(step + 2 * d + 2 * kSkPairs, d);
+        if (last) {
+          const int g = min(st / spg, G - 1); // past the end the dots are zero; any group's scales will do
+          const float wsc = sws[lc * G + g], w3sc = sw3s[lc * G + g];
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const float xsc = sxs[(16 * t + lr + e) * G + g];
-            acc[t][e] = fmaf((float)dot[t][e] * wsc, xsc, acc[t][e]);
-            if (swiglu)
-              acc3[t][e] = fmaf((float)dot3[t][e] * w3sc, xsc, acc3[t][e]);
-          }
+          for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const float xsc = sxs[(16 * t + lr + e) * G + g];
+              acc[t][e] = fmaf((float)dot[t][e] * wsc, xsc, acc[t][e]);
+              if (swiglu)
+                acc3[t][e] = fmaf((float)dot3[t][e] * w3sc, xsc, acc3[t][e]);
+            }
+        }
       }
     }
   }

@@ -374,11 +374,13 @@ def test_gemm_q8_all_kinds_within_budget(m, n, k, gs):
 
 
 @pytest.mark.parametrize("m", [1, 2, 7, 16, 17, 32])
-@pytest.mark.parametrize("n,k,gs", [(300, 4096, 64), (136, 14336, 256), (70, 2048, 128)])
+@pytest.mark.parametrize("n,k,gs", [(300, 4096, 64), (136, 14336, 256), (70, 2048, 128), (100, 2368, 64),
+                                    (48, 2496, 192)])
 def test_gemm_q8_short_batches(m, n, k, gs):
     """At most 32 rows take the skinny kernel (weights streamed once, K split over a block's waves): every kind and a
     three-segment QKV call within the budget, and each output equal to the tiled kernel's within the budget (a forced
-    split count selects the tiled kernel)."""
+    split count selects the tiled kernel). k = 2368 and 2496 give an odd number of K steps per wave, so a pair of
+    steps loaded together reaches into the next wave's range or past the row's end."""
     L = hu.lib()
     xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 1212 + m + n)
     ldc = n + 3
