@@ -3,10 +3,11 @@
 //
 // The tiled kernel (gemm.hip) computes 256 activation rows per tile whatever m is, so below a few dozen rows its time
 // is that of m = 256, about three times the time to stream the weights. Here the weights are streamed once, as in the
-// decode GEMV: a block owns 16 weight rows (16 output columns, and the same 16 of W3 under SWIGLU) and its waves (four
-// or eight) split K into consecutive ranges. A wave loads the weights of two 64-value K steps at once, as two loads of
-// 1 KB that each take 128 contiguous bytes of eight rows (a load of one step's operand would take 64 bytes of each of
-// 16 rows, half a cache line, and took up to 19% longer on the 8B shapes), and forms the B operand of v_mfma_i32_16x16x64_i8 for each
+// decode GEMV: a block owns 16 weight rows (16 output columns, and the same 16 of W3 under SWIGLU), or 32 as two MFMA
+// tiles sharing each activation load for batches of 17-32 rows on wide grids, and its waves (four or eight) split K
+// into consecutive ranges. A wave loads the weights of two 64-value K steps at once, as two loads of 1 KB that each
+// take 128 contiguous bytes of eight rows (a load of one step's operand would take 64 bytes of each of 16 rows, half a
+// cache line, and took up to 19% longer on the 8B shapes), and forms the B operand of v_mfma_i32_16x16x64_i8 for each
 // step with one DPP row shift per register. The activations (16 rows per MFMA tile, MT = 1 or 2 tiles) load straight
 // into the A operand; two pairs of steps are in flight. At a group's last step the exact int32 dots are rescaled,
 // acc += ((float)dot * ws) * xs, from scales staged in LDS. The waves' partial sums of an output meet in LDS and are
@@ -60,7 +61,8 @@ __device__ __forceinline__ float sk_silu_gate(float value, float gate) {
 
 constexpr int kStream = 2; // cache policy nt for the weights, read once
 
-template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_gemm_skinny(SkParams p) {
+template <int MT, int NT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_gemm_skinny(SkParams p) {
+  constexpr int RB = 16 * NT; // weight rows of the block: NT MFMA tiles of 16 sharing each activation load
   extern __shared__ __align__(16) float sk_smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -70,12 +72,12 @@ template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_ge
     s++;
   const SkSeg seg = sk_pick(p, s);
   const bool swiglu = seg.epi == EPI_SWIGLU;
-  const int col0 = (tile - seg.first_tile) * 16;
+  const int col0 = (tile - seg.first_tile) * RB;
   const int G = p.groups, spg = p.gs / 64;
 
-  // scales of the block's 16 weight rows (and their W3 rows) and of the activation rows, all groups
-  float *sws = sk_smem, *sw3s = sws + 16 * G, *sxs = sw3s + 16 * G;
-  for (int i = tid; i < 16 * G; i += 64 * WAVES) {
+  // scales of the block's RB weight rows (and their W3 rows) and of the activation rows, all groups
+  float *sws = sk_smem, *sw3s = sws + RB * G, *sxs = sw3s + RB * G;
+  for (int i = tid; i < RB * G; i += 64 * WAVES) {
     const int r = i / G, g = i % G, col = col0 + r;
     sws[i] = col < seg.n ? seg.ws[(long long)col * G + g] : 0.0f;
     sw3s[i] = swiglu && col < seg.n ? seg.w3s[(long long)col * G + g] : 0.0f;
@@ -88,9 +90,14 @@ template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_ge
   // this wave's K steps [s0, s1); steps past s1 load zeros
   const int s0 = wave * p.per, s1 = min(p.steps, s0 + p.per);
   const long long k = p.k;
-  const long long wrows = (long long)min(16, seg.n - col0);
-  const __amdgpu_buffer_rsrc_t rB = sk_buffer(seg.w + (long long)col0 * k, wrows * k);
-  const __amdgpu_buffer_rsrc_t rB3 = sk_buffer(swiglu ? seg.w3 + (long long)col0 * k : seg.w, swiglu ? wrows * k : 0);
+  __amdgpu_buffer_rsrc_t rB[NT], rB3[NT]; // weight tile j: rows col0 + 16 j .. (none past n: zero bytes)
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const int c = min(col0 + 16 * j, seg.n);
+    const long long wrows = (long long)min(16, seg.n - c);
+    rB[j] = sk_buffer(seg.w + (long long)c * k, wrows * k);
+    rB3[j] = sk_buffer(swiglu ? seg.w3 + (long long)c * k : seg.w, swiglu ? wrows * k : 0);
+  }
   const __amdgpu_buffer_rsrc_t rA = sk_buffer(p.xq, (long long)p.m * k);
   const __amdgpu_buffer_rsrc_t none = sk_buffer(p.xq, 0);
   const int off = (int)((lane & 15) * k) + (lane >> 4) * 16; // MFMA operand: row lane % 16, K bytes 16 (lane / 16) ..
@@ -101,15 +108,18 @@ template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_ge
   const int chunk = (lane >> 4) + 4 * ((lane >> 3) & 1);
   const int offX = (int)((lane & 7) * k) + 16 * chunk, offY = offX + (int)(8 * k);
 
-  v4i x[kSkPairs], y[kSkPairs], x3[kSkPairs], y3[kSkPairs], a[kSkPairs][2][MT];
+  v4i x[kSkPairs][NT], y[kSkPairs][NT], x3[kSkPairs][NT], y3[kSkPairs][NT], a[kSkPairs][2][MT];
   auto issue = [&](int st, int d) { // steps st and st + 1
     const bool live = st < s1;
     const int k0 = st * 64;
-    x[d] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB : none, offX, k0, kStream);
-    y[d] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB : none, offY, k0, kStream);
-    if (swiglu) {
-      x3[d] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3 : none, offX, k0, kStream);
-      y3[d] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3 : none, offY, k0, kStream);
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      x[d][j] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB[j] : none, offX, k0, kStream);
+      y[d][j] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB[j] : none, offY, k0, kStream);
+      if (swiglu) {
+        x3[d][j] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3[j] : none, offX, k0, kStream);
+        y3[d][j] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3[j] : none, offY, k0, kStream);
+      }
     }
 #pragma unroll
     for (int h = 0; h < 2; h++)
@@ -123,13 +133,15 @@ template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_ge
     issue(s0 + 2 * d, d);
   __syncthreads(); // the scales are staged
 
-  v4f acc[MT], acc3[MT];
-  v4i dot[MT], dot3[MT];
+  v4f acc[MT][NT], acc3[MT][NT];
+  v4i dot[MT][NT], dot3[MT][NT];
 #pragma unroll
-  for (int t = 0; t < MT; t++) {
-    acc[t] = acc3[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    dot[t] = dot3[t] = v4i{0, 0, 0, 0};
-  }
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      acc[t][j] = acc3[t][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      dot[t][j] = dot3[t][j] = v4i{0, 0, 0, 0};
+    }
   // The operand of step h of a pair (row lane % 16, chunk lane / 16): X with lanes 8-15 of each 16-lane row taken from
   // Y's lanes 0-7 (h = 0, DPP row_shr:8 into banks 2-3), or Y with lanes 0-7 taken from X's lanes 8-15 (h = 1,
   // row_shl:8 into banks 0-1).
@@ -150,57 +162,69 @@ template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_ge
       for (int h = 0; h < 2; h++) {
         const int st = step + 2 * d + h;
         const bool first = st % spg == 0, last = st % spg == spg - 1;
-        const v4i b = operand(x[d], y[d], h);
-        v4i b3 = b;
-        if (swiglu)
-          b3 = operand(x3[d], y3[d], h);
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-          dot[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b, first ? v4i{0, 0, 0, 0} : dot[t], 0, 0, 0);
+        for (int j = 0; j < NT; j++) {
+          const v4i b = operand(x[d][j], y[d][j], h);
+          v4i b3 = b;
           if (swiglu)
-            dot3[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b3, first ? v4i{0, 0, 0, 0} : dot3[t], 0, 0, 0);
+            b3 = operand(x3[d][j], y3[d][j], h);
+#pragma unroll
+          for (int t = 0; t < MT; t++) {
+            dot[t][j] =
+                __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b, first ? v4i{0, 0, 0, 0} : dot[t][j], 0, 0, 0);
+            if (swiglu)
+              dot3[t][j] =
+                  __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b3, first ? v4i{0, 0, 0, 0} : dot3[t][j], 0, 0, 0);
+          }
         }
         if (h == 1)
           issue(step + 2 * d + 2 * kSkPairs, d);
         if (last) {
           const int g = min(st / spg, G - 1); // past the end the dots are zero; any group's scales will do
-          const float wsc = sws[lc * G + g], w3sc = sw3s[lc * G + g];
 #pragma unroll
-          for (int t = 0; t < MT; t++)
+          for (int j = 0; j < NT; j++) {
+            const float wsc = sws[(16 * j + lc) * G + g], w3sc = sw3s[(16 * j + lc) * G + g];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-              const float xsc = sxs[(16 * t + lr + e) * G + g];
-              acc[t][e] = fmaf((float)dot[t][e] * wsc, xsc, acc[t][e]);
-              if (swiglu)
-                acc3[t][e] = fmaf((float)dot3[t][e] * w3sc, xsc, acc3[t][e]);
-            }
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                const float xsc = sxs[(16 * t + lr + e) * G + g];
+                acc[t][j][e] = fmaf((float)dot[t][j][e] * wsc, xsc, acc[t][j][e]);
+                if (swiglu)
+                  acc3[t][j][e] = fmaf((float)dot3[t][j][e] * w3sc, xsc, acc3[t][j][e]);
+              }
+          }
         }
       }
     }
   }
 
   // the waves' partial sums, added in wave order
-  float *red = sxs + 16 * MT * G; // [wave][t][e][lane], then the same for W3
-  const int red3 = WAVES * MT * 4 * 64;
+  constexpr int kParts = MT * NT * 4; // (activation tile, weight tile, element) of each lane
+  float *red = sxs + 16 * MT * G;     // [wave][part][lane], then the same for W3
+  const int red3 = WAVES * kParts * 64;
 #pragma unroll
   for (int t = 0; t < MT; t++)
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      red[((wave * MT + t) * 4 + e) * 64 + lane] = acc[t][e];
-      if (swiglu)
-        red[red3 + ((wave * MT + t) * 4 + e) * 64 + lane] = acc3[t][e];
-    }
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int part = (t * NT + j) * 4 + e;
+        red[(wave * kParts + part) * 64 + lane] = acc[t][j][e];
+        if (swiglu)
+          red[red3 + (wave * kParts + part) * 64 + lane] = acc3[t][j][e];
+      }
   __syncthreads();
-  // wave w finishes (activation tile t, element e) = (te / 4, te % 4) for te = w, w + WAVES, ... of every lane
-  for (int te = wave; te < MT * 4; te += WAVES) {
-    const int t = te / 4, e = te % 4;
+  // wave w finishes parts w, w + WAVES, ... of every lane
+  for (int part = wave; part < kParts; part += WAVES) {
+    const int t = part / (4 * NT), j = part / 4 % NT, e = part % 4;
     float total = 0.0f, gate = 0.0f;
     for (int w = 0; w < WAVES; w++) {
-      total += red[((w * MT + t) * 4 + e) * 64 + lane];
+      total += red[(w * kParts + part) * 64 + lane];
       if (swiglu)
-        gate += red[red3 + ((w * MT + t) * 4 + e) * 64 + lane];
+        gate += red[red3 + (w * kParts + part) * 64 + lane];
     }
-    const int row = 16 * t + lr + e, col = col0 + lc;
+    const int row = 16 * t + lr + e, col = col0 + 16 * j + lc;
     if (row >= p.m || col >= seg.n)
       continue;
     float *o = seg.c + (long long)row * seg.ldc + col;
@@ -213,17 +237,17 @@ template <int MT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_ge
   }
 }
 
-size_t skinny_lds(int mt, int waves, int groups) {
-  return ((size_t)(32 + 16 * mt) * groups + 2 * (size_t)waves * mt * 4 * 64) * sizeof(float);
+size_t skinny_lds(int mt, int nt, int waves, int groups) {
+  return ((size_t)(32 * nt + 16 * mt) * groups + 2 * (size_t)waves * mt * nt * 4 * 64) * sizeof(float);
 }
 
-template <int MT, int WAVES> bool skinny_launch(const SkParams &p, int tiles, hipStream_t stream) {
-  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<MT, WAVES>,
+template <int MT, int NT, int WAVES> bool skinny_launch(const SkParams &p, int tiles, hipStream_t stream) {
+  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<MT, NT, WAVES>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
     return false;
-  hipLaunchKernelGGL((q8_gemm_skinny<MT, WAVES>), dim3((unsigned)tiles), dim3(64 * WAVES),
-                     skinny_lds(MT, WAVES, p.groups), stream, p);
+  hipLaunchKernelGGL((q8_gemm_skinny<MT, NT, WAVES>), dim3((unsigned)tiles), dim3(64 * WAVES),
+                     skinny_lds(MT, NT, WAVES, p.groups), stream, p);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess || raise("launching q8_gemm_skinny failed: %s", hipGetErrorString(e));
 }
@@ -233,16 +257,24 @@ template <int MT, int WAVES> bool skinny_launch(const SkParams &p, int tiles, hi
 // Shapes the skinny kernel takes: at most 32 rows, gs a multiple of 64, 16-byte aligned rows, scales that fit LDS.
 bool q8_gemm_skinny_path(const int8_t *xq, int m, int k, int gs) {
   return m > 0 && m <= 32 && gs > 0 && gs % 64 == 0 && k % gs == 0 && ((uintptr_t)xq & 15) == 0 &&
-         32LL * k < (1LL << 31) && skinny_lds(m > 16 ? 2 : 1, 8, k / gs) <= 160 * 1024;
+         32LL * k < (1LL << 31) && skinny_lds(m > 16 ? 2 : 1, 1, 8, k / gs) <= 160 * 1024;
 }
 
 bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream) {
+  const int mt = job.m > 16 ? 2 : 1, groups = job.k / job.gs;
+  int tiles16 = 0;
+  for (int s = 0; s < job.nseg; s++)
+    tiles16 += (job.seg[s].n + 15) / 16;
+  // Two weight tiles per block halve the activation loads. That pays once the activations are 32 rows and the grid
+  // keeps at least 192 blocks (8B, m = 32: QKV 21.1 -> 16.6 us, W1/W3 43.9 -> 36.7 us); on the 256-tile W2 and Wo it
+  // leaves half the CUs idle (W2 16.4 -> 29.0 us at m = 1).
+  const int nt = mt == 2 && tiles16 >= 384 && skinny_lds(mt, 2, 8, groups) <= 160 * 1024 ? 2 : 1;
   SkParams p{};
   int tiles = 0;
   for (int s = 0; s < job.nseg; s++) {
     const GemmSegmentDev &d = job.seg[s];
     p.seg[s] = SkSeg{d.c, d.ldc, (const int8_t *)d.w, (const int8_t *)d.w3, d.ws, d.w3s, d.n, d.epi, tiles};
-    tiles += (d.n + 15) / 16;
+    tiles += (d.n + 16 * nt - 1) / (16 * nt);
   }
   if (tiles <= 0)
     return true;
@@ -252,16 +284,17 @@ bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream) {
   p.m = job.m;
   p.k = job.k;
   p.gs = job.gs;
-  p.groups = job.k / job.gs;
+  p.groups = groups;
   p.steps = job.k / 64;
   // Waves per block split K: eight for grids of fewer than 512 column tiles (W2, Wo: 256), four otherwise (W1/W3: 896),
   // which measured best on the 8B shapes (W2 17.5 vs 24.0 us with four; W1/W3 29.4 vs 31.6 with eight).
-  const int waves = tiles < 512 ? 8 : 4, spg = job.gs / 64;
+  const int waves = tiles16 < 512 ? 8 : 4, spg = job.gs / 64;
   p.per = ((p.steps + waves - 1) / waves + spg - 1) / spg * spg;
-  const int mt = job.m > 16 ? 2 : 1;
+  if (nt == 2)
+    return waves == 8 ? skinny_launch<2, 2, 8>(p, tiles, stream) : skinny_launch<2, 2, 4>(p, tiles, stream);
   if (mt == 1)
-    return waves == 8 ? skinny_launch<1, 8>(p, tiles, stream) : skinny_launch<1, 4>(p, tiles, stream);
-  return waves == 8 ? skinny_launch<2, 8>(p, tiles, stream) : skinny_launch<2, 4>(p, tiles, stream);
+    return waves == 8 ? skinny_launch<1, 1, 8>(p, tiles, stream) : skinny_launch<1, 1, 4>(p, tiles, stream);
+  return waves == 8 ? skinny_launch<2, 1, 8>(p, tiles, stream) : skinny_launch<2, 1, 4>(p, tiles, stream);
 }
 
 } // namespace llhip

@@ -428,6 +428,48 @@ def test_gemm_q8_short_batches(m, n, k, gs):
         L.llhip_set_gemm_splits(0)
 
 
+@pytest.mark.parametrize("m", [17, 32])
+@pytest.mark.parametrize("n", [6152, 6168])
+def test_gemm_q8_short_batches_two_weight_tiles(m, n):
+    """17-32 rows on a grid of at least 384 sixteen-row tiles take blocks of two weight tiles sharing each activation
+    load: every kind within the budget, bitwise equal to the same product split into segments narrow enough for blocks
+    of one tile (the same per-output sums in the same order). n = 6152 leaves the last block's second tile empty and
+    its first half full; 6168 leaves the second tile half full."""
+    L = hu.lib()
+    k, gs = 4096, 64
+    xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 3100 + m + n)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    r3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
+    dx = [hu.dev(a) for a in (xq, xs, wq, ws, w3q, w3s)]
+    base = rng.uniform(m * n, 3.0).reshape(m, n)
+    for kind in (lh.GEMM_STORE, lh.GEMM_ADD, lh.GEMM_SWIGLU):
+        c = hu.dev(base)
+        seg = lh.GemmQ8Segment(lh.ptr(c), n, lh.w8(dx[2], dx[3]), lh.w8(dx[4], dx[5]), None, None, n, kind)
+        L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+        got = hu.host(c)
+        assert lh.last_error() == "", lh.last_error()
+        what = f"two-tile skinny m {m} n {n} kind {kind}"
+        if kind == lh.GEMM_ADD:
+            hu.assert_within_budget(got, base + ref, mag + np.abs(base), what=what)
+        elif kind == lh.GEMM_SWIGLU:
+            want = ref / (1 + np.exp(-ref)) * r3
+            tol = 2e-5 * (mag * (np.abs(r3) + 1) + mag3 * (np.abs(ref) + 1)) + 1e-6
+            assert np.all(np.abs(got - want) <= tol), what
+        else:
+            hu.assert_within_budget(got, ref, mag, what=what)
+        # the same product as 24 segments of at most 16 * 15 rows (each call's grid stays under 384 tiles)
+        one = hu.dev(base)
+        bounds = list(range(0, n, 16 * 15)) + [n]
+        parts = []
+        for lo, hi in zip(bounds[:-1], bounds[1:]):
+            parts.append((lo, hi, hu.dev(wq[lo:hi]), hu.dev(ws[lo:hi]), hu.dev(w3q[lo:hi]), hu.dev(w3s[lo:hi])))
+        for lo, hi, a, b, a3, b3 in parts:
+            sub = one[:, lo:hi]
+            seg = lh.GemmQ8Segment(lh.ptr(sub), n, lh.w8(a, b), lh.w8(a3, b3), None, None, hi - lo, kind)
+            L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+        assert np.array_equal(hu.bits(hu.host(one)), hu.bits(got)), what + " vs one-tile blocks"
+
+
 @pytest.mark.parametrize("m,n,k,gs", [(5, 300, 4096, 64), (40, 136, 14336, 256), (257, 70, 2048, 128)])
 def test_gemm_q8_split_k(m, n, k, gs):
     """Grids of few tiles split K over several blocks per tile (partials added in split order by a second kernel).
