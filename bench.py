@@ -11,6 +11,9 @@ int8-MFMA GEMMs (QKV, Wo + residual, W1/W3 SwiGLU, W2 + residual), then the last
 `decode_1b` and `gemv_2048`: the Llama-3.2-1B decode matmul set and one cold 2048 x 2048 GEMV, launch-amortized.
 `forward_decode`: the whole 8B decode token on the device (the embedding row, the matmul set plus RMSNorm, RoPE, the K/V
 cache store and attention over 2048 cached positions), also from a HIP graph.
+`decode_batch`: one decode step of 4, 16 and 32 sequences through the same matmul set as k_quantize_rows + k_gemm_q8
+on that many rows (the short-batch int8 kernel streams each weight matrix once for all of them), classifier included
+(`--no-batch` skips it).
 `engine`: the engine end to end at the configuration of a Llama-3.1-8B Q8_0 forward (a version-3 checkpoint of
 random-init weights written to /dev/shm): a 2048-token prompt through engine_forward_batch, then 256 greedy
 engine_forward steps (`--no-engine` skips it; `--engine` runs only it).
@@ -308,6 +311,69 @@ def prefill_set(torch, lh, model, seed):
 
     ops = sum(o for _, o in gemms) + 2 * VOCAB * DIM
     return run, gemms, ops
+
+
+def decode_batch_set(torch, lh, model, seed, m):
+    """One decode step of m sequences (a token each) through the 8B matmul set: k_quantize_rows + k_gemm_q8 on m rows
+    per projection, the classifier on every row. Below 33 rows k_gemm_q8 streams each weight matrix once for all rows
+    (the short-batch kernel), so the step reads the weights once for m tokens."""
+    L = lh.load()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 5 + m)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    x_in, h_in = torch.randn(m, DIM, generator=gen, **f32), torch.randn(m, HIDDEN, generator=gen, **f32)
+    xq, xs = torch.empty(m, HIDDEN, dtype=torch.int8, device="cuda"), torch.empty(m, HIDDEN // GS, **f32)
+    q, k, v = torch.empty(m, DIM, **f32), torch.empty(m, KV_DIM, **f32), torch.empty(m, KV_DIM, **f32)
+    resid, hb, logits = torch.zeros(m, DIM, **f32), torch.empty(m, HIDDEN, **f32), torch.empty(m, VOCAB, **f32)
+    torch.cuda.synchronize()
+    P = lh.ptr
+
+    def seg(c, pair, n, kind, pair3=None):
+        w3 = lh.K8Weight(P(pair3[0]), P(pair3[1])) if pair3 else lh.K8Weight()
+        return lh.GemmQ8Segment(P(c), n, lh.K8Weight(P(pair[0]), P(pair[1])), w3, None, None, n, kind)
+
+    calls = []
+    for lay in model.layers:
+        qkv = (lh.GemmQ8Segment * 3)(seg(q, lay["wq"], DIM, lh.GEMM_STORE), seg(k, lay["wk"], KV_DIM, lh.GEMM_STORE),
+                                     seg(v, lay["wv"], KV_DIM, lh.GEMM_STORE))
+        calls += [(DIM, x_in, qkv, 3), (DIM, x_in, seg(resid, lay["wo"], DIM, lh.GEMM_ADD), 1),
+                  (DIM, x_in, seg(hb, lay["w1"], HIDDEN, lh.GEMM_SWIGLU, lay["w3"]), 1),
+                  (HIDDEN, h_in, seg(resid, lay["w2"], DIM, lh.GEMM_ADD), 1)]
+    calls.append((DIM, x_in, seg(logits, model.cls, VOCAB, lh.GEMM_STORE), 1))
+
+    def run_step():
+        for kdim, src, segs, nseg in calls:
+            L.k_quantize_rows(P(xq), P(xs), P(src), kdim, m, kdim, GS)
+            L.k_gemm_q8(P(xq), P(xs), m, kdim, GS, segs, nseg)
+
+    return run_step
+
+
+def decode_batch(torch, lh, model, seed, steps, warmup, sizes=(4, 16, 32)):
+    """The batched decode step at several batch sizes: tok/s = m tokens per step, and the weights' bytes per step over
+    its time (the activations are a few MB)."""
+    L = lh.load()
+    step_bytes = LAYERS * (q8_bytes(DIM + 2 * KV_DIM, DIM) + q8_bytes(DIM, DIM) + 2 * weight_bytes(HIDDEN, DIM)
+                           + q8_bytes(DIM, HIDDEN)) + q8_bytes(VOCAB, DIM)
+    out = {"unit": "tok/s", "workload": "Llama-3.1-8B Q8_0 decode step of m sequences: 32 x (quantize_rows + QKV, "
+                                        "Wo +resid, W1/W3 SwiGLU, W2 +resid as k_gemm_q8 on m rows) + classifier on "
+                                        "m rows, gs 64, HIP graph", "weight_bytes_per_step": step_bytes}
+    for m in sizes:
+        run = decode_batch_set(torch, lh, model, seed, m)
+        run()
+        L.llhip_synchronize()
+        assert L.llhip_graph_begin() == 0
+        run()
+        graph = L.llhip_graph_end()
+        if not graph:
+            raise SystemExit(f"graph capture of the batched decode failed: {lh.last_error()}")
+        sec = time_graph(torch, L, graph, steps, warmup) / steps
+        L.llhip_graph_destroy(graph)
+        out[f"m{m}"] = {"value": round(m / sec, 1), "ms_per_step": round(sec * 1e3, 4),
+                        "weights_gb_s": round(step_bytes / sec / 1e9, 1)}
+        print(f"# batched decode, {m} sequences: {sec * 1e3:.3f} ms/step, {m / sec:.0f} tok/s, "
+              f"{step_bytes / sec / 1e9:.0f} GB/s of weights", file=sys.stderr, flush=True)
+    return out
 
 
 def prefill_3b(torch, lh, seed, steps=3):
@@ -664,6 +730,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-batch", action="store_true", help="skip the batched decode step (4, 16, 32 sequences)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=None,
                     help="threads of the CPU baseline (default: one socket's physical cores, as lscpu reports them)")
@@ -810,6 +877,8 @@ def main():
               f"{ach:.0f} TOP/s in the W1/W3 GEMM", file=sys.stderr, flush=True)
     L.llhip_graph_destroy(graph)
 
+    if not args.no_batch:
+        result["decode_batch"] = decode_batch(torch, lh, model, args.seed, max(5, args.steps // 2), 2)
     if not args.no_1b:
         result["decode_1b"], result["gemv_2048"] = decode_1b(torch, lh, args.seed)
     if not args.no_c3:

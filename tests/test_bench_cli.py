@@ -20,5 +20,6 @@ def test_help_lists_the_sections():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--help"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 0
-    for flag in ("--gpus", "--steps", "--warmup", "--no-cpu", "--no-1b", "--no-c3", "--no-engine", "--no-forward"):
+    for flag in ("--gpus", "--steps", "--warmup", "--no-cpu", "--no-1b", "--no-c3", "--no-engine", "--no-forward",
+                 "--no-batch"):
         assert flag in r.stdout, flag
