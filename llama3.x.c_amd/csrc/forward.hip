@@ -986,7 +986,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
     const int c = grp + k * groups;
     held[k] = summer && c < chunks ? part[(size_t)c * p.slot + d] : 0.0f;
   }
-  const bool mine = threadIdx.x < chunks;
+  const bool mine = (int)threadIdx.x < chunks;
   const float m0 = mine ? part[(size_t)threadIdx.x * p.slot + hd] : -FLT_MAX;
   const float l0 = mine ? part[(size_t)threadIdx.x * p.slot + hd + 1] : 0.0f;
   float m = m0;
