@@ -13,7 +13,7 @@ extern "C" {
 #endif
 
 /* gemm.h:15-20 */
-typedef enum {
+typedef LLHIP_ENUM {
   GEMM_STORE,  /* c = acc */
   GEMM_ADD,    /* c += acc */
   GEMM_SWIGLU, /* c = silu(acc of w) * acc of w3 */
@@ -66,7 +66,7 @@ void amx_s8_tile_gemm(int32_t *c, size_t ldc, const int8_t *a, size_t lda, const
 
 /* gemm.h:78-83: a 64-byte-aligned host workspace (malloc'd here; the reference's accounted allocator is not part of
  * this library, so `kind` is only recorded). */
-typedef enum {
+typedef LLHIP_ENUM {
   MEM_KV,
   MEM_ACTIVATION,
   MEM_EMBEDDING,
@@ -119,7 +119,7 @@ typedef struct {
   int n;
   GemmKind kind;
 } GemmQ8Segment;
-typedef enum { Q8_GEMM_PORTABLE, Q8_GEMM_AVX512, Q8_GEMM_AMX, Q8_GEMM_HIP_MFMA } Q8GemmBackend;
+typedef LLHIP_ENUM { Q8_GEMM_PORTABLE, Q8_GEMM_AVX512, Q8_GEMM_AMX, Q8_GEMM_HIP_MFMA } Q8GemmBackend;
 
 /* gemm.h:130: k_quantize per row (row r of q has stride n, of s stride n / gs), bitwise the per-token result. */
 void k_quantize_rows(int8_t *q, float *s, const float *x, size_t ldx, int m, int n, int gs);
@@ -146,8 +146,8 @@ void pack_s8_vnni_many(const PackS8 *jobs, int count);
 
 /* shards.h:10, 28-38, 66-78: the loaded weight shard the packing jobs of gemm.h:146-153 read, in the reference's
  * layout (role is a TensorRole). */
-typedef enum { DT_F32, DT_Q8 } TensorDtype;
-typedef enum { SHARD_ROWS, SHARD_COLS, SHARD_COPY, SHARD_GLOBAL } ShardKind;
+typedef LLHIP_ENUM { DT_F32, DT_Q8 } TensorDtype;
+typedef LLHIP_ENUM { SHARD_ROWS, SHARD_COLS, SHARD_COPY, SHARD_GLOBAL } ShardKind;
 typedef struct {
   int role;
   int layer;

@@ -13,6 +13,17 @@
 #include <stddef.h>
 #include <stdint.h>
 
+/* C++ (this library) sees these C enums with int as their underlying type, so every int a C caller passes is a value
+ * of the enum: an invalid request reaches the library's check instead of being undefined behaviour to load. C callers
+ * see plain enums, the reference's declarations. */
+#ifndef LLHIP_ENUM
+#ifdef __cplusplus
+#define LLHIP_ENUM enum : int
+#else
+#define LLHIP_ENUM enum
+#endif
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 /* The callers' atomic_int: only its address crosses the boundary, and this library never dereferences it. */
@@ -23,7 +34,7 @@ typedef atomic_int llhip_atomic_int;
 #endif
 
 /* kernels.h:15. KERNELS_HIP is this library's one instruction set; the CPU ones are not compiled in. */
-typedef enum { KERNELS_SCALAR, KERNELS_AVX512, KERNELS_AMX, KERNELS_HIP } KernelIsa;
+typedef LLHIP_ENUM { KERNELS_SCALAR, KERNELS_AVX512, KERNELS_AMX, KERNELS_HIP } KernelIsa;
 void kernels_init(void);                 /* kernels.h:16: reads LLAMA_KERNELS (auto|hip) and opens the device */
 int kernels_select(KernelIsa isa);       /* kernels.h:17: 1 for KERNELS_HIP, 0 for the CPU instruction sets */
 const char *kernels_name(void);          /* kernels.h:18: "hip-gfx950" once initialized, NULL before */
@@ -53,7 +64,7 @@ void k_matmul_swiglu(float *out, const float *x, const float *w1, const float *w
  * form computes member `worker`'s static share of the rows (rows [d*worker/workers, d*(worker+1)/workers)), so the
  * union over members is the team-level result; `claim` is never used (every split here is static) and `done`, when
  * not NULL, is called once with the share after its rows are stored. */
-typedef enum { K_STORE, K_ADD, K_PARTIAL, K_SWIGLU } KernelEpilogue;
+typedef LLHIP_ENUM { K_STORE, K_ADD, K_PARTIAL, K_SWIGLU } KernelEpilogue;
 typedef void (*RowsDoneFn)(void *ctx, int r0, int r1);
 void k_matmul_ld(float *out, const float *x, const float *w, size_t ld, int n, int d, int kind);
 void k_matmul_ld_worker(float *out, const float *x, const float *w, size_t ld, int n, int d, int kind, int worker,

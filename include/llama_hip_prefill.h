@@ -7,6 +7,17 @@
 
 #include <stddef.h>
 
+/* C++ (this library) sees these C enums with int as their underlying type, so every int a C caller passes is a value
+ * of the enum: an invalid request reaches the library's check instead of being undefined behaviour to load. C callers
+ * see plain enums, the reference's declarations. */
+#ifndef LLHIP_ENUM
+#ifdef __cplusplus
+#define LLHIP_ENUM enum : int
+#else
+#define LLHIP_ENUM enum
+#endif
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -20,7 +31,7 @@ typedef struct { /* runtime.h:9-16 */
   char name[128];
 } Config;
 
-typedef enum { LOGITS_NONE, LOGITS_LAST, LOGITS_ALL } LogitsWanted; /* runtime.h:75 */
+typedef LLHIP_ENUM { LOGITS_NONE, LOGITS_LAST, LOGITS_ALL } LogitsWanted; /* runtime.h:75 */
 
 typedef struct { /* runtime.h:87-97 */
   Config config;
