@@ -13,6 +13,11 @@ using namespace llhip;
 
 namespace {
 
+// Positions pos0 .. pos0 + count - 1 lie in a cache of seq_len positions; no sum can overflow.
+bool positions_fit(int pos0, int count, int seq_len) {
+  return pos0 >= 0 && count >= 0 && seq_len > 0 && pos0 <= seq_len && count <= seq_len - pos0;
+}
+
 // src/attention.c:1375-1392: head (the default) is [kv_head][position][head_dim], rows is [position][kv_head][head_dim];
 // LLAMA_KV_LAYOUT=rows|head picks one, read at the first use.
 int kv_layout_head_flag = -1;
@@ -154,8 +159,8 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
           name, n_heads, n_kv_heads, head_dim);
     return;
   }
-  if (pos0 < 0 || pos0 + m > seq_len) {
-    raise("%s: positions %d..%d are outside the cache of %d", name, pos0, pos0 + m - 1, seq_len);
+  if (!positions_fit(pos0, m, seq_len)) {
+    raise("%s: positions %d..%lld are outside the cache of %d", name, pos0, (long long)pos0 + m - 1, seq_len);
     return;
   }
   if (pos_stride < (size_t)head_dim || pos_stride > (size_t)INT32_MAX) {
@@ -344,8 +349,8 @@ void k_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int cou
     raise("k_kv_store: null buffer");
     return;
   }
-  if (pos0 < 0 || pos0 + count > seq_len) {
-    raise("k_kv_store: positions %d..%d are outside the cache of %d", pos0, pos0 + count - 1, seq_len);
+  if (!positions_fit(pos0, count, seq_len)) {
+    raise("k_kv_store: positions %d..%lld are outside the cache of %d", pos0, (long long)pos0 + count - 1, seq_len);
     return;
   }
   size_t pos_stride, head_base;
@@ -385,8 +390,8 @@ void llhip_rope_kv_store_rows(float *q, size_t q_stride, float *k, const float *
     raise("%s: needs head_dim and the row strides multiples of 4, a table row per row and 16-byte aligned rows", name);
     return;
   }
-  if (pos0 < 0 || pos0 + rows > seq_len) {
-    raise("%s: positions %d..%d are outside the cache of %d", name, pos0, pos0 + rows - 1, seq_len);
+  if (!positions_fit(pos0, rows, seq_len)) {
+    raise("%s: positions %d..%lld are outside the cache of %d", name, pos0, (long long)pos0 + rows - 1, seq_len);
     return;
   }
   size_t pos_stride, head_base;

@@ -302,6 +302,27 @@ def test_prefill_validate(record):
     assert lh.last_error() == "forward input out of range: token=100 position=5"
 
 
+def test_cache_position_checks_cannot_overflow(record):
+    """The cache-position checks of k_kv_store, llhip_rope_kv_store_rows and the batched attention compare without
+    forming pos0 + count in int: a batch starting just below INT_MAX is refused (before any device work), not
+    wrapped into range."""
+    L = record
+    buf = np.zeros(256, np.float32)
+    big = 2**31 - 2
+    P = lh.ptr(buf)
+    L.k_kv_store(P, P, 8, big, 4, 1, 8, 100)
+    assert lh.last_error() == f"k_kv_store: positions {big}..{big + 3} are outside the cache of 100"
+    L.llhip_clear_error()
+    L.llhip_rope_kv_store_rows(P, 8, P, P, 8, P, 16, 4, 1, 1, 8, P, P, big, 100)
+    assert lh.last_error() == f"llhip_rope_kv_store_rows: positions {big}..{big + 3} are outside the cache of 100"
+    L.llhip_clear_error()
+    L.k_attention_batch_layout(P, P, P, P, None, None, 1, 1, 8, 100, big, 4, 8, 8)
+    assert f"positions {big}..{big + 3} are outside the cache of 100" in lh.last_error()
+    L.llhip_clear_error()
+    L.k_kv_store(P, P, 8, 0, 4, 1, 8, 0)  # an empty cache holds no position
+    assert "outside the cache of 0" in lh.last_error()
+
+
 def test_hbm_budget_parses_like_the_reference(record, monkeypatch):
     """placement_hbm_budget (src/loader.c:28-37): LLAMA_HBM_BUDGET_GIB in GiB, fractions allowed; zero, negative,
     trailing text and more than 2^20 GiB fail with the reference's message. (The default, the device's memory, needs
