@@ -373,7 +373,7 @@ def test_gemm_q8_all_kinds_within_budget(m, n, k, gs):
     del T
 
 
-@pytest.mark.parametrize("m", [1, 2, 7, 16, 17, 32])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 16, 17, 32])
 @pytest.mark.parametrize("n,k,gs", [(300, 4096, 64), (136, 14336, 256), (70, 2048, 128), (100, 2368, 64),
                                     (48, 2496, 192)])
 def test_gemm_q8_short_batches(m, n, k, gs):
