@@ -644,12 +644,12 @@ size_t attention_decode_lds(int kv_mul, int head_dim) {
          (size_t)kTileThreads * 16;
 }
 
-// Batched attention on the FP32 matrix cores (flash form): query rows in tiles of 128 / kv_mul (the tile's 128 query
-// vectors: row j, query head h of the group as vector j * kv_mul + h, in 8 waves of 16). Block (p, KV head g) takes
-// tile T - 1 - p and then tile p, so every block has about the same number of causal chunks (one block per CU). Per
-// tile it walks the 64-position chunks the tile's rows reach, the K and V rows of a chunk staged in LDS (row stride
-// HD + 4 floats, zero past the last position), double-buffered: the next chunk's loads are in flight while the
-// current one is computed, one barrier per chunk. Each wave
+// Batched attention on the FP32 matrix cores (flash form): query rows in tiles of 128 / kv_mul, rounded down (the tile's
+// query vectors: row j, query head h of the group as vector j * kv_mul + h, in 8 waves of 16; the 128 % kv_mul vectors
+// past the last row idle). Block (p, KV head g) takes tile T - 1 - p and then tile p, so every block has about the
+// same number of causal chunks (one block per CU). Per tile it walks the 64-position chunks the tile's rows reach,
+// the K and V rows of a chunk staged in LDS (row stride HD + 4 floats, zero past the last position), double-buffered:
+// the next chunk's loads are in flight while the current one is computed, one barrier per chunk. Each wave
 //   - scores its 16 vectors against the 64 positions on v_mfma_f32_16x16x4_f32, as S^T = K Q^T: four 16-position
 //     tiles, HD / 4 MFMAs each; the dot's terms go in a permuted order (MFMA step kk, lane group q takes dimension
 //     q * HD / 4 + kk), so a lane's share of its query vector is HD / 4 consecutive floats held in registers and its
@@ -659,7 +659,8 @@ size_t attention_decode_lds(int kv_mul, int head_dim) {
 //     2 (s * log2(e) / divisor, one multiply where the split form divides), so each exponential is the native exp2;
 //   - adds P V to its value sums as O^T = V^T P^T: the score accumulators are the B operand as they stand (MFMA step
 //     (tile t, element e) takes positions 16 t + 4 q + e from lane group q), and V^T is read from LDS, value tile d
-//     holding dimensions HD / 16 * m + d (m = 0..15), so a lane's values of a position are consecutive.
+//     holding dimensions 4 m + d % 4 + 64 (d / 4) (m = 0..15): a lane's values of a position are runs of four, and
+//     the 16 lanes of a read take one contiguous 64-float span of the row, free of LDS bank conflicts.
 // At the end each vector's value sum is divided by its running sum and stored. Every product is FP32 on the matrix
 // cores; the sums run in other orders than the split form's and the scores are rounded once more, within FP32
 // rounding of the same softmax.
@@ -711,9 +712,11 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
     if (pass == 1 && tile >= ntiles - 1 - (int)blockIdx.x)
       break; // the middle tile of an odd count is taken once
     const int r0 = tile * tile_rows, row = r0 + j;
-    const bool active = row < p.rows;
+    // vectors past tile_rows * kv_mul (when kv_mul does not divide 128) would be the next tile's: idle, like rows past
+    // the batch
+    const bool active = j < tile_rows && row < p.rows;
     const int pos = p.pos0 + (active ? row : 0);              // this lane's query row's position
-    const int wave_last = p.pos0 + min(r0 + (wave * 16 + 15) / kv_mul, p.rows - 1);
+    const int wave_last = p.pos0 + min(r0 + min((wave * 16 + 15) / kv_mul, tile_rows - 1), p.rows - 1);
     const int last = p.pos0 + min(r0 + tile_rows, p.rows) - 1; // the tile's last position
     // this lane's dimensions lq * HD / 4 .. + HD / 4 of its query vector
     float qr[kQ];
@@ -809,11 +812,11 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
       for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const float *vr = vs + (16 * t + 4 * lq + e) * kSt + kDt * lc;
+          const float *vr = vs + (16 * t + 4 * lq + e) * kSt + 4 * lc;
           float va[kDt];
 #pragma unroll
           for (int d = 0; d < kDt; d += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(vr + d);
+            const float4 v = *reinterpret_cast<const float4 *>(vr + 16 * d); // dimensions 64 (d / 4) + 4 lc ..
             va[d] = v.x, va[d + 1] = v.y, va[d + 2] = v.z, va[d + 3] = v.w;
           }
 #pragma unroll
@@ -824,14 +827,14 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
     __syncthreads(); // the next tile's first chunk reuses buffer 0
     if (!active)
       continue;
-    // lane (lq, lc) holds dimensions kDt * (4 lq + e) + d of vector lc: for each e, kDt consecutive floats
+    // lane (lq, lc) holds dimensions 4 (4 lq + e) + d % 4 + 64 (d / 4) of vector lc: for each e, runs of four floats
     const float inv = 1.0f / l_run;
     float *dst = p.out + ((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * HD;
 #pragma unroll
     for (int e = 0; e < 4; e++)
 #pragma unroll
       for (int d = 0; d < kDt; d += 4)
-        *reinterpret_cast<float4 *>(dst + kDt * (4 * lq + e) + d) =
+        *reinterpret_cast<float4 *>(dst + 16 * d + 4 * (4 * lq + e)) =
             float4{o[d][e] * inv, o[d + 1][e] * inv, o[d + 2][e] * inv, o[d + 3][e] * inv};
   }
   if (bad)
@@ -1174,7 +1177,7 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
     return raise("internal: a fused RoPE attention on operands the aligned kernel does not take");
   // batches of at least 16 rows with 64 or 128 dimensions per head: the flash kernel on the matrix cores, no merge
   const bool flash = !job.table && aligned && job.rows >= 16 && (job.head_dim == 64 || job.head_dim == 128) &&
-                     128 % kv_mul == 0 && ((uintptr_t)job.out & 15) == 0 && ((uintptr_t)job.value & 15) == 0;
+                     kv_mul <= 128 && ((uintptr_t)job.out & 15) == 0 && ((uintptr_t)job.value & 15) == 0;
   if (flash) {
     // two staged chunks of K and V rows: 4 x 64 x (HD + 4) floats (135 KB at HD = 128)
     static const hipError_t flash_allowed = [] {

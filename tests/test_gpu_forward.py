@@ -291,11 +291,16 @@ def test_attention_batch_rows(nh, nkv, hd, seq, pos0, m):
     (32, 4, 64, 260, 64, 96, "rows"),      # kv_mul 8: 16-row tiles, starting on a chunk boundary
     (64, 4, 128, 200, 33, 50, "head"),     # kv_mul 16: 8-row tiles
     (8, 2, 128, 1500, 1400, 16, "rows"),   # 16 rows, 23 chunks each
+    (24, 8, 128, 2100, 0, 2048, "head"),   # the 3B prompt: kv_mul 3, 42-row tiles of 126 query vectors
+    (12, 4, 64, 300, 21, 100, "rows"),     # kv_mul 3, a ragged last tile
+    (20, 4, 64, 200, 0, 60, "head"),       # kv_mul 5: 25-row tiles, 3 vectors idle
+    (48, 8, 128, 160, 3, 50, "rows"),      # kv_mul 6: 21-row tiles, 2 vectors idle
 ])
 def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout):
     """Batches of at least 16 rows with 64 or 128 dimensions per head run the flash kernel on the FP32 matrix cores:
     every checked row within the float64 budget of the decode attention at its position and within twice it of the
-    oracle, for GQA ratios 1-16, both layouts, ragged tiles and long contexts."""
+    oracle, for GQA ratios 1-16 (those that do not divide 128 leave the tile's last vectors idle), both layouts, ragged
+    tiles and long contexts."""
     L = hu.lib()
     rng = orc.Rng(orc.SEED + 900 + m + hd)
     kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(m * nh * hd, 0, 1)
