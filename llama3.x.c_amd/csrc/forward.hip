@@ -648,8 +648,9 @@ size_t attention_decode_lds(int kv_mul, int head_dim) {
 // query vectors: row j, query head h of the group as vector j * kv_mul + h, in 8 waves of 16; the 128 % kv_mul vectors
 // past the last row idle). Block (p, KV head g) takes tile T - 1 - p and then tile p, so every block has about the
 // same number of causal chunks (one block per CU). Per tile it walks the 64-position chunks the tile's rows reach,
-// the K and V rows of a chunk staged in LDS (row stride HD + 4 floats, zero past the last position), double-buffered:
-// the next chunk's loads are in flight while the current one is computed, one barrier per chunk. Each wave
+// the K and V rows of a chunk staged in LDS by DMA (row stride HD + 4 floats, zero past the last position), two
+// buffers each, with K one chunk ahead of V: step c scores chunk c + 1 while it takes chunk c's softmax and value
+// sums, and the loads of chunk c + 2's K and chunk c + 1's V are in flight meanwhile, one barrier per step. Each wave
 //   - scores its 16 vectors against the 64 positions on v_mfma_f32_16x16x4_f32, as S^T = K Q^T: four 16-position
 //     tiles, HD / 4 MFMAs each; the dot's terms go in a permuted order (MFMA step kk, lane group q takes dimension
 //     q * HD / 4 + kk), so a lane's share of its query vector is HD / 4 consecutive floats held in registers and its
@@ -664,39 +665,43 @@ size_t attention_decode_lds(int kv_mul, int head_dim) {
 // At the end each vector's value sum is divided by its running sum and stored. Every product is FP32 on the matrix
 // cores; the sums run in other orders than the split form's and the scores are rounded once more, within FP32
 // rounding of the same softmax.
-template <int HD> struct FlashStage {
-  static constexpr int kPer = kChunk * (HD / 4) / kTileThreads; // float4 of K (and of V) per thread and chunk
-  float4 k[kPer], v[kPer];
-  // the chunk at t0 of KV head rows kbase / vbase, zero past `last`
-  __device__ __forceinline__ void load(const AttnParams &p, const float *kbase, const float *vbase, int t0, int last) {
+
+// Staging of a 64-position chunk of K (or V) rows into LDS by DMA (buffer_load_dwordx4 ... lds): a load takes
+// 1 KB, lane l's 16 bytes landing at byte 16 l from the wave-uniform base. The rows lie HD + 4 floats apart, so a
+// chunk is 64 (HD / 4 + 1) pieces of 16 bytes, a whole number of loads; a lane whose piece is a row's padding loads
+// a copy of that row's first piece. The buffer resource ends after the tile's last position, so the rows past it
+// read as zero.
+template <int HD> struct FlashDma {
+  static constexpr int kWaves = kTileThreads / kWave;
+  static constexpr int kPieces = HD / 4 + 1;             // per staged row, the padding included
+  static constexpr int kLoads = kChunk * kPieces / kWave; // 1 KB loads per chunk
+  static_assert(kChunk * kPieces % kWave == 0, "a chunk is a whole number of loads");
+  __device__ __forceinline__ static void load(__amdgpu_buffer_rsrc_t r, float *dst, int t0, unsigned stride_bytes,
+                                              int wave, int lane) {
 #pragma unroll
-    for (int u = 0; u < kPer; u++) {
-      const int i = threadIdx.x + u * kTileThreads, t = i / (HD / 4), d4 = i % (HD / 4);
-      k[u] = v[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (t0 + t <= last) {
-        const size_t at = (size_t)(t0 + t) * p.pos_stride + 4 * d4;
-        k[u] = *reinterpret_cast<const float4 *>(kbase + at);
-        v[u] = *reinterpret_cast<const float4 *>(vbase + at);
+    for (int u = 0; u < (kLoads + kWaves - 1) / kWaves; u++) {
+      const int n = u * kWaves + wave;
+      if (n < kLoads) { // wave-uniform
+        const int slot = n * kWave + lane, row = slot / kPieces, piece = slot % kPieces;
+        const unsigned off = (unsigned)(t0 + row) * stride_bytes + 16u * (unsigned)(piece < HD / 4 ? piece : 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(dst + n * 4 * kWave),
+                                                 16, off, 0, 0, 0);
       }
-    }
-  }
-  __device__ __forceinline__ void store(float *ks, float *vs) const {
-#pragma unroll
-    for (int u = 0; u < kPer; u++) {
-      const int i = threadIdx.x + u * kTileThreads, t = i / (HD / 4), d4 = i % (HD / 4);
-      *reinterpret_cast<float4 *>(ks + t * (HD + 4) + 4 * d4) = k[u];
-      *reinterpret_cast<float4 *>(vs + t * (HD + 4) + 4 * d4) = v[u];
     }
   }
 };
 
+// s_waitcnt vmcnt(0): this wave's loads, LDS DMA included, are complete
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(AttnParams p) {
-  constexpr int kSt = HD + 4;      // LDS row stride of a staged K or V row
   constexpr int kQ = HD / 4;       // dimensions per lane group in the score MFMAs
   constexpr int kDt = HD / 16;     // 16-dimension tiles of the value sums
   constexpr int kQv = 128;         // query vectors per tile
-  constexpr int kBuf = 2 * kChunk * kSt; // floats of one staged chunk (K and V)
-  extern __shared__ __align__(16) float lds[];
+  // two K and two V buffers as separate arrays: the compiler then sees that a DMA into one does not alias the reads
+  // of another and lets them overlap
+  constexpr int kSt = HD + 4;      // LDS row stride of a staged K or V row
+  __shared__ __align__(16) float K0[kChunk * kSt], K1[kChunk * kSt], V0[kChunk * kSt], V1[kChunk * kSt];
   const int kv_mul = p.n_heads / p.n_kv_heads, tile_rows = kQv / kv_mul;
   const int ntiles = (p.rows + tile_rows - 1) / tile_rows;
   const int g = blockIdx.y;
@@ -704,6 +709,7 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
   const int lq = lane >> 4, lc = lane & 15;
   const int qv = wave * 16 + lc, j = qv / kv_mul, h = qv % kv_mul;
   const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
+  const unsigned stride_bytes = (unsigned)p.pos_stride * 4u;
   // scores in base 2: s * log2(e) / divisor, so that exp(s / divisor - m) is the native exp2 of (s2 - m2)
   const float scale2 = 1.4426950408889634f / p.divisor;
   bool bad = false;
@@ -715,9 +721,12 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
     // vectors past tile_rows * kv_mul (when kv_mul does not divide 128) would be the next tile's: idle, like rows past
     // the batch
     const bool active = j < tile_rows && row < p.rows;
-    const int pos = p.pos0 + (active ? row : 0);              // this lane's query row's position
+    const int live_to = active ? p.pos0 + row : -1; // this lane's query row's position (none for an idle lane)
     const int wave_last = p.pos0 + min(r0 + min((wave * 16 + 15) / kv_mul, tile_rows - 1), p.rows - 1);
     const int last = p.pos0 + min(r0 + tile_rows, p.rows) - 1; // the tile's last position
+    const int range = (int)(((unsigned)last * stride_bytes) + HD * 4); // bytes of K (V) rows up to `last`
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void *)kbase, (short)0, range, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vbase, (short)0, range, 0x00020000);
     // this lane's dimensions lq * HD / 4 .. + HD / 4 of its query vector
     float qr[kQ];
     {
@@ -733,81 +742,109 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
     for (int d = 0; d < kDt; d++)
       o[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -FLT_MAX, l_run = 0.0f;
-    const int chunks = last / kChunk + 1;
-    FlashStage<HD> st;
-    st.load(p, kbase, vbase, 0, last);
-    for (int c = 0; c < chunks; c++) {
-      const int t0 = c * kChunk;
-      float *ks = lds + (c & 1) * kBuf, *vs = ks + kChunk * kSt;
-      // buffer c % 2 was last read for chunk c - 2, before the barrier of chunk c - 1
-      st.store(ks, vs);
-      __syncthreads();
-      if (c + 1 < chunks)
-        st.load(p, kbase, vbase, t0 + kChunk, last); // in flight while this chunk is computed
-      if (t0 > wave_last)
-        continue; // no row of this wave reaches the chunk (wave-uniform)
-      // S^T: position 16 t + 4 lq + e (t = 0..3, e = 0..3) against this lane's query vector; the four position tiles'
-      // accumulators take turns, so consecutive MFMAs never wait on each other
-      v4f sc[4];
+    // S^T of the chunk staged at ks: position 16 t + 4 lq + e (t = 0..3, e = 0..3) against this lane's query vector;
+    // the four position tiles' accumulators take turns, so consecutive MFMAs never wait on each other. A slice is the
+    // 16 MFMAs of dimensions i .. i + 3 of each lane group's share.
+    auto score_slice = [&](const float *ks, v4f (&sc)[4], int i) {
+      float4 a[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+        a[t] = *reinterpret_cast<const float4 *>(ks + (16 * t + lc) * kSt + lq * kQ + i);
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].x, qr[i], sc[t], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].y, qr[i + 1], sc[t], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].z, qr[i + 2], sc[t], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].w, qr[i + 3], sc[t], 0, 0, 0);
+    };
+    auto score = [&](const float *ks, v4f (&sc)[4]) {
 #pragma unroll
       for (int t = 0; t < 4; t++)
         sc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < kQ; i += 4) {
-        float4 a[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-          a[t] = *reinterpret_cast<const float4 *>(ks + (16 * t + lc) * kSt + lq * kQ + i);
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-          sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].x, qr[i], sc[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-          sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].y, qr[i + 1], sc[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-          sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].z, qr[i + 2], sc[t], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-          sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t].w, qr[i + 3], sc[t], 0, 0, 0);
-      }
-      // causal mask, the chunk maximum over the vector's 64 positions (16 here, the rest in lanes lc + 16, 32, 48)
-      float cmax = -FLT_MAX;
-#pragma unroll
-      for (int t = 0; t < 4; t++)
+      for (int i = 0; i < kQ; i += 4)
+        score_slice(ks, sc, i);
+    };
+    // the softmax of the chunk at t0 (scores in, weights out) in eight phases: phase t < 4 masks and scales position
+    // tile t and takes its maximum (phase 3 also the chunk's maximum over the vector's 64 positions, 16 here and the
+    // rest in lanes lc + 16, 32, 48, and the rescale of the sums); phase 4 + t takes tile t's exponentials and their
+    // sum (phase 7 also the running sums)
+    struct Soft {
+      float cmax, alpha, m_new, psum;
+    };
+    auto weigh_phase = [&](int ph, int t0, v4f (&sc)[4], Soft &w) {
+      if (ph < 4) {
+        const int t = ph;
+        if (t == 0)
+          w.cmax = -FLT_MAX;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const int at = t0 + 16 * t + 4 * lq + e;
-          const bool live = active && at <= pos;
-          float s = -FLT_MAX;
-          if (live) {
-            s = sc[t][e] * scale2;
-            bad |= !isfinite(s);
-          }
+          const bool live = at <= live_to;
+          const float raw = sc[t][e] * scale2; // selected, not branched on: one block for the scheduler
+          bad |= live & !isfinite(raw);
+          const float s = live ? raw : -FLT_MAX;
           sc[t][e] = s;
-          cmax = fmaxf(cmax, s);
+          w.cmax = fmaxf(w.cmax, s);
         }
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-      const float m_new = fmaxf(m_run, cmax);
-      const float alpha = exp2f(m_run - m_new); // 0 before the first live position, 1 when the maximum stays
-      float psum = 0.0f;
-#pragma unroll
-      for (int t = 0; t < 4; t++)
+        if (t == 3) {
+          w.cmax = fmaxf(w.cmax, __shfl_xor(w.cmax, 16));
+          w.cmax = fmaxf(w.cmax, __shfl_xor(w.cmax, 32));
+          w.m_new = fmaxf(m_run, w.cmax);
+          w.alpha = exp2f(m_run - w.m_new); // 0 before the first live position, 1 when the maximum stays
+          w.psum = 0.0f;
+        }
+      } else {
+        const int t = ph - 4;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const float pe = sc[t][e] > -FLT_MAX ? exp2f(sc[t][e] - m_new) : 0.0f;
+          const float pe = sc[t][e] > -FLT_MAX ? exp2f(sc[t][e] - w.m_new) : 0.0f;
           sc[t][e] = pe;
-          psum += pe;
+          w.psum += pe;
         }
-      psum += __shfl_xor(psum, 16);
-      psum += __shfl_xor(psum, 32);
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
+        if (t == 3) {
+          w.psum += __shfl_xor(w.psum, 16);
+          w.psum += __shfl_xor(w.psum, 32);
+          l_run = l_run * w.alpha + w.psum;
+          m_run = w.m_new;
 #pragma unroll
-      for (int d = 0; d < kDt; d++)
-        o[d] *= alpha;
-      // O^T += V^T P^T; the dimension tiles' accumulators take turns
+          for (int d = 0; d < kDt; d++)
+            o[d] *= w.alpha;
+        }
+      }
+    };
+    auto weigh = [&](int t0, v4f (&sc)[4]) {
+      Soft w;
+#pragma unroll
+      for (int ph = 0; ph < 8; ph++)
+        weigh_phase(ph, t0, sc, w);
+    };
+    // the next chunk's scores into sn with this chunk's softmax between their slices, a scheduling barrier after
+    // each slice so that the vector work stays spread over the MFMAs
+    auto score_and_weigh = [&](const float *kn, v4f (&sn)[4], int t0, v4f (&sc)[4]) {
+      constexpr int kSlices = kQ / 4, kPhases = 8 / kSlices;
+      static_assert(8 % kSlices == 0, "the softmax phases spread evenly over the score slices");
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+        sn[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      Soft w;
+#pragma unroll
+      for (int k = 0; k < kSlices; k++) {
+        score_slice(kn, sn, 4 * k);
+#pragma unroll
+        for (int q = 0; q < kPhases; q++)
+          weigh_phase(k * kPhases + q, t0, sc, w);
+        __builtin_amdgcn_sched_barrier(0x100); // only LDS reads may move across: the next slice's K rows, early
+      }
+    };
+    // O^T += V^T P^T from the chunk staged at vs; the dimension tiles' accumulators take turns
+    auto accumulate = [&](const float *vs, const v4f (&sc)[4]) {
 #pragma unroll
       for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -823,8 +860,48 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
           for (int d = 0; d < kDt; d++)
             o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[d], sc[t][e], o[d], 0, 0, 0);
         }
+    };
+    // K of chunk c + 1 is staged one step ahead of V of chunk c, so step c scores chunk c + 1 on the matrix cores
+    // while the vector ALUs take chunk c's softmax, in one stretch of code the compiler interleaves. Chunk c's K lies
+    // in K(c % 2) and its V in V(c % 2). At the start of step c every wave has waited for its loads of the step
+    // before and passed the barrier; then K(c % 2), last read for chunk c (in step c - 1), takes chunk c + 2, and
+    // V((c + 1) % 2), last read for chunk c - 1, takes chunk c + 1.
+    const int chunks = last / kChunk + 1;
+    v4f sc[4];
+    auto step = [&](int c, const float *kn, float *kdma, const float *vs, float *vdma) {
+      const int t0 = c * kChunk;
+      wait_loads();
+      __syncthreads();
+      if (c + 2 < chunks)
+        FlashDma<HD>::load(krs, kdma, t0 + 2 * kChunk, stride_bytes, wave, lane);
+      if (c + 1 < chunks)
+        FlashDma<HD>::load(vrs, vdma, t0 + kChunk, stride_bytes, wave, lane);
+      // a wave skips the chunks past its last row (wave-uniform), and so scores the next chunk only if it reaches it
+      if (c + 1 < chunks && t0 + kChunk <= wave_last) {
+        v4f sn[4];
+        score_and_weigh(kn, sn, t0, sc);
+        accumulate(vs, sc);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          sc[t] = sn[t];
+      } else if (t0 <= wave_last) {
+        weigh(t0, sc);
+        accumulate(vs, sc);
+      }
+    };
+    FlashDma<HD>::load(krs, K0, 0, stride_bytes, wave, lane);
+    if (chunks > 1)
+      FlashDma<HD>::load(krs, K1, kChunk, stride_bytes, wave, lane);
+    FlashDma<HD>::load(vrs, V0, 0, stride_bytes, wave, lane);
+    wait_loads();
+    __syncthreads();
+    score(K0, sc); // every wave reaches chunk 0: wave_last >= pos0 >= 0
+    for (int c = 0; c < chunks; c += 2) {
+      step(c, K1, K0, V0, V1);
+      if (c + 1 < chunks)
+        step(c + 1, K0, K1, V1, V0);
     }
-    __syncthreads(); // the next tile's first chunk reuses buffer 0
+    __syncthreads(); // the next tile's first loads reuse K0, K1 and V0
     if (!active)
       continue;
     // lane (lq, lc) holds dimensions 4 (4 lq + e) + d % 4 + 64 (d / 4) of vector lc: for each e, runs of four floats
@@ -1175,27 +1252,21 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
                        ((uintptr_t)job.q & 15) == 0 && ((uintptr_t)job.key & 15) == 0;
   if (job.table && !aligned)
     return raise("internal: a fused RoPE attention on operands the aligned kernel does not take");
-  // batches of at least 16 rows with 64 or 128 dimensions per head: the flash kernel on the matrix cores, no merge
+  // batches of at least 16 rows with 64 or 128 dimensions per head: the flash kernel on the matrix cores, no merge.
+  // Its loads address a KV head's rows by 32-bit byte offsets, up to 64 positions past the batch's last.
+  const bool offsets_fit =
+      ((uint64_t)job.pos0 + (uint64_t)job.rows + kChunk) * job.pos_stride * 4 + (uint64_t)job.head_dim * 4 <= UINT32_MAX;
   const bool flash = !job.table && aligned && job.rows >= 16 && (job.head_dim == 64 || job.head_dim == 128) &&
-                     kv_mul <= 128 && ((uintptr_t)job.out & 15) == 0 && ((uintptr_t)job.value & 15) == 0;
+                     kv_mul <= 128 && offsets_fit && ((uintptr_t)job.out & 15) == 0 &&
+                     ((uintptr_t)job.value & 15) == 0;
   if (flash) {
-    // two staged chunks of K and V rows: 4 x 64 x (HD + 4) floats (135 KB at HD = 128)
-    static const hipError_t flash_allowed = [] {
-      const hipError_t e = hipFuncSetAttribute((const void *)attn_flash<128>,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, 4 * kChunk * 132 * 4);
-      return e != hipSuccess ? e
-                             : hipFuncSetAttribute((const void *)attn_flash<64>,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 4 * kChunk * 68 * 4);
-    }();
-    if (flash_allowed != hipSuccess)
-      return raise("allowing the attention kernel its LDS failed: %s", hipGetErrorString(flash_allowed));
+    // two staged chunks of K and two of V rows in static LDS: 4 x 64 x HD floats (128 KB at HD = 128)
     const int tile_rows = 128 / kv_mul, tiles = (job.rows + tile_rows - 1) / tile_rows;
     const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)job.n_kv_heads); // a block per pair of tiles
-    const size_t lds = 4 * (size_t)kChunk * (job.head_dim + 4) * sizeof(float);
     if (job.head_dim == 128)
-      hipLaunchKernelGGL(attn_flash<128>, grid, dim3(kTileThreads), lds, stream, p);
+      hipLaunchKernelGGL(attn_flash<128>, grid, dim3(kTileThreads), 0, stream, p);
     else
-      hipLaunchKernelGGL(attn_flash<64>, grid, dim3(kTileThreads), lds, stream, p);
+      hipLaunchKernelGGL(attn_flash<64>, grid, dim3(kTileThreads), 0, stream, p);
     return launch_ok("attn_flash");
   }
   // decode: the slice-parallel kernel for 64 or 128 dimensions and up to eight query vectors per KV head
