@@ -245,11 +245,12 @@ def test_attention_golden_cases_both_layouts():
                                                      (16, 1, 256, 70, (69,)), (4, 2, 32, 40, (39,)),
                                                      (24, 8, 128, 300, (0, 127, 130, 299)),
                                                      (64, 8, 128, 150, (1, 64, 149)), (32, 8, 64, 200, (5, 127, 199)),
-                                                     (16, 2, 64, 100, (63, 99))])
+                                                     (16, 2, 64, 100, (63, 99)),
+                                                     (8, 2, 64, 16500, (16383, 16384, 16499))])
 def test_attention_decode_shapes(nh, nkv, hd, seq, positions):
     """Decode attention at chunk boundaries (63, 64, 65) and GQA ratios 1-16, head_dim 32-256, head-major layout.
     head_dim 64 or 128 with up to 8 query heads per KV head take the decode kernel (the 3B model's 3, the 1B and 8B
-    models' 4, and 8); the others the general one."""
+    models' 4, and 8); the others the general one. The last case reaches 16384 positions (258 chunks to merge)."""
     L = hu.lib()
     rng = orc.Rng(orc.SEED + nh * 31 + hd + seq)
     kc, vc = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1)
