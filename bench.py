@@ -572,9 +572,9 @@ def gemm_bench(exe, threads, args, timeout=600):
 
 def cpu_baseline(threads=None, budget_s=30.0):
     """The reference's own instrument, gemm-bench (tests/gemm_bench.c, built from its sources into oracle/_ref), on
-    this host's cores, as BASELINE.md plans it: the W8A8 GEMV on the five 8B decode shapes with cold weights, scaled
-    to one token (32 x the layer set + the classifier), and the W8A8 Q8 GEMM at m = 2048 on the four 8B prefill
-    shapes, scaled to a 2048-token prompt (32 x the layer; the activation quantization it reports is added). Threads:
+    this host's cores: the W8A8 GEMV on the five 8B decode shapes with cold weights, scaled to one token (32 x the
+    layer set + the classifier), and the W8A8 Q8 GEMM at m = 2048 on the four 8B prefill shapes, scaled to a
+    2048-token prompt (32 x the layer; the activation quantization it reports is added). Threads:
     one socket's physical cores (the reference's single-socket configuration), capped by the CPUs this process may
     use. Falls back to the oracle's threaded scalar GEMV when the reference was not built here."""
     topo = host_topology()

@@ -1,8 +1,8 @@
 """Writes the golden vectors under tests/golden/ by running the reference itself.
 
 The reference (LucianCrainic/llama3.x.c) is C; oracle/Makefile's `ref` target compiles its own sources into
-oracle/_ref/libllama_ref.so (this container only: the sources are not on the GPU box). This script loads that
-library, selects the reference's scalar instruction set (kernels_select(KERNELS_SCALAR), include/kernels.h:15-17) so the
+oracle/_ref/libllama_ref.so (only where the reference's sources are; they do not travel with the tests). This
+script loads that library, selects the reference's scalar instruction set (kernels_select(KERNELS_SCALAR), include/kernels.h:15-17) so the
 portable kernels run, feeds it seeded inputs and stores inputs and outputs as small .npz fixtures. The tests check the
 CPU oracle against these fixtures bit for bit, and the GPU kernels against the oracle.
 

@@ -7,7 +7,7 @@ W8A8 requantizes every activation, so any change of FP32 order flips some roundi
 carry those flips into the logits. The reference's own gate for such comparisons is statistical (rms 0.2, argmax
 0.9, max 16; docs/architecture.md:274, written for real checkpoints). On this random model the reference does not
 meet its own argmax bar against itself: its batched prefill against its per-token path gives rms 0.086 and argmax
-0.79 over the last 256 prompt positions (measured on the GPU box). So the test measures that floor on the same file
+0.79 over the last 256 prompt positions (measured on the MI355X). So the test measures that floor on the same file
 and requires the engine to stay at it: every comparison within the rms and max bars of the gate, and within 1.25x the
 floor's rms and 0.08 (0.15 for the 64 decode rows) of its argmax agreement.
 
@@ -41,7 +41,7 @@ def say(*a):
 
 
 def scratch_dir(tmp_path):
-    """/dev/shm when it can hold the 8.5 GB file with room to spare (it is memory on the GPU box), else tmp_path."""
+    """/dev/shm when it can hold the 8.5 GB file with room to spare (it is host memory), else tmp_path."""
     shm = "/dev/shm"
     if os.path.isdir(shm) and shutil.disk_usage(shm).free > 40 << 30:
         d = os.path.join(shm, f"llhip-c5-{os.getpid()}")

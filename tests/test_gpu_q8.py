@@ -4,7 +4,7 @@ The oracle (oracle/, pinned to the reference by tests/test_oracle.py) is the che
 scales and the int32 group dots are bitwise the oracle's; FP32 outputs lie within the reference's budget
 2e-5 * sum|w x| + 1e-6 of the float64 dequantized reference (tests/q8.c:128-133), which also bounds the difference to
 the reference's own scalar results; the floored relative error d / (|ref| + 1e-3) (tests/q8_engine.c:71) is checked
-against the north-star tolerance 1e-4.
+against the stated tolerance 1e-4.
 """
 import ctypes
 import os
