@@ -296,12 +296,15 @@ def test_attention_batch_rows(nh, nkv, hd, seq, pos0, m):
     (12, 4, 64, 300, 21, 100, "rows"),     # kv_mul 3, a ragged last tile
     (20, 4, 64, 200, 0, 60, "head"),       # kv_mul 5: 25-row tiles, 3 vectors idle
     (48, 8, 128, 160, 3, 50, "rows"),      # kv_mul 6: 21-row tiles, 2 vectors idle
+    (32, 8, 128, 600, 0, 512, "head"),     # a short 8B prompt: 64 blocks
+    (24, 8, 128, 700, 40, 512, "rows"),    # the 3B heads from position 40
+    (32, 8, 64, 300, 0, 130, "head"),      # 1B heads, 130 rows
 ])
 def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout):
     """Batches of at least 16 rows with 64 or 128 dimensions per head run the flash kernel on the FP32 matrix cores:
     every checked row within the float64 budget of the decode attention at its position and within twice it of the
     oracle, for GQA ratios 1-16 (those that do not divide 128 leave the tile's last vectors idle), both layouts, ragged
-    tiles and long contexts."""
+    tiles, short prompts and long contexts."""
     L = hu.lib()
     rng = orc.Rng(orc.SEED + 900 + m + hd)
     kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(m * nh * hd, 0, 1)
@@ -311,7 +314,7 @@ def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout):
                                ps, hb)
     got = hu.host(do).reshape(m, -1)
     assert not lh.last_error()
-    rows = range(m) if m <= 200 else sorted({0, 1, 63, 64, 127, 128, 1000, m - 2, m - 1})
+    rows = range(m) if m <= 200 else sorted(r for r in {0, 1, 63, 64, 127, 128, 300, 1000, m - 2, m - 1} if r < m)
     for i in rows:
         check_attention(got[i], q.reshape(m, -1)[i], kc, vc, nh, nkv, hd, seq, pos0 + i, ps, hb, f"row {i}")
 
