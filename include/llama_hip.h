@@ -107,6 +107,13 @@ void llhip_set_bf16_tile(int tile);
  * int32 group dots are exact either way. For tuning and tests. */
 void llhip_set_q8_tile(int tile);
 
+/* Where the 256 x 256 INT8 kernel forms each group's scale products xs[r] * ws[c]: 2 = on the matrix cores (one bf16
+ * MFMA over exact bf16 parts of the scales per 64 x 16 outputs, then a convert and an FMA per output; the default),
+ * 1 = on the vector unit ((float)dot * ws, then an FMA with xs), 0 = the default (LLAMA_HIP_Q8_SCALES=mfma|valu sets
+ * the same at start-up). The two differ in FP32 rounding only; the int32 group dots are the same. For tuning and
+ * tests. */
+void llhip_set_q8_scales(int where);
+
 /* The int32 probe of the decode GEMV: dots[g * d + r] = the exact int32 dot of group g of input row xq and weight
  * row r, as the streaming GEMV kernel itself forms it before the FP32 rescale (gs % 16 == 0 takes the fast kernel). */
 void llhip_q8_gemv_group_dots(int32_t *dots, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws,

@@ -595,6 +595,8 @@ void llhip_set_bf16_tile(int tile) { set_bf16_tile(tile); }
 
 void llhip_set_q8_tile(int tile) { set_q8_tile(tile); }
 
+void llhip_set_q8_scales(int where) { set_q8_scales(where); }
+
 void llhip_q8_gemv_group_dots(int32_t *dots, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws,
                               size_t ld, int n, int d, int gs) {
   if (gs <= 0 || n % gs || (ld && (ld < (size_t)n || ld % (size_t)gs)))

@@ -29,7 +29,12 @@ struct Device {
   bool capturing = false;
   void *split_partial = nullptr;  // split-K partial tiles: LLHIP_SPLIT_SLOTS x 256 x 128 floats
   unsigned *split_count = nullptr; // split-K arrivals per tile, zero between launches
+  float *scale_ws = nullptr;       // group-major copies of a wide int8 GEMM's scales: LLHIP_SCALE_WS_FLOATS floats
 };
+// The wide int8 GEMM reads each K step's scales from group-major copies ([group][row], rows padded to whole tiles with
+// zeros) of xs and of every segment's ws: 4 Mi floats (16 MB) hold them for m = 2048 and k = 14336 with 4096 weight
+// rows, or k = 4096 with 2 x 14336 (larger calls take the kernel that reads the row-major scales).
+#define LLHIP_SCALE_WS_FLOATS (4u << 20)
 // Partial tiles of the split-K workspace (one per block of a split launch): 512 x 128 KB = 64 MB of HBM. Launches on
 // the library's stream are ordered, so one workspace per device serves them all.
 #define LLHIP_SPLIT_SLOTS 512
@@ -190,6 +195,7 @@ bool set_gemv_shape(int waves_per_row, int blocks_per_cu, int block_waves);
 void set_gemm_splits(int splits); // FP32 / BF16 / INT8 GEMM blocks per tile; 0 = chosen from the grid
 void set_bf16_tile(int tile);     // BF16 GEMM tile: 0 by grid, 1 256 x 128, 2 256 x 256
 void set_q8_tile(int tile);       // INT8 GEMM tile (gs = 64): 0 by grid, 1 256 x 128, 2 256 x 256
+void set_q8_scales(int where);    // wide INT8 GEMM scale products: 0 default, 1 VALU, 2 matrix cores
 bool gemv_fast_path(const GemvJob &job);
 bool launch_q8_gemv(const GemvJob &job, hipStream_t stream);
 

@@ -50,6 +50,8 @@ struct TileSeg {
   int ntiles;     // its column tiles
   int8_t *cq;     // SWIGLU output quantized in groups of 64 (the wide int8 kernel only), else null
   float *cs;
+  const float *wsg, *w3sg; // q8_gemm_wide_smma: ws and w3s group-major, [group][npad] (rows past n zero)
+  int npad;
 };
 
 struct TileGrid {
@@ -271,6 +273,8 @@ struct Q8Params {
   int32_t *probe; // optional (one segment, no SWIGLU): probe[(g * m + r) * n + c]
   SplitK sk;
   int *flags; // [0]: a non-finite value met by a quantizing epilogue
+  const float *xsg; // q8_gemm_wide_smma: xs group-major, [group][mpad] (rows past m zero)
+  int mpad;
 };
 
 __device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical, int tile_m = kQ8TileM,
@@ -305,6 +309,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t q8_buffer(const void *base, lo
 // s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14).
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+// The same with lgkmcnt = 0 too (every LDS access of this thread done).
+template <int N> __device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | ((N >> 4) << 14));
 }
 
 // Split K: a grid with fewer tiles than CUs runs each tile as `splits` blocks over consecutive K ranges, each writing
@@ -1190,6 +1198,308 @@ template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_w
   store_tile_wide(seg, t, acc, wm, wn, lane, p.m, p.flags);
 }
 
+// ---- W8A8 Q8_0, wide tiles, the scale products on the matrix cores ------------------------------------------------
+//
+// q8_gemm_wide spends three VALU instructions per output and group (convert, multiply by ws, FMA with xs): 48 cycles
+// of a 16-lane SIMD per 16 x 16 tile against the 16 of its int8 MFMA. This kernel takes the product xs[r] * ws[c]
+// from the matrix cores instead, so a tile's rescale is a convert and an FMA: c += (float)dot * S[r][c].
+//
+// S for a wave's 64 rows and one 16-column tile is one v_mfma_f32_32x32x16_bf16 (32 cycles for four tiles). Each FP32
+// scale x is split exactly into three bf16 parts, x = h + m + l: h the top 8 significant bits, m the next 8 of x - h,
+// l the 8 that remain (each part is the exact high half of a float). Slots 0..7 of K carry eight of the nine cross
+// products of the two scales (all but l * l, below 2^-32 of the product): A holds [h h m m h l m l] of xs and B
+// [h m h m l h l m] of ws, pairing hh, hm, mh, mm, hl, lh, ml, lm. In that order each dword of A and of B draws on
+// the same two of the three parts, so one v_perm with a wave-uniform selector builds either. Bf16 products are exact
+// in FP32, so S is xs * ws to FP32 rounding (the MFMA's sum of eight exact terms), where q8_gemm_wide rounds
+// (dot * ws) and then its product with xs: the two orders differ in FP32 rounding only.
+//
+// The 32 x 32 result puts element v of lane l at row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 (checked on the
+// hardware), where the int8 tiles need rows 16 i + 4 (l / 16) + e at column l % 16. So row o of the bf16 tile stands
+// for two rows of the wave, one per column half: K slots 0..7 of A row o hold the parts of row
+// 16 (o / 8) + 8 ((o % 8) / 4) + o % 4, slots 8..15 those of the row 4 further, and B column c holds its column's
+// parts in slots 0..7 when c < 16 and in slots 8..15 when c >= 16 (zeros elsewhere). Lane l then receives in element
+// 4 i + e exactly S of its int8 element e of row tile i.
+//
+// The parts are made once per group for the whole block: each thread splits one scale (xs of a row for waves 0..3, ws
+// of a B-tile row for waves 4..7) into a double-buffered parts area. A group's FP32 scales are loaded one step ahead
+// of its operands, so when the block waits for step s + 1's operands, step s + 2's scales have landed; they are split
+// during step s + 1's MFMAs, and the next barrier publishes them. Results differ from q8_gemm_wide's only in FP32
+// rounding; the int32 group dots are the same exact MFMA sums.
+constexpr int kQSStages = 4, kQSLoadsPerStep = 5; // per wave: two A blocks, two B blocks, one scale load
+constexpr int kQSBOff = 16 * kQSStages * 1024;
+constexpr int kQSSOff = kQSBOff + 16 * kQSStages * 1024;
+constexpr int kQSSStride = 512 * 4;                              // xs of the 256 rows, then ws of the 256 B-tile rows
+constexpr int kQSPOff = kQSSOff + kQSStages * kQSSStride;        // parts: [2 buffers][512 scales] x 16 bytes
+constexpr int kQSPBuf = 512 * 16;
+constexpr int kQSZOff = kQSPOff + 2 * kQSPBuf;                   // zeros read by the B lanes outside their half
+constexpr size_t kQSLds = (size_t)kQSZOff + 1024;                // 153 KB
+static_assert(kQSLds <= 160 * 1024, "one wide int8 block fits a CU's LDS");
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// The wave row whose scale parts sit in slots 0..7 (q = 0) or 8..15 (q = 1) of row o of the bf16 A operand.
+__device__ __forceinline__ int smma_row(int o, int q) { return 16 * (o >> 3) + 8 * ((o & 7) >> 2) + 4 * q + (o & 3); }
+
+// v_perm selectors over (S0, S1) picking the high halves: low half from S1 or S0, high half from S1 or S0.
+constexpr unsigned kLo1Hi1 = 0x03020302u, kLo1Hi0 = 0x07060302u, kLo0Hi0 = 0x07060706u, kLo0Hi1 = 0x03020706u;
+
+template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_wide_smma(Q8Params p) {
+  extern __shared__ __align__(16) unsigned char q8_smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int logical = xcd_logical(blockIdx.x, p.grid.total * (SPLIT ? p.sk.splits : 1));
+  const int tile = SPLIT ? __builtin_amdgcn_readfirstlane(logical / p.sk.splits) : logical;
+  const int split = SPLIT ? __builtin_amdgcn_readfirstlane(logical % p.sk.splits) : 0;
+  const TilePos t = q8_tile_of(p.grid, tile, kWTileM, kWTileN);
+  const TileSeg seg = q8_seg_of(p.grid, t.s);
+  const int groups = p.k / 64, steps = groups;
+  const int s0 = SPLIT ? split * p.sk.per : 0, s1 = SPLIT ? min(steps, s0 + p.sk.per) : steps;
+  const long long k = p.k;
+
+  // Operand loads as in q8_gemm_wide: lane l's 16 bytes at l * 16 of a 1 KB block (row l / 4, chunk l % 4 swizzled).
+  const int lrow4 = lane >> 2, chunk = lane & 3;
+  const int ra = 32 * wave + lrow4;
+  const __amdgpu_buffer_rsrc_t rA = q8_buffer(p.xq + (long long)t.m0 * k, (long long)min(kWTileM, p.m - t.m0) * k);
+  const int offA0 = (int)(ra * k) + ((chunk ^ q8_swizzle(ra)) << 4);
+  const int offA1 = (int)((ra + 16) * k) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
+  auto b_resource = [&](int blk) {
+    const int rb = 16 * blk;
+    const int colB = t.swiglu ? t.n0 + (rb & 127) : t.n0 + rb;
+    const int8_t *wmat = (const int8_t *)((t.swiglu && rb >= 128) ? seg.w3 : seg.w);
+    return q8_buffer(wmat + (long long)colB * k, (long long)min(16, seg.n - colB) * k);
+  };
+  const __amdgpu_buffer_rsrc_t rB0 = b_resource(2 * wave), rB1 = b_resource(2 * wave + 1);
+  const int offB = (int)(lrow4 * k) + ((chunk ^ q8_swizzle(lrow4)) << 4);
+  // Scale loads: thread (wave, lane) loads scale 64 wave + lane of the step: the xs of row 64 wave + lane (waves 0..3)
+  // or the ws of B-tile row 64 (wave - 4) + lane (waves 4..7), and later splits that same scale. They come from the
+  // group-major copies, so a wave's 64 scales of a step are 256 contiguous bytes (rows past m or n hold zeros).
+  __amdgpu_buffer_rsrc_t rS;
+  int offS, pitch; // byte offset of this lane's scale in group 0, bytes from one group to the next
+  if (wave < 4) {
+    rS = q8_buffer(p.xsg, (long long)groups * p.mpad * 4);
+    offS = (t.m0 + 64 * wave + lane) * 4;
+    pitch = p.mpad * 4;
+  } else {
+    const int h = wave - 4;
+    rS = q8_buffer((t.swiglu && h >= 2) ? seg.w3sg : seg.wsg, (long long)groups * seg.npad * 4);
+    offS = ((t.swiglu ? t.n0 + 64 * (h & 1) : t.n0 + 64 * h) + lane) * 4;
+    pitch = seg.npad * 4;
+  }
+  const __amdgpu_buffer_rsrc_t none = q8_buffer(p.xq, 0);
+
+  // The scales of K step `step` into scale stage SST (a step past the end loads zeros).
+  auto issue_scales = [&](int step, auto SST) {
+    constexpr int sst = decltype(SST)::value;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(step < s1 ? rS : none,
+                                             (void *)(q8_smem + kQSSOff + sst * kQSSStride + 64 * wave * 4), 4, offS,
+                                             step * pitch, 0, 0);
+  };
+  // Stage ST gets step `step`'s operands; the scales going out with them are step + 1's (scale stage ST + 1).
+  auto issue = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value;
+    const bool live = step < s1;
+    const int k0 = step * 64;
+    issue_scales(step + 1, std::integral_constant<int, (st + 1) % kQSStages>{});
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
+                                             (void *)(q8_smem + ((2 * wave) * kQSStages + st) * 1024), 16, offA0, k0,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
+                                             (void *)(q8_smem + ((2 * wave + 1) * kQSStages + st) * 1024), 16, offA1,
+                                             k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB0 : none,
+                                             (void *)(q8_smem + kQSBOff + ((2 * wave) * kQSStages + st) * 1024), 16,
+                                             offB, k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB1 : none,
+                                             (void *)(q8_smem + kQSBOff + ((2 * wave + 1) * kQSStages + st) * 1024),
+                                             16, offB, k0, 0, 0);
+  };
+
+  // Splitting this thread's scale of scale stage SST into parts buffer PAR (parts of scale i at 16 i of the buffer).
+  const unsigned char *own_scale = q8_smem + kQSSOff + (64 * wave + lane) * 4;
+  unsigned char *own_parts = q8_smem + kQSPOff + (64 * wave + lane) * 16;
+  // xs parts (waves 0..3) go to slots h h m m h l m l, ws parts (waves 4..7) to h m h m l h l m
+  const bool xs_wave = wave < 4;
+  const unsigned sel0 = xs_wave ? kLo1Hi1 : kLo1Hi0, sel1 = xs_wave ? kLo0Hi0 : kLo1Hi0;
+  const unsigned sel23 = xs_wave ? kLo1Hi0 : kLo0Hi1;
+  auto split_scale = [&](float x, auto PAR) {
+    constexpr int par = decltype(PAR)::value;
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const float r1 = x - __builtin_bit_cast(float, u & 0xFFFF0000u); // exact: the bits of x below its top 8
+    const unsigned u1 = __builtin_bit_cast(unsigned, r1);
+    const float r2 = r1 - __builtin_bit_cast(float, u1 & 0xFFFF0000u); // exact, and at most 8 significant bits
+    const unsigned u2 = __builtin_bit_cast(unsigned, r2);
+    const v4i parts{(int)__builtin_amdgcn_perm(u1, u, sel0), (int)__builtin_amdgcn_perm(u1, u, sel1),
+                    (int)__builtin_amdgcn_perm(u2, u, sel23), (int)__builtin_amdgcn_perm(u2, u1, sel23)};
+    *reinterpret_cast<v4i *>(own_parts + par * kQSPBuf) = parts;
+  };
+
+  // Per-lane LDS read bases.
+  const int lrow = lane & 15;
+  const int lane_part = lrow * 64 + (((lane >> 4) ^ q8_swizzle(lrow)) << 4);
+  const unsigned char *abase = q8_smem + (4 * wm) * kQSStages * 1024 + lane_part;
+  const unsigned char *blo = q8_smem + kQSBOff + (b_row_wide(t.swiglu, wn, 0) / 16) * kQSStages * 1024 + lane_part;
+  const unsigned char *bhi = q8_smem + kQSBOff + (b_row_wide(t.swiglu, wn, 4) / 16) * kQSStages * 1024 + lane_part;
+  // bf16 A operand: lane l holds row o = l % 32 of the 32 x 16 tile, slots 8 (l / 32) ..: the parts of one wave row
+  const unsigned char *xsparts = q8_smem + kQSPOff + (64 * wm + smma_row(lane & 31, lane >> 5)) * 16;
+  // bf16 B operand: lane l holds column l % 32, slots 8 (l / 32) ..: parts of column l % 16 of the column tile for
+  // lanes 0..15 and 48..63, zeros for lanes 16..47 (one base per parts buffer, so the zero block only needs to cover
+  // the column tiles' offsets, 256 bytes apart)
+  const bool bs_live = lane < 16 || lane >= 48;
+  const unsigned char *zeros = q8_smem + kQSZOff;
+  const unsigned char *wslo0 = bs_live ? q8_smem + kQSPOff + (kWTileM + b_row_wide(t.swiglu, wn, 0) + lrow) * 16 : zeros;
+  const unsigned char *wshi0 = bs_live ? q8_smem + kQSPOff + (kWTileM + b_row_wide(t.swiglu, wn, 4) + lrow) * 16 : zeros;
+  const unsigned char *wslo1 = bs_live ? wslo0 + kQSPBuf : zeros, *wshi1 = bs_live ? wshi0 + kQSPBuf : zeros;
+  if (threadIdx.x < 1024 / 16)
+    *reinterpret_cast<v4i *>(q8_smem + kQSZOff + threadIdx.x * 16) = v4i{0, 0, 0, 0};
+
+  v4f acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // Round j of a step writes the int32 results and the scale products of column tile j into set j % 2 while the
+  // VALU folds in the other set, written one round earlier (column tile j - 1, or tile 7 of the previous step).
+  v4i dot[2][4] = {};
+  v16f sprod[2] = {};
+
+  auto rescale = [&](const v4i &d, const v16f &s, int i, v4f &c) {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      c[e] = fmaf((float)d[e], s[4 * i + e], c[e]);
+  };
+  // One step's MFMAs from operand stage ST and parts buffer PAR; meanwhile this thread splits its scale of scale stage
+  // SST into parts buffer SPAR (SST < 0: none). CARRY: tile 7 of the previous step waits in set 1.
+  auto mma_step = [&](auto ST, auto PAR, auto CARRY, auto SST, auto SPAR) {
+    constexpr int st = decltype(ST)::value, par = decltype(PAR)::value;
+    constexpr bool carry = decltype(CARRY)::value;
+    constexpr int sst = decltype(SST)::value, spar = decltype(SPAR)::value;
+    auto b_op = [&](int j) {
+      return *reinterpret_cast<const v4i *>((j < 4 ? blo : bhi) + ((j & 3) * kQSStages + st) * 1024);
+    };
+    auto ws_op = [&](int j) {
+      const unsigned char *base = par ? (j < 4 ? wslo1 : wshi1) : (j < 4 ? wslo0 : wshi0);
+      return *reinterpret_cast<const v8bf *>(base + (j & 3) * 256);
+    };
+    v4i a[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      a[i] = *reinterpret_cast<const v4i *>(abase + (i * kQSStages + st) * 1024);
+    const v8bf xsp = *reinterpret_cast<const v8bf *>(xsparts + par * kQSPBuf);
+    v4i b = b_op(0);
+    v8bf wsp = ws_op(0);
+    float scale = 0.0f;
+    if constexpr (sst >= 0)
+      scale = *reinterpret_cast<const float *>(own_scale + sst * kQSSStride);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const v4i bn = j < 7 ? b_op(j + 1) : b;
+      const v8bf wspn = j < 7 ? ws_op(j + 1) : wsp;
+      sprod[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xsp, wsp, v16f{}, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        dot[j & 1][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b, v4i{0, 0, 0, 0}, 0, 0, 0);
+        if (j > 0 || carry)
+          rescale(dot[(j & 1) ^ 1][i], sprod[(j & 1) ^ 1], i, acc[i][j > 0 ? j - 1 : 7]);
+      }
+      if constexpr (sst >= 0) {
+        if (j == 3)
+          split_scale(scale, std::integral_constant<int, spar>{});
+      }
+      if (j < 7)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); // the next round's DS reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // the scale-product MFMA
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // one int8 MFMA
+        if (j > 0 || carry)
+          __builtin_amdgcn_sched_group_barrier(0x002, 8, 0); // one tile's convert and FMA
+      }
+      if (sst >= 0 && j == 3) {
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0); // splitting the scale
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0); // storing its parts
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      b = bn;
+      wsp = wspn;
+    }
+  };
+  // Step `step` is in stage ST: wait until step + 1's operands (and so step + 2's scales) have landed for every wave,
+  // load step + 3 (with step + 4's scales), then step + 1's MFMAs while step + 2's scales are split.
+  auto advance = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value, nst = (st + 1) % kQSStages, fill = (st + kQSStages - 1) % kQSStages;
+    wait_vmcnt_lgkm0<kQSLoadsPerStep>(); // ... and this thread's parts store of the last step
+    __builtin_amdgcn_s_barrier();
+    issue(step + kQSStages - 1, std::integral_constant<int, fill>{});
+    mma_step(std::integral_constant<int, nst>{}, std::integral_constant<int, nst % 2>{}, std::true_type{},
+             std::integral_constant<int, (st + 2) % kQSStages>{}, std::integral_constant<int, st % 2>{});
+  };
+
+  issue_scales(s0, std::integral_constant<int, 0>{});
+  issue_first<0, kQSStages - 1>(issue, s0);
+  wait_vmcnt<(kQSStages - 1) * kQSLoadsPerStep>(); // step s0's scales have landed for this wave
+  __builtin_amdgcn_s_barrier();                      // ... and for every wave (the zero block is written too)
+  split_scale(*reinterpret_cast<const float *>(own_scale), std::integral_constant<int, 0>{});
+  wait_vmcnt_lgkm0<(kQSStages - 2) * kQSLoadsPerStep>(); // step s0's operands, s0 + 1's scales, the parts store
+  __builtin_amdgcn_s_barrier();
+  mma_step(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::false_type{},
+           std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+  for (int step = s0; step < s1; step += kQSStages) {
+    advance(step, std::integral_constant<int, 0>{});
+    advance(step + 1, std::integral_constant<int, 1>{});
+    advance(step + 2, std::integral_constant<int, 2>{});
+    advance(step + 3, std::integral_constant<int, 3>{});
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if (SPLIT) {
+    v4f *slot = p.sk.partial + (size_t)(tile * p.sk.splits + split) * kWSlotV4 + threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        slot[(i * 8 + j) * kQ8Threads] = acc[i][j];
+    return;
+  }
+  store_tile_wide(seg, t, acc, wm, wn, lane, p.m, p.flags);
+}
+
+// The group-major scale copies q8_gemm_wide_smma reads: dst[g][r] = src[r][g] for r < rows and zero for the rows up
+// to rows_pad (a multiple of 64), over every matrix of one GEMM call in one launch (xs, then each segment's ws and
+// w3s). A block moves a 64-row x 64-group tile through LDS, reading along groups and writing along rows.
+struct ScaleJob {
+  const float *src;
+  float *dst;
+  int rows, rows_pad, first_block;
+};
+struct ScaleJobs {
+  ScaleJob job[7]; // xs and up to three segments' ws / w3s
+  int njobs, groups, tiles_g;
+};
+
+__global__ __launch_bounds__(256) void scales_by_group(ScaleJobs jobs) {
+  __shared__ float tile[64][65];
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < jobs.njobs && b >= jobs.job[j + 1].first_block)
+    j++;
+  const ScaleJob job = jobs.job[j];
+  const int local = b - job.first_block, tiles_r = job.rows_pad / 64;
+  const int r0 = (local % tiles_r) * 64, g0 = (local / tiles_r) * 64;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int rr = i >> 6, gg = i & 63, r = r0 + rr, g = g0 + gg;
+    tile[rr][gg] = r < job.rows && g < jobs.groups ? job.src[(long long)r * jobs.groups + g] : 0.0f;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int gg = i >> 6, rr = i & 63, r = r0 + rr, g = g0 + gg;
+    if (g < jobs.groups)
+      job.dst[(long long)g * job.rows_pad + r] = tile[rr][gg];
+  }
+}
+
 // Any group size (gs % 64 != 0): one thread per output, the per-group int32 dot in plain integer arithmetic.
 __global__ __launch_bounds__(kBlock) void q8_gemm_generic(TileGrid g, const int8_t *xq, const float *xs, int m, int k,
                                                           int gs) {
@@ -1334,7 +1644,7 @@ TileGrid make_grid(const GemmSegmentDev *segs, int nseg, int m) {
     const GemmSegmentDev &d = segs[s];
     const int width = d.epi == EPI_SWIGLU ? kTile / 2 : kTile;
     g.seg[s] = TileSeg{d.c,   d.ldc, d.w,   d.w3,  d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width,
-                       d.cq, d.cs};
+                       d.cq, d.cs, nullptr, nullptr, 0};
     tiles += g.seg[s].ntiles * g.mtiles;
   }
   g.total = tiles;
@@ -1350,7 +1660,7 @@ Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m, int tile_m = kQ
     const GemmSegmentDev &d = segs[s];
     const int width = d.epi == EPI_SWIGLU ? tile_n / 2 : tile_n;
     g.seg[s] = TileSeg{d.c,   d.ldc, d.w,   d.w3,  d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width,
-                       d.cq, d.cs};
+                       d.cq, d.cs, nullptr, nullptr, 0};
     tiles += g.seg[s].ntiles * g.mtiles;
   }
   g.total = tiles;
@@ -1460,23 +1770,87 @@ void q8_wide_grid(Q8Params &p, const SegList &segs) {
   p.sk.count = device().split_count;
 }
 
+std::atomic<int> forced_q8_scales{0}; // llhip_set_q8_scales: 0 unset, 1 VALU products, 2 matrix-core products
+
+// Which wide kernel forms the per-group scale products: q8_gemm_wide_smma (on the matrix cores) unless
+// LLAMA_HIP_Q8_SCALES = valu (read once) or llhip_set_q8_scales picks q8_gemm_wide.
+bool q8_scales_on_mfma() {
+  static const int env = [] {
+    const char *v = getenv("LLAMA_HIP_Q8_SCALES");
+    return v && !strcmp(v, "valu") ? 1 : v && !strcmp(v, "mfma") ? 2 : 0;
+  }();
+  const int forced = forced_q8_scales.load() ? forced_q8_scales.load() : env;
+  return forced != 1;
+}
+
+// The group-major scales of a q8_gemm_wide_smma call, written into the device's scale workspace by one launch; false
+// when they do not fit it (the call then takes q8_gemm_wide).
+bool q8_group_major_scales(Q8Params &p, hipStream_t stream) {
+  const int groups = p.k / 64;
+  ScaleJobs jobs{};
+  jobs.groups = groups;
+  jobs.tiles_g = (groups + 63) / 64;
+  size_t used = 0;
+  int blocks = 0;
+  auto add = [&](const float *src, int rows, int rows_pad) -> float * {
+    float *dst = device().scale_ws + used;
+    jobs.job[jobs.njobs++] = ScaleJob{src, dst, rows, rows_pad, blocks};
+    used += (size_t)rows_pad * groups;
+    blocks += rows_pad / 64 * jobs.tiles_g;
+    return dst;
+  };
+  p.mpad = (p.m + kWTileM - 1) / kWTileM * kWTileM;
+  p.xsg = add(p.xs, p.m, p.mpad);
+  for (int s = 0; s < p.grid.nseg; s++) {
+    TileSeg &seg = p.grid.seg[s];
+    seg.npad = (seg.n + kWTileN - 1) / kWTileN * kWTileN;
+    seg.wsg = add(seg.ws, seg.n, seg.npad);
+    seg.w3sg = seg.epi == EPI_SWIGLU ? add(seg.w3s, seg.n, seg.npad) : nullptr;
+  }
+  if (used > LLHIP_SCALE_WS_FLOATS)
+    return false;
+  hipLaunchKernelGGL(scales_by_group, dim3((unsigned)blocks), dim3(256), 0, stream, jobs);
+  return true;
+}
+
+// One launch of a wide int8 kernel (SPLIT: the partial-tile instantiation), its LDS allowance raised once.
+bool q8_wide_kernel(Q8Params p, bool split, unsigned blocks, hipStream_t stream) {
+  static const hipError_t a[4] = {
+      hipFuncSetAttribute((const void *)q8_gemm_wide<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds),
+      hipFuncSetAttribute((const void *)q8_gemm_wide<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds),
+      hipFuncSetAttribute((const void *)q8_gemm_wide_smma<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)kQSLds),
+      hipFuncSetAttribute((const void *)q8_gemm_wide_smma<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)kQSLds)};
+  bool smma = q8_scales_on_mfma();
+  if (smma) {
+    smma = q8_group_major_scales(p, stream);
+    if (smma && !launch_ok("scales_by_group"))
+      return false;
+  }
+  if (!check_hip(a[2 * smma + split], "allowing the Q8 GEMM its LDS"))
+    return false;
+  if (smma) {
+    if (split)
+      hipLaunchKernelGGL(q8_gemm_wide_smma<true>, dim3(blocks), dim3(kQ8Threads), kQSLds, stream, p);
+    else
+      hipLaunchKernelGGL(q8_gemm_wide_smma<false>, dim3(blocks), dim3(kQ8Threads), kQSLds, stream, p);
+    return launch_ok("q8_gemm_wide_smma");
+  }
+  if (split)
+    hipLaunchKernelGGL(q8_gemm_wide<true>, dim3(blocks), dim3(kQ8Threads), kQWLds, stream, p);
+  else
+    hipLaunchKernelGGL(q8_gemm_wide<false>, dim3(blocks), dim3(kQ8Threads), kQWLds, stream, p);
+  return launch_ok("q8_gemm_wide");
+}
+
 bool q8_wide_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
   q8_wide_grid(p, segs);
   if (p.grid.total <= 0)
     return true;
-  static const hipError_t a0 =
-      hipFuncSetAttribute((const void *)q8_gemm_wide<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds);
-  static const hipError_t a1 =
-      hipFuncSetAttribute((const void *)q8_gemm_wide<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds);
-  if (!check_hip(a0, "allowing the Q8 GEMM its LDS") || !check_hip(a1, "allowing the Q8 GEMM its LDS"))
-    return false;
-  if (p.sk.splits == 1) {
-    hipLaunchKernelGGL(q8_gemm_wide<false>, dim3((unsigned)p.grid.total), dim3(kQ8Threads), kQWLds, stream, p);
-    return launch_ok("q8_gemm_wide");
-  }
-  hipLaunchKernelGGL(q8_gemm_wide<true>, dim3((unsigned)(p.grid.total * p.sk.splits)), dim3(kQ8Threads), kQWLds,
-                     stream, p);
-  if (!launch_ok("q8_gemm_wide"))
+  if (p.sk.splits == 1)
+    return q8_wide_kernel(p, false, (unsigned)p.grid.total, stream);
+  if (!q8_wide_kernel(p, true, (unsigned)(p.grid.total * p.sk.splits), stream))
     return false;
   return launch_split_reduce<8, kQ8Threads>(p.grid, p.sk, p.m, kWTileM, kWTileN, stream);
 }
@@ -1532,12 +1906,7 @@ bool launch_q8_gemm_swiglu_quantized(const GemmQ8Job &job, hipStream_t stream) {
   q8_wide_grid(p, list);
   if (p.sk.splits != 1 || p.grid.total <= 0)
     return false;
-  static const hipError_t a0 =
-      hipFuncSetAttribute((const void *)q8_gemm_wide<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds);
-  if (!check_hip(a0, "allowing the Q8 GEMM its LDS"))
-    return false;
-  hipLaunchKernelGGL(q8_gemm_wide<false>, dim3((unsigned)p.grid.total), dim3(kQ8Threads), kQWLds, stream, p);
-  return launch_ok("q8_gemm_wide");
+  return q8_wide_kernel(p, false, (unsigned)p.grid.total, stream);
 }
 
 bool launch_q8_gemm_generic(const GemmQ8Job &job, hipStream_t stream) {
@@ -1688,6 +2057,8 @@ void set_gemm_splits(int splits) { forced_splits.store(splits > 0 ? splits : 0);
 void set_bf16_tile(int tile) { forced_bf16_tile.store(tile == 1 || tile == 2 ? tile : 0); }
 
 void set_q8_tile(int tile) { forced_q8_tile.store(tile == 1 || tile == 2 ? tile : 0); }
+
+void set_q8_scales(int where) { forced_q8_scales.store(where == 1 || where == 2 ? where : 0); }
 
 bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream) {
   if (job.m <= 0 || job.k <= 0)

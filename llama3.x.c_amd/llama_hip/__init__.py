@@ -254,6 +254,7 @@ _SIGNATURES = {
     "llhip_set_gemm_splits": (None, [I32]),
     "llhip_set_bf16_tile": (None, [I32]),
     "llhip_set_q8_tile": (None, [I32]),
+    "llhip_set_q8_scales": (None, [I32]),
 }
 
 _lib = None

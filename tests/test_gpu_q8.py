@@ -518,10 +518,16 @@ def test_gemm_q8_split_k(m, n, k, gs):
 @pytest.mark.parametrize("m,n,k", [(33, 20, 128), (40, 33, 192), (130, 257, 1024), (256, 384, 4096), (129, 129, 640),
                                    (600, 200, 1024), (300, 136, 14336), (513, 65, 320), (257, 513, 2048),
                                    (1, 64, 64)])
-def test_gemm_q8_wide_tiles(m, n, k):
-    """The 256 x 256 int8 kernel (gs = 64), forced: every kind within the budget, and bit for bit the 256 x 128
-    kernel's result at every forced split count (both add each group's ((float)dot * ws) * xs in group order, and
-    split partials in split order), so the two tilings differ in nothing but speed. Also a three-segment call."""
+@pytest.mark.parametrize("scales", [1, 2])
+def test_gemm_q8_wide_tiles(m, n, k, scales):
+    """The 256 x 256 int8 kernels (gs = 64), forced: every kind within the budget at every forced split count, and a
+    three-segment call.
+    scales = 1 (q8_gemm_wide, the scale products on the vector unit): bit for bit the 256 x 128 kernel's result (both
+    add each group's ((float)dot * ws) * xs in group order, and split partials in split order), so the two tilings
+    differ in nothing but speed.
+    scales = 2 (q8_gemm_wide_smma, xs * ws from a bf16 MFMA over exact three-part splits of the scales): within
+    1e-6 * sum|w x| of the scales = 1 result, the same exact group dots rescaled with the product rounded once instead
+    of twice (a dropped or mispaired part would be off by 2^-16 to 2^-8 of a term)."""
     L = hu.lib()
     gs = 64
     xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 4242 + m + n)
@@ -531,9 +537,10 @@ def test_gemm_q8_wide_tiles(m, n, k):
     r3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
     dx = [hu.dev(a) for a in (xq, xs, wq, ws, w3q, w3s)]
 
-    def run(kind, tile, splits):
+    def run(kind, tile, splits, where=scales):
         L.llhip_set_q8_tile(tile)
         L.llhip_set_gemm_splits(splits)
+        L.llhip_set_q8_scales(where)
         c = hu.dev(base)
         seg = lh.GemmQ8Segment(lh.ptr(c), ldc, lh.w8(dx[2], dx[3]), lh.w8(dx[4], dx[5]), None, None, n, kind)
         L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
@@ -555,10 +562,19 @@ def test_gemm_q8_wide_tiles(m, n, k):
                     assert np.all(np.abs(got - want) <= tol), what
                 else:
                     hu.assert_within_budget(got, ref, mag, what=what)
-                if splits:  # the automatic count differs between the tilings (a wide grid has half the tiles)
+                if splits and scales == 1:  # the automatic count differs between the tilings (a wide grid has half
+                    # the tiles)
                     assert np.array_equal(hu.bits(got), hu.bits(run(kind, 1, splits))), what + " vs 256 x 128"
+                if scales == 2:
+                    other = run(kind, 2, splits, 1)
+                    if kind == lh.GEMM_SWIGLU:  # |d silu(a) b| <= 1.1 |b| |da| + |silu(a)| |db|
+                        bound = 1e-6 * (mag * (np.abs(r3) + 1) + mag3 * (np.abs(ref) + 1)) + 1e-9
+                    else:
+                        bound = 1e-6 * mag + 1e-9
+                    assert np.all(np.abs(got - other) <= bound), what + " vs the vector-unit scale products"
         L.llhip_set_q8_tile(2)
         L.llhip_set_gemm_splits(1)
+        L.llhip_set_q8_scales(scales)
         widths = (n, max(16, n // 4), max(16, n // 4))
         outs = [hu.dev(np.zeros((m, nn), np.float32)) for nn in widths]
         mats = [(hu.dev(wq[:nn]), hu.dev(ws[:nn])) for nn in widths]  # kept alive across the call
@@ -570,6 +586,7 @@ def test_gemm_q8_wide_tiles(m, n, k):
     finally:
         L.llhip_set_q8_tile(0)
         L.llhip_set_gemm_splits(0)
+        L.llhip_set_q8_scales(0)
 
 
 @pytest.mark.parametrize("m,n,k", [(300, 256, 1024), (513, 640, 320), (257, 128, 4096), (1024, 384, 2048)])
