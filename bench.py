@@ -696,6 +696,15 @@ def engine_bench(lh, L, args, prompts=None):
             assert np.isfinite(logits).all()
             print(f"# engine prefill: {PROMPT} tokens in {psec * 1e3:.2f} ms, {PROMPT / psec:.0f} tok/s",
                   file=sys.stderr, flush=True)
+            stage = "prefill with every row's logits"
+            t0 = time.perf_counter()
+            for _ in range(prompts):
+                out_all = L.engine_forward_batch(ctypes.byref(model), pptr, PROMPT, 0, lh.LOGITS_ALL)
+            asec = (time.perf_counter() - t0) / prompts
+            assert out_all, lh.last_error()
+            assert np.isfinite(np.ctypeslib.as_array(out_all, shape=(PROMPT, VOCAB))[-1]).all()
+            print(f"# engine prefill with every row's logits ({PROMPT} x {VOCAB} floats to the host): "
+                  f"{asec * 1e3:.2f} ms", file=sys.stderr, flush=True)
             stage = "decode"
             t0 = time.perf_counter()
             for step in range(decode_steps):
@@ -720,7 +729,11 @@ def engine_bench(lh, L, args, prompts=None):
                                    f"{PROMPT}..{PROMPT + decode_steps - 1} after the prompt, logits to the host"},
             "prefill": {"value": round(PROMPT / psec, 1), "unit": "tok/s", "ms_per_prompt": round(psec * 1e3, 3),
                         "workload": f"engine_forward_batch of a {PROMPT}-token prompt of random ids from position 0, "
-                                    f"the last row's logits"}}
+                                    f"the last row's logits"},
+            "prefill_all_logits": {"value": round(PROMPT / asec, 1), "unit": "tok/s",
+                                   "ms_per_prompt": round(asec * 1e3, 3),
+                                   "workload": f"the same prompt with every row's logits ({PROMPT} x {VOCAB} FP32, "
+                                               f"1.05 GB) copied to the host"}}
 
 
 def main():

@@ -665,18 +665,29 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
     k_rmsnorm_rows(e->bx, e->bx, e->rms_final, count, d, c.norm_eps);
     const GemmBf16Segment seg{e->blogits, c.vocab_size, e->cls_packed, nullptr, c.vocab_size, GEMM_STORE};
     k_gemm_bf16(e->bx, d, count, d, &seg, 1, &e->panel);
+  } else if (want == LOGITS_ALL) {
+    // Every row's RMSNorm, then one GEMM over the classifier, where src/tp.c:610-618 runs the classifier GEMV row by
+    // row: a GEMM row equals the GEMV of that row within the kernel budget (tests/q8.c:158-183), and the classifier
+    // streams once per batch instead of once per row.
+    if (e->q8) {
+      norm_rows(e->rms_final);
+      const GemmQ8Segment seg{e->blogits, c.vocab_size, e->cls.k8(), K8Weight{}, nullptr, nullptr, c.vocab_size,
+                              GEMM_STORE};
+      k_gemm_q8(e->bxq, e->bxs, count, d, gs, &seg, 1);
+    } else {
+      k_rmsnorm_rows(e->bxb, e->bx, e->rms_final, count, d, c.norm_eps);
+      const GemmSegment seg{e->blogits, c.vocab_size, e->cls.f(), nullptr, (size_t)d, c.vocab_size, GEMM_STORE};
+      k_gemm_f32(e->bxb, d, count, d, &seg, 1);
+    }
   } else {
-    const K8Input in{e->xq, e->xs, nullptr};
-    for (int i = want == LOGITS_ALL ? 0 : count - 1; i < count; i++) {
-      float *x = e->bx + (size_t)i * d;
-      float *out = want == LOGITS_ALL ? e->blogits + (size_t)i * vocab : e->logits;
-      k_rmsnorm(x, x, e->rms_final, d, c.norm_eps);
-      if (e->q8) {
-        k_quantize(e->xq, e->xs, x, d, gs);
-        k_matmul_q8(out, &in, e->cls.k8(), d, c.vocab_size, gs);
-      } else {
-        k_matmul(out, x, e->cls.f(), d, c.vocab_size);
-      }
+    const K8Input in{e->xq, e->xs, nullptr}; // the last row (src/tp.c:610-618)
+    float *x = e->bx + (size_t)(count - 1) * d;
+    k_rmsnorm(x, x, e->rms_final, d, c.norm_eps);
+    if (e->q8) {
+      k_quantize(e->xq, e->xs, x, d, gs);
+      k_matmul_q8(e->logits, &in, e->cls.k8(), d, c.vocab_size, gs);
+    } else {
+      k_matmul(e->logits, x, e->cls.f(), d, c.vocab_size);
     }
   }
   float *host;

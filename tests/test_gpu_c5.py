@@ -97,9 +97,13 @@ def test_c5_8b_prefill_2048_then_256_greedy_steps(tmp_path):
                 decode.append(logits)
         say(f"{DECODE} greedy steps in {time.time() - t:.2f} s; first tokens {greedy[:8]}")
         assert all(0 <= g < V for g in greedy)
-        # LAST of the same batch is its ALL row
+        # LAST of the same batch is its ALL row up to the classifier: the last row's GEMV there, one GEMM over every
+        # row here, which agree within the kernel budget 2e-5 * sum|w x| (tests/q8.c:158-183); with N(0, 0.02)
+        # weights over 4096 RMSNorm-ed inputs sum|w x| is about 50, so 1e-3
         p = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens), PROMPT, 0, lh.LOGITS_LAST)
-        assert p and np.array_equal(np.ctypeslib.as_array(p, shape=(V,)), last_row)
+        assert p
+        last = np.ctypeslib.as_array(p, shape=(V,))
+        assert np.max(np.abs(last - last_row)) <= 1e-3 and int(np.argmax(last)) == int(np.argmax(last_row))
         # the prompt token by token (rewrites the cache rows in order)
         t = time.time()
         ours_tokens = np.empty((LAST, V), np.float32)
