@@ -38,7 +38,8 @@ void k_rope_apply_rows(float *q, size_t q_stride, float *k, size_t k_stride, con
 /* No counterpart in the reference: k_rope_apply_rows of q and k, then k_kv_store of k and of v at positions pos0 ..
  * pos0 + rows - 1 of the caches (the selected layout), in one launch and bitwise those three calls (k is also left
  * rotated in place); for the engine's batched forward (src/tp.c:550-557). head_dim and the strides multiples of 4, one
- * table row of 2 * head_dim values per row (table_stride >= 2 * head_dim), 16-byte aligned q, k, v and table. */
+ * table row of 2 * head_dim values per row (table_stride >= 2 * head_dim), 16-byte aligned q, k, v, table and caches,
+ * and the k and v rows outside both caches; anything else fails with a message. */
 void llhip_rope_kv_store_rows(float *q, size_t q_stride, float *k, const float *v, size_t kv_stride, const float *table,
                               size_t table_stride, int rows, int n_heads, int n_kv_heads, int head_dim,
                               float *key_cache, float *value_cache, int pos0, int seq_len);
@@ -94,9 +95,12 @@ void k_attention_batch_layout(float *out, const float *q, const float *key_cache
  * capture, tight serving loops, harnesses that forbid hipMalloc). It allocates nothing: its split-K partials live in
  * a fixed per-device array of 4 Mi floats (16 MiB, located when llhip_init opens the device), not in the workspace the
  * other forms grow on first use. Every buffer must be device memory or inside a registered range (host buffers would
- * need the staging arena), the library must be initialized (llhip_init), and m rows of n_heads heads up to position
- * pos0 + m - 1 must fit: m * n_heads * ((pos0 + m - 1) / 64 + 1) * ((head_dim + 5) & ~3) floats, at most 4 Mi
- * (decode with 32 heads of 128 reaches position 63487). Anything else fails with a message. The results equal
+ * need the staging arena), the library must be initialized (llhip_init), and a call that runs a split kernel (fewer
+ * than 16 rows, or a head_dim other than 64 and 128, or unaligned operands) must fit: m rows of n_heads heads up to
+ * position pos0 + m - 1 take m * n_heads * ((pos0 + m - 1) / 64 + 1) * ((head_dim + 5) & ~3) floats, at most 4 Mi
+ * (decode with 32 heads of 128 reaches position 63487); batches the flash kernel takes (16 rows and more, head_dim
+ * 64 or 128, 16-byte aligned operands) keep no partials and have no such limit. Anything else fails with a message.
+ * The results equal
  * k_attention_batch_layout's bit for bit. Every call on a device shares its array, which keeps the last call's
  * contents (every slot a call reads it writes first); calls ordered on the library's stream are safe, two that may
  * run concurrently on one GPU (graphs replayed on other streams) race. */

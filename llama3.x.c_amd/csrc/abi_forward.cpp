@@ -178,11 +178,6 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
             "allocates)", name);
       return;
     }
-    if (partial_floats > kAttentionScratchFloats) {
-      raise("%s: %d rows of %d heads up to position %d need %zu floats of scratch; it holds %zu", name, m, n_heads,
-            pos0 + m - 1, partial_floats, kAttentionScratchFloats);
-      return;
-    }
   }
   Call call(name, true); // a recorded RoPE with its cache stores may be taken along
   const size_t f = sizeof(float), row = (size_t)n_heads * head_dim * f;
@@ -195,14 +190,21 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
   }
   if (!call.ready())
     return;
+  AttentionJob job{call.ptr<float>(O), call.ptr<const float>(Q), call.ptr<const float>(K), call.ptr<const float>(V),
+                   n_heads, n_kv_heads, head_dim, pos0, m, pos_stride, head_base, nullptr, nullptr, nullptr};
+  // the flash kernel (16 rows and more) keeps no split partials, so only the split kernels' need is checked; a fused
+  // RoPE is taken only for one row, which never runs the flash kernel
+  if (noalloc && !attention_uses_flash(job) && partial_floats > kAttentionScratchFloats) {
+    raise("%s: %d rows of %d heads up to position %d need %zu floats of scratch; it holds %zu", name, m, n_heads,
+          pos0 + m - 1, partial_floats, kAttentionScratchFloats);
+    return;
+  }
   float *partial = noalloc ? attention_scratch(device().ordinal) : attention_partials(partial_floats);
   if (!partial) {
     if (noalloc)
       raise("%s: the attention scratch has no device address", name);
     return;
   }
-  AttentionJob job{call.ptr<float>(O), call.ptr<const float>(Q), call.ptr<const float>(K), call.ptr<const float>(V),
-                   n_heads, n_kv_heads, head_dim, pos0, m, pos_stride, head_base, nullptr, nullptr, nullptr};
   // the fused form reads the caches, q and the new rows as 16-byte vectors
   const bool aligned = head_dim % 4 == 0 && pos_stride % 4 == 0 && head_base % 4 == 0 &&
                        (((uintptr_t)job.q | (uintptr_t)job.key | (uintptr_t)job.value) & 15) == 0;
@@ -373,7 +375,9 @@ void k_kv_store(float *cache, const float *src, size_t src_ld, int pos0, int cou
 }
 
 // No counterpart in the reference: k_rope_apply_rows of q and k, then k_kv_store of k and of v at pos0.. (the engine's
-// batched forward, src/tp.c:550-557), in one launch and bitwise those calls; rows of q, k and v 16-byte aligned.
+// batched forward, src/tp.c:550-557), in one launch and bitwise those calls; rows of q, k and v and both caches
+// 16-byte aligned, and the k and v rows outside both caches (a thread's cache store must not land on a row another
+// thread has still to read).
 void llhip_rope_kv_store_rows(float *q, size_t q_stride, float *k, const float *v, size_t kv_stride, const float *table,
                               size_t table_stride, int rows, int n_heads, int n_kv_heads, int head_dim,
                               float *key_cache, float *value_cache, int pos0, int seq_len) {
@@ -386,8 +390,10 @@ void llhip_rope_kv_store_rows(float *q, size_t q_stride, float *k, const float *
   }
   if (head_dim % 4 || n_kv_heads > n_heads || q_stride % 4 || kv_stride % 4 || table_stride % 4 ||
       table_stride < 2 * (size_t)head_dim ||
-      ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)table) & 15) {
-    raise("%s: needs head_dim and the row strides multiples of 4, a table row per row and 16-byte aligned rows", name);
+      ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)table | (uintptr_t)key_cache |
+       (uintptr_t)value_cache) & 15) {
+    raise("%s: needs head_dim and the row strides multiples of 4, a table row per row and 16-byte aligned rows and "
+          "caches", name);
     return;
   }
   if (!positions_fit(pos0, rows, seq_len)) {
@@ -397,6 +403,16 @@ void llhip_rope_kv_store_rows(float *q, size_t q_stride, float *k, const float *
   size_t pos_stride, head_base;
   strides(n_kv_heads, head_dim, seq_len, kv_head_major(), &pos_stride, &head_base);
   const size_t f = sizeof(float), kv_dim = (size_t)n_kv_heads * head_dim;
+  {
+    const uintptr_t rows_bytes = ((size_t)(rows - 1) * kv_stride + kv_dim) * f, cache_bytes = (size_t)seq_len * kv_dim * f;
+    auto overlaps = [&](const void *a, const void *cache) {
+      return (uintptr_t)a < (uintptr_t)cache + cache_bytes && (uintptr_t)cache < (uintptr_t)a + rows_bytes;
+    };
+    if (overlaps(k, key_cache) || overlaps(k, value_cache) || overlaps(v, key_cache) || overlaps(v, value_cache)) {
+      raise("%s: the k and v rows must lie outside both caches", name);
+      return;
+    }
+  }
   Call call(name);
   Ref Q = call.out2d(q, (size_t)n_heads * head_dim * f, q_stride * f, (size_t)rows, true);
   Ref K = call.out2d(k, kv_dim * f, kv_stride * f, (size_t)rows, true);

@@ -250,6 +250,7 @@ struct AttentionJob {
 bool attention_shape_ok(int n_heads, int n_kv_heads, int head_dim); // kv_mul <= 16, head_dim <= 256
 size_t attention_partial_floats(int rows, int n_heads, int head_dim, int last_position);
 bool launch_attention(const AttentionJob &job, float *partial, hipStream_t stream);
+bool attention_uses_flash(const AttentionJob &job); // the batched kernel with no split partials takes the job
 
 struct GemmSegmentDev {
   float *c;

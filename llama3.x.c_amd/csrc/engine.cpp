@@ -445,13 +445,16 @@ bool forward(Engine *e, int token, int pos, bool want_logits) {
   const int d = c.dim, hidden = c.hidden_dim, hd = c.head_dim, gs = e->gs, nh = c.n_heads, nkv = c.n_kv_heads;
   const size_t kvl = (size_t)hd * nkv;
   // the id goes in through pinned memory on the library's stream, behind the previous token's work (which ended
-  // with a synchronization, so the pinned word is free again)
+  // with a synchronization on every path, so the pinned word is free again)
+  auto fail_after_wait = [](const char *message) {
+    (void)hipStreamSynchronize(device().stream); // the queued copies are done with the pinned buffers
+    (void)hipGetLastError();
+    return raise("%s", message);
+  };
   *e->token_host = token;
   if (!flush_pending_quantize() ||
-      hipMemcpyAsync(e->token_dev, e->token_host, sizeof(int), hipMemcpyHostToDevice, device().stream) != hipSuccess) {
-    (void)hipGetLastError();
-    return raise("engine_forward: copying the token id to the device failed");
-  }
+      hipMemcpyAsync(e->token_dev, e->token_host, sizeof(int), hipMemcpyHostToDevice, device().stream) != hipSuccess)
+    return fail_after_wait("engine_forward: copying the token id to the device failed");
   if (e->q8)
     k_embed_q8_rows(e->x, e->embed.q(), e->embed.s, e->token_dev, 1, d, gs, c.vocab_size);
   else
@@ -509,10 +512,8 @@ bool forward(Engine *e, int token, int pos, bool want_logits) {
       k_matmul(e->logits, e->x, e->cls.f(), d, c.vocab_size);
     if (!flush_pending_quantize() ||
         hipMemcpyAsync(e->host_logits, e->logits, (size_t)c.vocab_size * sizeof(float), hipMemcpyDeviceToHost,
-                       device().stream) != hipSuccess) {
-      (void)hipGetLastError();
-      return raise("engine_forward: copying the logits to the host failed");
-    }
+                       device().stream) != hipSuccess)
+      return fail_after_wait("engine_forward: copying the logits to the host failed");
   }
   llhip_synchronize(); // the logits have landed; reports a non-finite activation or score of this token
   return llhip_last_error()[0] == 0;

@@ -1223,6 +1223,19 @@ size_t attention_tile_lds(int tile_rows, int kv_mul, int head_dim) {
   return ((size_t)kChunk * (2 * head_dim + 4) + (size_t)tile_rows * kv_mul * (head_dim + kChunk)) * sizeof(float);
 }
 
+// Batches of at least 16 rows with 64 or 128 dimensions per head, aligned, no fused RoPE: the flash kernel on the
+// matrix cores, which needs no split partials. Its loads address a KV head's rows by 32-bit byte offsets, up to 64
+// positions past the batch's last.
+bool attention_uses_flash(const AttentionJob &job) {
+  const int kv_mul = job.n_heads / job.n_kv_heads;
+  const bool aligned = job.head_dim % 4 == 0 && job.pos_stride % 4 == 0 && job.head_base % 4 == 0 &&
+                       ((uintptr_t)job.q & 15) == 0 && ((uintptr_t)job.key & 15) == 0;
+  const bool offsets_fit =
+      ((uint64_t)job.pos0 + (uint64_t)job.rows + kChunk) * job.pos_stride * 4 + (uint64_t)job.head_dim * 4 <= UINT32_MAX;
+  return !job.table && aligned && job.rows >= 16 && (job.head_dim == 64 || job.head_dim == 128) && kv_mul <= 128 &&
+         offsets_fit && ((uintptr_t)job.out & 15) == 0 && ((uintptr_t)job.value & 15) == 0;
+}
+
 bool launch_attention(const AttentionJob &job, float *partial, hipStream_t stream) {
   AttnParams p{};
   p.out = job.out;
@@ -1252,14 +1265,7 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
                        ((uintptr_t)job.q & 15) == 0 && ((uintptr_t)job.key & 15) == 0;
   if (job.table && !aligned)
     return raise("internal: a fused RoPE attention on operands the aligned kernel does not take");
-  // batches of at least 16 rows with 64 or 128 dimensions per head: the flash kernel on the matrix cores, no merge.
-  // Its loads address a KV head's rows by 32-bit byte offsets, up to 64 positions past the batch's last.
-  const bool offsets_fit =
-      ((uint64_t)job.pos0 + (uint64_t)job.rows + kChunk) * job.pos_stride * 4 + (uint64_t)job.head_dim * 4 <= UINT32_MAX;
-  const bool flash = !job.table && aligned && job.rows >= 16 && (job.head_dim == 64 || job.head_dim == 128) &&
-                     kv_mul <= 128 && offsets_fit && ((uintptr_t)job.out & 15) == 0 &&
-                     ((uintptr_t)job.value & 15) == 0;
-  if (flash) {
+  if (attention_uses_flash(job)) {
     // two staged chunks of K and two of V rows in static LDS: 4 x 64 x HD floats (128 KB at HD = 128)
     const int tile_rows = 128 / kv_mul, tiles = (job.rows + tile_rows - 1) / tile_rows;
     const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)job.n_kv_heads); // a block per pair of tiles

@@ -302,6 +302,26 @@ def test_prefill_validate(record):
     assert lh.last_error() == "forward input out of range: token=100 position=5"
 
 
+def test_rope_kv_store_rows_refuses_overlap_and_misalignment(record):
+    """llhip_rope_kv_store_rows writes the caches as 16-byte vectors while other threads still read the k and v rows:
+    an unaligned cache, or k or v rows inside either cache, fail with a message before any device work."""
+    L = record
+    raw = np.zeros(4096 + 16, np.float32)
+    base = (-raw.ctypes.data % 16) // 4  # first 16-byte aligned element
+    buf = raw[base:base + 4096]
+    P = lh.ptr(buf)
+    rows, nkv, hd, seq = 4, 1, 8, 100  # caches of 800 floats; rows of 8
+    at = lambda i: P + 4 * i  # noqa: E731
+    L.llhip_rope_kv_store_rows(at(1024), 8, at(1100), at(1200), 8, at(1300), 16, rows, 1, nkv, hd, at(1), at(2048), 0,
+                               seq)
+    assert "16-byte aligned rows and caches" in lh.last_error(), lh.last_error()
+    L.llhip_clear_error()
+    for k, v in ((0, 1200), (1100, 2100), (800 - 8, 1200)):  # k in key_cache, v in value_cache, k's last row in it
+        L.llhip_rope_kv_store_rows(at(1024), 8, at(k), at(v), 8, at(1300), 16, rows, 1, nkv, hd, at(0), at(2048), 0, seq)
+        assert lh.last_error() == "llhip_rope_kv_store_rows: the k and v rows must lie outside both caches", (k, v)
+        L.llhip_clear_error()
+
+
 def test_cache_position_checks_cannot_overflow(record):
     """The cache-position checks of k_kv_store, llhip_rope_kv_store_rows and the batched attention compare without
     forming pos0 + count in int: a batch starting just below INT_MAX is refused (before any device work), not

@@ -1,6 +1,8 @@
 """k_attention_batch_layout_noalloc, the attention entry point that allocates nothing (its split-K partials live in a
-fixed per-device array): equal bit for bit to k_attention_batch_layout on two calls in a row, the second smaller; no
-HBM claimed by the calls; replayable from a HIP graph captured around it; host buffers, an oversized call and an
+fixed per-device array): equal bit for bit to k_attention_batch_layout on calls in a row, each smaller than the one
+before (a 16-row batch on the flash kernel, which keeps no partials, then 8 rows and one decode row, whose split
+kernels write and read the array); no HBM claimed by the calls; replayable from a HIP graph captured around it; a
+2048-row batch, which needs no partials, accepted; host buffers, a split call too large for the array and an
 uninitialized library refused with a message."""
 import os
 import subprocess
@@ -36,7 +38,7 @@ def test_noalloc_attention_equals_the_workspace_form():
     rng = np.random.default_rng(31)
     k, v, ps, hb = head_major(rng, SEQ)
     kd, vd = hu.dev(k), hu.dev(v)
-    cases = [(1000, 16), (300, 1)]  # a 16-row batch, then a smaller call: one decode row
+    cases = [(1000, 16), (1000, 8), (300, 1)]  # 16 rows (flash), 8 rows (attn_tile + attn_merge), a decode row
     for pos0, m in cases:
         assert m * NH * ((pos0 + m - 1) // 64 + 1) * 132 <= SCRATCH_FLOATS
     outs = []
@@ -80,10 +82,12 @@ def test_noalloc_attention_replays_from_a_graph():
             out.zero_()
             T.cuda.synchronize()
             other = hu.empty((4, NH * HD), T.float32)  # eager work on the same array between replays
-            run(L, "k_attention_batch_layout_noalloc", other, hu.dev(rng.standard_normal((4, NH * HD),
-                                                                                          dtype=np.float32)),
-                kd, vd, 100, 4, ps, hb, seq=2048)
+            q4 = hu.dev(rng.standard_normal((4, NH * HD), dtype=np.float32))
+            run(L, "k_attention_batch_layout_noalloc", other, q4, kd, vd, 100, 4, ps, hb, seq=2048)
             L.llhip_synchronize()
+            ref4 = hu.empty((4, NH * HD), T.float32)
+            run(L, "k_attention_batch_layout", ref4, q4, kd, vd, 100, 4, ps, hb, seq=2048)
+            assert np.array_equal(hu.host(other), hu.host(ref4)), i
             assert L.llhip_graph_launch(graph) == 0, lh.last_error()
             L.llhip_synchronize()
             assert np.array_equal(hu.host(out), want), i
@@ -100,11 +104,22 @@ def test_noalloc_attention_refusals():
     kd, vd = hu.dev(k), hu.dev(v)
     lh.record_failures()
     try:
+        # a 2048-row batch runs the flash kernel, which keeps no partials: accepted, and equal to the workspace form
         big = 2048
-        q = hu.empty((big, NH * HD), T.float32)
-        out = hu.empty((big, NH * HD), T.float32)
-        kb, vb = hu.empty((NKV, big, HD), T.float32), hu.empty((NKV, big, HD), T.float32)
-        run(L, "k_attention_batch_layout_noalloc", out, q, kb, vb, 0, big, HD, big * HD, seq=big)
+        kb, vb, bps, bhb = head_major(rng, big)
+        kb, vb = hu.dev(kb), hu.dev(vb)
+        q = hu.dev(rng.standard_normal((big, NH * HD), dtype=np.float32))
+        out, want = hu.empty((big, NH * HD), T.float32), hu.empty((big, NH * HD), T.float32)
+        run(L, "k_attention_batch_layout_noalloc", out, q, kb, vb, 0, big, bps, bhb, seq=big)
+        assert lh.last_error() == "", lh.last_error()
+        run(L, "k_attention_batch_layout", want, q, kb, vb, 0, big, bps, bhb, seq=big)
+        assert np.array_equal(hu.host(out), hu.host(want))
+        # 8 rows at position 16384 take the split kernels: 8 * 32 * 257 chunks * 132 floats exceed the array
+        far, m8 = 16392, 8
+        q8 = hu.empty((m8, NH * HD), T.float32)
+        out8 = hu.empty((m8, NH * HD), T.float32)
+        kf, vf = hu.empty((NKV, far, HD), T.float32), hu.empty((NKV, far, HD), T.float32)
+        run(L, "k_attention_batch_layout_noalloc", out8, q8, kf, vf, far - m8, m8, HD, far * HD, seq=far)
         assert "floats of scratch; it holds 4194304" in lh.last_error(), lh.last_error()
         L.llhip_clear_error()
         qh = rng.standard_normal((1, NH * HD), dtype=np.float32)  # host memory: staging would allocate
