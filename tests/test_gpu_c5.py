@@ -13,7 +13,10 @@ floor's rms and 0.08 (0.15 for the 64 decode rows) of its argmax agreement.
 
 Compared: our batched rows and our token-by-token replay of the prompt (last 256 positions) with each other and
 with the reference's batched and per-token rows; our first 64 greedy decode steps with the reference's per-token
-forwards of the same tokens (probe tail mode, tools/compare_engines.py --tail)."""
+forwards of the same tokens (probe tail mode, tools/compare_engines.py --tail).
+
+The same file in W8A32 (FP32 activations, no requantization) pins the whole 32-layer forward tightly: 64 positions
+against the reference's W8A32 engine at its FP32-class gate."""
 import ctypes
 import os
 import shutil
@@ -57,19 +60,32 @@ def at_floor(ref, got, floor, what, argmax_slack):
     assert s["argmax"] >= floor["argmax"] - argmax_slack, (what, s, floor)
 
 
-def test_c5_8b_prefill_2048_then_256_greedy_steps(tmp_path):
+@pytest.fixture(scope="module")
+def c5_checkpoint(tmp_path_factory):
+    """The 8B Q8_0 checkpoint of random-init weights, written once for the module's tests."""
     if not rp.have("probe-int8"):
         pytest.skip("oracle/_ref/probe-int8 not built (make -C oracle ref)")
-    L = hu.lib()
-    assert L.llhip_init() == 0, lh.last_error()
-    d = scratch_dir(tmp_path)
+    d = scratch_dir(tmp_path_factory.mktemp("c5"))
     path = os.path.join(d, "c5-8b-q8.bin")
-    model = lh.Model()
     try:
         t = time.time()
         size = ck.write_q8_v3_normal(path, CFG, 64, seed=88172645463325252)
         assert os.path.getsize(path) == size
         say(f"wrote {size / 1e9:.2f} GB in {time.time() - t:.1f} s")
+        yield path
+    finally:
+        if os.path.exists(path):
+            os.unlink(path)
+        if d.startswith("/dev/shm/"):
+            shutil.rmtree(d, ignore_errors=True)
+
+
+def test_c5_8b_prefill_2048_then_256_greedy_steps(c5_checkpoint):
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    path = c5_checkpoint
+    model = lh.Model()
+    try:
         V = CFG["vocab_size"]
         tokens = np.random.default_rng(2048).integers(0, V, PROMPT).astype(np.int32)
         L.engine_load(ctypes.byref(model), path.encode())
@@ -132,7 +148,53 @@ def test_c5_8b_prefill_2048_then_256_greedy_steps(tmp_path):
     finally:
         if model.implementation:
             L.engine_free(ctypes.byref(model))
-        if os.path.exists(path):
-            os.unlink(path)
-        if d.startswith("/dev/shm/"):
-            shutil.rmtree(d, ignore_errors=True)
+
+
+W8A32_POSITIONS = 64
+
+
+def test_c5_8b_w8a32_full_depth_at_the_fp32_gate(c5_checkpoint, monkeypatch):
+    """The same 32-layer 8B file with LLAMA_Q8_ACTIVATIONS=fp32 (src/engine.c:132-135): W8A32 has no quantizer to
+    flip, so the whole forward is held to the reference's FP32-class gate (docs/architecture.md:272: every position
+    finite, max |d| <= 1e-3, the same argmax) against runq's W8A32 engine on the same tokens, position by position over
+    64 positions. The bar is widened only to what the reference shows against itself on this file (its scalar kernels
+    against its AVX-512 kernels, twice their max |d|) should that exceed 1e-3; the argmax must agree everywhere. A
+    batch of the 64 tokens runs them one at a time (W8A32 takes no batched GEMM, src/engine.c:65-81), bit for bit the
+    per-token rows."""
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    path = c5_checkpoint
+    V = CFG["vocab_size"]
+    tokens = np.random.default_rng(32).integers(0, V, W8A32_POSITIONS).astype(np.int32)
+    monkeypatch.setenv("LLAMA_Q8_ACTIVATIONS", "fp32")
+    monkeypatch.setenv("LLAMA_PREFILL_BATCH", str(W8A32_POSITIONS))  # W8A32's default batch is one row
+    model = lh.Model()
+    ours = np.empty((W8A32_POSITIONS, V), np.float32)
+    try:
+        L.engine_load(ctypes.byref(model), path.encode())
+        assert model.implementation, lh.last_error()
+        assert L.engine_max_batch(ctypes.byref(model)) == W8A32_POSITIONS and model.prefill_gemm == 0
+        t = time.time()
+        for pos in range(W8A32_POSITIONS):
+            p = L.engine_forward(ctypes.byref(model), int(tokens[pos]), pos)
+            assert p, (pos, lh.last_error())
+            ours[pos] = np.ctypeslib.as_array(p, shape=(V,))
+        say(f"W8A32: {W8A32_POSITIONS} positions in {time.time() - t:.2f} s")
+        p = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens), W8A32_POSITIONS, 0, lh.LOGITS_ALL)
+        assert p, lh.last_error()
+        assert np.array_equal(np.ctypeslib.as_array(p, shape=(W8A32_POSITIONS, V)), ours)
+    finally:
+        if model.implementation:
+            L.engine_free(ctypes.byref(model))
+    env = {"LLAMA_Q8_ACTIVATIONS": "fp32"}
+    t = time.time()
+    ref = rp.run("probe-int8", path, list(tokens), V, env=env, timeout=900)
+    ref_scalar = rp.run("probe-int8", path, list(tokens), V, env={**env, "LLAMA_KERNELS": "scalar"}, timeout=1800)
+    say(f"reference W8A32 (CPU, {rp.threads()} threads), AVX-512 and scalar kernels: {time.time() - t:.1f} s")
+    floor = rp.compare(ref, ref_scalar)[1]
+    rows, s = rp.compare(ref, ours)
+    say(f"W8A32 ours against the reference: max |d| {s['max_abs']:.2e} rms {s['rms']:.2e} argmax {s['argmax']:.3f}; "
+        f"the reference's scalar against its AVX-512: max |d| {floor['max_abs']:.2e} rms {floor['rms']:.2e} "
+        f"argmax {floor['argmax']:.3f}")
+    bar = max(rp.FP32_MAX_ABS, 2.0 * floor["max_abs"])
+    rp.gate_strict(ref, ours, bar, f"W8A32 at 8B, {W8A32_POSITIONS} positions (bar {bar:.2e})")
