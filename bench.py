@@ -197,6 +197,107 @@ def forward_decode_set(torch, lh, model, seed):
     return run_step, x
 
 
+def decode_fp_sets(torch, lh, model, seed, steps, warmup):
+    """The 8B decode-step matmul set in the two other forms the reference runs (src/gemv.c:141-181 and 252-396):
+    W8A32 (runq with LLAMA_Q8_ACTIVATIONS=fp32: the Q8_0 weights above, the FP32 activations handed to the GEMVs
+    unquantized) and FP32 (run's k_matmul*: FP32 weights ~N(0, 0.02), 30 GB per token, drawn here and freed after).
+    Each is one HIP graph per token, in the decode order of src/tp.c:352-374 / 401-435; tok/s and the algorithmic bytes
+    of the step over its time against 8 TB/s."""
+    L = lh.load()
+    P = lh.ptr
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 9)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    acts = [{k: torch.randn(n, generator=gen, **f32) for k, n in (("att", DIM), ("o", DIM), ("ffn", DIM),
+                                                                    ("h", HIDDEN))} for _ in range(LAYERS)]
+    x_cls = torch.randn(DIM, generator=gen, **f32)
+    q, k, v = torch.empty(DIM, **f32), torch.empty(KV_DIM, **f32), torch.empty(KV_DIM, **f32)
+    resid, hb, logits = torch.zeros(DIM, **f32), torch.empty(HIDDEN, **f32), torch.empty(VOCAB, **f32)
+    torch.cuda.synchronize()
+
+    def timed(run_step):
+        run_step()
+        L.llhip_synchronize()
+        assert L.llhip_graph_begin() == 0
+        run_step()
+        graph = L.llhip_graph_end()
+        if not graph:
+            raise SystemExit(f"graph capture failed: {lh.last_error()}")
+        sec = time_graph(torch, L, graph, steps, warmup) / steps
+        L.llhip_graph_destroy(graph)
+        return sec
+
+    def w8(pair):
+        return lh.K8Weight(P(pair[0]), P(pair[1]))
+
+    def a32(x):
+        return lh.K8Input(None, None, P(x))
+
+    def a32_step():
+        for lay, a in zip(model.layers, acts):
+            L.k_matmul_q8_qkv(P(q), P(k), P(v), a32(a["att"]), w8(lay["wq"]), w8(lay["wk"]), w8(lay["wv"]), DIM, DIM,
+                              KV_DIM, GS)
+            L.k_matmul_q8_add(P(resid), a32(a["o"]), w8(lay["wo"]), DIM, DIM, GS)
+            L.k_matmul_q8_swiglu(P(hb), a32(a["ffn"]), w8(lay["w1"]), w8(lay["w3"]), DIM, HIDDEN, GS)
+            L.k_matmul_q8_add(P(resid), a32(a["h"]), w8(lay["w2"]), HIDDEN, DIM, GS)
+        L.k_matmul_q8(P(logits), a32(x_cls), w8(model.cls), DIM, VOCAB, GS)
+
+    def a32_bytes(rows, kk):  # weights and scales, the FP32 input, the FP32 output
+        return weight_bytes(rows, kk) + 4 * kk + 4 * rows
+
+    a32_sec = timed(a32_step)
+    a32_b = LAYERS * (a32_bytes(DIM + 2 * KV_DIM, DIM) + a32_bytes(DIM, DIM) + 2 * weight_bytes(HIDDEN, DIM)
+                      + 4 * DIM + 4 * HIDDEN + a32_bytes(DIM, HIDDEN)) + a32_bytes(VOCAB, DIM)
+    out = {"w8a32": {"value": round(1 / a32_sec, 2), "unit": "tok/s", "ms_per_token": round(a32_sec * 1e3, 4),
+                     "bytes_per_step": a32_b, "hbm_frac": round(a32_b / a32_sec / 1e9 / HBM_PEAK_GBS, 4),
+                     "workload": "Llama-3.1-8B Q8_0 decode-step matmul set with FP32 activations (W8A32, "
+                                 "LLAMA_Q8_ACTIVATIONS=fp32): 32 x (QKV, Wo +resid, W1/W3 SwiGLU, W2 +resid) + "
+                                 "classifier, gs 64, HIP graph"}}
+    print(f"# decode W8A32: {a32_sec * 1e3:.3f} ms/token, {a32_b / a32_sec / 1e9:.0f} GB/s", file=sys.stderr,
+          flush=True)
+
+    shapes = [("wq", DIM, DIM), ("wk", KV_DIM, DIM), ("wv", KV_DIM, DIM), ("wo", DIM, DIM), ("w1", HIDDEN, DIM),
+              ("w3", HIDDEN, DIM), ("w2", DIM, HIDDEN)]
+    per_layer = sum(r * c for _, r, c in shapes)
+    w_all = torch.empty(per_layer * LAYERS + VOCAB * DIM, **f32)
+    w_all.normal_(0.0, 0.02, generator=gen)
+    layers, at = [], 0
+    for _ in range(LAYERS):
+        lay = {}
+        for name, r, c in shapes:
+            lay[name] = w_all[at: at + r * c]
+            at += r * c
+        layers.append(lay)
+    cls = w_all[at:]
+    torch.cuda.synchronize()
+
+    def f32_step():
+        for lay, a in zip(layers, acts):
+            L.k_matmul_qkv(P(q), P(k), P(v), P(a["att"]), P(lay["wq"]), P(lay["wk"]), P(lay["wv"]), DIM, DIM, KV_DIM)
+            L.k_matmul_add(P(resid), P(a["o"]), P(lay["wo"]), DIM, DIM)
+            L.k_matmul_swiglu(P(hb), P(a["ffn"]), P(lay["w1"]), P(lay["w3"]), DIM, HIDDEN)
+            L.k_matmul_add(P(resid), P(a["h"]), P(lay["w2"]), HIDDEN, DIM)
+        L.k_matmul(P(logits), P(x_cls), P(cls), DIM, VOCAB)
+
+    def f32_bytes(rows, kk):
+        return 4 * rows * kk + 4 * kk + 4 * rows
+
+    f32_sec = timed(f32_step)
+    f32_b = LAYERS * (f32_bytes(DIM + 2 * KV_DIM, DIM) + f32_bytes(DIM, DIM) + 2 * 4 * HIDDEN * DIM + 4 * DIM
+                      + 4 * HIDDEN + f32_bytes(DIM, HIDDEN)) + f32_bytes(VOCAB, DIM)
+    del w_all, layers, cls
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    out["fp32"] = {"value": round(1 / f32_sec, 2), "unit": "tok/s", "ms_per_token": round(f32_sec * 1e3, 4),
+                   "bytes_per_step": f32_b, "hbm_frac": round(f32_b / f32_sec / 1e9 / HBM_PEAK_GBS, 4),
+                   "workload": "Llama-3.1-8B FP32 decode-step matmul set (run's k_matmul*, FP32 weights ~N(0, 0.02), "
+                               "30 GB per token): 32 x (QKV, Wo +resid, W1/W3 SwiGLU, W2 +resid) + classifier, HIP "
+                               "graph"}
+    print(f"# decode FP32: {f32_sec * 1e3:.3f} ms/token, {f32_b / f32_sec / 1e9:.0f} GB/s", file=sys.stderr,
+          flush=True)
+    return out
+
+
 def time_graph(torch, L, graph, steps, warmup):
     stream = torch.cuda.ExternalStream(L.llhip_stream())
     for _ in range(warmup):
@@ -697,6 +798,8 @@ def engine_bench(lh, L, args, prompts=None):
             print(f"# engine prefill: {PROMPT} tokens in {psec * 1e3:.2f} ms, {PROMPT / psec:.0f} tok/s",
                   file=sys.stderr, flush=True)
             stage = "prefill with every row's logits"
+            out_all = L.engine_forward_batch(ctypes.byref(model), pptr, PROMPT, 0, lh.LOGITS_ALL)  # warm-up (the
+            assert out_all, lh.last_error()  # engine pins its host buffer for the batch's logits on the first call)
             t0 = time.perf_counter()
             for _ in range(prompts):
                 out_all = L.engine_forward_batch(ctypes.byref(model), pptr, PROMPT, 0, lh.LOGITS_ALL)
@@ -755,6 +858,8 @@ def main():
     ap.add_argument("--no-forward", action="store_true",
                     help="skip the full device decode token (matmuls + RMSNorm, RoPE, K/V store, attention)")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine's end-to-end measurement")
+    ap.add_argument("--no-fp", action="store_true",
+                    help="skip the W8A32 and FP32 decode-step matmul sets (the FP32 one draws 30 GB of weights)")
     ap.add_argument("--engine", action="store_true",
                     help="measure engine_load + engine_forward on a synthetic 8B checkpoint instead")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -882,7 +987,7 @@ def main():
             "ops_per_prompt": ops, "tops": round(ops / (psec / args.prefill_steps) / 1e12, 1),
             "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                          "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": measured_traffic("q8_gemm_wide_swiglu"),
-                         "kernel": "q8_gemm_wide (W1/W3 SwiGLU 2048x(2x14336)x4096)",
+                         "kernel": "q8_gemm_wide_smma (W1/W3 SwiGLU 2048x(2x14336)x4096)",
                          "avg_launch_us": round(pavg * 1e6, 1)},
         }
         L.llhip_graph_destroy(pgraph)
@@ -890,6 +995,8 @@ def main():
               f"{ach:.0f} TOP/s in the W1/W3 GEMM", file=sys.stderr, flush=True)
     L.llhip_graph_destroy(graph)
 
+    if not args.no_fp:
+        result["decode_w8a32_fp32"] = decode_fp_sets(torch, lh, model, args.seed, max(5, args.steps // 2), 2)
     if not args.no_batch:
         result["decode_batch"] = decode_batch(torch, lh, model, args.seed, max(5, args.steps // 2), 2)
     if not args.no_1b:
@@ -904,7 +1011,7 @@ def main():
             eng = engine_bench(lh, L, args, prompts=2)
             result["engine"] = {"decode": {"value": eng["value"], "unit": "tok/s", "ms_per_token": eng["ms_per_step"],
                                            "workload": eng["config"]["workload"]},
-                                "prefill": eng["prefill"]}
+                                "prefill": eng["prefill"], "prefill_all_logits": eng["prefill_all_logits"]}
         except Exception as err:  # noqa: BLE001 - the main metric must still print
             result["engine"] = {"error": f"{type(err).__name__}: {err}"}
         finally:

@@ -21,5 +21,5 @@ def test_help_lists_the_sections():
                        timeout=120)
     assert r.returncode == 0
     for flag in ("--gpus", "--steps", "--warmup", "--no-cpu", "--no-1b", "--no-c3", "--no-engine", "--no-forward",
-                 "--no-batch"):
+                 "--no-batch", "--no-fp"):
         assert flag in r.stdout, flag
