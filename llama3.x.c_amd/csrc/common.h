@@ -29,12 +29,7 @@ struct Device {
   bool capturing = false;
   void *split_partial = nullptr;  // split-K partial tiles: LLHIP_SPLIT_SLOTS x 256 x 128 floats
   unsigned *split_count = nullptr; // split-K arrivals per tile, zero between launches
-  float *scale_ws = nullptr;       // group-major copies of a wide int8 GEMM's scales: LLHIP_SCALE_WS_FLOATS floats
 };
-// The wide int8 GEMM reads each K step's scales from group-major copies ([group][row], rows padded to whole tiles with
-// zeros) of xs and of every segment's ws: 4 Mi floats (16 MB) hold them for m = 2048 and k = 14336 with 4096 weight
-// rows, or k = 4096 with 2 x 14336 (larger calls take the kernel that reads the row-major scales).
-#define LLHIP_SCALE_WS_FLOATS (4u << 20)
 // Partial tiles of the split-K workspace (one per block of a split launch): 512 x 128 KB = 64 MB of HBM. Launches on
 // the library's stream are ordered, so one workspace per device serves them all.
 #define LLHIP_SPLIT_SLOTS 512

@@ -50,8 +50,6 @@ struct TileSeg {
   int ntiles;     // its column tiles
   int8_t *cq;     // SWIGLU output quantized in groups of 64 (the wide int8 kernel only), else null
   float *cs;
-  const float *wsg, *w3sg; // q8_gemm_wide_smma: ws and w3s group-major, [group][npad] (rows past n zero)
-  int npad;
 };
 
 struct TileGrid {
@@ -273,8 +271,6 @@ struct Q8Params {
   int32_t *probe; // optional (one segment, no SWIGLU): probe[(g * m + r) * n + c]
   SplitK sk;
   int *flags; // [0]: a non-finite value met by a quantizing epilogue
-  const float *xsg; // q8_gemm_wide_smma: xs group-major, [group][mpad] (rows past m zero)
-  int mpad;
 };
 
 __device__ __forceinline__ TilePos q8_tile_of(const Q8Grid &g, int logical, int tile_m = kQ8TileM,
@@ -1273,20 +1269,19 @@ template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_w
   const __amdgpu_buffer_rsrc_t rB0 = b_resource(2 * wave), rB1 = b_resource(2 * wave + 1);
   const int offB = (int)(lrow4 * k) + ((chunk ^ q8_swizzle(lrow4)) << 4);
   // Scale loads: thread (wave, lane) loads scale 64 wave + lane of the step: the xs of row 64 wave + lane (waves 0..3)
-  // or the ws of B-tile row 64 (wave - 4) + lane (waves 4..7), and later splits that same scale. They come from the
-  // group-major copies, so a wave's 64 scales of a step are 256 contiguous bytes (rows past m or n hold zeros).
+  // or the ws of B-tile row 64 (wave - 4) + lane (waves 4..7), and later splits that same scale. Rows past m or n
+  // load zeros (bounded resources).
   __amdgpu_buffer_rsrc_t rS;
-  int offS, pitch; // byte offset of this lane's scale in group 0, bytes from one group to the next
   if (wave < 4) {
-    rS = q8_buffer(p.xsg, (long long)groups * p.mpad * 4);
-    offS = (t.m0 + 64 * wave + lane) * 4;
-    pitch = p.mpad * 4;
+    const int r0 = t.m0 + 64 * wave;
+    rS = q8_buffer(p.xs + (long long)r0 * groups, (long long)min(64, p.m - r0) * groups * 4);
   } else {
     const int h = wave - 4;
-    rS = q8_buffer((t.swiglu && h >= 2) ? seg.w3sg : seg.wsg, (long long)groups * seg.npad * 4);
-    offS = ((t.swiglu ? t.n0 + 64 * (h & 1) : t.n0 + 64 * h) + lane) * 4;
-    pitch = seg.npad * 4;
+    const float *src = (t.swiglu && h >= 2) ? seg.w3s : seg.ws;
+    const int c0 = t.swiglu ? t.n0 + 64 * (h & 1) : t.n0 + 64 * h;
+    rS = q8_buffer(src + (long long)c0 * groups, (long long)min(64, seg.n - c0) * groups * 4);
   }
+  const int offS = lane * groups * 4;
   const __amdgpu_buffer_rsrc_t none = q8_buffer(p.xq, 0);
 
   // The scales of K step `step` into scale stage SST (a step past the end loads zeros).
@@ -1294,7 +1289,7 @@ template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_w
     constexpr int sst = decltype(SST)::value;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(step < s1 ? rS : none,
                                              (void *)(q8_smem + kQSSOff + sst * kQSSStride + 64 * wave * 4), 4, offS,
-                                             step * pitch, 0, 0);
+                                             step * 4, 0, 0);
   };
   // Stage ST gets step `step`'s operands; the scales going out with them are step + 1's (scale stage ST + 1).
   auto issue = [&](int step, auto ST) {
@@ -1466,40 +1461,6 @@ template <bool SPLIT> __global__ __launch_bounds__(kQ8Threads, 2) void q8_gemm_w
   store_tile_wide(seg, t, acc, wm, wn, lane, p.m, p.flags);
 }
 
-// The group-major scale copies q8_gemm_wide_smma reads: dst[g][r] = src[r][g] for r < rows and zero for the rows up
-// to rows_pad (a multiple of 64), over every matrix of one GEMM call in one launch (xs, then each segment's ws and
-// w3s). A block moves a 64-row x 64-group tile through LDS, reading along groups and writing along rows.
-struct ScaleJob {
-  const float *src;
-  float *dst;
-  int rows, rows_pad, first_block;
-};
-struct ScaleJobs {
-  ScaleJob job[7]; // xs and up to three segments' ws / w3s
-  int njobs, groups, tiles_g;
-};
-
-__global__ __launch_bounds__(256) void scales_by_group(ScaleJobs jobs) {
-  __shared__ float tile[64][65];
-  const int b = blockIdx.x;
-  int j = 0;
-  while (j + 1 < jobs.njobs && b >= jobs.job[j + 1].first_block)
-    j++;
-  const ScaleJob job = jobs.job[j];
-  const int local = b - job.first_block, tiles_r = job.rows_pad / 64;
-  const int r0 = (local % tiles_r) * 64, g0 = (local / tiles_r) * 64;
-  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-    const int rr = i >> 6, gg = i & 63, r = r0 + rr, g = g0 + gg;
-    tile[rr][gg] = r < job.rows && g < jobs.groups ? job.src[(long long)r * jobs.groups + g] : 0.0f;
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-    const int gg = i >> 6, rr = i & 63, r = r0 + rr, g = g0 + gg;
-    if (g < jobs.groups)
-      job.dst[(long long)g * job.rows_pad + r] = tile[rr][gg];
-  }
-}
-
 // Any group size (gs % 64 != 0): one thread per output, the per-group int32 dot in plain integer arithmetic.
 __global__ __launch_bounds__(kBlock) void q8_gemm_generic(TileGrid g, const int8_t *xq, const float *xs, int m, int k,
                                                           int gs) {
@@ -1644,7 +1605,7 @@ TileGrid make_grid(const GemmSegmentDev *segs, int nseg, int m) {
     const GemmSegmentDev &d = segs[s];
     const int width = d.epi == EPI_SWIGLU ? kTile / 2 : kTile;
     g.seg[s] = TileSeg{d.c,   d.ldc, d.w,   d.w3,  d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width,
-                       d.cq, d.cs, nullptr, nullptr, 0};
+                       d.cq, d.cs};
     tiles += g.seg[s].ntiles * g.mtiles;
   }
   g.total = tiles;
@@ -1660,7 +1621,7 @@ Q8Grid make_q8_grid(const GemmSegmentDev *segs, int nseg, int m, int tile_m = kQ
     const GemmSegmentDev &d = segs[s];
     const int width = d.epi == EPI_SWIGLU ? tile_n / 2 : tile_n;
     g.seg[s] = TileSeg{d.c,   d.ldc, d.w,   d.w3,  d.ws, d.w3s, (long long)d.ldw, d.n, d.epi, tiles, (d.n + width - 1) / width,
-                       d.cq, d.cs, nullptr, nullptr, 0};
+                       d.cq, d.cs};
     tiles += g.seg[s].ntiles * g.mtiles;
   }
   g.total = tiles;
@@ -1783,38 +1744,8 @@ bool q8_scales_on_mfma() {
   return forced != 1;
 }
 
-// The group-major scales of a q8_gemm_wide_smma call, written into the device's scale workspace by one launch; false
-// when they do not fit it (the call then takes q8_gemm_wide).
-bool q8_group_major_scales(Q8Params &p, hipStream_t stream) {
-  const int groups = p.k / 64;
-  ScaleJobs jobs{};
-  jobs.groups = groups;
-  jobs.tiles_g = (groups + 63) / 64;
-  size_t used = 0;
-  int blocks = 0;
-  auto add = [&](const float *src, int rows, int rows_pad) -> float * {
-    float *dst = device().scale_ws + used;
-    jobs.job[jobs.njobs++] = ScaleJob{src, dst, rows, rows_pad, blocks};
-    used += (size_t)rows_pad * groups;
-    blocks += rows_pad / 64 * jobs.tiles_g;
-    return dst;
-  };
-  p.mpad = (p.m + kWTileM - 1) / kWTileM * kWTileM;
-  p.xsg = add(p.xs, p.m, p.mpad);
-  for (int s = 0; s < p.grid.nseg; s++) {
-    TileSeg &seg = p.grid.seg[s];
-    seg.npad = (seg.n + kWTileN - 1) / kWTileN * kWTileN;
-    seg.wsg = add(seg.ws, seg.n, seg.npad);
-    seg.w3sg = seg.epi == EPI_SWIGLU ? add(seg.w3s, seg.n, seg.npad) : nullptr;
-  }
-  if (used > LLHIP_SCALE_WS_FLOATS)
-    return false;
-  hipLaunchKernelGGL(scales_by_group, dim3((unsigned)blocks), dim3(256), 0, stream, jobs);
-  return true;
-}
-
 // One launch of a wide int8 kernel (SPLIT: the partial-tile instantiation), its LDS allowance raised once.
-bool q8_wide_kernel(Q8Params p, bool split, unsigned blocks, hipStream_t stream) {
+bool q8_wide_kernel(const Q8Params &p, bool split, unsigned blocks, hipStream_t stream) {
   static const hipError_t a[4] = {
       hipFuncSetAttribute((const void *)q8_gemm_wide<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds),
       hipFuncSetAttribute((const void *)q8_gemm_wide<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQWLds),
@@ -1822,12 +1753,7 @@ bool q8_wide_kernel(Q8Params p, bool split, unsigned blocks, hipStream_t stream)
                           (int)kQSLds),
       hipFuncSetAttribute((const void *)q8_gemm_wide_smma<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)kQSLds)};
-  bool smma = q8_scales_on_mfma();
-  if (smma) {
-    smma = q8_group_major_scales(p, stream);
-    if (smma && !launch_ok("scales_by_group"))
-      return false;
-  }
+  const bool smma = q8_scales_on_mfma();
   if (!check_hip(a[2 * smma + split], "allowing the Q8 GEMM its LDS"))
     return false;
   if (smma) {

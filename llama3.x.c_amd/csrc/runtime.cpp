@@ -129,9 +129,8 @@ bool ensure_device() {
   if (!LLHIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking)))
     return false;
   device_total = props.totalGlobalMem;
-  if (!hbm_claim((size_t)LLHIP_SPLIT_SLOTS * (256 * 128 * sizeof(float) + sizeof(unsigned)) + 64 +
-                     (size_t)LLHIP_SCALE_WS_FLOATS * sizeof(float),
-                 "the split-K and scale workspaces"))
+  if (!hbm_claim((size_t)LLHIP_SPLIT_SLOTS * (256 * 128 * sizeof(float) + sizeof(unsigned)) + 64,
+                 "the split-K workspace"))
     return false;
   int *flags;
   if (!LLHIP_CHECK(hipMalloc(&flags, 64)))
@@ -145,14 +144,10 @@ bool ensure_device() {
       !LLHIP_CHECK(hipMalloc((void **)&arrivals, LLHIP_SPLIT_SLOTS * sizeof(unsigned))) ||
       !LLHIP_CHECK(hipMemset(arrivals, 0, LLHIP_SPLIT_SLOTS * sizeof(unsigned))))
     return false;
-  float *scale_ws;
-  if (!LLHIP_CHECK(hipMalloc((void **)&scale_ws, (size_t)LLHIP_SCALE_WS_FLOATS * sizeof(float))))
-    return false;
   if (!attention_scratch_setup(ordinal)) // the allocation-free attention's array: its address on this device
     return false;
   the_device.split_partial = partial;
   the_device.split_count = arrivals;
-  the_device.scale_ws = scale_ws;
   the_device.ordinal = ordinal;
   the_device.stream = stream;
   the_device.error_flags = flags;
