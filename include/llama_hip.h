@@ -44,6 +44,10 @@ void llhip_synchronize(void);
 /* Uploads [host, host + bytes) to HBM once; pointers inside the range then resolve to the copy. The host bytes must
  * not change afterwards (re-register to refresh). Returns 0, or -1 after a failure. */
 int llhip_register_host(const void *host, size_t bytes);
+/* LLAMA_HIP_REGISTER_MAPPINGS=1 (read when first needed) registers on its own: the first time an entry point receives
+ * an input inside a read-only mapping of a regular file that no executable segment maps (a checkpoint, not a program
+ * or a library), the whole mapping is registered as above, so a caller that takes its weight views from a mapped
+ * checkpoint needs no call of its own to run on resident weights. */
 int llhip_unregister_host(const void *host);
 /* The device address a host address resolves to (NULL when it is not inside a registered range). */
 void *llhip_resolve(const void *host);

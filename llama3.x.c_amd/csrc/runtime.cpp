@@ -5,6 +5,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <vector>
 
 #include "common.h"
 
@@ -227,6 +228,93 @@ int device_extent(const void *p, size_t bytes) {
   return (uintptr_t)p + bytes <= (uintptr_t)base + size ? 1 : -1;
 }
 
+// LLAMA_HIP_REGISTER_MAPPINGS=1 (read once): a host input that lies in a read-only mapping of a regular file, a file
+// no executable segment maps (so not a program or a library), is registered whole on its first use: uploaded to HBM
+// once, and resolved to that copy by every later call. An unchanged caller that takes its weight views from a mapped
+// checkpoint (the reference maps it read-only, src/runtime.c:306, and views its tensors in place, src/tp.c:897-903)
+// then runs on resident weights instead of staging them over PCIe per call.
+bool register_mappings_enabled() {
+  static const bool on = [] {
+    const char *v = getenv("LLAMA_HIP_REGISTER_MAPPINGS");
+    return v && !strcmp(v, "1");
+  }();
+  return on;
+}
+
+struct MapEntry {
+  uintptr_t start, end;
+  unsigned long long offset, inode;
+  unsigned dev_major, dev_minor;
+  bool read, write, exec, file;
+};
+
+std::vector<MapEntry> read_maps() {
+  std::vector<MapEntry> out;
+  FILE *f = fopen("/proc/self/maps", "r");
+  if (!f)
+    return out;
+  char line[4096];
+  while (fgets(line, sizeof(line), f)) {
+    MapEntry m{};
+    char perms[8] = {0};
+    int used = 0;
+    unsigned long start, end;
+    if (sscanf(line, "%lx-%lx %7s %llx %x:%x %llu %n", &start, &end, perms, &m.offset, &m.dev_major, &m.dev_minor,
+               &m.inode, &used) < 7)
+      continue;
+    m.start = start;
+    m.end = end;
+    m.read = perms[0] == 'r';
+    m.write = perms[1] == 'w';
+    m.exec = perms[2] == 'x';
+    m.file = m.inode != 0 && line[used] == '/';
+    out.push_back(m);
+  }
+  fclose(f);
+  return out;
+}
+
+std::mutex mapping_mutex;
+std::vector<std::pair<uintptr_t, uintptr_t>> mappings_declined; // ranges already found not to qualify
+
+// Registers the file mapping around host address p when it qualifies; false otherwise (p then stays staged).
+bool register_file_mapping(const void *p) {
+  const uintptr_t a = (uintptr_t)p;
+  std::lock_guard<std::mutex> lock(mapping_mutex);
+  for (const auto &r : mappings_declined)
+    if (a >= r.first && a < r.second)
+      return false;
+  if (lookup(p)) // registered meanwhile by another thread
+    return true;
+  const std::vector<MapEntry> maps = read_maps();
+  size_t i = 0;
+  while (i < maps.size() && !(a >= maps[i].start && a < maps[i].end))
+    i++;
+  if (i == maps.size())
+    return false;
+  const MapEntry &m = maps[i];
+  bool ok = m.file && m.read && !m.write;
+  for (const MapEntry &o : maps) // a program or a library: some segment of the same file is executable
+    if (o.exec && o.inode == m.inode && o.dev_major == m.dev_major && o.dev_minor == m.dev_minor)
+      ok = false;
+  if (!ok) {
+    if (mappings_declined.size() < 64)
+      mappings_declined.emplace_back(m.start, m.end);
+    return false;
+  }
+  // the whole mapping: neighbouring entries of the same file with continuing offsets and the same permissions
+  auto same = [&](const MapEntry &x, const MapEntry &y) {
+    return x.inode == y.inode && x.dev_major == y.dev_major && x.dev_minor == y.dev_minor && x.read == y.read &&
+           x.write == y.write && x.exec == y.exec && x.end == y.start && x.offset + (y.start - x.start) == y.offset;
+  };
+  size_t lo = i, hi = i;
+  while (lo > 0 && same(maps[lo - 1], maps[lo]))
+    lo--;
+  while (hi + 1 < maps.size() && same(maps[hi], maps[hi + 1]))
+    hi++;
+  return llhip_register_host((const void *)maps[lo].start, maps[hi].end - maps[lo].start) == 0;
+}
+
 // The staging arena for host buffers: grown on demand, reused by every staged call.
 void *arena = nullptr;
 size_t arena_bytes = 0;
@@ -434,6 +522,12 @@ Ref Call::in2d(const void *p, size_t row_bytes, size_t pitch, size_t rows) {
   }
   if (where > 0)
     return Ref{const_cast<void *>(p), -1};
+  if (register_mappings_enabled() && !the_device.capturing && register_file_mapping(p)) {
+    if (void *dev = lookup(p, &room)) {
+      if (room >= extent)
+        return Ref{dev, -1};
+    }
+  }
   return stage(const_cast<void *>(p), row_bytes, pitch, rows, true, false);
 }
 

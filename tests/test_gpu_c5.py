@@ -198,3 +198,32 @@ def test_c5_8b_w8a32_full_depth_at_the_fp32_gate(c5_checkpoint, monkeypatch):
         f"argmax {floor['argmax']:.3f}")
     bar = max(rp.FP32_MAX_ABS, 2.0 * floor["max_abs"])
     rp.gate_strict(ref, ours, bar, f"W8A32 at 8B, {W8A32_POSITIONS} positions (bar {bar:.2e})")
+
+
+def test_c5_8b_dropin_on_resident_weights(c5_checkpoint):
+    """The drop-in at full size: the reference's own engine (engine.c, tp.c, runq.c and its probe, tests/probe.c)
+    linked against the library in place of gemv.c, gemm.c and prefill.c (oracle/_ref/probe-int8-hip), on the 8B file,
+    with LLAMA_HIP_REGISTER_MAPPINGS=1: its read-only checkpoint mapping is uploaded on first use and every later
+    matmul reads the resident copy. Its logits are held to the reference's (all CPU, probe-int8, the same tokens) at
+    the W8A8 gate's rms and max, and at the argmax floor this file shows the reference against itself (0.79, less the
+    0.08 the C5 comparisons allow), and its decode rate per token comes from the difference of two runs of 4 and 36 tokens (load and upload
+    cancel; the reference's RMSNorm, RoPE and attention stay on the CPU)."""
+    if not rp.have("probe-int8-hip"):
+        pytest.skip("oracle/_ref/probe-int8-hip not built (make -C oracle dropin)")
+    path = c5_checkpoint
+    V = CFG["vocab_size"]
+    tokens = [int(t) for t in np.random.default_rng(36).integers(0, V, 36)]
+    env = {"LLAMA_HIP_REGISTER_MAPPINGS": "1"}
+    timings = {}
+    for n in (4, 4, 36):  # the first run warms the file's pages
+        t = time.time()
+        got = rp.run("probe-int8-hip", path, tokens[:n], V, env=env, timeout=900)
+        timings[n] = time.time() - t
+    sec = (timings[36] - timings[4]) / 32
+    say(f"drop-in (the reference's engine on the library, resident weights): {sec * 1e3:.2f} ms/token, "
+        f"{1 / sec:.1f} tok/s; 36 tokens in {timings[36]:.2f} s including load and upload")
+    t = time.time()
+    ref = rp.run("probe-int8", path, tokens, V, timeout=900)
+    say(f"the reference on the CPU ({rp.threads()} threads): 36 tokens in {time.time() - t:.2f} s")
+    s = rp.gate_statistical(ref, got, what="drop-in at 8B", rms_max=0.2, argmax_min=0.71, max_abs=16.0)
+    say(f"drop-in against the reference: rms {s['rms']:.4f} argmax {s['argmax']:.3f} max {s['max_abs']:.3f}")

@@ -243,14 +243,23 @@ def test_dropin_probes_against_the_reference(models):
     got = rp.run("probe-int8-hip", models["q8"], TOKENS, V)
     rp.gate_statistical(ref, got, what="drop-in runq per token", **rp.W8A8)
     within_floor(ref, got, floor, "drop-in runq per token")
+    # with the checkpoint mapping registered on first use (resident weights instead of staging per call): the same
+    # kernels on the same bytes, so bit for bit the staged run
+    resident = rp.run("probe-int8-hip", models["q8"], TOKENS, V, env={"LLAMA_HIP_REGISTER_MAPPINGS": "1"})
+    assert np.array_equal(resident, got)
     ref = rp.run("probe-int8", models["q8"], TOKENS, V, mode="batch", batch=32)
     got = rp.run("probe-int8-hip", models["q8"], TOKENS, V, mode="batch", batch=32)
     rp.gate_statistical(ref, got, what="drop-in runq batch 32", **rp.W8A8)
     within_floor(ref, got, floor, "drop-in runq batch 32")
+    assert np.array_equal(rp.run("probe-int8-hip", models["q8"], TOKENS, V, mode="batch", batch=32,
+                                 env={"LLAMA_HIP_REGISTER_MAPPINGS": "1"}), got)
     for mode in ("tokens", "batch"):
         ref = rp.run("probe-fp32", models["f32"], TOKENS, V, mode=mode, batch=32)
         got = rp.run("probe-fp32-hip", models["f32"], TOKENS, V, mode=mode, batch=32)
         rp.gate_strict(ref, got, rp.FP32_MAX_ABS, f"drop-in run {mode}")
+        resident = rp.run("probe-fp32-hip", models["f32"], TOKENS, V, mode=mode, batch=32,
+                          env={"LLAMA_HIP_REGISTER_MAPPINGS": "1"})
+        assert np.array_equal(resident, got), mode
     env = {"LLAMA_PRECISION": "bf16"}
     ref = rp.run("probe-fp32", models["f32"], TOKENS, V, mode="batch", batch=32, env=env)
     got = rp.run("probe-fp32-hip", models["f32"], TOKENS, V, mode="batch", batch=32, env=env)
