@@ -138,6 +138,7 @@ class Call {
   int ncopies_ = 0;
   size_t arena_used_ = 0;
   bool staged_ = false, failed_ = false;
+  bool bounced_ = false; // the copies go through the pinned twin of the arena
 };
 
 // ---- kernel launchers (stream-ordered, no synchronization) ------------------------------------------------------

@@ -1,4 +1,5 @@
 // Device state, failure handling, the host-range registry, host staging, copies and graph capture.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -157,6 +158,19 @@ bool ensure_device() {
   return true;
 }
 
+// A device error flag set since the last check becomes the failure of this call (the flags then cleared).
+bool report_flags(const int *flags) {
+  Device &dev = the_device;
+  if (flags[0] || flags[1] || flags[2]) {
+    int zero[16] = {0};
+    (void)hipMemcpy(dev.error_flags, zero, sizeof(zero), hipMemcpyHostToDevice);
+    return raise(flags[0]   ? "nonfinite activation during INT8 quantization"
+                 : flags[1] ? "nonfinite value in softmax"
+                            : "embedding row id outside the table");
+  }
+  return true;
+}
+
 bool synchronize_and_check() {
   if (!ensure_device())
     return false;
@@ -170,14 +184,7 @@ bool synchronize_and_check() {
   int flags[16];
   if (!LLHIP_CHECK(hipMemcpy(flags, dev.error_flags, sizeof(flags), hipMemcpyDeviceToHost)))
     return false;
-  if (flags[0] || flags[1] || flags[2]) {
-    int zero[16] = {0};
-    (void)hipMemcpy(dev.error_flags, zero, sizeof(zero), hipMemcpyHostToDevice);
-    return raise(flags[0]   ? "nonfinite activation during INT8 quantization"
-                 : flags[1] ? "nonfinite value in softmax"
-                            : "embedding row id outside the table");
-  }
-  return true;
+  return report_flags(flags);
 }
 
 // ---- registry of uploaded host ranges ----------------------------------------------------------------------------
@@ -315,10 +322,41 @@ bool register_file_mapping(const void *p) {
   return llhip_register_host((const void *)maps[lo].start, maps[hi].end - maps[lo].start) == 0;
 }
 
-// The staging arena for host buffers: grown on demand, reused by every staged call.
+// The staging arena for host buffers: grown on demand, reused by every staged call. Calls that stage at most
+// kBounceMax bytes copy through a pinned host twin of the arena (the caller's bytes are memcpy'd into it, then one DMA
+// per buffer), and read the device error flags back through pinned memory in the same wait, where pageable copies
+// take the runtime's slower staging and the flags a second synchronous copy.
 void *arena = nullptr;
 size_t arena_bytes = 0;
 std::mutex arena_mutex;
+constexpr size_t kBounceMax = 64u << 20;
+void *bounce = nullptr;
+size_t bounce_bytes = 0;
+int *bounce_flags = nullptr; // 16 ints
+
+bool bounce_room(size_t bytes) {
+  if (!bounce_flags) {
+    if (hipHostMalloc((void **)&bounce_flags, 16 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      bounce_flags = nullptr;
+      return false;
+    }
+  }
+  if (bytes <= bounce_bytes)
+    return true;
+  if (bounce)
+    (void)hipHostFree(bounce);
+  bounce = nullptr;
+  bounce_bytes = 0;
+  const size_t want = std::min(kBounceMax, bytes + (bytes >> 2) + 4096);
+  if (hipHostMalloc(&bounce, want, hipHostMallocDefault) != hipSuccess) {
+    (void)hipGetLastError();
+    bounce = nullptr;
+    return false;
+  }
+  bounce_bytes = want;
+  return true;
+}
 } // namespace
 
 // ---- Call ---------------------------------------------------------------------------------------------------------
@@ -577,12 +615,26 @@ bool Call::ready() {
     }
     arena_bytes = want;
   }
+  bounced_ = arena_used_ <= kBounceMax && bounce_room(arena_used_);
   for (int i = 0; i < ncopies_; i++) {
     Copy &c = copies_[i];
     if (!c.to_device || !c.rows)
       continue;
-    if (!LLHIP_CHECK(hipMemcpy2DAsync((char *)arena + c.offset, c.pitch, c.host, c.pitch, c.row_bytes, c.rows,
-                                      hipMemcpyHostToDevice, the_device.stream))) {
+    bool ok;
+    if (bounced_) { // the rows into the pinned twin (the pitch gaps are never read), then one DMA of the extent
+      char *b = (char *)bounce + c.offset;
+      if (c.pitch == c.row_bytes)
+        memcpy(b, c.host, c.row_bytes * c.rows);
+      else
+        for (size_t r = 0; r < c.rows; r++)
+          memcpy(b + r * c.pitch, (const char *)c.host + r * c.pitch, c.row_bytes);
+      ok = LLHIP_CHECK(hipMemcpyAsync((char *)arena + c.offset, b, (c.rows - 1) * c.pitch + c.row_bytes,
+                                      hipMemcpyHostToDevice, the_device.stream));
+    } else {
+      ok = LLHIP_CHECK(hipMemcpy2DAsync((char *)arena + c.offset, c.pitch, c.host, c.pitch, c.row_bytes, c.rows,
+                                        hipMemcpyHostToDevice, the_device.stream));
+    }
+    if (!ok) {
       failed_ = true;
       return false;
     }
@@ -595,6 +647,33 @@ bool Call::finish() {
     return false;
   if (!staged_)
     return true;
+  if (bounced_) { // outputs and the error flags into pinned memory, one wait, then the rows to the caller
+    if (!flush_pending_quantize())
+      return false;
+    for (int i = 0; i < ncopies_; i++) {
+      Copy &c = copies_[i];
+      if (c.to_host && c.rows &&
+          !LLHIP_CHECK(hipMemcpyAsync((char *)bounce + c.offset, (char *)arena + c.offset,
+                                      (c.rows - 1) * c.pitch + c.row_bytes, hipMemcpyDeviceToHost, the_device.stream)))
+        return false;
+    }
+    if (!LLHIP_CHECK(hipMemcpyAsync(bounce_flags, the_device.error_flags, 16 * sizeof(int), hipMemcpyDeviceToHost,
+                                    the_device.stream)) ||
+        !LLHIP_CHECK(hipStreamSynchronize(the_device.stream)))
+      return false;
+    for (int i = 0; i < ncopies_; i++) {
+      Copy &c = copies_[i];
+      if (!c.to_host || !c.rows)
+        continue;
+      const char *b = (const char *)bounce + c.offset;
+      if (c.pitch == c.row_bytes)
+        memcpy(c.host, b, c.row_bytes * c.rows);
+      else
+        for (size_t r = 0; r < c.rows; r++)
+          memcpy((char *)c.host + r * c.pitch, b + r * c.pitch, c.row_bytes);
+    }
+    return report_flags(bounce_flags);
+  }
   for (int i = 0; i < ncopies_; i++) {
     Copy &c = copies_[i];
     if (!c.to_host || !c.rows)
