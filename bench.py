@@ -986,7 +986,7 @@ def main():
                         "(QKV, Wo +resid, W1/W3 SwiGLU, W2 +resid) + last-row classifier GEMV, gs 64",
             "ops_per_prompt": ops, "tops": round(ops / (psec / args.prefill_steps) / 1e12, 1),
             "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                         "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": measured_traffic("q8_gemm_wide_swiglu"),
+                         "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": measured_traffic("q8_gemm_wide_smma_swiglu"),
                          "kernel": "q8_gemm_wide_smma (W1/W3 SwiGLU 2048x(2x14336)x4096)",
                          "avg_launch_us": round(pavg * 1e6, 1)},
         }
