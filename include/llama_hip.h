@@ -47,7 +47,10 @@ int llhip_register_host(const void *host, size_t bytes);
 /* LLAMA_HIP_REGISTER_MAPPINGS=1 (read when first needed) registers on its own: the first time an entry point receives
  * an input inside a read-only mapping of a regular file that no executable segment maps (a checkpoint, not a program
  * or a library), the whole mapping is registered as above, so a caller that takes its weight views from a mapped
- * checkpoint needs no call of its own to run on resident weights. */
+ * checkpoint needs no call of its own to run on resident weights. Each later call that resolves into such a range
+ * first checks that the same place of the same file is still mapped there (one PROCMAP_QUERY on Linux 6.11 and
+ * later, a read of /proc/self/maps before); once the caller has unmapped it, the copy is dropped and the addresses
+ * mean whatever is mapped there now. The file's bytes must not change while it is mapped. */
 int llhip_unregister_host(const void *host);
 /* The device address a host address resolves to (NULL when it is not inside a registered range). */
 void *llhip_resolve(const void *host);

@@ -133,7 +133,9 @@ class Call {
   };
   void *address(const Ref &r) const;
   Ref stage(void *host, size_t row_bytes, size_t pitch, size_t rows, bool to_device, bool to_host);
+  void *resolve_registered(const void *p, size_t *room = nullptr);
   const char *name_;
+  uintptr_t current_mapping_ = 0; // a registered file mapping found current during this call
   Copy copies_[16];
   int ncopies_ = 0;
   size_t arena_used_ = 0;

@@ -4,9 +4,15 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
+#include <cerrno>
 #include <map>
 #include <mutex>
 #include <vector>
+
+#include <fcntl.h>
+#include <sys/ioctl.h>
+#include <unistd.h>
 
 #include "common.h"
 
@@ -190,17 +196,25 @@ bool synchronize_and_check() {
 // ---- registry of uploaded host ranges ----------------------------------------------------------------------------
 
 namespace {
+// A mapped segment of a file registered on its own (LLAMA_HIP_REGISTER_MAPPINGS): its address range and what it
+// maps, the file (device and inode) and the file offset at its start.
+struct Segment {
+  uintptr_t start, end;
+  unsigned long long offset, ino;
+  unsigned dev_major, dev_minor;
+};
 struct Region {
   size_t bytes;
   void *device;
+  std::vector<Segment> segments; // empty for llhip_register_host's ranges
 };
 std::mutex registry_mutex;
 std::map<uintptr_t, Region> registry;
 std::map<void *, size_t> allocations; // llhip_malloc's buffers and their claimed bytes (under registry_mutex)
 
 // The device copy of p when p lies inside a registered range, else nullptr; *room receives the bytes of the range
-// from p to its end.
-void *lookup(const void *p, size_t *room = nullptr) {
+// from p to its end, *start the range's start and *automatic whether it was registered as a file mapping.
+void *lookup(const void *p, size_t *room = nullptr, uintptr_t *start = nullptr, bool *automatic = nullptr) {
   std::lock_guard<std::mutex> lock(registry_mutex);
   if (registry.empty())
     return nullptr;
@@ -213,8 +227,13 @@ void *lookup(const void *p, size_t *room = nullptr) {
     return nullptr;
   if (room)
     *room = it->first + it->second.bytes - addr;
+  if (start)
+    *start = it->first;
+  if (automatic)
+    *automatic = !it->second.segments.empty();
   return (char *)it->second.device + (addr - it->first);
 }
+
 
 // 1: device memory with at least `bytes` from p to the end of its allocation; -1: device memory that is shorter
 // (the launch would read or write past it); 0: not device memory.
@@ -281,8 +300,59 @@ std::vector<MapEntry> read_maps() {
   return out;
 }
 
+// The mapping that covers address a now. PROCMAP_QUERY (an ioctl on /proc/self/maps, Linux 6.11 and later; its
+// structure is the kernel's uapi one) asks for that one mapping directly; where the kernel lacks it, the whole table
+// is read.
+struct ProcmapQuery {
+  uint64_t size, query_flags, query_addr, vma_start, vma_end, vma_flags, vma_page_size, vma_offset, inode;
+  uint32_t dev_major, dev_minor, vma_name_size, build_id_size;
+  uint64_t vma_name_addr, build_id_addr;
+};
+const unsigned long kProcmapQuery = _IOWR('f', 17, ProcmapQuery);
+constexpr uint64_t kVmaReadable = 1, kVmaWritable = 2, kVmaExecutable = 4;
+
+bool vma_at(uintptr_t a, MapEntry *out) {
+  // kept open for the process; a forked child, whose inherited descriptor would show the parent's table, opens its own
+  static std::mutex fd_mutex;
+  static int fd = -1;
+  static pid_t owner = 0;
+  static std::atomic<bool> no_query{false};
+  int qfd;
+  {
+    std::lock_guard<std::mutex> lock(fd_mutex);
+    if (owner != getpid()) {
+      if (fd >= 0)
+        close(fd);
+      fd = open("/proc/self/maps", O_RDONLY | O_CLOEXEC);
+      owner = getpid();
+    }
+    qfd = fd;
+  }
+  if (qfd >= 0 && !no_query.load()) {
+    ProcmapQuery q{};
+    q.size = sizeof(q);
+    q.query_addr = a;
+    if (ioctl(qfd, kProcmapQuery, &q) == 0) {
+      *out = MapEntry{(uintptr_t)q.vma_start, (uintptr_t)q.vma_end, q.vma_offset, q.inode, q.dev_major, q.dev_minor,
+                      (q.vma_flags & kVmaReadable) != 0, (q.vma_flags & kVmaWritable) != 0,
+                      (q.vma_flags & kVmaExecutable) != 0, q.inode != 0};
+      return true;
+    }
+    if (errno == ENOENT)
+      return false; // nothing is mapped there
+    no_query.store(true); // an older kernel: ENOTTY or EINVAL
+  }
+  for (const MapEntry &m : read_maps())
+    if (a >= m.start && a < m.end) {
+      *out = m;
+      return true;
+    }
+  return false;
+}
+
 std::mutex mapping_mutex;
 std::vector<std::pair<uintptr_t, uintptr_t>> mappings_declined; // ranges already found not to qualify
+int register_range(const void *host, size_t bytes, std::vector<Segment> segments);
 
 // Registers the file mapping around host address p when it qualifies; false otherwise (p then stays staged).
 bool register_file_mapping(const void *p) {
@@ -319,7 +389,61 @@ bool register_file_mapping(const void *p) {
     lo--;
   while (hi + 1 < maps.size() && same(maps[hi], maps[hi + 1]))
     hi++;
-  return llhip_register_host((const void *)maps[lo].start, maps[hi].end - maps[lo].start) == 0;
+  // what each segment maps, checked again by every later call that resolves into the range (mapping_current)
+  std::vector<Segment> segments;
+  for (size_t j = lo; j <= hi; j++)
+    segments.push_back(Segment{maps[j].start, maps[j].end, maps[j].offset, maps[j].inode, maps[j].dev_major,
+                               maps[j].dev_minor});
+  return register_range((const void *)maps[lo].start, maps[hi].end - maps[lo].start, std::move(segments)) == 0;
+}
+
+// Whether the file mapping registered at `start` still maps, at p, the same place of the same file, read-only: false
+// once the caller has unmapped it (and perhaps mapped something else at the same addresses).
+bool mapping_current(uintptr_t start, const void *p) {
+  const uintptr_t a = (uintptr_t)p;
+  Segment seg{};
+  {
+    std::lock_guard<std::mutex> lock(registry_mutex);
+    auto it = registry.find(start);
+    if (it == registry.end())
+      return false;
+    bool found = false;
+    for (const Segment &g : it->second.segments)
+      if (a >= g.start && a < g.end) {
+        seg = g;
+        found = true;
+        break;
+      }
+    if (!found)
+      return false;
+  }
+  MapEntry now{};
+  return vma_at(a, &now) && now.file && now.read && !now.write && now.inode == seg.ino &&
+         now.dev_major == seg.dev_major && now.dev_minor == seg.dev_minor &&
+         now.offset + (a - now.start) == seg.offset + (a - seg.start);
+}
+
+// Drops the file mapping registered at `start` (its device copy freed once the stream's work is done): the caller
+// unmapped it, so a later call with addresses inside it means whatever is mapped there now. False after raise (under
+// graph capture, where the stream cannot wait).
+bool retire_mapping(uintptr_t start) {
+  std::lock_guard<std::mutex> lock(mapping_mutex);
+  if (the_device.capturing)
+    return raise("a registered file mapping was unmapped or replaced during graph capture");
+  size_t bytes = 0;
+  {
+    std::lock_guard<std::mutex> rl(registry_mutex);
+    auto it = registry.find(start);
+    if (it == registry.end() || it->second.segments.empty())
+      return true; // retired meanwhile by another call
+    bytes = it->second.bytes;
+  }
+  mappings_declined.erase(std::remove_if(mappings_declined.begin(), mappings_declined.end(),
+                                         [&](const std::pair<uintptr_t, uintptr_t> &r) {
+                                           return r.first < start + bytes && start < r.second;
+                                         }),
+                          mappings_declined.end());
+  return llhip_unregister_host((const void *)start) == 0;
 }
 
 // The staging arena for host buffers: grown on demand, reused by every staged call. Calls that stage at most
@@ -539,12 +663,29 @@ void *Call::address(const Ref &r) const {
   return r.staged < 0 ? r.direct : (void *)((char *)arena + copies_[r.staged].offset);
 }
 
+// lookup(p), with a range registered as a file mapping checked once per call against what is mapped there now: a
+// stale range (the caller unmapped it) is retired first, so p resolves to nothing and takes the unregistered route.
+void *Call::resolve_registered(const void *p, size_t *room) {
+  uintptr_t start = 0;
+  bool automatic = false;
+  void *dev = lookup(p, room, &start, &automatic);
+  if (!dev || !automatic || start == current_mapping_)
+    return dev;
+  if (mapping_current(start, p)) {
+    current_mapping_ = start;
+    return dev;
+  }
+  if (!retire_mapping(start))
+    failed_ = true;
+  return nullptr;
+}
+
 Ref Call::in2d(const void *p, size_t row_bytes, size_t pitch, size_t rows) {
   if (!p || failed_ || !rows)
     return Ref{const_cast<void *>(p), -1};
   const size_t extent = (rows - 1) * pitch + row_bytes;
   size_t room = 0;
-  if (void *dev = lookup(p, &room)) {
+  if (void *dev = resolve_registered(p, &room)) {
     if (room < extent) {
       failed_ = true;
       raise("%s: %zu bytes at %p run past the end of their registered range", name_, extent, p);
@@ -560,8 +701,12 @@ Ref Call::in2d(const void *p, size_t row_bytes, size_t pitch, size_t rows) {
   }
   if (where > 0)
     return Ref{const_cast<void *>(p), -1};
+  if (failed_)
+    return Ref{};
   if (register_mappings_enabled() && !the_device.capturing && register_file_mapping(p)) {
-    if (void *dev = lookup(p, &room)) {
+    uintptr_t start = 0;
+    if (void *dev = lookup(p, &room, &start)) {
+      current_mapping_ = start; // registered just now from what is mapped
       if (room >= extent)
         return Ref{dev, -1};
     }
@@ -572,7 +717,7 @@ Ref Call::in2d(const void *p, size_t row_bytes, size_t pitch, size_t rows) {
 Ref Call::out2d(void *p, size_t row_bytes, size_t pitch, size_t rows, bool read_too) {
   if (!p || failed_ || !rows)
     return Ref{p, -1};
-  if (lookup(p)) {
+  if (resolve_registered(p)) {
     failed_ = true;
     raise("%s: an output lies inside a registered (read-only) weight range", name_);
     return Ref{};
@@ -685,25 +830,8 @@ bool Call::finish() {
   return synchronize_and_check();
 }
 
-} // namespace llhip
-
-// ---- C ABI: device and residency ----------------------------------------------------------------------------------
-
-using namespace llhip;
-
-extern "C" {
-
-int llhip_init(void) { return ensure_device() ? 0 : -1; }
-
-const char *llhip_device_name(void) { return ensure_device() ? device_name : ""; }
-
-int llhip_device_cu_count(void) { return ensure_device() ? the_device.cu_count : 0; }
-
-void *llhip_stream(void) { return ensure_device() ? (void *)the_device.stream : nullptr; }
-
-void llhip_synchronize(void) { (void)synchronize_and_check(); }
-
-int llhip_register_host(const void *host, size_t bytes) {
+namespace {
+int register_range(const void *host, size_t bytes, std::vector<Segment> segments) {
   if (!ensure_device())
     return -1;
   if (!host || !bytes)
@@ -726,9 +854,34 @@ int llhip_register_host(const void *host, size_t bytes) {
     return -1;
   }
   std::lock_guard<std::mutex> lock(registry_mutex);
-  registry[(uintptr_t)host] = Region{bytes, dev};
+  registry[(uintptr_t)host] = Region{bytes, dev, std::move(segments)};
   return 0;
 }
+} // namespace
+
+// llhip_register_host: a range with no file identity to check.
+int register_range_host(const void *host, size_t bytes) { return register_range(host, bytes, {}); }
+
+} // namespace llhip
+
+// ---- C ABI: device and residency ----------------------------------------------------------------------------------
+
+using namespace llhip;
+
+extern "C" {
+
+int llhip_init(void) { return ensure_device() ? 0 : -1; }
+
+const char *llhip_device_name(void) { return ensure_device() ? device_name : ""; }
+
+int llhip_device_cu_count(void) { return ensure_device() ? the_device.cu_count : 0; }
+
+void *llhip_stream(void) { return ensure_device() ? (void *)the_device.stream : nullptr; }
+
+void llhip_synchronize(void) { (void)synchronize_and_check(); }
+
+
+int llhip_register_host(const void *host, size_t bytes) { return llhip::register_range_host(host, bytes); }
 
 int llhip_unregister_host(const void *host) {
   if (!ensure_device())
