@@ -192,8 +192,10 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
     return;
   AttentionJob job{call.ptr<float>(O), call.ptr<const float>(Q), call.ptr<const float>(K), call.ptr<const float>(V),
                    n_heads, n_kv_heads, head_dim, pos0, m, pos_stride, head_base, nullptr, nullptr, nullptr};
-  // the flash kernel (16 rows and more) keeps no split partials, so only the split kernels' need is checked; a fused
-  // RoPE is taken only for one row, which never runs the flash kernel
+  // the flash kernel (16 rows and more) splits a tile's positions only as far as its partials fit the scratch, so only
+  // the split kernels' need is checked; a fused RoPE is taken only for one row, which never runs the flash kernel
+  if (noalloc)
+    job.partial_room = kAttentionScratchFloats;
   if (noalloc && !attention_uses_flash(job) && partial_floats > kAttentionScratchFloats) {
     raise("%s: %d rows of %d heads up to position %d need %zu floats of scratch; it holds %zu", name, m, n_heads,
           pos0 + m - 1, partial_floats, kAttentionScratchFloats);

@@ -244,11 +244,15 @@ struct AttentionJob {
   // k_new written back rotated, and k_new / v_new stored at position pos0 of the caches, which key / value then are.
   float *k_new;
   const float *v_new, *table;
+  // floats of `partial` the batched kernel may use when it splits a tile's positions over blocks (0: the
+  // attention_partial_floats of the job, which any split fits)
+  size_t partial_room = 0;
 };
 bool attention_shape_ok(int n_heads, int n_kv_heads, int head_dim); // kv_mul <= 16, head_dim <= 256
 size_t attention_partial_floats(int rows, int n_heads, int head_dim, int last_position);
 bool launch_attention(const AttentionJob &job, float *partial, hipStream_t stream);
-bool attention_uses_flash(const AttentionJob &job); // the batched kernel with no split partials takes the job
+// The batched kernel takes the job; its partials, when it splits a tile's positions, stay within job.partial_room.
+bool attention_uses_flash(const AttentionJob &job);
 
 struct GemmSegmentDev {
   float *c;

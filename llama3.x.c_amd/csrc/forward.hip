@@ -236,6 +236,7 @@ struct AttnParams {
   const float *v_new, *table;
   size_t pos_stride, head_base;
   float divisor; // sqrtf(head_dim)
+  int splits;    // batched flash form: blocks per tile, each over a share of its chunks (0: the tile whole)
 };
 
 constexpr int kTileThreads = 512;
@@ -713,9 +714,10 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
   // scores in base 2: s * log2(e) / divisor, so that exp(s / divisor - m) is the native exp2 of (s2 - m2)
   const float scale2 = 1.4426950408889634f / p.divisor;
   bool bad = false;
+  const bool split = p.splits > 0; // block (tile, g, s) takes share s of the tile's chunks and stores a partial
   for (int pass = 0; pass < 2; pass++) {
-    const int tile = pass == 0 ? ntiles - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    if (pass == 1 && tile >= ntiles - 1 - (int)blockIdx.x)
+    const int tile = split ? (int)blockIdx.x : pass == 0 ? ntiles - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    if (pass == 1 && (split || tile >= ntiles - 1 - (int)blockIdx.x))
       break; // the middle tile of an odd count is taken once
     const int r0 = tile * tile_rows, row = r0 + j;
     // vectors past tile_rows * kv_mul (when kv_mul does not divide 128) would be the next tile's: idle, like rows past
@@ -866,10 +868,12 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
     // in K(c % 2) and its V in V(c % 2). At the start of step c every wave has waited for its loads of the step
     // before and passed the barrier; then K(c % 2), last read for chunk c (in step c - 1), takes chunk c + 2, and
     // V((c + 1) % 2), last read for chunk c - 1, takes chunk c + 1.
-    const int chunks = last / kChunk + 1;
+    // this block's chunks: c0 .. c0 + chunks - 1 (all of the tile's unless split)
+    const int all = last / kChunk + 1, share = split ? (all + p.splits - 1) / p.splits : all;
+    const int c0 = split ? min(all, (int)blockIdx.z * share) : 0, chunks = min(all, c0 + share) - c0;
     v4f sc[4];
     auto step = [&](int c, const float *kn, float *kdma, const float *vs, float *vdma) {
-      const int t0 = c * kChunk;
+      const int t0 = (c0 + c) * kChunk;
       wait_loads();
       __syncthreads();
       if (c + 2 < chunks)
@@ -889,21 +893,37 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
         accumulate(vs, sc);
       }
     };
-    FlashDma<HD>::load(krs, K0, 0, stride_bytes, wave, lane);
-    if (chunks > 1)
-      FlashDma<HD>::load(krs, K1, kChunk, stride_bytes, wave, lane);
-    FlashDma<HD>::load(vrs, V0, 0, stride_bytes, wave, lane);
-    wait_loads();
-    __syncthreads();
-    score(K0, sc); // every wave reaches chunk 0: wave_last >= pos0 >= 0
-    for (int c = 0; c < chunks; c += 2) {
-      step(c, K1, K0, V0, V1);
-      if (c + 1 < chunks)
-        step(c + 1, K0, K1, V1, V0);
+    if (chunks > 0) {
+      FlashDma<HD>::load(krs, K0, c0 * kChunk, stride_bytes, wave, lane);
+      if (chunks > 1)
+        FlashDma<HD>::load(krs, K1, (c0 + 1) * kChunk, stride_bytes, wave, lane);
+      FlashDma<HD>::load(vrs, V0, c0 * kChunk, stride_bytes, wave, lane);
+      wait_loads();
+      __syncthreads();
+      score(K0, sc); // unused by a wave that does not reach the chunk (the steps check)
+      for (int c = 0; c < chunks; c += 2) {
+        step(c, K1, K0, V0, V1);
+        if (c + 1 < chunks)
+          step(c + 1, K0, K1, V1, V0);
+      }
     }
     __syncthreads(); // the next tile's first loads reuse K0, K1 and V0
     if (!active)
       continue;
+    if (split) { // the share's value sums, maximum (in natural units, as the merge takes it) and sum, unnormalized
+      float *slot = p.partial + (((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * p.chunks + blockIdx.z) * p.slot;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int d = 0; d < kDt; d += 4)
+          *reinterpret_cast<float4 *>(slot + 16 * d + 4 * (4 * lq + e)) =
+              float4{o[d][e], o[d + 1][e], o[d + 2][e], o[d + 3][e]};
+      if (lq == 0) {
+        slot[HD] = m_run > -FLT_MAX ? m_run * 0.6931471805599453f : -FLT_MAX;
+        slot[HD + 1] = l_run;
+      }
+      continue;
+    }
     // lane (lq, lc) holds dimensions 4 (4 lq + e) + d % 4 + 64 (d / 4) of vector lc: for each e, runs of four floats
     const float inv = 1.0f / l_run;
     float *dst = p.out + ((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * HD;
@@ -1055,7 +1075,8 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
   __shared__ float weight[kMaxMergeChunks];
   __shared__ float red[kThreads];
   const int h = blockIdx.x, r = blockIdx.y;
-  const int hd = p.head_dim, chunks = (p.pos0 + r) / kChunk + 1;
+  // the row's chunk partials, or the flash form's split partials (some of them empty: m = -FLT_MAX, l = 0)
+  const int hd = p.head_dim, chunks = p.splits > 0 ? p.splits : (p.pos0 + r) / kChunk + 1;
   const float *part = p.partial + ((size_t)(r * p.n_heads + h) * p.chunks) * p.slot;
   const int groups = kThreads / hd > 0 ? kThreads / hd : 1;
   const int d = threadIdx.x % hd, grp = threadIdx.x / hd;
@@ -1236,6 +1257,47 @@ bool attention_uses_flash(const AttentionJob &job) {
          offsets_fit && ((uintptr_t)job.out & 15) == 0 && ((uintptr_t)job.value & 15) == 0;
 }
 
+// Blocks per tile of the batched kernel (0: one block per pair of tiles, no partials). A block walks its tiles' 64-position
+// chunks at about the same time per chunk whatever the grid, so a grid of few blocks with long walks (a short batch
+// late in a sequence: a prompt prefilled in batches) leaves most CUs idle for the whole walk. Split S gives each tile S
+// blocks over shares of its chunks and adds attn_merge, whose launch grows with the rows and heads. The choice is the
+// S in {1, 2, 4, 8, 16} of least estimated time, in units of one chunk's walk (about 10 us at head_dim 128, 6 at 64,
+// measured on 8B, 3B and 1B heads): unsplit, the longest pair's chunks times the rounds of the CUs its grid takes;
+// split, the longest share's chunks times the rounds, plus the merge (about 4 + 0.08 us per row at 32 heads); a split
+// must save a tenth. Its partials stay within job.partial_room. LLAMA_HIP_FLASH_SPLITS = n forces n (1: never
+// split), for tuning and tests.
+int flash_splits(const AttentionJob &job, int chunks) {
+  const int kv_mul = job.n_heads / job.n_kv_heads;
+  const int tile_rows = 128 / kv_mul, tiles = (job.rows + tile_rows - 1) / tile_rows;
+  const int cus = device().cu_count > 0 ? device().cu_count : 256;
+  const char *env = getenv("LLAMA_HIP_FLASH_SPLITS");
+  int splits = env && *env ? atoi(env) : 0;
+  if (splits <= 0) {
+    auto walk = [&](int t) { return (job.pos0 + min((t + 1) * tile_rows, job.rows) - 1) / kChunk + 1; };
+    auto rounds = [&](long long blocks) { return (double)((blocks + cus - 1) / cus); };
+    const double chunk_us = job.head_dim == 128 ? 10.0 : 6.0;
+    const int pairs = (tiles + 1) / 2;
+    const double unsplit = chunk_us * (walk(tiles - 1) + (tiles > 1 ? walk(0) : 0)) *
+                           rounds((long long)pairs * job.n_kv_heads);
+    const double merge = 4.0 + 0.08 * job.rows * job.n_heads / 32.0;
+    double best = 0.9 * unsplit;
+    splits = 1;
+    for (int s = 2; s <= 16; s *= 2) {
+      const double t = chunk_us * ((chunks + s - 1) / s) * rounds((long long)tiles * job.n_kv_heads * s) + merge;
+      if (t < best)
+        best = t, splits = s;
+    }
+  }
+  splits = min(min(splits, 16), chunks);
+  const size_t slot = slot_floats(job.head_dim);
+  const size_t room = job.partial_room ? job.partial_room
+                                       : attention_partial_floats(job.rows, job.n_heads, job.head_dim,
+                                                                  job.pos0 + job.rows - 1);
+  while (splits > 1 && (size_t)job.rows * job.n_heads * splits * slot > room)
+    splits--;
+  return splits > 1 ? splits : 0;
+}
+
 bool launch_attention(const AttentionJob &job, float *partial, hipStream_t stream) {
   AttnParams p{};
   p.out = job.out;
@@ -1266,14 +1328,22 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
   if (job.table && !aligned)
     return raise("internal: a fused RoPE attention on operands the aligned kernel does not take");
   if (attention_uses_flash(job)) {
-    // two staged chunks of K and two of V rows in static LDS: 4 x 64 x HD floats (128 KB at HD = 128)
+    // two staged chunks of K and two of V rows in static LDS: 4 x 64 x HD floats (128 KB at HD = 128); a block per
+    // pair of tiles, or per tile and share of its chunks (flash_splits)
     const int tile_rows = 128 / kv_mul, tiles = (job.rows + tile_rows - 1) / tile_rows;
-    const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)job.n_kv_heads); // a block per pair of tiles
+    p.splits = flash_splits(job, p.chunks);
+    const dim3 grid(p.splits ? (unsigned)tiles : (unsigned)((tiles + 1) / 2), (unsigned)job.n_kv_heads,
+                    p.splits ? (unsigned)p.splits : 1u);
     if (job.head_dim == 128)
       hipLaunchKernelGGL(attn_flash<128>, grid, dim3(kTileThreads), 0, stream, p);
     else
       hipLaunchKernelGGL(attn_flash<64>, grid, dim3(kTileThreads), 0, stream, p);
-    return launch_ok("attn_flash");
+    if (!launch_ok("attn_flash"))
+      return false;
+    if (!p.splits)
+      return true;
+    hipLaunchKernelGGL(attn_merge, dim3((unsigned)job.n_heads, (unsigned)job.rows), dim3(kThreads), 0, stream, p);
+    return launch_ok("attn_merge");
   }
   // decode: the slice-parallel kernel for 64 or 128 dimensions and up to eight query vectors per KV head
   if (aligned && job.rows == 1 && (job.head_dim == 64 || job.head_dim == 128) && kv_mul <= kDecodeMaxQv &&

@@ -299,12 +299,19 @@ def test_attention_batch_rows(nh, nkv, hd, seq, pos0, m):
     (32, 8, 128, 600, 0, 512, "head"),     # a short 8B prompt: 64 blocks
     (24, 8, 128, 700, 40, 512, "rows"),    # the 3B heads from position 40
     (32, 8, 64, 300, 0, 130, "head"),      # 1B heads, 130 rows
+    (32, 8, 128, 2100, 1792, 256, "head"), # a 256-row batch late in an 8B prompt: tiles split over 4 blocks each
+    (32, 8, 128, 2100, 1984, 64, "rows"),  # 64 rows at 1984: 16 blocks per tile
+    (24, 8, 128, 4100, 3968, 128, "head"), # 3B heads at 3968: 8 blocks per tile
+    (32, 8, 64, 2100, 1792, 256, "rows"),  # 1B heads late: 4 blocks per tile
 ])
-def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout):
+def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout, monkeypatch, splits=None):
     """Batches of at least 16 rows with 64 or 128 dimensions per head run the flash kernel on the FP32 matrix cores:
     every checked row within the float64 budget of the decode attention at its position and within twice it of the
     oracle, for GQA ratios 1-16 (those that do not divide 128 leave the tile's last vectors idle), both layouts, ragged
-    tiles, short prompts and long contexts."""
+    tiles, short prompts and long contexts. A short batch late in a sequence splits each tile's positions over several
+    blocks whose partials attn_merge combines (the last four cases, and the 16-row one)."""
+    if splits:
+        monkeypatch.setenv("LLAMA_HIP_FLASH_SPLITS", str(splits))
     L = hu.lib()
     rng = orc.Rng(orc.SEED + 900 + m + hd)
     kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(m * nh * hd, 0, 1)
@@ -317,6 +324,14 @@ def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout):
     rows = range(m) if m <= 200 else sorted(r for r in {0, 1, 63, 64, 127, 128, 300, 1000, m - 2, m - 1} if r < m)
     for i in rows:
         check_attention(got[i], q.reshape(m, -1)[i], kc, vc, nh, nkv, hd, seq, pos0 + i, ps, hb, f"row {i}")
+
+
+@pytest.mark.parametrize("splits,shape", [(3, (16, 8, 128, 400, 130, 77, "head")), (16, (32, 8, 128, 600, 0, 512, "head")),
+                                          (5, (12, 4, 64, 300, 21, 100, "rows")), (2, (24, 8, 128, 2100, 0, 2048, "head"))])
+def test_attention_flash_forced_splits(splits, shape, monkeypatch):
+    """LLAMA_HIP_FLASH_SPLITS forces the blocks per tile: shares that hold no chunk (3 shares of a 4-chunk tile), more
+    shares than a tile's chunks, an odd count and the whole 3B prompt, each row within the float64 budget."""
+    test_attention_batch_flash_shapes(*shape, monkeypatch, splits=splits)
 
 
 def test_attention_flash_nonfinite_score_fails():
