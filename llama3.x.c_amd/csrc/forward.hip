@@ -1075,8 +1075,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
   __shared__ float weight[kMaxMergeChunks];
   __shared__ float red[kThreads];
   const int h = blockIdx.x, r = blockIdx.y;
-  // the row's chunk partials, or the flash form's split partials (some of them empty: m = -FLT_MAX, l = 0)
-  const int hd = p.head_dim, chunks = p.splits > 0 ? p.splits : (p.pos0 + r) / kChunk + 1;
+  const int hd = p.head_dim, chunks = (p.pos0 + r) / kChunk + 1;
   const float *part = p.partial + ((size_t)(r * p.n_heads + h) * p.chunks) * p.slot;
   const int groups = kThreads / hd > 0 ? kThreads / hd : 1;
   const int d = threadIdx.x % hd, grp = threadIdx.x / hd;
@@ -1130,6 +1129,34 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnParams p) {
       o += red[g2 * hd + d];
     p.out[((size_t)r * p.n_heads + h) * hd + d] = o / l;
   }
+}
+
+// The flash form's split partials combined, a thread per (row, head, four dimensions): M the maximum of the shares'
+// maxima (a share that held no chunk stores -FLT_MAX and zero sums), weights exp(m_s - M) in share order, and the
+// output sum_s w_s o_s / sum_s w_s l_s. The same combination as attn_merge with the sums in share order; with at most
+// 16 shares a thread needs no reduction across the block, so the grid is as small as the output.
+__global__ __launch_bounds__(kThreads) void attn_merge_shares(AttnParams p) {
+  const int q4 = p.head_dim / 4;
+  const long long idx = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= (long long)p.rows * p.n_heads * q4)
+    return;
+  const int d4 = (int)(idx % q4);
+  const long long rh = idx / q4; // row * n_heads + head
+  const float *part = p.partial + (size_t)rh * p.chunks * p.slot;
+  const int hd = p.head_dim;
+  float m = -FLT_MAX;
+  for (int s = 0; s < p.splits; s++)
+    m = fmaxf(m, part[(size_t)s * p.slot + hd]);
+  float4 o = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  float l = 0.0f;
+  for (int s = 0; s < p.splits; s++) {
+    const float *share = part + (size_t)s * p.slot;
+    const float w = expf(share[hd] - m);
+    l = fmaf(w, share[hd + 1], l);
+    const float4 v = *reinterpret_cast<const float4 *>(share + 4 * d4);
+    o = float4{fmaf(w, v.x, o.x), fmaf(w, v.y, o.y), fmaf(w, v.z, o.z), fmaf(w, v.w, o.w)};
+  }
+  *reinterpret_cast<float4 *>(p.out + rh * hd + 4 * d4) = float4{o.x / l, o.y / l, o.z / l, o.w / l};
 }
 
 } // namespace
@@ -1260,12 +1287,11 @@ bool attention_uses_flash(const AttentionJob &job) {
 // Blocks per tile of the batched kernel (0: one block per pair of tiles, no partials). A block walks its tiles' 64-position
 // chunks at about the same time per chunk whatever the grid, so a grid of few blocks with long walks (a short batch
 // late in a sequence: a prompt prefilled in batches) leaves most CUs idle for the whole walk. Split S gives each tile S
-// blocks over shares of its chunks and adds attn_merge, whose launch grows with the rows and heads. The choice is the
-// S in {1, 2, 4, 8, 16} of least estimated time, in units of one chunk's walk (about 10 us at head_dim 128, 6 at 64,
-// measured on 8B, 3B and 1B heads): unsplit, the longest pair's chunks times the rounds of the CUs its grid takes;
-// split, the longest share's chunks times the rounds, plus the merge (about 4 + 0.08 us per row at 32 heads); a split
-// must save a tenth. Its partials stay within job.partial_room. LLAMA_HIP_FLASH_SPLITS = n forces n (1: never
-// split), for tuning and tests.
+// blocks over shares of its chunks and adds attn_merge_shares. The choice is the S in {1, 2, 4, 8, 16} of least
+// estimated time, with one chunk's walk about 10 us at head_dim 128 and 6 at 64 (measured on 8B, 3B and 1B heads):
+// unsplit, the longest pair's chunks times the rounds of the CUs its grid takes; split, the longest share's chunks
+// times the rounds, plus the merge (about 2 us + 0.012 us per row at 32 heads); a split must save a tenth. Its
+// partials stay within job.partial_room. LLAMA_HIP_FLASH_SPLITS = n forces n (1: never split), for tuning and tests.
 int flash_splits(const AttentionJob &job, int chunks) {
   const int kv_mul = job.n_heads / job.n_kv_heads;
   const int tile_rows = 128 / kv_mul, tiles = (job.rows + tile_rows - 1) / tile_rows;
@@ -1279,7 +1305,7 @@ int flash_splits(const AttentionJob &job, int chunks) {
     const int pairs = (tiles + 1) / 2;
     const double unsplit = chunk_us * (walk(tiles - 1) + (tiles > 1 ? walk(0) : 0)) *
                            rounds((long long)pairs * job.n_kv_heads);
-    const double merge = 4.0 + 0.08 * job.rows * job.n_heads / 32.0;
+    const double merge = 2.0 + 0.012 * job.rows * job.n_heads / 32.0;
     double best = 0.9 * unsplit;
     splits = 1;
     for (int s = 2; s <= 16; s *= 2) {
@@ -1342,8 +1368,10 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
       return false;
     if (!p.splits)
       return true;
-    hipLaunchKernelGGL(attn_merge, dim3((unsigned)job.n_heads, (unsigned)job.rows), dim3(kThreads), 0, stream, p);
-    return launch_ok("attn_merge");
+    const long long threads = (long long)job.rows * job.n_heads * (job.head_dim / 4);
+    hipLaunchKernelGGL(attn_merge_shares, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       stream, p);
+    return launch_ok("attn_merge_shares");
   }
   // decode: the slice-parallel kernel for 64 or 128 dimensions and up to eight query vectors per KV head
   if (aligned && job.rows == 1 && (job.head_dim == 64 || job.head_dim == 128) && kv_mul <= kDecodeMaxQv &&
