@@ -1,7 +1,7 @@
 """LLAMA_HIP_REGISTER_MAPPINGS=1: host weights inside a read-only file mapping are uploaded once, on first use, and the
 registration follows the mapping. The reference unmaps its checkpoint when the model is freed (src/engine.c:55), and
 a process that loads another checkpoint may get the same addresses back; the library must then read the new file,
-not the copy of the old one.
+or the new place in the same file, not the copy of the old one.
 
 The switch is read once per process, so the checks run in a child process with it set. Each GEMV on mapped weights
 is compared bit for bit with the same call on the weights in plain host memory (staged per call: the same kernel on
@@ -54,20 +54,22 @@ def gemv(base):
     assert lh.last_error() == "", lh.last_error()
     return out
 
-def mapped(path, addr=None, fixed=False):
+def mapped(path, addr=None, fixed=False, offset=0):
     fd = os.open(path, os.O_RDONLY)
-    p = libc.mmap(addr, size, PROT_READ, MAP_PRIVATE | (MAP_FIXED if fixed else 0), fd, 0)
+    p = libc.mmap(addr, size, PROT_READ, MAP_PRIVATE | (MAP_FIXED if fixed else 0), fd, offset)
     os.close(fd)
     assert p not in (None, ctypes.c_void_p(-1).value), ctypes.get_errno()
     return p
 
-A, B = weights(1), weights(2)
+A, B, C = weights(1), weights(2), weights(3)
 want = {}
-for name, raw in (("A", A), ("B", B)):
+for name, raw in (("A", A), ("B", B), ("C", C)):
     want[name] = gemv(raw.ctypes.data)  # plain host memory: staged per call
-    with open(os.path.join(tmp, name), "wb") as f:
-        f.write(raw.tobytes())
-assert not np.array_equal(want["A"], want["B"])
+with open(os.path.join(tmp, "A"), "wb") as f:
+    f.write(A.tobytes())
+with open(os.path.join(tmp, "B"), "wb") as f:  # B, then C one page further on
+    f.write(B.tobytes() + bytes(4096) + C.tobytes())
+assert not np.array_equal(want["A"], want["B"]) and not np.array_equal(want["B"], want["C"])
 base_claim = L.llhip_hbm_claimed()
 
 a = mapped(os.path.join(tmp, "A"))
@@ -84,7 +86,14 @@ assert b == a
 assert np.array_equal(gemv(b), want["B"])
 assert L.llhip_hbm_claimed() == claim_a  # A's copy dropped, B's made
 
-# the same addresses, anonymous memory holding B's bytes: not a file mapping, so staged, and B's copy dropped
+# the same addresses and file, another place in it (C, mapped from offset size + 4096)
+assert libc.munmap(b, size) == 0
+b = mapped(os.path.join(tmp, "B"), a, fixed=True, offset=size + 4096)
+assert b == a
+assert np.array_equal(gemv(b), want["C"])
+assert L.llhip_hbm_claimed() == claim_a
+
+# the same addresses, anonymous memory holding B's bytes: not a file mapping, so staged, and the copy dropped
 assert libc.munmap(b, size) == 0
 c = libc.mmap(a, size, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_FIXED, -1, 0)
 assert c == a
