@@ -45,6 +45,7 @@ F32_PEAK_TFS = 157.3  # MI355X fp32 matrix
 # Llama-3.1-8B
 DIM, KV_DIM, HIDDEN, VOCAB, LAYERS, GS = 4096, 1024, 14336, 128256, 32, 64
 PROMPT = 2048
+BATCH_DEFAULT = 256  # the reference's default prefill batch for Q8_0 (src/engine.c:98)
 
 
 def q8_bytes(rows, k, gs=GS):
@@ -818,6 +819,37 @@ def engine_bench(lh, L, args, prompts=None):
             assert np.isfinite(logits).all()
             print(f"# engine decode: {decode_steps} greedy steps at positions {PROMPT}..{PROMPT + decode_steps - 1}, "
                   f"{sec * 1e3:.3f} ms/token, {1.0 / sec:.1f} tok/s", file=sys.stderr, flush=True)
+            # the same prompt in the reference's default batches for Q8_0 (256 rows, src/engine.c:98): a second load
+            # with LLAMA_PREFILL_BATCH=256, the prompt in 8 calls, the last row's logits from the last
+            stage = "prefill in batches of 256"
+            L.engine_free(ctypes.byref(model))
+            saved = os.environ.get("LLAMA_PREFILL_BATCH")
+            os.environ["LLAMA_PREFILL_BATCH"] = str(BATCH_DEFAULT)
+            try:
+                L.engine_load(ctypes.byref(model), path.encode())
+            finally:
+                if saved is None:
+                    os.environ.pop("LLAMA_PREFILL_BATCH")
+                else:
+                    os.environ["LLAMA_PREFILL_BATCH"] = saved
+            assert model.implementation and L.engine_max_batch(ctypes.byref(model)) == BATCH_DEFAULT, lh.last_error()
+
+            def batched():
+                out = None
+                for c in range(0, PROMPT, BATCH_DEFAULT):
+                    want = lh.LOGITS_LAST if c + BATCH_DEFAULT >= PROMPT else lh.LOGITS_NONE
+                    out = L.engine_forward_batch(ctypes.byref(model), prompt[c:].ctypes.data_as(ctypes.c_void_p),
+                                                 BATCH_DEFAULT, c, want)
+                assert out, lh.last_error()
+                return out
+            batched()  # warm-up
+            t0 = time.perf_counter()
+            for _ in range(prompts):
+                out = batched()
+            bsec = (time.perf_counter() - t0) / prompts
+            assert np.isfinite(np.ctypeslib.as_array(out, shape=(VOCAB,))).all()
+            print(f"# engine prefill in batches of {BATCH_DEFAULT}: {bsec * 1e3:.2f} ms, {PROMPT / bsec:.0f} tok/s",
+                  file=sys.stderr, flush=True)
         except Exception as e:
             raise RuntimeError(f"engine {stage}: {e}") from e
         finally:
@@ -833,6 +865,10 @@ def engine_bench(lh, L, args, prompts=None):
             "prefill": {"value": round(PROMPT / psec, 1), "unit": "tok/s", "ms_per_prompt": round(psec * 1e3, 3),
                         "workload": f"engine_forward_batch of a {PROMPT}-token prompt of random ids from position 0, "
                                     f"the last row's logits"},
+            "prefill_batches": {"value": round(PROMPT / bsec, 1), "unit": "tok/s", "ms_per_prompt": round(bsec * 1e3, 3),
+                                "workload": f"the same prompt in the reference's default Q8_0 batches of "
+                                            f"{BATCH_DEFAULT} rows (LLAMA_PREFILL_BATCH={BATCH_DEFAULT}, "
+                                            f"{PROMPT // BATCH_DEFAULT} calls), the last row's logits"},
             "prefill_all_logits": {"value": round(PROMPT / asec, 1), "unit": "tok/s",
                                    "ms_per_prompt": round(asec * 1e3, 3),
                                    "workload": f"the same prompt with every row's logits ({PROMPT} x {VOCAB} FP32, "
@@ -1011,7 +1047,8 @@ def main():
             eng = engine_bench(lh, L, args, prompts=2)
             result["engine"] = {"decode": {"value": eng["value"], "unit": "tok/s", "ms_per_token": eng["ms_per_step"],
                                            "workload": eng["config"]["workload"]},
-                                "prefill": eng["prefill"], "prefill_all_logits": eng["prefill_all_logits"]}
+                                "prefill": eng["prefill"], "prefill_all_logits": eng["prefill_all_logits"],
+                                "prefill_batches": eng["prefill_batches"]}
         except Exception as err:  # noqa: BLE001 - the main metric must still print
             result["engine"] = {"error": f"{type(err).__name__}: {err}"}
         finally:
