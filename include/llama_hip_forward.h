@@ -99,9 +99,11 @@ void k_attention_batch_layout(float *out, const float *q, const float *key_cache
  * than 16 rows, or a head_dim other than 64 and 128, or unaligned operands) must fit: m rows of n_heads heads up to
  * position pos0 + m - 1 take m * n_heads * ((pos0 + m - 1) / 64 + 1) * ((head_dim + 5) & ~3) floats, at most 4 Mi
  * (decode with 32 heads of 128 reaches position 63487); batches the flash kernel takes (16 rows and more, head_dim
- * 64 or 128, 16-byte aligned operands) keep no partials and have no such limit. Anything else fails with a message.
- * The results equal
- * k_attention_batch_layout's bit for bit. Every call on a device shares its array, which keeps the last call's
+ * 64 or 128, 16-byte aligned operands) have no such limit: they keep partials only when a short batch late in a
+ * sequence splits its positions over blocks, and then split only as far as the array holds. Anything else fails with
+ * a message. The results equal k_attention_batch_layout's bit for bit, except for a flash batch whose position split
+ * had to be narrower to fit the array (then they differ in FP32 summation order only). Every call on a device shares
+ * its array, which keeps the last call's
  * contents (every slot a call reads it writes first); calls ordered on the library's stream are safe, two that may
  * run concurrently on one GPU (graphs replayed on other streams) race. */
 void k_attention_batch_layout_noalloc(float *out, const float *q, const float *key_cache, const float *value_cache,

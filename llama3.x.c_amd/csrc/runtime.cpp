@@ -234,7 +234,6 @@ void *lookup(const void *p, size_t *room = nullptr, uintptr_t *start = nullptr, 
   return (char *)it->second.device + (addr - it->first);
 }
 
-
 // 1: device memory with at least `bytes` from p to the end of its allocation; -1: device memory that is shorter
 // (the launch would read or write past it); 0: not device memory.
 int device_extent(const void *p, size_t bytes) {

@@ -1,9 +1,9 @@
 """k_attention_batch_layout_noalloc, the attention entry point that allocates nothing (its split-K partials live in a
 fixed per-device array): equal bit for bit to k_attention_batch_layout on calls in a row, each smaller than the one
-before (a 16-row batch on the flash kernel, which keeps no partials, then 8 rows and one decode row, whose split
-kernels write and read the array); no HBM claimed by the calls; replayable from a HIP graph captured around it; a
-2048-row batch, which needs no partials, accepted; host buffers, a split call too large for the array and an
-uninitialized library refused with a message."""
+before (a 16-row batch at position 1000 on the flash kernel, its positions split over 16 blocks per tile, then 8 rows
+and one decode row on the split kernels, each writing and reading the array); no HBM claimed by the calls; replayable
+from a HIP graph captured around it; a 2048-row batch, which needs no partials, accepted; host buffers, a split call
+too large for the array and an uninitialized library refused with a message."""
 import os
 import subprocess
 import sys
@@ -38,7 +38,8 @@ def test_noalloc_attention_equals_the_workspace_form():
     rng = np.random.default_rng(31)
     k, v, ps, hb = head_major(rng, SEQ)
     kd, vd = hu.dev(k), hu.dev(v)
-    cases = [(1000, 16), (1000, 8), (300, 1)]  # 16 rows (flash), 8 rows (attn_tile + attn_merge), a decode row
+    # 16 rows (attn_flash split + attn_merge_shares), 8 rows (attn_tile + attn_merge), a decode row
+    cases = [(1000, 16), (1000, 8), (300, 1)]
     for pos0, m in cases:
         assert m * NH * ((pos0 + m - 1) // 64 + 1) * 132 <= SCRATCH_FLOATS
     outs = []
