@@ -910,8 +910,9 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
     __syncthreads(); // the next tile's first loads reuse K0, K1 and V0
     if (!active)
       continue;
-    if (split) { // the share's value sums, maximum (in natural units, as the merge takes it) and sum, unnormalized
-      float *slot = p.partial + (((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * p.chunks + blockIdx.z) * p.slot;
+    if (split) { // the share's value sums, maximum (in natural units, as the merge takes it) and sum, unnormalized;
+      // slots [row][head][share]: rows x n_heads x splits x slot floats in all, the room flash_splits checked
+      float *slot = p.partial + (((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * p.splits + blockIdx.z) * p.slot;
 #pragma unroll
       for (int e = 0; e < 4; e++)
 #pragma unroll
@@ -1142,7 +1143,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_shares(AttnParams p) {
     return;
   const int d4 = (int)(idx % q4);
   const long long rh = idx / q4; // row * n_heads + head
-  const float *part = p.partial + (size_t)rh * p.chunks * p.slot;
+  const float *part = p.partial + (size_t)rh * p.splits * p.slot; // the slots of row * n_heads + head
   const int hd = p.head_dim;
   float m = -FLT_MAX;
   for (int s = 0; s < p.splits; s++)

@@ -96,6 +96,39 @@ def test_noalloc_attention_replays_from_a_graph():
         L.llhip_graph_destroy(graph)
 
 
+def test_noalloc_flash_split_narrowed_to_the_array():
+    """256 rows at position 1792 (8B heads): the workspace form splits each tile's positions over 4 blocks, whose
+    partials (256 x 32 x 4 x 132 floats) would overflow the 4 Mi array, so the allocation-free form splits them over 3;
+    the two agree to FP32 summation order, and both to the float64 attention of sampled rows."""
+    L = hu.lib()
+    T = hu.torch()
+    assert L.llhip_init() == 0, lh.last_error()
+    rng = np.random.default_rng(33)
+    seq, pos0, m = 2048, 1792, 256
+    assert m * NH * 4 * 132 > SCRATCH_FLOATS >= m * NH * 3 * 132
+    k, v, ps, hb = head_major(rng, seq)
+    kd, vd = hu.dev(k), hu.dev(v)
+    qh = rng.standard_normal((m, NH * HD), dtype=np.float32)
+    q = hu.dev(qh)
+    got, want = hu.empty((m, NH * HD), T.float32), hu.empty((m, NH * HD), T.float32)
+    claimed = L.llhip_hbm_claimed()
+    run(L, "k_attention_batch_layout_noalloc", got, q, kd, vd, pos0, m, ps, hb, seq=seq)
+    L.llhip_synchronize()
+    assert not lh.last_error() and L.llhip_hbm_claimed() == claimed
+    run(L, "k_attention_batch_layout", want, q, kd, vd, pos0, m, ps, hb, seq=seq)
+    g, w = hu.host(got), hu.host(want)
+    assert np.all(np.abs(g - w) <= 1e-5 * np.abs(w).max() + 1e-6)
+    kv_mul = NH // NKV
+    for r in (0, 101, m - 1):  # the float64 attention of row r: query head h reads KV head h // kv_mul
+        for h in (0, 13, NH - 1):
+            kk = k[h // kv_mul, :pos0 + r + 1].astype(np.float64)
+            vv = v[h // kv_mul, :pos0 + r + 1].astype(np.float64)
+            s = kk @ qh[r, h * HD:(h + 1) * HD].astype(np.float64) / np.sqrt(HD)
+            p = np.exp(s - s.max())
+            ref = (p / p.sum()) @ vv
+            assert np.all(np.abs(g[r, h * HD:(h + 1) * HD] - ref) <= 1e-5 * np.abs(vv).max() + 1e-6), (r, h)
+
+
 def test_noalloc_attention_refusals():
     L = hu.lib()
     T = hu.torch()
