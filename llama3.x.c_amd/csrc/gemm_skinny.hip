@@ -61,7 +61,10 @@ __device__ __forceinline__ float sk_silu_gate(float value, float gate) {
 
 constexpr int kStream = 2; // cache policy nt for the weights, read once
 
-template <int MT, int NT, int WAVES> __global__ __launch_bounds__(64 * WAVES) void q8_gemm_skinny(SkParams p) {
+// G64: gs = 64, so every K step is a whole group, rescaled as soon as its MFMAs are done (no int32 sums carried
+// from step to step, no group index to divide out).
+template <int MT, int NT, int WAVES, bool G64>
+__global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
   constexpr int RB = 16 * NT; // weight rows of the block: NT MFMA tiles of 16 sharing each activation load
   extern __shared__ __align__(16) float sk_smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -75,16 +78,17 @@ template <int MT, int NT, int WAVES> __global__ __launch_bounds__(64 * WAVES) vo
   const int col0 = (tile - seg.first_tile) * RB;
   const int G = p.groups, spg = p.gs / 64;
 
-  // scales of the block's RB weight rows (and their W3 rows) and of the activation rows, all groups
+  // scales of the block's RB weight rows (and their W3 rows) and of the activation rows, all groups, group-major
+  // (group g's at g * RB + r and g * 16 MT + r), so a lane reads the four activation rows of its elements at once
   float *sws = sk_smem, *sw3s = sws + RB * G, *sxs = sw3s + RB * G;
   for (int i = tid; i < RB * G; i += 64 * WAVES) {
     const int r = i / G, g = i % G, col = col0 + r;
-    sws[i] = col < seg.n ? seg.ws[(long long)col * G + g] : 0.0f;
-    sw3s[i] = swiglu && col < seg.n ? seg.w3s[(long long)col * G + g] : 0.0f;
+    sws[g * RB + r] = col < seg.n ? seg.ws[(long long)col * G + g] : 0.0f;
+    sw3s[g * RB + r] = swiglu && col < seg.n ? seg.w3s[(long long)col * G + g] : 0.0f;
   }
   for (int i = tid; i < 16 * MT * G; i += 64 * WAVES) {
     const int r = i / G, g = i % G;
-    sxs[i] = r < p.m ? p.xs[(long long)r * G + g] : 0.0f;
+    sxs[g * 16 * MT + r] = r < p.m ? p.xs[(long long)r * G + g] : 0.0f;
   }
 
   // this wave's K steps [s0, s1); steps past s1 load zeros
@@ -154,6 +158,51 @@ template <int MT, int NT, int WAVES> __global__ __launch_bounds__(64 * WAVES) vo
     return r;
   };
   const int lr = (lane >> 4) * 4, lc = lane & 15;
+  // group g's scales of this lane's elements: activation rows 16 t + lr + e (one 16-byte read per tile), weight rows
+  // 16 j + lc
+  auto xscales = [&](int g, int t) { return *reinterpret_cast<const v4f *>(sxs + g * 16 * MT + 16 * t + lr); };
+  if constexpr (G64) {
+    // whole rounds of kSkPairs pairs (the ring's slots are constants); steps past s1 multiply zero activations, and
+    // their (any) group's scales leave the sums as they are
+    for (int step = s0; step < s1; step += 2 * kSkPairs) {
+#pragma unroll
+      for (int d = 0; d < kSkPairs; d++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int g = min(step + 2 * d + h, G - 1);
+          v4f xsc[MT];
+#pragma unroll
+          for (int t = 0; t < MT; t++)
+            xsc[t] = xscales(g, t);
+#pragma unroll
+          for (int j = 0; j < NT; j++) {
+            const v4i b = operand(x[d][j], y[d][j], h);
+            const float wsc = sws[g * RB + 16 * j + lc];
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+              const v4i dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int e = 0; e < 4; e++)
+                acc[t][j][e] = fmaf((float)dd[e] * wsc, xsc[t][e], acc[t][j][e]);
+            }
+            if (swiglu) {
+              const v4i b3 = operand(x3[d][j], y3[d][j], h);
+              const float w3sc = sw3s[g * RB + 16 * j + lc];
+#pragma unroll
+              for (int t = 0; t < MT; t++) {
+                const v4i dd3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b3, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                  acc3[t][j][e] = fmaf((float)dd3[e] * w3sc, xsc[t][e], acc3[t][j][e]);
+              }
+            }
+          }
+          if (h == 1)
+            issue(step + 2 * d + 2 * kSkPairs, d);
+        }
+      }
+    }
+  } else
   // whole rounds of kSkPairs pairs (the ring's slots are constants); steps past s1 multiply zero activations
   for (int step = s0; step < s1; step += 2 * kSkPairs) {
 #pragma unroll
@@ -183,16 +232,17 @@ template <int MT, int NT, int WAVES> __global__ __launch_bounds__(64 * WAVES) vo
           const int g = min(st / spg, G - 1); // past the end the dots are zero; any group's scales will do
 #pragma unroll
           for (int j = 0; j < NT; j++) {
-            const float wsc = sws[(16 * j + lc) * G + g], w3sc = sw3s[(16 * j + lc) * G + g];
+            const float wsc = sws[g * RB + 16 * j + lc], w3sc = sw3s[g * RB + 16 * j + lc];
 #pragma unroll
-            for (int t = 0; t < MT; t++)
+            for (int t = 0; t < MT; t++) {
+              const v4f xsc = xscales(g, t);
 #pragma unroll
               for (int e = 0; e < 4; e++) {
-                const float xsc = sxs[(16 * t + lr + e) * G + g];
-                acc[t][j][e] = fmaf((float)dot[t][j][e] * wsc, xsc, acc[t][j][e]);
+                acc[t][j][e] = fmaf((float)dot[t][j][e] * wsc, xsc[e], acc[t][j][e]);
                 if (swiglu)
-                  acc3[t][j][e] = fmaf((float)dot3[t][j][e] * w3sc, xsc, acc3[t][j][e]);
+                  acc3[t][j][e] = fmaf((float)dot3[t][j][e] * w3sc, xsc[e], acc3[t][j][e]);
               }
+            }
           }
         }
       }
@@ -241,15 +291,20 @@ size_t skinny_lds(int mt, int nt, int waves, int groups) {
   return ((size_t)(32 * nt + 16 * mt) * groups + 2 * (size_t)waves * mt * nt * 4 * 64) * sizeof(float);
 }
 
-template <int MT, int NT, int WAVES> bool skinny_launch(const SkParams &p, int tiles, hipStream_t stream) {
-  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<MT, NT, WAVES>,
+template <int MT, int NT, int WAVES, bool G64> bool skinny_launch_gs(const SkParams &p, int tiles, hipStream_t stream) {
+  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<MT, NT, WAVES, G64>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
     return false;
-  hipLaunchKernelGGL((q8_gemm_skinny<MT, NT, WAVES>), dim3((unsigned)tiles), dim3(64 * WAVES),
+  hipLaunchKernelGGL((q8_gemm_skinny<MT, NT, WAVES, G64>), dim3((unsigned)tiles), dim3(64 * WAVES),
                      skinny_lds(MT, NT, WAVES, p.groups), stream, p);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess || raise("launching q8_gemm_skinny failed: %s", hipGetErrorString(e));
+}
+
+template <int MT, int NT, int WAVES> bool skinny_launch(const SkParams &p, int tiles, hipStream_t stream) {
+  return p.gs == 64 ? skinny_launch_gs<MT, NT, WAVES, true>(p, tiles, stream)
+                    : skinny_launch_gs<MT, NT, WAVES, false>(p, tiles, stream);
 }
 
 } // namespace
