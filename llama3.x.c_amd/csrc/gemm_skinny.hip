@@ -62,8 +62,10 @@ __device__ __forceinline__ float sk_silu_gate(float value, float gate) {
 constexpr int kStream = 2; // cache policy nt for the weights, read once
 
 // G64: gs = 64, so every K step is a whole group, rescaled as soon as its MFMAs are done (no int32 sums carried
-// from step to step, no group index to divide out).
-template <int MT, int NT, int WAVES, bool G64>
+// from step to step, no group index to divide out). SW: some segment is SWIGLU; without it the kernel holds no W3
+// registers at all, and with it every block loads its W3 operand registers unconditionally (from an empty buffer when
+// its own segment has no W3: zeros, no memory traffic), so no load is left pending on a conditionally kept register.
+template <int MT, int NT, int WAVES, bool G64, bool SW>
 __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
   constexpr int RB = 16 * NT; // weight rows of the block: NT MFMA tiles of 16 sharing each activation load
   extern __shared__ __align__(16) float sk_smem[];
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
   while (s + 1 < p.nseg && tile >= p.seg[s + 1].first_tile)
     s++;
   const SkSeg seg = sk_pick(p, s);
-  const bool swiglu = seg.epi == EPI_SWIGLU;
+  const bool swiglu = SW && seg.epi == EPI_SWIGLU;
   const int col0 = (tile - seg.first_tile) * RB;
   const int G = p.groups, spg = p.gs / 64;
 
@@ -120,7 +122,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
     for (int j = 0; j < NT; j++) {
       x[d][j] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB[j] : none, offX, k0, kStream);
       y[d][j] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB[j] : none, offY, k0, kStream);
-      if (swiglu) {
+      if constexpr (SW) {
         x3[d][j] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3[j] : none, offX, k0, kStream);
         y3[d][j] = __builtin_amdgcn_raw_buffer_load_b128(live ? rB3[j] : none, offY, k0, kStream);
       }
@@ -197,8 +199,11 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
               }
             }
           }
-          if (h == 1)
+          if (h == 1) { // the pair's registers are free: its next loads go out here, not after the round's MFMAs
+            __builtin_amdgcn_sched_barrier(0);
             issue(step + 2 * d + 2 * kSkPairs, d);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
     }
@@ -291,20 +296,27 @@ size_t skinny_lds(int mt, int nt, int waves, int groups) {
   return ((size_t)(32 * nt + 16 * mt) * groups + 2 * (size_t)waves * mt * nt * 4 * 64) * sizeof(float);
 }
 
-template <int MT, int NT, int WAVES, bool G64> bool skinny_launch_gs(const SkParams &p, int tiles, hipStream_t stream) {
-  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<MT, NT, WAVES, G64>,
+template <int MT, int NT, int WAVES, bool G64, bool SW>
+bool skinny_launch_gs(const SkParams &p, int tiles, hipStream_t stream) {
+  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_skinny<MT, NT, WAVES, G64, SW>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
     return false;
-  hipLaunchKernelGGL((q8_gemm_skinny<MT, NT, WAVES, G64>), dim3((unsigned)tiles), dim3(64 * WAVES),
+  hipLaunchKernelGGL((q8_gemm_skinny<MT, NT, WAVES, G64, SW>), dim3((unsigned)tiles), dim3(64 * WAVES),
                      skinny_lds(MT, NT, WAVES, p.groups), stream, p);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess || raise("launching q8_gemm_skinny failed: %s", hipGetErrorString(e));
 }
 
 template <int MT, int NT, int WAVES> bool skinny_launch(const SkParams &p, int tiles, hipStream_t stream) {
-  return p.gs == 64 ? skinny_launch_gs<MT, NT, WAVES, true>(p, tiles, stream)
-                    : skinny_launch_gs<MT, NT, WAVES, false>(p, tiles, stream);
+  bool sw = false;
+  for (int s = 0; s < p.nseg; s++)
+    sw = sw || p.seg[s].epi == EPI_SWIGLU;
+  if (sw)
+    return p.gs == 64 ? skinny_launch_gs<MT, NT, WAVES, true, true>(p, tiles, stream)
+                      : skinny_launch_gs<MT, NT, WAVES, false, true>(p, tiles, stream);
+  return p.gs == 64 ? skinny_launch_gs<MT, NT, WAVES, true, false>(p, tiles, stream)
+                    : skinny_launch_gs<MT, NT, WAVES, false, false>(p, tiles, stream);
 }
 
 } // namespace
