@@ -61,6 +61,14 @@ __device__ __forceinline__ float sk_silu_gate(float value, float gate) {
 
 constexpr int kStream = 2; // cache policy nt for the weights, read once
 
+// s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int N> __device__ __forceinline__ void sk_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+__host__ __device__ constexpr int sk_pad64(int n) { return (n + 63) / 64 * 64; }
+
 // G64: gs = 64, so every K step is a whole group, rescaled as soon as its MFMAs are done (no int32 sums carried
 // from step to step, no group index to divide out). SW: some segment is SWIGLU; without it the kernel holds no W3
 // registers at all, and with it every block loads its W3 operand registers unconditionally (from an empty buffer when
@@ -80,17 +88,34 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
   const int col0 = (tile - seg.first_tile) * RB;
   const int G = p.groups, spg = p.gs / 64;
 
-  // scales of the block's RB weight rows (and their W3 rows) and of the activation rows, all groups, group-major
-  // (group g's at g * RB + r and g * 16 MT + r), so a lane reads the four activation rows of its elements at once
-  float *sws = sk_smem, *sw3s = sws + RB * G, *sxs = sw3s + RB * G;
-  for (int i = tid; i < RB * G; i += 64 * WAVES) {
-    const int r = i / G, g = i % G, col = col0 + r;
-    sws[g * RB + r] = col < seg.n ? seg.ws[(long long)col * G + g] : 0.0f;
-    sw3s[g * RB + r] = swiglu && col < seg.n ? seg.w3s[(long long)col * G + g] : 0.0f;
-  }
-  for (int i = tid; i < 16 * MT * G; i += 64 * WAVES) {
-    const int r = i / G, g = i % G;
-    sxs[g * 16 * MT + r] = r < p.m ? p.xs[(long long)r * G + g] : 0.0f;
+  // Scales of the block's RB weight rows (and their W3 rows) and of the activation rows, all groups, group-major
+  // (group g's at g * RB + r and g * 16 MT + r), so a lane reads the four activation rows of its elements at once.
+  // They go global -> LDS by DMA, one scale per lane and 64 per load (each region padded to whole loads; a padding
+  // lane reads past its buffer: zero), before the first weight loads and without waiting on either: a register copy
+  // waits for each load in turn, a dozen memory latencies before the block's first weight load.
+  const int nw = sk_pad64(RB * G), nx = sk_pad64(16 * MT * G);
+  float *sws = sk_smem, *sw3s = sws + nw, *sxs = sw3s + (SW ? nw : 0);
+  {
+    constexpr unsigned kPast = 1u << 30; // past any scale buffer here (at most 2^23 bytes on this path)
+    const long long wrows = (long long)min(RB, seg.n - col0);
+    const __amdgpu_buffer_rsrc_t rws = sk_buffer(seg.ws + (long long)col0 * G, wrows * G * 4);
+    const __amdgpu_buffer_rsrc_t rw3s = sk_buffer(swiglu ? seg.w3s + (long long)col0 * G : seg.ws, swiglu ? wrows * G * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rxs = sk_buffer(p.xs, (long long)p.m * G * 4);
+    for (int base = 64 * wave; base < nw; base += 64 * WAVES) { // entry base + lane: group g, weight row r
+      const int i = base + lane, g = i / RB, r = i % RB;
+      const unsigned off = i < RB * G ? (unsigned)(r * G + g) * 4u : kPast;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rws, (__attribute__((address_space(3))) void *)(sws + base), 4, off, 0,
+                                               0, 0);
+      if constexpr (SW)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw3s, (__attribute__((address_space(3))) void *)(sw3s + base), 4,
+                                                 off, 0, 0, 0);
+    }
+    for (int base = 64 * wave; base < nx; base += 64 * WAVES) { // activation row r >= m: past the buffer, zero
+      const int i = base + lane, g = i / (16 * MT), r = i % (16 * MT);
+      const unsigned off = i < 16 * MT * G ? (unsigned)(r * G + g) * 4u : kPast;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rxs, (__attribute__((address_space(3))) void *)(sxs + base), 4, off, 0,
+                                               0, 0);
+    }
   }
 
   // this wave's K steps [s0, s1); steps past s1 load zeros
@@ -137,6 +162,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
 #pragma unroll
   for (int d = 0; d < kSkPairs; d++)
     issue(s0 + 2 * d, d);
+  // this wave's scale loads are older than its operand loads: wait for them alone, then for every wave's
+  constexpr int kPairLoads = 2 * NT * (SW ? 2 : 1) + 2 * MT;
+  sk_wait_vmcnt<kSkPairs * kPairLoads>();
   __syncthreads(); // the scales are staged
 
   v4f acc[MT][NT], acc3[MT][NT];
@@ -254,10 +282,11 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
     }
   }
 
-  // the waves' partial sums, added in wave order
+  // the waves' partial sums, added in wave order, in the scales' place once every wave is past its last step
   constexpr int kParts = MT * NT * 4; // (activation tile, weight tile, element) of each lane
-  float *red = sxs + 16 * MT * G;     // [wave][part][lane], then the same for W3
+  float *red = sk_smem;               // [wave][part][lane], then the same for W3
   const int red3 = WAVES * kParts * 64;
+  __syncthreads();
 #pragma unroll
   for (int t = 0; t < MT; t++)
 #pragma unroll
@@ -292,8 +321,12 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
   }
 }
 
-size_t skinny_lds(int mt, int nt, int waves, int groups) {
-  return ((size_t)(32 * nt + 16 * mt) * groups + 2 * (size_t)waves * mt * nt * 4 * 64) * sizeof(float);
+// LDS bytes: the staged scales (W3's only with a SWIGLU segment), or the waves' partial sums where they go after the
+// loop, whichever is more
+size_t skinny_lds(int mt, int nt, int waves, int groups, bool sw) {
+  const size_t scales = (size_t)sk_pad64(16 * nt * groups) * (sw ? 2 : 1) + sk_pad64(16 * mt * groups);
+  const size_t sums = (size_t)waves * mt * nt * 4 * 64 * (sw ? 2 : 1);
+  return (scales > sums ? scales : sums) * sizeof(float);
 }
 
 template <int MT, int NT, int WAVES, bool G64, bool SW>
@@ -303,7 +336,7 @@ bool skinny_launch_gs(const SkParams &p, int tiles, hipStream_t stream) {
   if (!check_hip(status, "allowing the skinny Q8 GEMM its LDS"))
     return false;
   hipLaunchKernelGGL((q8_gemm_skinny<MT, NT, WAVES, G64, SW>), dim3((unsigned)tiles), dim3(64 * WAVES),
-                     skinny_lds(MT, NT, WAVES, p.groups), stream, p);
+                     skinny_lds(MT, NT, WAVES, p.groups, SW), stream, p);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess || raise("launching q8_gemm_skinny failed: %s", hipGetErrorString(e));
 }
@@ -324,7 +357,7 @@ template <int MT, int NT, int WAVES> bool skinny_launch(const SkParams &p, int t
 // Shapes the skinny kernel takes: at most 32 rows, gs a multiple of 64, 16-byte aligned rows, scales that fit LDS.
 bool q8_gemm_skinny_path(const int8_t *xq, int m, int k, int gs) {
   return m > 0 && m <= 32 && gs > 0 && gs % 64 == 0 && k % gs == 0 && ((uintptr_t)xq & 15) == 0 &&
-         32LL * k < (1LL << 31) && skinny_lds(m > 16 ? 2 : 1, 1, 8, k / gs) <= 160 * 1024;
+         32LL * k < (1LL << 31) && skinny_lds(m > 16 ? 2 : 1, 1, 8, k / gs, true) <= 160 * 1024;
 }
 
 bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream) {
@@ -335,7 +368,7 @@ bool launch_q8_gemm_skinny(const GemmQ8Job &job, hipStream_t stream) {
   // Two weight tiles per block halve the activation loads. That pays once the activations are 32 rows and the grid
   // keeps at least 192 blocks (8B, m = 32: QKV 21.1 -> 16.6 us, W1/W3 43.9 -> 36.7 us); on the 256-tile W2 and Wo it
   // leaves half the CUs idle (W2 16.4 -> 29.0 us at m = 1).
-  const int nt = mt == 2 && tiles16 >= 384 && skinny_lds(mt, 2, 8, groups) <= 160 * 1024 ? 2 : 1;
+  const int nt = mt == 2 && tiles16 >= 384 && skinny_lds(mt, 2, 8, groups, true) <= 160 * 1024 ? 2 : 1;
   SkParams p{};
   int tiles = 0;
   for (int s = 0; s < job.nseg; s++) {
