@@ -388,31 +388,65 @@ template <int J, int THREADS> __global__ __launch_bounds__(256) void split_reduc
   const TilePos t = q8_tile_of(p.grid, tile, p.tile_m, p.tile_n);
   const TileSeg seg = q8_seg_of(p.grid, t.s);
   const v4f *part = p.partial + (size_t)tile * p.splits * (4 * J * THREADS) + tid;
-  v4f lo = part[(i * J + jp) * THREADS], hi = part[(i * J + jp + J / 2) * THREADS];
-  for (int s = 1; s < p.splits; s++) {
-    lo += part[(size_t)s * (4 * J * THREADS) + (i * J + jp) * THREADS];
-    hi += part[(size_t)s * (4 * J * THREADS) + (i * J + jp + J / 2) * THREADS];
+  // The partials are added in split order; they are loaded kBatch splits at a time, all in flight together (a loop
+  // that adds each as it arrives waits for one load per split). Past the last split a load repeats the last one and
+  // its sum is not taken.
+  constexpr int kBatch = 8;
+  const size_t lo_at = (size_t)(i * J + jp) * THREADS, hi_at = (size_t)(i * J + jp + J / 2) * THREADS;
+  v4f lo{}, hi{};
+  for (int s0 = 0; s0 < p.splits; s0 += kBatch) {
+    v4f l[kBatch], h[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      const size_t at = (size_t)min(s0 + u, p.splits - 1) * (4 * J * THREADS);
+      l[u] = part[at + lo_at];
+      h[u] = part[at + hi_at];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      if (s0 + u == 0) {
+        lo = l[u];
+        hi = h[u];
+      } else if (s0 + u < p.splits) {
+        lo += l[u];
+        hi += h[u];
+      }
+    }
   }
   const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
   const int lc = lane & 15, lr = (lane >> 4) * 4;
   constexpr int kSpan = 16 * J; // columns a wave covers
+  const int rows = min(4, p.m - (t.m0 + wm * 64 + 16 * i + lr)); // this thread's rows below m
+  if (t.swiglu) {
+    const int col = t.n0 + (kSpan / 2) * wn + 16 * jp + lc;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      if (e < rows && col < seg.n)
+        seg.c[(long long)(t.m0 + wm * 64 + 16 * i + lr + e) * seg.ldc + col] = silu_gate(lo[e], hi[e]);
+    return;
+  }
+  const int c0 = t.n0 + kSpan * wn + 16 * jp + lc, c1 = c0 + 16 * (J / 2);
+  const bool in0 = c0 < seg.n, in1 = c1 < seg.n;
+  float *crow0 = seg.c + (long long)(t.m0 + wm * 64 + 16 * i + lr) * seg.ldc;
+  if (seg.epi == EPI_ADD) { // every current value read before any sum is written back
+    float prior0[4], prior1[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      prior0[e] = e < rows && in0 ? crow0[(long long)e * seg.ldc + c0] : 0.0f;
+      prior1[e] = e < rows && in1 ? crow0[(long long)e * seg.ldc + c1] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      lo[e] = prior0[e] + lo[e];
+      hi[e] = prior1[e] + hi[e];
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 4; e++) {
-    const int row = t.m0 + wm * 64 + 16 * i + lr + e;
-    if (row >= p.m)
-      continue;
-    float *crow = seg.c + (long long)row * seg.ldc;
-    if (t.swiglu) {
-      const int col = t.n0 + (kSpan / 2) * wn + 16 * jp + lc;
-      if (col < seg.n)
-        crow[col] = silu_gate(lo[e], hi[e]);
-    } else {
-      const int c0 = t.n0 + kSpan * wn + 16 * jp + lc, c1 = c0 + 16 * (J / 2);
-      if (c0 < seg.n)
-        crow[c0] = seg.epi == EPI_ADD ? crow[c0] + lo[e] : lo[e];
-      if (c1 < seg.n)
-        crow[c1] = seg.epi == EPI_ADD ? crow[c1] + hi[e] : hi[e];
-    }
+    if (e < rows && in0)
+      crow0[(long long)e * seg.ldc + c0] = lo[e];
+    if (e < rows && in1)
+      crow0[(long long)e * seg.ldc + c1] = hi[e];
   }
 }
 
