@@ -88,11 +88,13 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
   const int col0 = (tile - seg.first_tile) * RB;
   const int G = p.groups, spg = p.gs / 64;
 
-  // Scales of the block's RB weight rows (and their W3 rows) and of the activation rows, all groups, group-major
-  // (group g's at g * RB + r and g * 16 MT + r), so a lane reads the four activation rows of its elements at once.
-  // They go global -> LDS by DMA, one scale per lane and 64 per load (each region padded to whole loads; a padding
-  // lane reads past its buffer: zero), before the first weight loads and without waiting on either: a register copy
-  // waits for each load in turn, a dozen memory latencies before the block's first weight load.
+  // Scales of the block's RB weight rows (and their W3 rows), all groups, as they lie in memory (row r's group g at
+  // r * G + g: one contiguous range), and of the activation rows group-major (group g's at g * 16 MT + r), so a lane
+  // reads the four activation rows of its elements at once. They go global -> LDS by DMA, one scale per lane and 64
+  // per load (each region padded to whole loads; a padding lane reads past its buffer: zero), before the first weight
+  // loads and without waiting on either: a register copy waits for each load in turn, a dozen memory latencies
+  // before the block's first weight load. (Weight scales gathered group-major took 16 cache lines per load where the
+  // contiguous copy takes two.)
   const int nw = sk_pad64(RB * G), nx = sk_pad64(16 * MT * G);
   float *sws = sk_smem, *sw3s = sws + nw, *sxs = sw3s + (SW ? nw : 0);
   {
@@ -101,9 +103,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
     const __amdgpu_buffer_rsrc_t rws = sk_buffer(seg.ws + (long long)col0 * G, wrows * G * 4);
     const __amdgpu_buffer_rsrc_t rw3s = sk_buffer(swiglu ? seg.w3s + (long long)col0 * G : seg.ws, swiglu ? wrows * G * 4 : 0);
     const __amdgpu_buffer_rsrc_t rxs = sk_buffer(p.xs, (long long)p.m * G * 4);
-    for (int base = 64 * wave; base < nw; base += 64 * WAVES) { // entry base + lane: group g, weight row r
-      const int i = base + lane, g = i / RB, r = i % RB;
-      const unsigned off = i < RB * G ? (unsigned)(r * G + g) * 4u : kPast;
+    for (int base = 64 * wave; base < nw; base += 64 * WAVES) { // entry base + lane, a straight copy
+      const int i = base + lane;
+      const unsigned off = i < RB * G ? (unsigned)i * 4u : kPast;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rws, (__attribute__((address_space(3))) void *)(sws + base), 4, off, 0,
                                                0, 0);
       if constexpr (SW)
@@ -207,7 +209,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
 #pragma unroll
           for (int j = 0; j < NT; j++) {
             const v4i b = operand(x[d][j], y[d][j], h);
-            const float wsc = sws[g * RB + 16 * j + lc];
+            const float wsc = sws[(16 * j + lc) * G + g];
 #pragma unroll
             for (int t = 0; t < MT; t++) {
               const v4i dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b, v4i{0, 0, 0, 0}, 0, 0, 0);
@@ -217,7 +219,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
             }
             if (swiglu) {
               const v4i b3 = operand(x3[d][j], y3[d][j], h);
-              const float w3sc = sw3s[g * RB + 16 * j + lc];
+              const float w3sc = sw3s[(16 * j + lc) * G + g];
 #pragma unroll
               for (int t = 0; t < MT; t++) {
                 const v4i dd3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d][h][t], b3, v4i{0, 0, 0, 0}, 0, 0, 0);
@@ -265,7 +267,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void q8_gemm_skinny(SkParams p) {
           const int g = min(st / spg, G - 1); // past the end the dots are zero; any group's scales will do
 #pragma unroll
           for (int j = 0; j < NT; j++) {
-            const float wsc = sws[g * RB + 16 * j + lc], w3sc = sw3s[g * RB + 16 * j + lc];
+            const float wsc = sws[(16 * j + lc) * G + g], w3sc = sw3s[(16 * j + lc) * G + g];
 #pragma unroll
             for (int t = 0; t < MT; t++) {
               const v4f xsc = xscales(g, t);
