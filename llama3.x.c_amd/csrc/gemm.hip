@@ -1804,10 +1804,49 @@ bool q8_wide_kernel(const Q8Params &p, bool split, unsigned blocks, hipStream_t 
   return launch_ok("q8_gemm_wide");
 }
 
+// A wide grid of whole rounds of one tile per CU plus a partial last round: the partial round costs a whole round's
+// time (a wide block is bound by its own MFMA and VALU work, not by bandwidth the idle CUs would leave it), so when
+// that round is at most half the CUs and whole column tiles across every row tile, its columns go to the 256 x 128
+// kernel instead, one round of tiles that take 1 / 1.7 of a wide tile's time. One segment without the quantized
+// output only. Returns the first columns' segment in `head` and the rest in `tail`, or false to leave the grid whole.
+bool q8_wide_tail(const Q8Params &p, const GemmSegmentDev &seg, GemmSegmentDev &head, GemmSegmentDev &tail) {
+  if (p.grid.nseg != 1 || seg.cq || p.sk.splits != 1)
+    return false;
+  const int cus = device().cu_count > 0 ? device().cu_count : 256;
+  const int rest = p.grid.total % cus, mtiles = p.grid.mtiles;
+  if (p.grid.total < cus || rest == 0 || 2 * rest > cus || rest % mtiles)
+    return false;
+  const int width = seg.epi == EPI_SWIGLU ? kWTileN / 2 : kWTileN;
+  const int n1 = (p.grid.seg[0].ntiles - rest / mtiles) * width;
+  if (n1 <= 0 || n1 >= seg.n)
+    return false;
+  const long long groups = p.k / p.gs;
+  head = seg;
+  head.n = n1;
+  tail = seg;
+  tail.n = seg.n - n1;
+  tail.c = seg.c + n1;
+  tail.w = (const int8_t *)seg.w + (long long)n1 * p.k;
+  tail.ws = seg.ws + n1 * groups;
+  if (seg.epi == EPI_SWIGLU) {
+    tail.w3 = (const int8_t *)seg.w3 + (long long)n1 * p.k;
+    tail.w3s = seg.w3s + n1 * groups;
+  }
+  return true;
+}
+
 bool q8_wide_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
   q8_wide_grid(p, segs);
   if (p.grid.total <= 0)
     return true;
+  GemmSegmentDev head, tail;
+  if (q8_wide_tail(p, segs.seg[0], head, tail)) {
+    q8_wide_grid(p, SegList{&head, 1});
+    if (!q8_wide_kernel(p, false, (unsigned)p.grid.total, stream))
+      return false;
+    const SegList rest{&tail, 1};
+    return q8_tile_m() == 256 ? q8_launch<Q8Wide, false, true>(p, rest, stream) : q8_launch<Q8Pair, false, true>(p, rest, stream);
+  }
   if (p.sk.splits == 1)
     return q8_wide_kernel(p, false, (unsigned)p.grid.total, stream);
   if (!q8_wide_kernel(p, true, (unsigned)(p.grid.total * p.sk.splits), stream))

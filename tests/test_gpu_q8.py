@@ -589,6 +589,54 @@ def test_gemm_q8_wide_tiles(m, n, k, scales):
         L.llhip_set_q8_scales(0)
 
 
+@pytest.mark.parametrize("m,n,k,kind", [(512, 20480, 128, lh.GEMM_SWIGLU), (512, 40960, 128, lh.GEMM_STORE),
+                                        (300, 40960, 192, lh.GEMM_ADD), (512, 20416, 128, lh.GEMM_SWIGLU)])
+def test_gemm_q8_wide_grid_tail_on_narrow_tiles(m, n, k, kind):
+    """A wide grid whose last round would hold at most half the CUs, in whole column tiles across every row tile (here
+    2 x 160 = 320 wide tiles on 256 CUs): its last columns go to the 256 x 128 kernel. Every kind within the budget,
+    those columns bit for bit the 256 x 128 kernel's over the whole matrix, and the rest within twice the budget of it.
+    n = 20416 leaves the last wide tile partly past n (a narrower tail)."""
+    L = hu.lib()
+    gs = 64
+    xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 5150 + m + n)
+    ref, mag = hu.dequant_reference(xq, xs, wq, ws, gs)
+    r3, mag3 = hu.dequant_reference(xq, xs, w3q, w3s, gs)
+    base = rng.uniform(m * n, 3.0).reshape(m, n)
+    dx = [hu.dev(a) for a in (xq, xs, wq, ws, w3q, w3s)]
+
+    def run(tile):
+        L.llhip_set_q8_tile(tile)
+        c = hu.dev(base)
+        seg = lh.GemmQ8Segment(lh.ptr(c), n, lh.w8(dx[2], dx[3]), lh.w8(dx[4], dx[5]), None, None, n, kind)
+        L.k_gemm_q8(lh.ptr(dx[0]), lh.ptr(dx[1]), m, k, gs, seg, 1)
+        got = hu.host(c)
+        assert lh.last_error() == "", lh.last_error()
+        return got
+
+    try:
+        got, narrow = run(2), run(1)
+        what = f"wide grid with a narrow tail {m}x{n}x{k} kind {kind}"
+        width, cus = (128 if kind == lh.GEMM_SWIGLU else 256), L.llhip_device_cu_count()
+        tiles = -(-n // width)  # per row tile; two row tiles
+        assert 2 * tiles > cus and (2 * tiles) % cus % 2 == 0 and 2 * ((2 * tiles) % cus) <= cus, "not a tail case"
+        n1 = (tiles - (2 * tiles) % cus // 2) * width  # wide columns: the whole rounds' tiles
+        assert 0 < n1 < n
+        assert np.array_equal(hu.bits(got[:, n1:]), hu.bits(narrow[:, n1:])), what + ": tail columns"
+        if kind == lh.GEMM_ADD:
+            hu.assert_within_budget(got, base + ref, mag + np.abs(base), what=what)
+            hu.assert_within_budget(got, narrow, 2 * (mag + np.abs(base)), what=what + " vs 256 x 128")
+        elif kind == lh.GEMM_SWIGLU:
+            want = ref / (1 + np.exp(-ref)) * r3
+            tol = 2e-5 * (mag * (np.abs(r3) + 1) + mag3 * (np.abs(ref) + 1)) + 1e-6
+            assert np.all(np.abs(got - want) <= tol), what
+            assert np.all(np.abs(got - narrow) <= 2 * tol), what + " vs 256 x 128"
+        else:
+            hu.assert_within_budget(got, ref, mag, what=what)
+            hu.assert_within_budget(got, narrow, 2 * mag, what=what + " vs 256 x 128")
+    finally:
+        L.llhip_set_q8_tile(0)
+
+
 @pytest.mark.parametrize("m,n,k", [(300, 256, 1024), (513, 640, 320), (257, 128, 4096), (1024, 384, 2048)])
 def test_gemm_q8_swiglu_quantized(m, n, k):
     """llhip_gemm_q8_swiglu_quantize: hb quantized in the wide int8 kernel's epilogue, bitwise k_gemm_q8 GEMM_SWIGLU then
