@@ -1022,7 +1022,7 @@ def main():
                         "(QKV, Wo +resid, W1/W3 SwiGLU, W2 +resid) + last-row classifier GEMV, gs 64",
             "ops_per_prompt": ops, "tops": round(ops / (psec / args.prefill_steps) / 1e12, 1),
             "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                         "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": measured_traffic("q8_gemm_wide_smma_swiglu"),
+                         "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": measured_traffic("q8_gemm_w13_2048"),
                          "kernel": "k_gemm_q8 W1/W3 SwiGLU 2048x(2x14336)x4096: q8_gemm_wide_smma over the first "
                                    "12288 columns (768 tiles, three rounds) + q8_gemm_lds over the last 2048",
                          "avg_launch_us": round(pavg * 1e6, 1)},
