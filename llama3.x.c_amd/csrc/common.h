@@ -25,6 +25,7 @@ struct Device {
   hipStream_t stream = nullptr;
   int *error_flags = nullptr; // device: [0] non-finite activation seen by a quantizer, [1] non-finite attention score,
                               // [2] an embedding row id outside the table
+  int *host_flags = nullptr;  // pinned host copy of the 16 flag words, read back with the synchronization
   int cu_count = 0;
   bool capturing = false;
   void *split_partial = nullptr;  // split-K partial tiles: LLHIP_SPLIT_SLOTS x 256 x 128 floats

@@ -140,8 +140,8 @@ bool ensure_device() {
   if (!hbm_claim((size_t)LLHIP_SPLIT_SLOTS * (256 * 128 * sizeof(float) + sizeof(unsigned)) + 64,
                  "the split-K workspace"))
     return false;
-  int *flags;
-  if (!LLHIP_CHECK(hipMalloc(&flags, 64)))
+  int *flags, *host_flags;
+  if (!LLHIP_CHECK(hipMalloc(&flags, 64)) || !LLHIP_CHECK(hipHostMalloc((void **)&host_flags, 64, hipHostMallocDefault)))
     return false;
   int zero[16] = {0};
   if (!LLHIP_CHECK(hipMemcpy(flags, zero, sizeof(zero), hipMemcpyHostToDevice)))
@@ -159,6 +159,7 @@ bool ensure_device() {
   the_device.ordinal = ordinal;
   the_device.stream = stream;
   the_device.error_flags = flags;
+  the_device.host_flags = host_flags;
   the_device.cu_count = props.multiProcessorCount;
   the_device.ready = true;
   return true;
@@ -185,11 +186,14 @@ bool synchronize_and_check() {
     return raise("a host-visible wait was requested during graph capture");
   if (!flush_pending_quantize())
     return false;
-  if (!LLHIP_CHECK(hipStreamSynchronize(dev.stream)))
+  // the flags come back behind the stream's work, so one wait covers both (a blocking copy after the wait would be a
+  // second round trip to the device)
+  if (!LLHIP_CHECK(hipMemcpyAsync(dev.host_flags, dev.error_flags, 16 * sizeof(int), hipMemcpyDeviceToHost,
+                                  dev.stream)) ||
+      !LLHIP_CHECK(hipStreamSynchronize(dev.stream)))
     return false;
   int flags[16];
-  if (!LLHIP_CHECK(hipMemcpy(flags, dev.error_flags, sizeof(flags), hipMemcpyDeviceToHost)))
-    return false;
+  memcpy(flags, dev.host_flags, sizeof(flags));
   return report_flags(flags);
 }
 
