@@ -127,6 +127,59 @@ __device__ __forceinline__ void store_tile(const TileSeg &seg, const TilePos &t,
     }
 }
 
+// The 256 x 128 int8 tile's SWIGLU epilogue with seg.cq set: a tile's 64 outputs of a row are one quantization group,
+// 32 in each of the row's two waves (wn). Each wave takes its 32 values' maximum (the row's 16 lanes by a DPP row
+// reduction), the two meet in LDS (`xchg`, free once every wave has left the K loop), and each quantizes its values
+// with the group's scale by the k_quantize rule, as store_tile_wide does (bitwise the FP32 output then
+// k_quantize_rows); a non-finite value sets flags[0]. Every wave of the block calls it (two barriers).
+__device__ __forceinline__ void store_tile_quantized(const TileSeg &seg, const TilePos &t, const v4f (&acc)[4][4],
+                                                     int wm, int wn, int lane, int m, float *xchg, int *flags) {
+  const int lc = lane & 15, lr = (lane >> 4) * 4;
+  // two passes over the sums (the SwiGLU values formed twice) so that only the sums stay live across the barriers
+  __syncthreads(); // every wave is past its K loop: the LDS is free
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      float pk = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        pk = fmaxf(pk, fabsf(silu_gate(acc[i][j][e], acc[i][j + 2][e]))); // a NaN: caught by quantize_fast
+      pk = group_reduce_max(pk, 16);
+      if (lc == 0)
+        xchg[(wm * 64 + 16 * i + lr + e) * 2 + wn] = pk;
+    }
+  __syncthreads();
+  const int c0 = t.n0; // the tile's group (seg.n % 64 == 0)
+  const int groups = seg.ldc / 64; // row strides of cq and cs: the whole width (a tail segment has its share)
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int r = wm * 64 + 16 * i + lr + e, row = t.m0 + r;
+      const float scale = fmaxf(xchg[r * 2], xchg[r * 2 + 1]) / 127.0f;
+      bool ok;
+      const float inv = group_reciprocal(scale, ok);
+      float v[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        v[j] = silu_gate(acc[i][j][e], acc[i][j + 2][e]);
+      int q[2];
+      quantize_fast(v, scale, inv, ok, q, bad);
+      if (row < m && c0 < seg.n) {
+        int8_t *qrow = seg.cq + (long long)row * seg.ldc;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          qrow[c0 + 32 * wn + 16 * j + lc] = (int8_t)q[j];
+        if (wn == 0 && lc == 0)
+          seg.cs[(long long)row * groups + c0 / 64] = scale;
+      }
+    }
+  if (bad && flags)
+    flags[0] = 1;
+}
+
 // The wide BF16 tile's epilogue: rows 64 wm + 16 i + 4 (l / 16) + e, columns 128 wn + 16 j + l % 16, or under SWIGLU
 // silu(W1 column 64 wn + 16 j + l % 16) * (the same W3 column) from tiles j and j + 4. With seg.cq set (SWIGLU, the
 // int8 kernel) a wave's 64 columns of a row are one quantization group, held by the 16 lanes of the row's lane group:
@@ -137,7 +190,7 @@ __device__ __forceinline__ void store_tile_wide(const TileSeg &seg, const TilePo
   const int lc = lane & 15, lr = (lane >> 4) * 4;
   if (t.swiglu && seg.cq) {
     const int c0 = t.n0 + 64 * wn; // the wave's group (seg.n % 64 == 0)
-    const int groups = seg.n / 64;
+    const int groups = seg.ldc / 64; // row strides of cq and cs: the whole width (a tail segment has its share)
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -158,7 +211,7 @@ __device__ __forceinline__ void store_tile_wide(const TileSeg &seg, const TilePo
         int q[4];
         quantize_fast(v, scale, inv, ok, q, bad);
         if (row < m && c0 < seg.n) {
-          int8_t *qrow = seg.cq + (long long)row * seg.n;
+          int8_t *qrow = seg.cq + (long long)row * seg.ldc;
 #pragma unroll
           for (int j = 0; j < 4; j++)
             qrow[c0 + 16 * j + lc] = (int8_t)q[j];
@@ -469,7 +522,9 @@ template <int I, int N, class F> __device__ __forceinline__ void issue_first(F &
   }
 }
 
-template <class C, bool PROBE, bool GS64, bool SPLIT>
+// QUANT: SWIGLU segments with the quantized output (seg.cq) take store_tile_quantized (an instantiation of its own:
+// the epilogue's registers would otherwise crowd the K loop of every other launch).
+template <class C, bool PROBE, bool GS64, bool SPLIT, bool QUANT = false>
 __global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
   extern __shared__ __align__(16) unsigned char q8_smem[];
   const int lane = threadIdx.x & 63;
@@ -662,7 +717,10 @@ __global__ __launch_bounds__(C::Threads, 2) void q8_gemm_lds(Q8Params p) {
         slot[(i * 4 + j) * C::Threads] = acc[i][j];
     return;
   }
-  store_tile(seg, t, acc, wm, wn, lane, p.m);
+  if constexpr (QUANT)
+    store_tile_quantized(seg, t, acc, wm, wn, lane, p.m, reinterpret_cast<float *>(q8_smem), p.flags);
+  else
+    store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
 
@@ -1685,13 +1743,14 @@ struct SegList {
 };
 
 // The pipelined kernel takes more than the default 64 KB of dynamic LDS: raised once per instantiation.
-template <class C, bool PROBE, bool GS64, bool SPLIT> bool q8_ready() {
-  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_lds<C, PROBE, GS64, SPLIT>,
+template <class C, bool PROBE, bool GS64, bool SPLIT, bool QUANT = false> bool q8_ready() {
+  static const hipError_t status = hipFuncSetAttribute((const void *)q8_gemm_lds<C, PROBE, GS64, SPLIT, QUANT>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::Lds);
   return check_hip(status, "allowing the Q8 GEMM its LDS");
 }
 
-template <class C, bool PROBE, bool GS64> bool q8_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
+template <class C, bool PROBE, bool GS64, bool QUANT = false>
+bool q8_launch(Q8Params p, const SegList &segs, hipStream_t stream) {
   p.grid = make_q8_grid(segs.seg, segs.nseg, p.m, C::TileM);
   if (p.grid.total <= 0)
     return true;
@@ -1702,12 +1761,14 @@ template <class C, bool PROBE, bool GS64> bool q8_launch(Q8Params p, const SegLi
   p.sk.partial = (v4f *)device().split_partial;
   p.sk.count = device().split_count;
   if (p.sk.splits == 1) {
-    if (!q8_ready<C, PROBE, GS64, false>())
+    if (!q8_ready<C, PROBE, GS64, false, QUANT>())
       return false;
-    hipLaunchKernelGGL((q8_gemm_lds<C, PROBE, GS64, false>), dim3((unsigned)p.grid.total), dim3(C::Threads), C::Lds,
+    hipLaunchKernelGGL((q8_gemm_lds<C, PROBE, GS64, false, QUANT>), dim3((unsigned)p.grid.total), dim3(C::Threads), C::Lds,
                        stream, p);
     return launch_ok("q8_gemm_lds");
   }
+  if (QUANT) // the quantized epilogue has no split form
+    return raise("q8_gemm_lds: a quantized SwiGLU output cannot be split");
   if (!q8_ready<C, PROBE, GS64, true>())
     return false;
   hipLaunchKernelGGL((q8_gemm_lds<C, PROBE, GS64, true>), dim3((unsigned)(p.grid.total * p.sk.splits)),
@@ -1807,14 +1868,17 @@ bool q8_wide_kernel(const Q8Params &p, bool split, unsigned blocks, hipStream_t 
 // A wide grid of whole rounds of one tile per CU plus a partial last round: the partial round costs a whole round's
 // time (a wide block is bound by its own MFMA and VALU work, not by bandwidth the idle CUs would leave it), so when
 // that round is at most half the CUs and whole column tiles across every row tile, its columns go to the 256 x 128
-// kernel instead, one round of tiles that take 1 / 1.7 of a wide tile's time. One segment without the quantized
-// output only. Returns the first columns' segment in `head` and the rest in `tail`, or false to leave the grid whole.
+// kernel instead, one round of tiles that take 1 / 1.7 of a wide tile's time. One segment; with the quantized output
+// (seg.cq) only where the 256 x 128 tiles are exactly one round (they then run unsplit, and their epilogue quantizes
+// whole 64-column groups). Returns the first columns' segment in `head` and the rest in `tail`, or false to leave the
+// grid whole.
 bool q8_wide_tail(const Q8Params &p, const GemmSegmentDev &seg, GemmSegmentDev &head, GemmSegmentDev &tail) {
-  if (p.grid.nseg != 1 || seg.cq || p.sk.splits != 1)
+  if (p.grid.nseg != 1 || p.sk.splits != 1)
     return false;
   const int cus = device().cu_count > 0 ? device().cu_count : 256;
   const int rest = p.grid.total % cus, mtiles = p.grid.mtiles;
-  if (p.grid.total < cus || rest == 0 || 2 * rest > cus || rest % mtiles)
+  if (p.grid.total < cus || rest == 0 || 2 * rest > cus || rest % mtiles ||
+      (seg.cq && (2 * rest != cus || forced_splits.load() > 1)))
     return false;
   const int width = seg.epi == EPI_SWIGLU ? kWTileN / 2 : kWTileN;
   const int n1 = (p.grid.seg[0].ntiles - rest / mtiles) * width;
@@ -1825,7 +1889,11 @@ bool q8_wide_tail(const Q8Params &p, const GemmSegmentDev &seg, GemmSegmentDev &
   head.n = n1;
   tail = seg;
   tail.n = seg.n - n1;
-  tail.c = seg.c + n1;
+  tail.c = seg.c ? seg.c + n1 : nullptr;
+  if (seg.cq) { // the same row strides (seg.n): the tail's columns of cq and their groups' scales
+    tail.cq = seg.cq + n1;
+    tail.cs = seg.cs + n1 / 64;
+  }
   tail.w = (const int8_t *)seg.w + (long long)n1 * p.k;
   tail.ws = seg.ws + n1 * groups;
   if (seg.epi == EPI_SWIGLU) {
@@ -1905,6 +1973,15 @@ bool launch_q8_gemm_swiglu_quantized(const GemmQ8Job &job, hipStream_t stream) {
   q8_wide_grid(p, list);
   if (p.sk.splits != 1 || p.grid.total <= 0)
     return false;
+  GemmSegmentDev head, tail;
+  if (q8_wide_tail(p, job.seg[0], head, tail)) { // a partial last round: its columns on the 256 x 128 kernel
+    q8_wide_grid(p, SegList{&head, 1});
+    if (!q8_wide_kernel(p, false, (unsigned)p.grid.total, stream))
+      return false;
+    const SegList rest{&tail, 1};
+    return q8_tile_m() == 256 ? q8_launch<Q8Wide, false, true, true>(p, rest, stream)
+                              : q8_launch<Q8Pair, false, true, true>(p, rest, stream);
+  }
   return q8_wide_kernel(p, false, (unsigned)p.grid.total, stream);
 }
 

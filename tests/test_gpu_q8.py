@@ -637,11 +637,14 @@ def test_gemm_q8_wide_grid_tail_on_narrow_tiles(m, n, k, kind):
         L.llhip_set_q8_tile(0)
 
 
-@pytest.mark.parametrize("m,n,k", [(300, 256, 1024), (513, 640, 320), (257, 128, 4096), (1024, 384, 2048)])
+@pytest.mark.parametrize("m,n,k", [(300, 256, 1024), (513, 640, 320), (257, 128, 4096), (1024, 384, 2048),
+                                   (512, 24576, 128)])
 def test_gemm_q8_swiglu_quantized(m, n, k):
     """llhip_gemm_q8_swiglu_quantize: hb quantized in the wide int8 kernel's epilogue, bitwise k_gemm_q8 GEMM_SWIGLU then
     k_quantize_rows of its output; it declines (returns 0, writes nothing) where the launcher would not run the wide
-    kernel unsplit, and a non-finite hb value fails as k_quantize_rows does."""
+    kernel unsplit, and a non-finite hb value fails as k_quantize_rows does. n = 24576 at 512 rows is 384 wide tiles
+    on 256 CUs: the last 8192 columns go to the 256 x 128 kernel, whose epilogue quantizes each tile's 64-column
+    group across its two waves."""
     L = hu.lib()
     gs = 64
     xq, xs, wq, ws, w3q, w3s, rng = gemm_case(m, n, k, gs, 6161 + m + n)
@@ -662,8 +665,10 @@ def test_gemm_q8_swiglu_quantized(m, n, k):
         assert lh.last_error() == "", lh.last_error()
         assert np.array_equal(hu.host(hq), hu.host(q2)), "quantized values"
         assert np.array_equal(hu.bits(hu.host(hs)), hu.bits(hu.host(s2))), "scales"
-        # declined: the 256 x 128 kernel forced, or split K, or another group size; nothing is written
-        for tile, splits in ((1, 1), (2, 2)):
+        # declined: the 256 x 128 kernel forced, or split K, or another group size; nothing is written (a wide grid of
+        # more tiles than the split workspace holds is never split, so a forced split count leaves it as it is)
+        wide_tiles = -(-m // 256) * -(-n // 128)
+        for tile, splits in ((1, 1), (2, 2)) if wide_tiles <= 256 else ((1, 1),):
             L.llhip_set_q8_tile(tile)
             L.llhip_set_gemm_splits(splits)
             hq0 = hu.dev(np.full((m, n), 7, np.int8))
