@@ -68,70 +68,94 @@ __global__ __launch_bounds__(kBlock) void quantize_lanes(int8_t *__restrict__ q,
     s[(size_t)row * (n / gs) + off / gs] = scale;
 }
 
-// RMSNorm of each row, then k_quantize of the normalized values, without the normalized row in memory: one 1024-thread
-// block per row, thread t holding values 4 t + 4096 p. The sum of squares runs in rmsnorm_rows' order (each thread's
-// values by fmaf, the wave's by the DPP sum, the waves' in order) and w * (ss * x) rounds as there, so the values
-// quantized are rmsnorm_rows' bit for bit; a group of gs values is gs / 4 consecutive lanes (the group maximum a lane
-// reduction) quantized by the k_quantize rule as quantize_lanes applies it. Bitwise k_rmsnorm_rows then
-// k_quantize_rows. n <= kNormQPasses * 4096, n % gs == 0, gs a power of two from 4 to 256.
-constexpr int kNormQThreads = 1024, kNormQPasses = 2;
+// RMSNorm of each row, then k_quantize of the normalized values, without the normalized row in memory: one 256-thread
+// block per row. The sum of squares runs in rmsnorm_rows' order, whose 1024 threads (16 waves) each hold values
+// 4 t + 4096 p: here logical thread t = 64 (4 W + r) + l lives in register set r of lane l of wave W, so each of the
+// block's four waves holds four of those logical waves in registers and takes each one's DPP sum over the same lane
+// positions; each logical thread's values go by fmaf and the 16 wave sums in order, and w * (ss * x) rounds as there,
+// so the values quantized are rmsnorm_rows' bit for bit. Four rows' worth of waves per 1024 threads keeps every row of
+// a 2048-row batch resident at once (one 1024-thread block per row took four rounds). A group of gs values is gs / 4
+// consecutive lanes of one register set (the group maximum a lane reduction) quantized by the k_quantize rule as
+// quantize_lanes applies it. Bitwise k_rmsnorm_rows then k_quantize_rows. n <= PASSES * 4096 (one pass holds 32 values
+// a thread, in few enough registers for eight waves per SIMD), n % gs == 0, gs a power of two from 4 to 256.
+constexpr int kNormQThreads = 256, kNormQLogical = 1024, kNormQSets = kNormQLogical / kNormQThreads, kNormQPasses = 2;
+template <int PASSES>
 __global__ __launch_bounds__(kNormQThreads) void rmsnorm_quantize_rows(int8_t *__restrict__ q, float *__restrict__ s,
                                                                        const float *__restrict__ x,
                                                                        const float *__restrict__ weight, int n,
                                                                        float epsilon, int gs, int *__restrict__ flags) {
-  __shared__ float part[kNormQThreads / kWave];
-  const int tid = threadIdx.x;
+  __shared__ float part[kNormQLogical / kWave];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const float *row = x + (size_t)blockIdx.x * n;
-  float4 v[kNormQPasses], w[kNormQPasses];
-  float ss = 0.0f;
+  float4 v[kNormQSets][PASSES], w[kNormQSets][PASSES];
+  float ss[kNormQSets];
 #pragma unroll
-  for (int p = 0; p < kNormQPasses; p++) {
-    const int j = 4 * tid + p * 4 * kNormQThreads;
-    v[p] = w[p] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (j < n) {
-      v[p] = *reinterpret_cast<const float4 *>(row + j);
-      w[p] = *reinterpret_cast<const float4 *>(weight + j);
-      ss = fmaf(v[p].x, v[p].x, ss);
-      ss = fmaf(v[p].y, v[p].y, ss);
-      ss = fmaf(v[p].z, v[p].z, ss);
-      ss = fmaf(v[p].w, v[p].w, ss);
+  for (int r = 0; r < kNormQSets; r++) {
+    const int t = kWave * (kNormQSets * wave + r) + lane; // the logical thread
+    ss[r] = 0.0f;
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+      const int j = 4 * t + p * 4 * kNormQLogical;
+      v[r][p] = w[r][p] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (j < n) {
+        v[r][p] = *reinterpret_cast<const float4 *>(row + j);
+        w[r][p] = *reinterpret_cast<const float4 *>(weight + j);
+      }
     }
   }
-  ss = wave_sum(ss);
-  if ((tid & (kWave - 1)) == 0)
-    part[tid / kWave] = ss;
-  __syncthreads();
-  ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kNormQThreads / kWave; i++)
-    ss += part[i];
+  for (int r = 0; r < kNormQSets; r++) {
+    const int t = kWave * (kNormQSets * wave + r) + lane;
+#pragma unroll
+    for (int p = 0; p < PASSES; p++)
+      if (4 * t + p * 4 * kNormQLogical < n) {
+        ss[r] = fmaf(v[r][p].x, v[r][p].x, ss[r]);
+        ss[r] = fmaf(v[r][p].y, v[r][p].y, ss[r]);
+        ss[r] = fmaf(v[r][p].z, v[r][p].z, ss[r]);
+        ss[r] = fmaf(v[r][p].w, v[r][p].w, ss[r]);
+      }
+    ss[r] = wave_sum(ss[r]);
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int r = 0; r < kNormQSets; r++)
+      part[kNormQSets * wave + r] = ss[r];
+  __syncthreads();
+  float inv_rms = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormQLogical / kWave; i++)
+    inv_rms += part[i];
   // src/kernels.c:15-17, the same three roundings
-  ss /= n;
-  ss += epsilon;
-  ss = 1.0f / sqrtf(ss);
+  inv_rms /= n;
+  inv_rms += epsilon;
+  inv_rms = 1.0f / sqrtf(inv_rms);
   const int lpg = gs / 4, groups = n / gs;
   bool bad = false;
 #pragma unroll
-  for (int p = 0; p < kNormQPasses; p++) {
-    const int base = p * 4 * kNormQThreads, j = 4 * tid + base;
-    if (base + 4 * (tid & ~(kWave - 1)) >= n)
-      continue; // the whole wave is past the row (groups never straddle it: n % gs == 0)
-    const float e[4] = {w[p].x * (ss * v[p].x), w[p].y * (ss * v[p].y), w[p].z * (ss * v[p].z),
-                        w[p].w * (ss * v[p].w)};
-    float peak = 0.0f;
+  for (int r = 0; r < kNormQSets; r++) {
+    const int lw = kNormQSets * wave + r, t = kWave * lw + lane;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      peak = fmaxf(peak, fabsf(e[i])); // a NaN is skipped here and caught by quantize_fast
-    peak = group_reduce_max(peak, lpg);
-    const float scale = peak / 127.0f;
-    bool ok;
-    const float inv = group_reciprocal(scale, ok);
-    int qv[4];
-    quantize_fast(e, scale, inv, ok, qv, bad);
-    if (j < n) {
-      *reinterpret_cast<int *>(q + (size_t)blockIdx.x * n + j) = pack_bytes(qv[0], qv[1], qv[2], qv[3]);
-      if ((tid & (lpg - 1)) == 0)
-        s[(size_t)blockIdx.x * groups + j / gs] = scale;
+    for (int p = 0; p < PASSES; p++) {
+      const int base = p * 4 * kNormQLogical, j = 4 * t + base;
+      if (base + 4 * kWave * lw >= n)
+        continue; // the whole logical wave is past the row (groups never straddle it: n % gs == 0)
+      const float e[4] = {w[r][p].x * (inv_rms * v[r][p].x), w[r][p].y * (inv_rms * v[r][p].y),
+                          w[r][p].z * (inv_rms * v[r][p].z), w[r][p].w * (inv_rms * v[r][p].w)};
+      float peak = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        peak = fmaxf(peak, fabsf(e[i])); // a NaN is skipped here and caught by quantize_fast
+      peak = group_reduce_max(peak, lpg);
+      const float scale = peak / 127.0f;
+      bool ok;
+      const float inv = group_reciprocal(scale, ok);
+      int qv[4];
+      quantize_fast(e, scale, inv, ok, qv, bad);
+      if (j < n) {
+        *reinterpret_cast<int *>(q + (size_t)blockIdx.x * n + j) = pack_bytes(qv[0], qv[1], qv[2], qv[3]);
+        if ((lane & (lpg - 1)) == 0)
+          s[(size_t)blockIdx.x * groups + j / gs] = scale;
+      }
     }
   }
   if (bad)
@@ -832,7 +856,7 @@ bool launch_ok(const char *what) {
 } // namespace
 
 bool rmsnorm_quantize_fits(int n, int gs) {
-  return n > 0 && n <= kNormQPasses * 4 * kNormQThreads && gs >= 4 && gs <= 256 && (gs & (gs - 1)) == 0 &&
+  return n > 0 && n <= kNormQPasses * 4 * kNormQLogical && gs >= 4 && gs <= 256 && (gs & (gs - 1)) == 0 &&
          n % gs == 0;
 }
 
@@ -840,8 +864,12 @@ bool launch_rmsnorm_quantize(int8_t *q, float *s, const float *x, const float *w
                              int gs, hipStream_t stream) {
   if (rows <= 0)
     return true;
-  hipLaunchKernelGGL(rmsnorm_quantize_rows, dim3((unsigned)rows), dim3(kNormQThreads), 0, stream, q, s, x, weight, n,
-                     epsilon, gs, device().error_flags);
+  if (n <= 4 * kNormQLogical)
+    hipLaunchKernelGGL(rmsnorm_quantize_rows<1>, dim3((unsigned)rows), dim3(kNormQThreads), 0, stream, q, s, x, weight,
+                       n, epsilon, gs, device().error_flags);
+  else
+    hipLaunchKernelGGL(rmsnorm_quantize_rows<kNormQPasses>, dim3((unsigned)rows), dim3(kNormQThreads), 0, stream, q, s,
+                       x, weight, n, epsilon, gs, device().error_flags);
   return launch_ok("rmsnorm_quantize_rows");
 }
 
