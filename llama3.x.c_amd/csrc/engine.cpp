@@ -92,6 +92,9 @@ struct Engine {
   // the link's rate instead of through the runtime's staging of pageable memory; grown on demand
   float *host_batch = nullptr;
   size_t host_batch_floats = 0;
+  // every row's logits copy to the host on a stream of their own, piece by piece behind the classifier GEMM
+  hipStream_t copy_stream = nullptr;
+  hipEvent_t piece_done = nullptr;
 };
 
 // Room for `floats` logits in the pinned batch buffer (false after raise when the host cannot pin that much).
@@ -142,6 +145,12 @@ void release(Engine *e) {
     (void)hipHostFree(e->host_logits);
   if (e->host_batch)
     (void)hipHostFree(e->host_batch);
+  if (e->copy_stream) {
+    (void)hipStreamSynchronize(e->copy_stream);
+    (void)hipStreamDestroy(e->copy_stream);
+  }
+  if (e->piece_done)
+    (void)hipEventDestroy(e->piece_done);
   drop(e->packed), drop(e->cls_packed);
   if (e->map) {
     (void)llhip_unregister_host(e->map);
@@ -584,6 +593,68 @@ void gemm_f32_or_bf16(Engine *e, const float *a, int lda, int m, int k, const Ge
   k_gemm_bf16(a, lda, m, k, b, count, &e->panel);
 }
 
+// Every row's logits for Q8_0 (src/tp.c:610-618 runs the classifier GEMV row by row): the classifier GEMM over pieces
+// of kLogitsPiece rows, each piece's logits copied into the pinned host buffer on the engine's copy stream (a DMA
+// engine, not the CUs) while the next piece computes, so the copy at the link's rate waits only for the first piece.
+// Every piece has at least kLogitsPiece rows, the classifier's 128256 columns make far more tiles than CUs (no split
+// K), and each row's sums do not depend on the other rows, so the logits are bit for bit those of one GEMM over all
+// rows; a batch of fewer than 2 * kLogitsPiece rows is one piece. The rows' RMSNorm and quantization are in bxq / bxs.
+// LLAMA_HIP_LOGITS_PIECE (read per call) sets the piece's rows (at least 64), 0 one GEMM over all rows.
+constexpr int kLogitsPiece = 256;
+int logits_piece() {
+  const char *env = getenv("LLAMA_HIP_LOGITS_PIECE");
+  if (!env || !*env)
+    return kLogitsPiece;
+  const int v = atoi(env);
+  return v <= 0 ? INT_MAX / 2 : v < 64 ? 64 : v;
+}
+
+bool logits_all_q8(Engine *e, int count) {
+  const Config &c = e->c;
+  const int d = c.dim, gs = e->gs;
+  const size_t vocab = c.vocab_size;
+  if (!host_batch_room(e, (size_t)count * vocab))
+    return false;
+  if (!e->copy_stream && hipStreamCreateWithFlags(&e->copy_stream, hipStreamNonBlocking) != hipSuccess) {
+    (void)hipGetLastError();
+    e->copy_stream = nullptr;
+    return raise("engine_forward_batch: no stream for the logits copy");
+  }
+  if (!e->piece_done && hipEventCreateWithFlags(&e->piece_done, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    e->piece_done = nullptr;
+    return raise("engine_forward_batch: no event for the logits copy");
+  }
+  bool copied = true;
+  const int piece = logits_piece();
+  for (int r0 = 0; r0 < count;) {
+    const int n = count - r0 < 2 * piece ? count - r0 : piece;
+    const GemmQ8Segment seg{e->blogits + (size_t)r0 * vocab, c.vocab_size, e->cls.k8(), K8Weight{}, nullptr, nullptr,
+                            c.vocab_size, GEMM_STORE};
+    k_gemm_q8(e->bxq + (size_t)r0 * d, e->bxs + (size_t)r0 * (d / gs), n, d, gs, &seg, 1);
+    if (llhip_last_error()[0])
+      break;
+    if (hipEventRecord(e->piece_done, device().stream) != hipSuccess ||
+        hipStreamWaitEvent(e->copy_stream, e->piece_done, 0) != hipSuccess ||
+        hipMemcpyAsync(e->host_batch + (size_t)r0 * vocab, e->blogits + (size_t)r0 * vocab,
+                       (size_t)n * vocab * sizeof(float), hipMemcpyDeviceToHost, e->copy_stream) != hipSuccess) {
+      copied = false;
+      break;
+    }
+    r0 += n;
+  }
+  // the copies queued so far end before the buffers are reused or the call returns, on failure too
+  if (hipStreamSynchronize(e->copy_stream) != hipSuccess)
+    copied = false;
+  if (!copied) {
+    (void)hipGetLastError();
+    if (!llhip_last_error()[0])
+      raise("engine_forward_batch: copying the logits to the host failed");
+    return false;
+  }
+  return !llhip_last_error()[0];
+}
+
 // count tokens at pos0 .. pos0 + count - 1 through the GEMMs (src/tp.c:528-622 with one socket): the embedding rows
 // and RoPE tables, per layer RMSNorm of the rows, (quantize,) the QKV GEMM, RoPE, the cache rows, batched causal
 // attention, (quantize,) Wo + residual, RMSNorm, (quantize,) W1/W3 SwiGLU, (quantize,) W2 + residual; then the final
@@ -690,14 +761,15 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
     const GemmBf16Segment seg{e->blogits, c.vocab_size, e->cls_packed, nullptr, c.vocab_size, GEMM_STORE};
     k_gemm_bf16(e->bx, d, count, d, &seg, 1, &e->panel);
   } else if (want == LOGITS_ALL) {
-    // Every row's RMSNorm, then one GEMM over the classifier, where src/tp.c:610-618 runs the classifier GEMV row by
-    // row: a GEMM row equals the GEMV of that row within the kernel budget (tests/q8.c:158-183), and the classifier
-    // streams once per batch instead of once per row.
+    // Every row's RMSNorm, then the classifier as a GEMM (in pieces whose logits copy meanwhile for Q8_0), where
+    // src/tp.c:610-618 runs the classifier GEMV row by row: a GEMM row equals the GEMV of that row within the kernel
+    // budget (tests/q8.c:158-183), and the classifier streams once per batch instead of once per row.
     if (e->q8) {
       norm_rows(e->rms_final);
-      const GemmQ8Segment seg{e->blogits, c.vocab_size, e->cls.k8(), K8Weight{}, nullptr, nullptr, c.vocab_size,
-                              GEMM_STORE};
-      k_gemm_q8(e->bxq, e->bxs, count, d, gs, &seg, 1);
+      if (!logits_all_q8(e, count))
+        return nullptr;
+      llhip_synchronize();
+      return llhip_last_error()[0] ? nullptr : e->host_batch;
     } else {
       k_rmsnorm_rows(e->bxb, e->bx, e->rms_final, count, d, c.norm_eps);
       const GemmSegment seg{e->blogits, c.vocab_size, e->cls.f(), nullptr, (size_t)d, c.vocab_size, GEMM_STORE};

@@ -80,7 +80,7 @@ def c5_checkpoint(tmp_path_factory):
             shutil.rmtree(d, ignore_errors=True)
 
 
-def test_c5_8b_prefill_2048_then_256_greedy_steps(c5_checkpoint):
+def test_c5_8b_prefill_2048_then_256_greedy_steps(c5_checkpoint, monkeypatch):
     L = hu.lib()
     assert L.llhip_init() == 0, lh.last_error()
     path = c5_checkpoint
@@ -98,6 +98,16 @@ def test_c5_8b_prefill_2048_then_256_greedy_steps(c5_checkpoint):
         assert np.isfinite(rows).all()
         ours_batch, last_row = rows[-LAST:].copy(), rows[-1].copy()
         say(f"prefill of {PROMPT} tokens with every row's logits in {time.time() - t:.2f} s")
+        # the classifier GEMM ran in 256-row pieces whose logits copied while the next piece computed; at this
+        # classifier's 128256 columns every piece takes the whole batch's unsplit tiles, so one GEMM over all rows
+        # (the same prompt again: the same cache rows, bit for bit) gives the same bits
+        pieces = rows.copy()
+        monkeypatch.setenv("LLAMA_HIP_LOGITS_PIECE", "0")
+        p = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens), PROMPT, 0, lh.LOGITS_ALL)
+        monkeypatch.delenv("LLAMA_HIP_LOGITS_PIECE")
+        assert p, lh.last_error()
+        assert np.array_equal(np.ctypeslib.as_array(p, shape=(PROMPT, V)), pieces)
+        del pieces
         # greedy decode from the prefill's last row
         greedy, decode = [], []
         logits = last_row

@@ -42,8 +42,8 @@ def rope_table(cfg, pos):
 class OracleForward:
     """The decode forward from the oracle's kernels, head-major K/V cache as the engine's default layout."""
 
-    def __init__(self, cfg, norms, t, a32=False):
-        self.c, self.n, self.t, self.a32 = cfg, norms, t, a32
+    def __init__(self, cfg, norms, t, a32=False, gs=GS):
+        self.c, self.n, self.t, self.a32, self.gs = cfg, norms, t, a32, gs
         d, L, S = cfg["dim"], cfg["n_layers"], cfg["seq_len"]
         self.hd = d // cfg["n_heads"]
         self.kv = self.hd * cfg["n_kv_heads"]
@@ -53,9 +53,9 @@ class OracleForward:
     def mm(self, x, wq, ws, **kw):
         """A GEMV of x: W8A8 (x quantized per group) or, in W8A32, the FP32 x against the dequantized weights."""
         if self.a32:
-            return orc.matmul_q8(None, None, wq, ws, GS, xf=np.ascontiguousarray(x, np.float32), **kw)
-        xq, xs = orc.quantize(x, GS)
-        return orc.matmul_q8(xq, xs, wq, ws, GS, **kw)
+            return orc.matmul_q8(None, None, wq, ws, self.gs, xf=np.ascontiguousarray(x, np.float32), **kw)
+        xq, xs = orc.quantize(x, self.gs)
+        return orc.matmul_q8(xq, xs, wq, ws, self.gs, **kw)
 
     def w(self, role, l):
         q, s = self.t[role]
@@ -64,7 +64,7 @@ class OracleForward:
     def step(self, token, pos):
         c, d, nh, nkv, hd, S = self.c, self.c["dim"], self.c["n_heads"], self.c["n_kv_heads"], self.hd, self.c["seq_len"]
         eq, es = self.t["embed"]
-        x = (eq[token].astype(np.float32) * np.repeat(es.reshape(eq.shape[0], -1)[token], GS)).astype(np.float32)
+        x = (eq[token].astype(np.float32) * np.repeat(es.reshape(eq.shape[0], -1)[token], self.gs)).astype(np.float32)
         table = rope_table(c, pos)
         ps, hb = orc.kv_strides(nkv, hd, S, True)
         for l in range(c["n_layers"]):
@@ -163,6 +163,47 @@ def test_engine_forward_batch_matches_the_oracle_forward(tmp_path, layout, cfg):
     finally:
         L.engine_free(ctypes.byref(model))
         assert L.kernels_kv_layout_select(b"head") == 1
+
+
+# group size 64 (the int8 GEMM's tiled kernels) and a classifier wide enough that a 256-row piece is 256 tiles
+CFG_PIECES = dict(CFG, n_layers=2, vocab_size=32768, seq_len=640)
+
+
+def test_engine_all_logits_in_pieces(tmp_path, monkeypatch):
+    """Every row's logits of a 600-row batch: the classifier GEMM runs in pieces of LLAMA_HIP_LOGITS_PIECE rows (256
+    by default: 256 + 344; 100: six pieces), each piece's logits copied to the host on a second stream while the next
+    piece computes. Every row of every layout agrees with one GEMM over the whole batch (the knob at 0) within FP32
+    rounding (a piece may take other tiles than the whole batch), so each piece's rows land in their own place, and the
+    first 48 rows agree with the token-by-token oracle forward."""
+    L = hu.lib()
+    assert L.llhip_init() == 0, lh.last_error()
+    gs, count = 64, 600
+    norms, t = ck.synthetic(CFG_PIECES, gs, 14)
+    path = os.path.join(tmp_path, "pieces.bin")
+    ck.write_q8_v3(path, CFG_PIECES, gs, norms, t)
+    V = CFG_PIECES["vocab_size"]
+    tokens = np.random.default_rng(6).integers(0, V, count).astype(np.int32)
+    model = lh.Model()
+    got = {}
+    try:
+        L.engine_load(ctypes.byref(model), path.encode())
+        assert model.implementation and L.engine_max_batch(ctypes.byref(model)) >= count, lh.last_error()
+        for piece in ("0", "256", "100"):
+            monkeypatch.setenv("LLAMA_HIP_LOGITS_PIECE", piece)
+            out = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens), count, 0, lh.LOGITS_ALL)
+            assert out, (piece, lh.last_error())
+            got[piece] = np.ctypeslib.as_array(out, shape=(count, V)).copy()
+    finally:
+        L.engine_free(ctypes.byref(model))
+    whole = got["0"]
+    assert np.isfinite(whole).all()
+    for piece in ("256", "100"):
+        d = np.abs(got[piece] - whole).max(axis=1)
+        assert np.all(d <= 1e-5 * np.abs(whole).max(axis=1) + 1e-6), (piece, int(d.argmax()), float(d.max()))
+        assert np.array_equal(got[piece].argmax(axis=1), whole.argmax(axis=1)), piece
+    ref = OracleForward(CFG_PIECES, norms, t, gs=gs)
+    for pos in range(48):
+        check_logits(got["256"][pos], ref.step(int(tokens[pos]), pos), f"ALL row {pos} in pieces")
 
 
 def test_engine_load_context_sizes_the_cache(tmp_path):
