@@ -14,6 +14,8 @@
 #include <cfloat>
 #include <type_traits>
 
+#include <cstring>
+
 #include "common.h"
 #include "lanes.h"
 
@@ -939,6 +941,262 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
     p.flags[1] = 1;
 }
 
+// The flash form on the BF16 matrix cores (attn_flash3): the same tiles, pairs of tiles, position split and online
+// softmax as attn_flash, with every product of the scores and the value sums formed from exact three-part BF16 splits
+// of its FP32 operands. A value x is h + m + l exactly (h the top 8 significant bits of x, m the next 8 of x - h, l the
+// rest, at most 8 bits), and x y is taken as hh + hm + mh + mm + hl + lh: the three dropped products are below 2^-23 of
+// |x y| and every BF16 product is exact in FP32, so each score and value sum is FP32-accurate, as on the FP32 matrix
+// cores, at six v_mfma_f32_16x16x32_bf16 (16 cycles) per 16 x 16 x 32 block against eight v_mfma_f32_16x16x4_f32
+// (32 cycles each). Chunks are 32 positions. A chunk's K and V rows are loaded into registers one chunk ahead (buffer
+// loads, zero past the tile's last position), split once per block (each thread 8 values of K and 8 of V) and
+// written to LDS as parts, two buffers, one barrier per chunk:
+//   - K parts [part][position][dimension], rows padded to HD + 8 values, so the score MFMA's A operand (16 positions x
+//     32 dimensions: lane l reads dimensions 8 (l / 16) .. + 7 of position l % 16) is one 16-byte read per part, free
+//     of bank conflicts; the query vector's parts stay in registers as the B operand;
+//   - V parts transposed, [part][dimension][slot], a dimension's 32 slots padded to 40: the value sums' B operand is
+//     the scores' accumulator as it stands (lane (q, c) holds positions 16 t + 4 q + e of vector c), so slot
+//     8 q + 4 t + e holds position 16 t + 4 q + e, and the A operand (16 dimensions x 32 slots) is again one 16-byte
+//     read per part.
+// Lane (q, c) ends with dimensions 16 d + 4 q + e of its vector c.
+template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash3(AttnParams p) {
+  typedef int v4i_t __attribute__((ext_vector_type(4)));
+  typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+  constexpr int kC = 32;                   // positions per chunk
+  constexpr int kSs = HD / 32;             // 32-dimension steps of the scores
+  constexpr int kDt = HD / 16;             // 16-dimension tiles of the value sums
+  constexpr int kQv = 128;                 // query vectors per tile
+  constexpr int kKRow = HD + 8, kVRow = kC + 8;
+  constexpr int kKPart = kC * kKRow, kVPart = HD * kVRow;
+  constexpr int kKThreads = kC * HD / 8, kVThreads = HD * 4; // threads that stage 8 values of K, of V
+  static_assert(kKThreads <= kTileThreads && kVThreads <= kTileThreads, "one staging item per thread");
+  __shared__ __align__(16) uint16_t Kp[2][3 * kKPart];
+  __shared__ __align__(16) uint16_t Vp[2][3 * kVPart];
+  const int kv_mul = p.n_heads / p.n_kv_heads, tile_rows = kQv / kv_mul;
+  const int ntiles = (p.rows + tile_rows - 1) / tile_rows;
+  const int g = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int lq = lane >> 4, lc = lane & 15;
+  const int qv = wave * 16 + lc, j = qv / kv_mul, h = qv % kv_mul;
+  const float *kbase = p.key + (size_t)g * p.head_base, *vbase = p.value + (size_t)g * p.head_base;
+  const unsigned stride_bytes = (unsigned)p.pos_stride * 4u;
+  const float scale2 = 1.4426950408889634f / p.divisor;
+  // staging roles: K position kpos, dimensions 8 kdg ..; V dimension vdim, slots 8 va .. (positions 4 va + e and
+  // 16 + 4 va + e)
+  const int kpos = tid / (HD / 8), kdg = tid % (HD / 8), vdim = tid % HD, va = tid / HD;
+  const bool kstage = tid < kKThreads, vstage = tid < kVThreads;
+  // the high halves of x's three parts: h in the word of x, m in the word of x - h, l in the word of the rest
+  auto split3 = [](float x, unsigned &uh, unsigned &um, unsigned &ul) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const float r1 = x - __builtin_bit_cast(float, u & 0xFFFF0000u);
+    const unsigned u1 = __builtin_bit_cast(unsigned, r1);
+    const float r2 = r1 - __builtin_bit_cast(float, u1 & 0xFFFF0000u);
+    uh = u, um = u1, ul = __builtin_bit_cast(unsigned, r2);
+  };
+  // eight values in slot order -> three parts of eight BF16 values (value 2 w in the low half of dword w)
+  auto parts8 = [&](const float (&v)[8], v4i_t &ph, v4i_t &pm, v4i_t &pl) {
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      unsigned ah, am, al, bh, bm, bl;
+      split3(v[2 * w], ah, am, al);
+      split3(v[2 * w + 1], bh, bm, bl);
+      ph[w] = (int)__builtin_amdgcn_perm(bh, ah, 0x07060302u);
+      pm[w] = (int)__builtin_amdgcn_perm(bm, am, 0x07060302u);
+      pl[w] = (int)__builtin_amdgcn_perm(bl, al, 0x07060302u);
+    }
+  };
+  auto mfma = [](const v4i_t &a, const v4i_t &b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0,
+                                                    0);
+  };
+  bool bad = false;
+  const bool split = p.splits > 0;
+  for (int pass = 0; pass < 2; pass++) {
+    const int tile = split ? (int)blockIdx.x : pass == 0 ? ntiles - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    if (pass == 1 && (split || tile >= ntiles - 1 - (int)blockIdx.x))
+      break;
+    const int r0 = tile * tile_rows, row = r0 + j;
+    const bool active = j < tile_rows && row < p.rows;
+    const int live_to = active ? p.pos0 + row : -1;
+    const int wave_last = p.pos0 + min(r0 + min((wave * 16 + 15) / kv_mul, tile_rows - 1), p.rows - 1);
+    const int last = p.pos0 + min(r0 + tile_rows, p.rows) - 1;
+    const int range = (int)(((unsigned)last * stride_bytes) + HD * 4);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void *)kbase, (short)0, range, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vbase, (short)0, range, 0x00020000);
+    // the query vector's parts: step s holds dimensions 32 s + 8 lq .. + 7
+    v4i_t qh[kSs], qm[kSs], ql[kSs];
+    {
+      const float *src = p.q + ((size_t)(active ? row : 0) * p.n_heads + (size_t)g * kv_mul + h) * HD + 8 * lq;
+#pragma unroll
+      for (int st = 0; st < kSs; st++) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i += 4) {
+          const float4 x = active ? *reinterpret_cast<const float4 *>(src + 32 * st + i) : float4{0.f, 0.f, 0.f, 0.f};
+          v[i] = x.x, v[i + 1] = x.y, v[i + 2] = x.z, v[i + 3] = x.w;
+        }
+        parts8(v, qh[st], qm[st], ql[st]);
+      }
+    }
+    v4f o[kDt];
+#pragma unroll
+    for (int d = 0; d < kDt; d++)
+      o[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -FLT_MAX, l_run = 0.0f;
+    const int all = last / kC + 1, share = split ? (all + p.splits - 1) / p.splits : all;
+    const int c0 = split ? min(all, (int)blockIdx.z * share) : 0, chunks = min(all, c0 + share) - c0;
+    float kr[8], vr[8]; // the next chunk's K and V values of this thread's staging items
+    auto load = [&](int c) {
+      const int t0 = (c0 + c) * kC;
+      if (kstage) {
+        const unsigned off = (unsigned)(t0 + kpos) * stride_bytes + 32u * (unsigned)kdg;
+        const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
+        const float4 b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 16u, 0, 0));
+        kr[0] = a.x, kr[1] = a.y, kr[2] = a.z, kr[3] = a.w, kr[4] = b.x, kr[5] = b.y, kr[6] = b.z, kr[7] = b.w;
+      }
+      if (vstage) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int at = t0 + (e < 4 ? 4 * va + e : 16 + 4 * va + e - 4);
+          vr[e] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(vrs, (unsigned)at * stride_bytes + 4u * (unsigned)vdim, 0, 0));
+        }
+      }
+    };
+    auto stage = [&](int b) {
+      if (kstage) {
+        v4i_t ph, pm, pl;
+        parts8(kr, ph, pm, pl);
+        uint16_t *dst = &Kp[b][kpos * kKRow + 8 * kdg];
+        *reinterpret_cast<v4i_t *>(dst) = ph;
+        *reinterpret_cast<v4i_t *>(dst + kKPart) = pm;
+        *reinterpret_cast<v4i_t *>(dst + 2 * kKPart) = pl;
+      }
+      if (vstage) {
+        v4i_t ph, pm, pl;
+        parts8(vr, ph, pm, pl);
+        uint16_t *dst = &Vp[b][vdim * kVRow + 8 * va];
+        *reinterpret_cast<v4i_t *>(dst) = ph;
+        *reinterpret_cast<v4i_t *>(dst + kVPart) = pm;
+        *reinterpret_cast<v4i_t *>(dst + 2 * kVPart) = pl;
+      }
+    };
+    // chunk at t0 from buffer b: S^T = K Q^T (leading and correction products in separate accumulators), the online
+    // softmax, O^T += V^T P^T
+    auto compute = [&](int b, int t0) {
+      v4f sc[2], sx[2];
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+        sc[t] = sx[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < kSs; st++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          const uint16_t *kb = &Kp[b][(16 * t + lc) * kKRow + 32 * st + 8 * lq];
+          const v4i_t kh = *reinterpret_cast<const v4i_t *>(kb), km = *reinterpret_cast<const v4i_t *>(kb + kKPart),
+                      kl = *reinterpret_cast<const v4i_t *>(kb + 2 * kKPart);
+          sc[t] = mfma(kh, qh[st], sc[t]);
+          sx[t] = mfma(kh, qm[st], sx[t]);
+          sx[t] = mfma(km, qh[st], sx[t]);
+          sx[t] = mfma(km, qm[st], sx[t]);
+          sx[t] = mfma(kh, ql[st], sx[t]);
+          sx[t] = mfma(kl, qh[st], sx[t]);
+        }
+      float cmax = -FLT_MAX;
+      float pv[8]; // slot 4 t + e: position 16 t + 4 lq + e
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int at = t0 + 16 * t + 4 * lq + e;
+          const bool live = at <= live_to;
+          const float raw = (sc[t][e] + sx[t][e]) * scale2;
+          bad |= live & !isfinite(raw);
+          pv[4 * t + e] = live ? raw : -FLT_MAX;
+          cmax = fmaxf(cmax, pv[4 * t + e]);
+        }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+      const float m_new = fmaxf(m_run, cmax);
+      const float alpha = exp2f(m_run - m_new);
+      float psum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float pe = pv[i] > -FLT_MAX ? exp2f(pv[i] - m_new) : 0.0f;
+        pv[i] = pe;
+        psum += pe;
+      }
+      psum += __shfl_xor(psum, 16);
+      psum += __shfl_xor(psum, 32);
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+      v4i_t ph, pm, pl;
+      parts8(pv, ph, pm, pl);
+      v4f ox[kDt];
+#pragma unroll
+      for (int d = 0; d < kDt; d++) {
+        o[d] *= alpha;
+        ox[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int d = 0; d < kDt; d++) {
+        const uint16_t *vb = &Vp[b][(16 * d + lc) * kVRow + 8 * lq];
+        const v4i_t vh = *reinterpret_cast<const v4i_t *>(vb), vm = *reinterpret_cast<const v4i_t *>(vb + kVPart),
+                    vl = *reinterpret_cast<const v4i_t *>(vb + 2 * kVPart);
+        o[d] = mfma(vh, ph, o[d]);
+        ox[d] = mfma(vh, pm, ox[d]);
+        ox[d] = mfma(vm, ph, ox[d]);
+        ox[d] = mfma(vm, pm, ox[d]);
+        ox[d] = mfma(vh, pl, ox[d]);
+        ox[d] = mfma(vl, ph, ox[d]);
+      }
+#pragma unroll
+      for (int d = 0; d < kDt; d++)
+        o[d] += ox[d];
+    };
+    if (chunks > 0) {
+      load(0);
+      wait_loads();
+      stage(0);
+      if (chunks > 1)
+        load(1);
+      __syncthreads();
+      for (int c = 0; c < chunks; c++) {
+        const int b = c & 1, t0 = (c0 + c) * kC;
+        if (c + 1 < chunks) { // chunk c + 1 into the other buffer, last read in step c - 1
+          wait_loads();
+          stage(b ^ 1);
+          if (c + 2 < chunks)
+            load(c + 2);
+        }
+        if (t0 <= wave_last) // wave-uniform: a wave whose rows end before the chunk has nothing to add
+          compute(b, t0);
+        __syncthreads();
+      }
+    }
+    if (!active)
+      continue;
+    if (split) { // the share's value sums, maximum (natural units) and sum, unnormalized, in slot [row][head][share]
+      float *slot = p.partial + (((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * p.splits + blockIdx.z) * p.slot;
+#pragma unroll
+      for (int d = 0; d < kDt; d++)
+        *reinterpret_cast<float4 *>(slot + 16 * d + 4 * lq) = float4{o[d][0], o[d][1], o[d][2], o[d][3]};
+      if (lq == 0) {
+        slot[HD] = m_run > -FLT_MAX ? m_run * 0.6931471805599453f : -FLT_MAX;
+        slot[HD + 1] = l_run;
+      }
+      continue;
+    }
+    const float inv = 1.0f / l_run;
+    float *dst = p.out + ((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * HD;
+#pragma unroll
+    for (int d = 0; d < kDt; d++)
+      *reinterpret_cast<float4 *>(dst + 16 * d + 4 * lq) =
+          float4{o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv};
+  }
+  if (bad)
+    p.flags[1] = 1;
+}
+
 // Block (chunk c, KV head g, query row r). Waves take positions t0 + w, t0 + w + 4, ...: lane l holds dimensions
 // l, l + 64, ... of the K row, dots it with each query head of the group held the same way, and the wave sum over the
 // lanes gives the score, (dot) / sqrtf(head_dim) like the reference. Then per head the chunk maximum, the
@@ -1361,11 +1619,17 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
     p.splits = flash_splits(job, p.chunks);
     const dim3 grid(p.splits ? (unsigned)tiles : (unsigned)((tiles + 1) / 2), (unsigned)job.n_kv_heads,
                     p.splits ? (unsigned)p.splits : 1u);
-    if (job.head_dim == 128)
+    const char *form = getenv("LLAMA_HIP_FLASH_FORM"); // fp32: attn_flash; unset or bf16x3: attn_flash3
+    const bool bf3 = !form || strcmp(form, "fp32") != 0;
+    if (bf3 && job.head_dim == 128)
+      hipLaunchKernelGGL(attn_flash3<128>, grid, dim3(kTileThreads), 0, stream, p);
+    else if (bf3)
+      hipLaunchKernelGGL(attn_flash3<64>, grid, dim3(kTileThreads), 0, stream, p);
+    else if (job.head_dim == 128)
       hipLaunchKernelGGL(attn_flash<128>, grid, dim3(kTileThreads), 0, stream, p);
     else
       hipLaunchKernelGGL(attn_flash<64>, grid, dim3(kTileThreads), 0, stream, p);
-    if (!launch_ok("attn_flash"))
+    if (!launch_ok(bf3 ? "attn_flash3" : "attn_flash"))
       return false;
     if (!p.splits)
       return true;

@@ -24,9 +24,13 @@ CFG = dict(dim=128, hidden_dim=256, n_layers=3, n_heads=8, n_kv_heads=2, vocab_s
 # three query heads per KV head (as Llama-3.2-3B's 24 over 8) with 64 dimensions: prompt batches take the
 # matrix-core attention with the tiles' last query vectors idle. At 384 dimensions (6 over 2 heads) seed 12 puts a
 # layer-0 attention output of position 15 exactly on an INT8 rounding tie, and the flip, kept in the KV cache, moves
-# every later row's logits by 0.6-0.9% in L2 on every device path alike; at 192 every quantizer input of the 71
-# positions stays at least 7e-6 of a quantum from a tie.
+# every later row's logits by 0.6-0.9% in L2 on every device path alike. At 192 the model quantizes about 190k values
+# over the 71 positions, so some lie within 1e-5 of a quantum of a tie, and FP32 rounding of the attention decides
+# them: with the FP32-product flash kernel every row matches the oracle to 0.00%, with the BF16-part kernel (the same
+# accuracy, other roundings) one value of position 22 flips and rows 22-39 move by 0.31-0.68%. Its batch rows are held
+# to 1.5% in L2, which one flip meets and an error in the kernels (a mask, a rotation, a row out of place) does not.
 CFG_GQA3 = dict(CFG, dim=192, n_heads=3, n_kv_heads=1)
+L2_ONE_TIE = 0.015
 GS = 32
 
 
@@ -115,10 +119,10 @@ def test_engine_forward_matches_the_oracle_forward(tmp_path, layout):
         assert L.kernels_kv_layout_select(b"head") == 1
 
 
-def check_logits(got, want, what, rel=0.02):
+def check_logits(got, want, what, rel=0.02, l2=0.005):
     span = float(want.max() - want.min())
     assert np.abs(got - want).max() <= rel * span, (what, np.abs(got - want).max(), span)
-    assert np.linalg.norm(got - want) <= 0.005 * np.linalg.norm(want), what
+    assert np.linalg.norm(got - want) <= l2 * np.linalg.norm(want), what
     assert got.argmax() == want.argmax(), what
 
 
@@ -142,17 +146,18 @@ def test_engine_forward_batch_matches_the_oracle_forward(tmp_path, layout, cfg):
         out = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens[:40]), 40, 0, lh.LOGITS_ALL)
         assert out, lh.last_error()
         got = np.ctypeslib.as_array(out, shape=(40, cfg["vocab_size"])).copy()
+        l2 = L2_ONE_TIE if cfg is CFG_GQA3 else 0.005
         for pos in range(40):
-            check_logits(got[pos], ref.step(int(tokens[pos]), pos), f"{layout} ALL row {pos}")
+            check_logits(got[pos], ref.step(int(tokens[pos]), pos), f"{layout} ALL row {pos}", l2=l2)
         out = L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens[40:70]), 30, 40, lh.LOGITS_LAST)
         assert out, lh.last_error()
         got = np.ctypeslib.as_array(out, shape=(cfg["vocab_size"],)).copy()
         for pos in range(40, 70):
             want = ref.step(int(tokens[pos]), pos)
-        check_logits(got, want, f"{layout} LAST at 69")
+        check_logits(got, want, f"{layout} LAST at 69", l2=l2)
         out = L.engine_forward(ctypes.byref(model), int(tokens[70]), 70)
         check_logits(np.ctypeslib.as_array(out, shape=(cfg["vocab_size"],)).copy(), ref.step(int(tokens[70]), 70),
-                     f"{layout} decode after the batches")
+                     f"{layout} decode after the batches", l2=l2)
         lh.record_failures()
         try:
             assert not L.engine_forward_batch(ctypes.byref(model), lh.ptr(tokens), 20, 70, lh.LOGITS_LAST)

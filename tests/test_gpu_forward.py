@@ -305,8 +305,8 @@ def test_attention_batch_rows(nh, nkv, hd, seq, pos0, m):
     (32, 8, 64, 2100, 1792, 256, "rows"),  # 1B heads late: 4 blocks per tile
 ])
 def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout, monkeypatch, splits=None):
-    """Batches of at least 16 rows with 64 or 128 dimensions per head run the flash kernel on the FP32 matrix cores:
-    every checked row within the float64 budget of the decode attention at its position and within twice it of the
+    """Batches of at least 16 rows with 64 or 128 dimensions per head run the flash kernel (its products from exact
+    BF16 parts on the BF16 matrix cores): every checked row within the float64 budget of the decode attention at its position and within twice it of the
     oracle, for GQA ratios 1-16 (those that do not divide 128 leave the tile's last vectors idle), both layouts, ragged
     tiles, short prompts and long contexts. A short batch late in a sequence splits each tile's positions over several
     blocks whose partials attn_merge combines (the last four cases, and the 16-row one)."""
@@ -324,6 +324,16 @@ def test_attention_batch_flash_shapes(nh, nkv, hd, seq, pos0, m, layout, monkeyp
     rows = range(m) if m <= 200 else sorted(r for r in {0, 1, 63, 64, 127, 128, 300, 1000, m - 2, m - 1} if r < m)
     for i in rows:
         check_attention(got[i], q.reshape(m, -1)[i], kc, vc, nh, nkv, hd, seq, pos0 + i, ps, hb, f"row {i}")
+
+
+@pytest.mark.parametrize("shape", [(16, 8, 128, 400, 130, 77, "head"), (32, 4, 64, 260, 64, 96, "rows"),
+                                   (24, 8, 128, 2100, 0, 2048, "head"), (32, 8, 128, 2100, 1792, 256, "head")])
+def test_attention_flash_fp32_form(shape, monkeypatch):
+    """LLAMA_HIP_FLASH_FORM=fp32 keeps the flash kernel whose products run on the FP32 matrix cores (attn_flash; the
+    default forms them from exact BF16 parts, attn_flash3): ragged tiles, 64 dimensions, the 3B prompt, a split late
+    batch, each row within the float64 budget."""
+    monkeypatch.setenv("LLAMA_HIP_FLASH_FORM", "fp32")
+    test_attention_batch_flash_shapes(*shape, monkeypatch)
 
 
 @pytest.mark.parametrize("splits,shape", [(3, (16, 8, 128, 400, 130, 77, "head")), (16, (32, 8, 128, 600, 0, 512, "head")),
