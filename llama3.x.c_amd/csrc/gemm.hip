@@ -930,6 +930,183 @@ template <bool F32> __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_lds
   store_tile(seg, t, acc, wm, wn, lane, p.m);
 }
 
+// ---- FP32 on the BF16 matrix cores -----------------------------------------------------------------------------
+//
+// mm_gemm_f32x3: the FP32 GEMM with every product formed from exact three-part BF16 splits of its FP32 operands, as
+// the batched attention forms them: x = h + m + l exactly (h the top 8 significant bits of x, m the next 8 of x - h, l
+// the rest, at most 8 bits) and x y is taken as hh + hm + mh + mm + hl + lh, the dropped products below 2^-23 of |x y|
+// and every BF16 product exact in FP32, so each sum is FP32-accurate. Six v_mfma_f32_16x16x32_bf16 (16 cycles) replace
+// eight v_mfma_f32_16x16x4_f32 (32 cycles each). The tiles, A and W staging (64 bytes of 16 rows per 1 KB block, XOR
+// swizzle, buffer loads straight into LDS), split K and epilogues are mm_gemm_lds's FP32 ones, with six stages so
+// that a round of steps is a whole number of pairs: the MFMAs run at every second step on the K values of the pair,
+// lane group q's slots 8 q .. 8 q + 3 from the first step's values 4 q .. 4 q + 3 and slots 8 q + 4 .. from the
+// second's, the same in A and in W, and each lane splits its own operands in registers.
+constexpr int kX3Stages = 6;
+constexpr int kX3BOff = kQ8ABlocks * kX3Stages * 1024;
+constexpr size_t kX3Lds = (size_t)kX3BOff + (size_t)kQ8BBlocks * kX3Stages * 1024;
+
+__global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_f32x3(MmParams p) {
+  extern __shared__ __align__(16) unsigned char q8_smem[];
+  typedef int v4i_t __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int logical = xcd_logical(blockIdx.x, p.grid.total * p.sk.splits);
+  const int tile = __builtin_amdgcn_readfirstlane(logical / p.sk.splits);
+  const int split = __builtin_amdgcn_readfirstlane(logical % p.sk.splits);
+  const TilePos t = q8_tile_of(p.grid, tile);
+  const TileSeg seg = q8_seg_of(p.grid, t.s);
+  const int s0 = split * p.sk.per, s1 = min(p.steps, s0 + p.sk.per);
+
+  const int lrow4 = lane >> 2, chunk = lane & 3;
+  const int ra = 32 * wave + lrow4;
+  const __amdgpu_buffer_rsrc_t rA = q8_buffer(p.a + (long long)t.m0 * p.arow, (long long)min(kQ8TileM, p.m - t.m0) * p.arow);
+  const int offA0 = (int)(ra * p.arow) + ((chunk ^ q8_swizzle(ra)) << 4);
+  const int offA1 = (int)((ra + 16) * p.arow) + ((chunk ^ q8_swizzle(ra + 16)) << 4);
+  const int rb0 = 16 * wave;
+  const int colB = t.swiglu ? t.n0 + (rb0 & 63) : t.n0 + rb0;
+  const unsigned char *wmat = (const unsigned char *)((t.swiglu && rb0 >= 64) ? seg.w3 : seg.w);
+  const long long brow = seg.ldw * 4;
+  const __amdgpu_buffer_rsrc_t rB = q8_buffer(wmat + (long long)colB * brow, (long long)min(16, seg.n - colB) * brow);
+  const int offB = (int)(lrow4 * brow) + ((chunk ^ q8_swizzle(lrow4)) << 4);
+  const __amdgpu_buffer_rsrc_t none = q8_buffer(p.a, 0);
+
+  auto issue = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value;
+    const bool live = step < s1;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none, (void *)(q8_smem + ((2 * wave) * kX3Stages + st) * 1024),
+                                             16, offA0, step * 64, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rA : none,
+                                             (void *)(q8_smem + ((2 * wave + 1) * kX3Stages + st) * 1024), 16, offA1,
+                                             step * 64, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(live ? rB : none,
+                                             (void *)(q8_smem + kX3BOff + (wave * kX3Stages + st) * 1024), 16, offB,
+                                             step * 64, 0, 0);
+  };
+
+  const int lrow = lane & 15, lq = lane >> 4;
+  const int lane_part = lrow * 64 + ((lq ^ q8_swizzle(lrow)) << 4);
+  const unsigned char *abase = q8_smem + (4 * wm) * kX3Stages * 1024 + lane_part;
+  const unsigned char *bbase[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    bbase[j] = q8_smem + kX3BOff + (b_row(t.swiglu, wn, j) / 16) * kX3Stages * 1024 + lane_part;
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  struct Operands {
+    v4f a[4], b[4];
+  };
+  auto operands = [&](auto ST, Operands &o) {
+    constexpr int st = decltype(ST)::value;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      o.a[i] = *reinterpret_cast<const v4f *>(abase + (i * kX3Stages + st) * 1024);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      o.b[j] = *reinterpret_cast<const v4f *>(bbase[j] + st * 1024);
+  };
+  // the high halves of the three parts of x and y, packed: x in the low half of each dword
+  struct Parts2 {
+    int h, m, l;
+  };
+  auto parts2 = [](float x, float y) {
+    const unsigned ux = __builtin_bit_cast(unsigned, x), uy = __builtin_bit_cast(unsigned, y);
+    const float rx = x - __builtin_bit_cast(float, ux & 0xFFFF0000u), ry = y - __builtin_bit_cast(float, uy & 0xFFFF0000u);
+    const unsigned ux1 = __builtin_bit_cast(unsigned, rx), uy1 = __builtin_bit_cast(unsigned, ry);
+    const float rx2 = rx - __builtin_bit_cast(float, ux1 & 0xFFFF0000u), ry2 = ry - __builtin_bit_cast(float, uy1 & 0xFFFF0000u);
+    return Parts2{(int)__builtin_amdgcn_perm(uy, ux, 0x07060302u), (int)__builtin_amdgcn_perm(uy1, ux1, 0x07060302u),
+                  (int)__builtin_amdgcn_perm(__builtin_bit_cast(unsigned, ry2), __builtin_bit_cast(unsigned, rx2),
+                                             0x07060302u)};
+  };
+  auto parts8 = [&](const v4f &e, const v4f &o, v4i_t &ph, v4i_t &pm, v4i_t &pl) {
+    const Parts2 p0 = parts2(e[0], e[1]), p1 = parts2(e[2], e[3]), p2 = parts2(o[0], o[1]), p3 = parts2(o[2], o[3]);
+    ph = v4i_t{p0.h, p1.h, p2.h, p3.h};
+    pm = v4i_t{p0.m, p1.m, p2.m, p3.m};
+    pl = v4i_t{p0.l, p1.l, p2.l, p3.l};
+  };
+  auto mfma = [](const v4i_t &a, const v4i_t &b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf_t, a), __builtin_bit_cast(v8bf_t, b), c, 0,
+                                                    0, 0);
+  };
+  // the MFMAs of a pair of steps (e the first, o the second): the small products first
+  auto mfmas3 = [&](const Operands &e, const Operands &o) {
+    v4i_t bh[4], bm[4], bl[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      parts8(e.b[j], o.b[j], bh[j], bm[j], bl[j]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v4i_t ah, am, al;
+      parts8(e.a[i], o.a[i], ah, am, al);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] = mfma(al, bh[j], acc[i][j]);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] = mfma(ah, bl[j], acc[i][j]);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] = mfma(am, bm[j], acc[i][j]);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] = mfma(am, bh[j], acc[i][j]);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] = mfma(ah, bm[j], acc[i][j]);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[i][j] = mfma(ah, bh[j], acc[i][j]);
+    }
+  };
+
+  // As mm_gemm_lds: step + 1's loads have landed once only the later steps' may be outstanding, the barrier makes that
+  // true of every wave and frees the stage step - 1 used, which step + 5 now fills; the operands of step + 1 are read
+  // a step ahead. The MFMAs run at odd stages on the pair (held, cur).
+  Operands held, cur, next;
+  auto advance = [&](int step, auto ST) {
+    constexpr int st = decltype(ST)::value, nst = (st + 1) % kX3Stages, fill = (st + kX3Stages - 1) % kX3Stages;
+    wait_vmcnt<(kX3Stages - 3) * kMmLoadsPerStep>();
+    __builtin_amdgcn_s_barrier();
+    issue(step + kX3Stages - 1, std::integral_constant<int, fill>{});
+    operands(std::integral_constant<int, nst>{}, next);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (st % 2 == 1) {
+      mfmas3(held, cur);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      held = cur;
+    }
+    cur = next;
+  };
+
+  issue(s0, std::integral_constant<int, 0>{});
+  issue(s0 + 1, std::integral_constant<int, 1>{});
+  issue(s0 + 2, std::integral_constant<int, 2>{});
+  issue(s0 + 3, std::integral_constant<int, 3>{});
+  issue(s0 + 4, std::integral_constant<int, 4>{});
+  wait_vmcnt<(kX3Stages - 2) * kMmLoadsPerStep>();
+  __builtin_amdgcn_s_barrier();
+  operands(std::integral_constant<int, 0>{}, cur);
+  for (int step = s0; step < s1; step += kX3Stages) {
+    advance(step, std::integral_constant<int, 0>{});
+    advance(step + 1, std::integral_constant<int, 1>{});
+    advance(step + 2, std::integral_constant<int, 2>{});
+    advance(step + 3, std::integral_constant<int, 3>{});
+    advance(step + 4, std::integral_constant<int, 4>{});
+    advance(step + 5, std::integral_constant<int, 5>{});
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if (p.sk.splits > 1 && !split_combine<kQ8Threads>(p.sk, tile, split, acc))
+    return;
+  store_tile(seg, t, acc, wm, wn, lane, p.m);
+}
+
 // ---- BF16, wide tiles ---------------------------------------------------------------------------------------------
 //
 // The BF16 kernel above waits on L2: its operands arrive at about 18 bytes per clock per CU, far below the L1's rate,
@@ -2053,6 +2230,27 @@ bool launch_q8_group_dots(int32_t *dots, const int8_t *xq, int m, int k, int gs,
 
 namespace {
 
+// Which kernel takes the aligned FP32 GEMM: mm_gemm_f32x3 (products from exact BF16 parts; 3B prefill GEMMs at 512
+// rows 23.7 -> 17.0 ms) unless LLAMA_HIP_F32_FORM = fp32 picks mm_gemm_lds<true> (FP32 products); read on every call.
+bool f32_on_bf16_parts() {
+  const char *form = getenv("LLAMA_HIP_F32_FORM");
+  return !form || strcmp(form, "fp32") != 0;
+}
+
+bool x3_launch(MmParams p, hipStream_t stream) {
+  static const hipError_t status =
+      hipFuncSetAttribute((const void *)mm_gemm_f32x3, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kX3Lds);
+  if (!check_hip(status, "allowing the FP32 GEMM on BF16 parts its LDS"))
+    return false;
+  p.sk.splits = p.grid.total > kSplitSlots ? 1 : choose_splits(p.grid.total, p.steps, &p.sk.per);
+  if (p.sk.splits == 1)
+    p.sk.per = p.steps;
+  p.sk.partial = (v4f *)device().split_partial;
+  p.sk.count = device().split_count;
+  hipLaunchKernelGGL(mm_gemm_f32x3, dim3((unsigned)(p.grid.total * p.sk.splits)), dim3(kQ8Threads), kX3Lds, stream, p);
+  return launch_ok("mm_gemm_f32x3");
+}
+
 template <bool F32> bool mm_launch(MmParams p, hipStream_t stream) {
   static const hipError_t status =
       hipFuncSetAttribute((const void *)mm_gemm_lds<F32>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMmLds);
@@ -2165,7 +2363,7 @@ bool launch_f32_gemm(const GemmF32Job &job, hipStream_t stream) {
     p.a = (const unsigned char *)job.a;
     p.arow = (long long)job.lda * 4;
     p.steps = job.k / 16;
-    return mm_launch<true>(p, stream);
+    return f32_on_bf16_parts() ? x3_launch(p, stream) : mm_launch<true>(p, stream);
   }
   F32Params f{};
   f.grid = make_grid(job.seg, job.nseg, job.m);

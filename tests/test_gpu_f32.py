@@ -279,13 +279,17 @@ def test_bf16_gemm_reference_golden():
 
 @pytest.mark.parametrize("m,n,k", [(300, 200, 1024), (513, 136, 3072), (40, 130, 16 * 37), (256, 256, 8192),
                                    (600, 600, 512)])
-@pytest.mark.parametrize("mode", ["f32", "bf16", "bf16-wide"])
-def test_pipelined_gemm_split_k(m, n, k, mode):
-    """Rows 16-byte aligned and K a multiple of 16 take the pipelined kernel. Every split count (0 = the automatic
-    choice) meets the budget for every kind and for three segments sharing A; a repeated call with the same split count
-    gives the same bits (the arrival counters are back at zero and partial sums are added in split order)."""
+@pytest.mark.parametrize("mode", ["f32", "f32-fp32", "bf16", "bf16-wide"])
+def test_pipelined_gemm_split_k(m, n, k, mode, monkeypatch):
+    """Rows 16-byte aligned and K a multiple of 16 take the pipelined kernel: for FP32 mm_gemm_f32x3 (products from
+    exact BF16 parts, pairs of 16-value K steps; 37 steps leave a pair's second half empty) or, with
+    LLAMA_HIP_F32_FORM=fp32, mm_gemm_lds (FP32 products). Every split count (0 = the automatic choice) meets the budget
+    for every kind and for three segments sharing A; a repeated call with the same split count gives the same bits
+    (the arrival counters are back at zero and partial sums are added in split order)."""
     L = hu.lib()
     L.llhip_set_bf16_tile(2 if mode == "bf16-wide" else 1)
+    if mode == "f32-fp32":
+        monkeypatch.setenv("LLAMA_HIP_F32_FORM", "fp32")
     mode = mode[:4]
     rng = orc.Rng(orc.SEED + 81 * m + n + k)
     lda, ldc = k + 4, n + 7
