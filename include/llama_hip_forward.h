@@ -121,6 +121,15 @@ void k_attention_kv(float *out, const float *q, const float *key_cache, const fl
                     AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int position);
 void k_attention_batch_kv(float *out, const float *q, const float *key_cache, const float *value_cache, float *att,
                           AttentionWork *work, int n_heads, int n_kv_heads, int head_dim, int seq_len, int pos0, int m);
+/* No counterpart in the reference: k_attention_batch_kv, then k_quantize_rows of its m rows of n_heads * head_dim
+ * values in groups of gs into q and s, bitwise those two calls (for the engine's batched forward, src/tp.c:558-576,
+ * where the attention rows are quantized for Wo). The batched kernel quantizes its own output where it runs a tile
+ * whole (out is then not written); otherwise out receives the FP32 rows and they are quantized from there, so out must
+ * hold them. gs one of 16, 32, 64, 128 dividing head_dim; q 4-byte aligned; a non-finite value fails at the next
+ * synchronization, as k_quantize_rows does. */
+void llhip_attention_batch_quantize(int8_t *q, float *s, int gs, float *out, const float *query, const float *key_cache,
+                                    const float *value_cache, int n_heads, int n_kv_heads, int head_dim, int seq_len,
+                                    int pos0, int m);
 
 /* kernels.h:46-47 and testing.h: the attention kernels' names ("split" for both: one device kernel) and the test-time
  * selectors, which accept the reference's names (tiled / split, split / group; rows / head). */

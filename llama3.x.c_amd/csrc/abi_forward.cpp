@@ -148,9 +148,11 @@ size_t cache_floats(int n_kv_heads, int head_dim, int last, size_t pos_stride, s
 
 // noalloc: the partials go to the per-device scratch array instead of the grown workspace, and nothing may allocate
 // (no staging of host buffers, no device init).
+// The attention entry points (k_attention*, the allocation-free form, and with qout the rows quantized in groups of
+// qgs as k_quantize_rows would quantize them from out).
 void attention(const char *name, float *out, const float *q, const float *key_cache, const float *value_cache,
                int n_heads, int n_kv_heads, int head_dim, int seq_len, int pos0, int m, size_t pos_stride,
-               size_t head_base, bool noalloc = false) {
+               size_t head_base, bool noalloc = false, int8_t *qout = nullptr, float *qscale = nullptr, int qgs = 0) {
   if (m <= 0 || n_heads <= 0)
     return;
   if (!attention_shape_ok(n_heads, n_kv_heads, head_dim)) {
@@ -184,6 +186,12 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
   const size_t cache = cache_floats(n_kv_heads, head_dim, pos0 + m - 1, pos_stride, head_base) * f;
   Ref Q = call.in(q, row * m), K = call.in(key_cache, cache), V = call.in(value_cache, cache);
   Ref O = call.out(out, row * m, false);
+  const size_t qrow = (size_t)n_heads * head_dim;
+  Ref QO{}, QS{};
+  if (qout) {
+    QO = call.out(qout, qrow * m, false);
+    QS = call.out(qscale, qrow / qgs * m * f, false);
+  }
   if (noalloc && call.staged()) { // staging would allocate the arena
     raise("%s: every buffer must be device memory or inside a registered range", name);
     return;
@@ -196,6 +204,11 @@ void attention(const char *name, float *out, const float *q, const float *key_ca
   // the split kernels' need is checked; a fused RoPE is taken only for one row, which never runs the flash kernel
   if (noalloc)
     job.partial_room = kAttentionScratchFloats;
+  if (qout) {
+    job.qout = call.ptr<int8_t>(QO);
+    job.qscale = call.ptr<float>(QS);
+    job.qgs = qgs;
+  }
   if (noalloc && !attention_uses_flash(job) && partial_floats > kAttentionScratchFloats) {
     raise("%s: %d rows of %d heads up to position %d need %zu floats of scratch; it holds %zu", name, m, n_heads,
           pos0 + m - 1, partial_floats, kAttentionScratchFloats);
@@ -585,6 +598,28 @@ void k_attention_batch_kv(float *out, const float *q, const float *key_cache, co
   strides(n_kv_heads, head_dim, seq_len, kv_head_major(), &pos_stride, &head_base);
   k_attention_batch_layout(out, q, key_cache, value_cache, att, work, n_heads, n_kv_heads, head_dim, seq_len, pos0, m,
                            pos_stride, head_base);
+}
+
+void llhip_attention_batch_quantize(int8_t *q, float *s, int gs, float *out, const float *query, const float *key_cache,
+                                    const float *value_cache, int n_heads, int n_kv_heads, int head_dim, int seq_len,
+                                    int pos0, int m) {
+  const char *name = "llhip_attention_batch_quantize";
+  if (!q || !s) {
+    raise("%s: null buffer", name);
+    return;
+  }
+  if ((gs != 16 && gs != 32 && gs != 64 && gs != 128) || head_dim <= 0 || head_dim % gs) {
+    raise("%s: group size %d must be 16, 32, 64 or 128 and divide head_dim %d", name, gs, head_dim);
+    return;
+  }
+  if ((uintptr_t)q & 3) {
+    raise("%s: q must be 4-byte aligned", name);
+    return;
+  }
+  size_t pos_stride, head_base;
+  strides(n_kv_heads, head_dim, seq_len, kv_head_major(), &pos_stride, &head_base);
+  attention(name, out, query, key_cache, value_cache, n_heads, n_kv_heads, head_dim, seq_len, pos0, m, pos_stride,
+            head_base, false, q, s, gs);
 }
 
 // kernels.h:45-47 and testing.h: one device kernel serves both forms (split K over 64-position chunks).

@@ -248,6 +248,12 @@ struct AttentionJob {
   // floats of `partial` the batched kernel may use when it splits a tile's positions over blocks (0: the
   // attention_partial_floats of the job, which any split fits)
   size_t partial_room = 0;
+  // the rows quantized by the k_quantize rule in groups of qgs values (qout rows of n_heads * head_dim bytes, qscale
+  // rows of n_heads * head_dim / qgs scales): in the flash kernel's epilogue where it runs a tile unsplit, otherwise
+  // from out by a quantize launch after it (out then holds the FP32 rows; in the fused case it is not written)
+  int8_t *qout = nullptr;
+  float *qscale = nullptr;
+  int qgs = 0;
 };
 bool attention_shape_ok(int n_heads, int n_kv_heads, int head_dim); // kv_mul <= 16, head_dim <= 256
 size_t attention_partial_floats(int rows, int n_heads, int head_dim, int last_position);

@@ -713,9 +713,15 @@ float *forward_rows(Model *model, Engine *e, const int *tokens, int count, int p
         k_kv_store(vc, vd, kvl, pos0, count, nkv, hd, c.seq_len);
       }
     }
-    k_attention_batch_kv(e->bxb, e->bq, kc, vc, nullptr, &e->work, nh, nkv, hd, c.seq_len, pos0, count);
+    // for Q8_0 the attention rows quantized in the batched kernel's epilogue where the group size allows (bitwise
+    // k_attention_batch_kv then k_quantize_rows)
+    if (e->q8 && (gs == 16 || gs == 32 || gs == 64 || gs == 128) && hd % gs == 0)
+      llhip_attention_batch_quantize(e->bxq, e->bxs, gs, e->bxb, e->bq, kc, vc, nh, nkv, hd, c.seq_len, pos0, count);
+    else
+      k_attention_batch_kv(e->bxb, e->bq, kc, vc, nullptr, &e->work, nh, nkv, hd, c.seq_len, pos0, count);
     if (e->q8) {
-      k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
+      if (!((gs == 16 || gs == 32 || gs == 64 || gs == 128) && hd % gs == 0))
+        k_quantize_rows(e->bxq, e->bxs, e->bxb, d, count, d, gs);
       const GemmQ8Segment wo{e->bx, d, e->wo[l].k8(), K8Weight{}, nullptr, nullptr, d, GEMM_ADD};
       k_gemm_q8(e->bxq, e->bxs, count, d, gs, &wo, 1);
     } else {

@@ -18,6 +18,7 @@
 
 #include "common.h"
 #include "lanes.h"
+#include "quant.h"
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
@@ -182,6 +183,42 @@ __global__ __launch_bounds__(kThreads) void rope_kv_rows(float *__restrict__ q, 
   }
 }
 
+// rope_kv_rows for head_dim HD = 64 or 128: block (x, row) takes units 256 x .. of one row (no division by a runtime
+// size, so none in 64 bits), each unit the float4 rope_kv_rows gives the thread of the same row and unit; the same
+// products in the same order, so the results are bitwise those of rope_kv_rows.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void rope_kv_rows_hd(float *__restrict__ q, size_t q_stride, float *__restrict__ k,
+                                                            const float *__restrict__ v, size_t kv_stride,
+                                                            const float *__restrict__ table, size_t table_stride,
+                                                            int n_heads, int n_kv_heads, float *__restrict__ key_cache,
+                                                            float *__restrict__ value_cache, int pos0,
+                                                            size_t pos_stride, size_t head_base) {
+  constexpr int hd4 = HD / 4;
+  const int qu = n_heads * hd4, ku = n_kv_heads * hd4;
+  const int u = blockIdx.x * kThreads + threadIdx.x, r = blockIdx.y;
+  if (u >= qu + 2 * ku)
+    return;
+  const float *t = table + (size_t)r * table_stride;
+  if (u < qu) {
+    const int h = u / hd4, d = 4 * (u % hd4);
+    float4 *p = reinterpret_cast<float4 *>(q + (size_t)r * q_stride + (size_t)h * HD + d);
+    *p = rotate4(*p, t, HD, d);
+    return;
+  }
+  const bool is_k = u < qu + ku;
+  const int w = is_k ? u - qu : u - qu - ku, g = w / hd4, d = 4 * (w % hd4);
+  const size_t at = (size_t)r * kv_stride + (size_t)g * HD + d;
+  const size_t slot = (size_t)(pos0 + r) * pos_stride + (size_t)g * head_base + d;
+  if (is_k) {
+    float4 *p = reinterpret_cast<float4 *>(k + at);
+    const float4 x = rotate4(*p, t, HD, d);
+    *p = x;
+    *reinterpret_cast<float4 *>(key_cache + slot) = x;
+  } else {
+    *reinterpret_cast<float4 *>(value_cache + slot) = *reinterpret_cast<const float4 *>(v + at);
+  }
+}
+
 // ---- embedding rows -------------------------------------------------------------------------------------------------
 
 // out[i][j] = table[ids[i]][j] * scales[(ids[i] * dim + j) / gs]: the int8 value converted exactly and one float
@@ -239,6 +276,10 @@ struct AttnParams {
   size_t pos_stride, head_base;
   float divisor; // sqrtf(head_dim)
   int splits;    // batched flash form: blocks per tile, each over a share of its chunks (0: the tile whole)
+  // attn_flash3 unsplit: the output rows quantized in groups of qgs values (k_quantize) instead of stored in FP32
+  int8_t *qout;
+  float *qscale;
+  int qgs;
 };
 
 constexpr int kTileThreads = 512;
@@ -1008,7 +1049,7 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash3(At
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0,
                                                     0);
   };
-  bool bad = false;
+  bool bad = false, qbad = false;
   const bool split = p.splits > 0;
   for (int pass = 0; pass < 2; pass++) {
     const int tile = split ? (int)blockIdx.x : pass == 0 ? ntiles - 1 - (int)blockIdx.x : (int)blockIdx.x;
@@ -1187,7 +1228,39 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash3(At
       continue;
     }
     const float inv = 1.0f / l_run;
-    float *dst = p.out + ((size_t)row * p.n_heads + (size_t)g * kv_mul + h) * HD;
+    const size_t vec = (size_t)row * p.n_heads + (size_t)g * kv_mul + h; // this lane's query vector
+    if (p.qout) { // k_quantize of the rows the FP32 store below would write: a group of qgs dimensions is qgs / 16 of
+      // the lane's dimension tiles and the same tiles of the vector's other three lanes (lq), so its maximum is the
+      // lanes' maximum over those tiles; each value is quantized as quantize_lanes does, the group's scale from lq 0
+      const int tiles = p.qgs / 16;
+      int8_t *qrow = p.qout + vec * HD;
+      for (int d0 = 0; d0 < kDt; d0 += tiles) {
+        float peak = 0.0f;
+#pragma unroll
+        for (int d = 0; d < kDt; d++)
+          if (d >= d0 && d < d0 + tiles)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              peak = fmaxf(peak, fabsf(o[d][e] * inv)); // a NaN is skipped here and caught by quantize_fast
+        peak = fmaxf(peak, __shfl_xor(peak, 16));
+        peak = fmaxf(peak, __shfl_xor(peak, 32));
+        const float scale = peak / 127.0f;
+        bool ok;
+        const float rinv = group_reciprocal(scale, ok);
+#pragma unroll
+        for (int d = 0; d < kDt; d++)
+          if (d >= d0 && d < d0 + tiles) {
+            const float x[4] = {o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv};
+            int qv[4];
+            quantize_fast(x, scale, rinv, ok, qv, qbad);
+            *reinterpret_cast<int *>(qrow + 16 * d + 4 * lq) = pack_bytes(qv[0], qv[1], qv[2], qv[3]);
+          }
+        if (lq == 0)
+          p.qscale[(vec * HD + 16 * d0) / p.qgs] = scale;
+      }
+      continue;
+    }
+    float *dst = p.out + vec * HD;
 #pragma unroll
     for (int d = 0; d < kDt; d++)
       *reinterpret_cast<float4 *>(dst + 16 * d + 4 * lq) =
@@ -1195,6 +1268,8 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash3(At
   }
   if (bad)
     p.flags[1] = 1;
+  if (qbad)
+    p.flags[0] = 1;
 }
 
 // Block (chunk c, KV head g, query row r). Waves take positions t0 + w, t0 + w + 4, ...: lane l holds dimensions
@@ -1439,7 +1514,18 @@ bool launch_rope(float *q, size_t q_stride, float *k, size_t k_stride, const flo
 bool launch_rope_kv_rows(float *q, size_t q_stride, float *k, const float *v, size_t kv_stride, const float *table,
                          size_t table_stride, int rows, int n_heads, int n_kv_heads, int head_dim, float *key_cache,
                          float *value_cache, int pos0, size_t pos_stride, size_t head_base, hipStream_t stream) {
-  const long long threads = (long long)rows * (n_heads + 2LL * n_kv_heads) * (head_dim / 4);
+  const int per_row = (n_heads + 2 * n_kv_heads) * (head_dim / 4);
+  if ((head_dim == 128 || head_dim == 64) && rows <= 65535) {
+    const dim3 grid((unsigned)((per_row + kThreads - 1) / kThreads), (unsigned)rows);
+    if (head_dim == 128)
+      hipLaunchKernelGGL(rope_kv_rows_hd<128>, grid, dim3(kThreads), 0, stream, q, q_stride, k, v, kv_stride, table,
+                         table_stride, n_heads, n_kv_heads, key_cache, value_cache, pos0, pos_stride, head_base);
+    else
+      hipLaunchKernelGGL(rope_kv_rows_hd<64>, grid, dim3(kThreads), 0, stream, q, q_stride, k, v, kv_stride, table,
+                         table_stride, n_heads, n_kv_heads, key_cache, value_cache, pos0, pos_stride, head_base);
+    return launch_ok("rope_kv_rows_hd");
+  }
+  const long long threads = (long long)rows * per_row;
   hipLaunchKernelGGL(rope_kv_rows, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, stream, q,
                      q_stride, k, v, kv_stride, table, table_stride, rows, n_heads, n_kv_heads, head_dim, key_cache,
                      value_cache, pos0, pos_stride, head_base);
@@ -1583,6 +1669,22 @@ int flash_splits(const AttentionJob &job, int chunks) {
   return splits > 1 ? splits : 0;
 }
 
+// The rows of a job that asks for them quantized, from its FP32 output (the paths that do not quantize in their
+// epilogue): k_quantize_rows of n_heads * head_dim values per row.
+bool quantize_attention_rows(const AttentionJob &job, hipStream_t stream) {
+  if (!job.qout)
+    return true;
+  QuantizeJob qj{};
+  qj.q = job.qout;
+  qj.s = job.qscale;
+  qj.x = job.out;
+  qj.ldx = (size_t)job.n_heads * job.head_dim;
+  qj.m = job.rows;
+  qj.n = job.n_heads * job.head_dim;
+  qj.gs = job.qgs;
+  return launch_quantize(qj, stream);
+}
+
 bool launch_attention(const AttentionJob &job, float *partial, hipStream_t stream) {
   AttnParams p{};
   p.out = job.out;
@@ -1621,6 +1723,12 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
                     p.splits ? (unsigned)p.splits : 1u);
     const char *form = getenv("LLAMA_HIP_FLASH_FORM"); // fp32: attn_flash; unset or bf16x3: attn_flash3
     const bool bf3 = !form || strcmp(form, "fp32") != 0;
+    const bool fused_quant = job.qout && bf3 && !p.splits;
+    if (fused_quant) {
+      p.qout = job.qout;
+      p.qscale = job.qscale;
+      p.qgs = job.qgs;
+    }
     if (bf3 && job.head_dim == 128)
       hipLaunchKernelGGL(attn_flash3<128>, grid, dim3(kTileThreads), 0, stream, p);
     else if (bf3)
@@ -1631,12 +1739,14 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
       hipLaunchKernelGGL(attn_flash<64>, grid, dim3(kTileThreads), 0, stream, p);
     if (!launch_ok(bf3 ? "attn_flash3" : "attn_flash"))
       return false;
-    if (!p.splits)
-      return true;
-    const long long threads = (long long)job.rows * job.n_heads * (job.head_dim / 4);
-    hipLaunchKernelGGL(attn_merge_shares, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       stream, p);
-    return launch_ok("attn_merge_shares");
+    if (p.splits) {
+      const long long threads = (long long)job.rows * job.n_heads * (job.head_dim / 4);
+      hipLaunchKernelGGL(attn_merge_shares, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                         stream, p);
+      if (!launch_ok("attn_merge_shares"))
+        return false;
+    }
+    return fused_quant || quantize_attention_rows(job, stream);
   }
   // decode: the slice-parallel kernel for 64 or 128 dimensions and up to eight query vectors per KV head
   if (aligned && job.rows == 1 && (job.head_dim == 64 || job.head_dim == 128) && kv_mul <= kDecodeMaxQv &&
@@ -1684,7 +1794,7 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
       return false;
   }
   hipLaunchKernelGGL(attn_merge, dim3((unsigned)job.n_heads, (unsigned)job.rows), dim3(kThreads), 0, stream, p);
-  return launch_ok("attn_merge");
+  return launch_ok("attn_merge") && quantize_attention_rows(job, stream);
 }
 
 } // namespace llhip

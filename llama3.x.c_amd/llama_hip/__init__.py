@@ -117,6 +117,7 @@ _SIGNATURES = {
     "k_rmsnorm_rows": (None, [P, P, P, I32, I32, ctypes.c_float]),
     "llhip_rmsnorm_quantize_rows": (None, [P, P, P, P, I32, I32, ctypes.c_float, I32]),
     "llhip_rope_kv_store_rows": (None, [P, SZ, P, P, SZ, P, SZ, I32, I32, I32, I32, P, P, I32, I32]),
+    "llhip_attention_batch_quantize": (None, [P, P, I32, P, P, P, P, I32, I32, I32, I32, I32, I32]),
     "llhip_gemm_q8_swiglu_quantize": (I32, [P, P, I32, I32, I32, P, P, I32, P, P]),
     "k_rope_table": (None, [P, I32, P]),
     "k_rope_apply": (None, [P, P, P, I32, I32, I32]),

@@ -336,6 +336,42 @@ def test_attention_flash_fp32_form(shape, monkeypatch):
     test_attention_batch_flash_shapes(*shape, monkeypatch)
 
 
+@pytest.mark.parametrize("nh,nkv,hd,seq,pos0,m,gs,layout,form", [
+    (32, 8, 128, 600, 0, 512, 64, "head", None),      # 8B heads: quantized in the flash kernel's epilogue
+    (24, 8, 128, 300, 10, 100, 32, "rows", None),     # kv_mul 3 (idle vectors), groups of 32
+    (32, 8, 64, 300, 0, 130, 64, "head", None),       # 64 dimensions, a group per head
+    (16, 4, 128, 200, 3, 40, 128, "head", None),      # a group of a whole head
+    (32, 8, 128, 2100, 1792, 256, 64, "head", None),  # a late batch split over blocks: merged, then quantized
+    (8, 2, 128, 200, 50, 8, 64, "rows", None),        # 8 rows: the tile kernels, then quantized
+    (32, 8, 128, 600, 0, 200, 16, "head", "fp32"),    # the FP32-product kernel, then quantized
+])
+def test_attention_batch_quantize_fused(nh, nkv, hd, seq, pos0, m, gs, layout, form, monkeypatch):
+    """llhip_attention_batch_quantize: bitwise k_attention_batch_kv then k_quantize_rows of its rows, whether the
+    flash kernel quantizes in its epilogue or the rows are quantized after it."""
+    if form:
+        monkeypatch.setenv("LLAMA_HIP_FLASH_FORM", form)
+    L = hu.lib()
+    assert L.kernels_kv_layout_select(layout.encode()) == 1
+    try:
+        T = hu.torch()
+        rng = orc.Rng(orc.SEED + 950 + m + hd + gs)
+        kc, vc, q = rng.normal(seq * nkv * hd, 0, 1), rng.normal(seq * nkv * hd, 0, 1), rng.normal(m * nh * hd, 0, 1)
+        dq, dk, dv = hu.dev(q), hu.dev(kc), hu.dev(vc)
+        n = nh * hd
+        out, out2 = hu.empty(m * n, T.float32), hu.empty(m * n, T.float32)
+        xq, xq2 = hu.empty(m * n, T.int8), hu.empty(m * n, T.int8)
+        xs, xs2 = hu.empty(m * n // gs, T.float32), hu.empty(m * n // gs, T.float32)
+        L.llhip_attention_batch_quantize(lh.ptr(xq), lh.ptr(xs), gs, lh.ptr(out), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), nh,
+                                         nkv, hd, seq, pos0, m)
+        L.k_attention_batch_kv(lh.ptr(out2), lh.ptr(dq), lh.ptr(dk), lh.ptr(dv), None, None, nh, nkv, hd, seq, pos0, m)
+        L.k_quantize_rows(lh.ptr(xq2), lh.ptr(xs2), lh.ptr(out2), n, m, n, gs)
+        assert not lh.last_error()
+        assert np.array_equal(hu.host(xq), hu.host(xq2))
+        assert np.array_equal(hu.bits(hu.host(xs)), hu.bits(hu.host(xs2)))
+    finally:
+        assert L.kernels_kv_layout_select(b"head") == 1
+
+
 @pytest.mark.parametrize("splits,shape", [(3, (16, 8, 128, 400, 130, 77, "head")), (16, (32, 8, 128, 600, 0, 512, "head")),
                                           (5, (12, 4, 64, 300, 21, 100, "rows")), (2, (24, 8, 128, 2100, 0, 2048, "head"))])
 def test_attention_flash_forced_splits(splits, shape, monkeypatch):
