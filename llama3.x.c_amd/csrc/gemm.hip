@@ -1024,51 +1024,61 @@ __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_f32x3(MmParams p) {
                   (int)__builtin_amdgcn_perm(__builtin_bit_cast(unsigned, ry2), __builtin_bit_cast(unsigned, rx2),
                                              0x07060302u)};
   };
-  auto parts8 = [&](const v4f &e, const v4f &o, v4i_t &ph, v4i_t &pm, v4i_t &pl) {
-    const Parts2 p0 = parts2(e[0], e[1]), p1 = parts2(e[2], e[3]), p2 = parts2(o[0], o[1]), p3 = parts2(o[2], o[3]);
-    ph = v4i_t{p0.h, p1.h, p2.h, p3.h};
-    pm = v4i_t{p0.m, p1.m, p2.m, p3.m};
-    pl = v4i_t{p0.l, p1.l, p2.l, p3.l};
-  };
   auto mfma = [](const v4i_t &a, const v4i_t &b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf_t, a), __builtin_bit_cast(v8bf_t, b), c, 0,
                                                     0, 0);
   };
-  // the MFMAs of a pair of steps (e the first, o the second): the small products first
-  auto mfmas3 = [&](const Operands &e, const Operands &o) {
-    v4i_t bh[4], bm[4], bl[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      parts8(e.b[j], o.b[j], bh[j], bm[j], bl[j]);
+  // A pair's operands as BF16 parts: dwords 0 and 1 of each part from the first step's four values (split at the
+  // first step, while the previous pair's MFMAs drain), dwords 2 and 3 from the second's
+  struct PairParts {
+    v4i_t ah[4], am[4], al[4], bh[4], bm[4], bl[4];
+  };
+  auto split_half = [&](const Operands &o, PairParts &pp, int half) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      v4i_t ah, am, al;
-      parts8(e.a[i], o.a[i], ah, am, al);
+      const Parts2 lo = parts2(o.a[i][0], o.a[i][1]), hi = parts2(o.a[i][2], o.a[i][3]);
+      pp.ah[i][2 * half] = lo.h, pp.ah[i][2 * half + 1] = hi.h;
+      pp.am[i][2 * half] = lo.m, pp.am[i][2 * half + 1] = hi.m;
+      pp.al[i][2 * half] = lo.l, pp.al[i][2 * half + 1] = hi.l;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const Parts2 lo = parts2(o.b[j][0], o.b[j][1]), hi = parts2(o.b[j][2], o.b[j][3]);
+      pp.bh[j][2 * half] = lo.h, pp.bh[j][2 * half + 1] = hi.h;
+      pp.bm[j][2 * half] = lo.m, pp.bm[j][2 * half + 1] = hi.m;
+      pp.bl[j][2 * half] = lo.l, pp.bl[j][2 * half + 1] = hi.l;
+    }
+  };
+  // the MFMAs of a pair: the small products first
+  auto mfmas3 = [&](const PairParts &pp) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        acc[i][j] = mfma(al, bh[j], acc[i][j]);
+        acc[i][j] = mfma(pp.al[i], pp.bh[j], acc[i][j]);
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        acc[i][j] = mfma(ah, bl[j], acc[i][j]);
+        acc[i][j] = mfma(pp.ah[i], pp.bl[j], acc[i][j]);
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        acc[i][j] = mfma(am, bm[j], acc[i][j]);
+        acc[i][j] = mfma(pp.am[i], pp.bm[j], acc[i][j]);
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        acc[i][j] = mfma(am, bh[j], acc[i][j]);
+        acc[i][j] = mfma(pp.am[i], pp.bh[j], acc[i][j]);
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        acc[i][j] = mfma(ah, bm[j], acc[i][j]);
+        acc[i][j] = mfma(pp.ah[i], pp.bm[j], acc[i][j]);
 #pragma unroll
       for (int j = 0; j < 4; j++)
-        acc[i][j] = mfma(ah, bh[j], acc[i][j]);
+        acc[i][j] = mfma(pp.ah[i], pp.bh[j], acc[i][j]);
     }
   };
 
   // As mm_gemm_lds: step + 1's loads have landed once only the later steps' may be outstanding, the barrier makes that
   // true of every wave and frees the stage step - 1 used, which step + 5 now fills; the operands of step + 1 are read
-  // a step ahead. The MFMAs run at odd stages on the pair (held, cur).
-  Operands held, cur, next;
+  // a step ahead. An even stage splits its step's half of the pair, an odd stage the other half and runs the MFMAs.
+  Operands cur, next;
+  PairParts pp;
   auto advance = [&](int step, auto ST) {
     constexpr int st = decltype(ST)::value, nst = (st + 1) % kX3Stages, fill = (st + kX3Stages - 1) % kX3Stages;
     wait_vmcnt<(kX3Stages - 3) * kMmLoadsPerStep>();
@@ -1076,11 +1086,10 @@ __global__ __launch_bounds__(kQ8Threads, 2) void mm_gemm_f32x3(MmParams p) {
     issue(step + kX3Stages - 1, std::integral_constant<int, fill>{});
     operands(std::integral_constant<int, nst>{}, next);
     __builtin_amdgcn_sched_barrier(0);
+    split_half(cur, pp, st % 2);
     if constexpr (st % 2 == 1) {
-      mfmas3(held, cur);
+      mfmas3(pp);
       __builtin_amdgcn_sched_barrier(0);
-    } else {
-      held = cur;
     }
     cur = next;
   };
