@@ -998,7 +998,8 @@ template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash(Att
 //     the scores' accumulator as it stands (lane (q, c) holds positions 16 t + 4 q + e of vector c), so slot
 //     8 q + 4 t + e holds position 16 t + 4 q + e, and the A operand (16 dimensions x 32 slots) is again one 16-byte
 //     read per part.
-// Lane (q, c) ends with dimensions 16 d + 4 q + e of its vector c.
+// Lane (q, c) ends with dimensions 16 d + 4 q + e of its vector c; unsplit with qout set, the epilogue quantizes them
+// in groups of qgs dimensions instead of storing FP32.
 template <int HD> __global__ __launch_bounds__(kTileThreads) void attn_flash3(AttnParams p) {
   typedef int v4i_t __attribute__((ext_vector_type(4)));
   typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -1629,14 +1630,21 @@ bool attention_uses_flash(const AttentionJob &job) {
          offsets_fit && ((uintptr_t)job.out & 15) == 0 && ((uintptr_t)job.value & 15) == 0;
 }
 
+// The batched kernel's form: attn_flash3 (products from exact BF16 parts) unless LLAMA_HIP_FLASH_FORM = fp32 picks
+// attn_flash (FP32 products); read on every call.
+bool attention_flash_bf3() {
+  const char *form = getenv("LLAMA_HIP_FLASH_FORM");
+  return !form || strcmp(form, "fp32") != 0;
+}
+
 // Blocks per tile of the batched kernel (0: one block per pair of tiles, no partials). A block walks its tiles' 64-position
 // chunks at about the same time per chunk whatever the grid, so a grid of few blocks with long walks (a short batch
 // late in a sequence: a prompt prefilled in batches) leaves most CUs idle for the whole walk. Split S gives each tile S
 // blocks over shares of its chunks and adds attn_merge_shares. The choice is the S in {1, 2, 4, 8, 16} of least
-// estimated time, with one chunk's walk about 10 us at head_dim 128 and 6 at 64 (measured on 8B, 3B and 1B heads):
-// unsplit, the longest pair's chunks times the rounds of the CUs its grid takes; split, the longest share's chunks
-// times the rounds, plus the merge (about 2 us + 0.012 us per row at 32 heads); a split must save a tenth. Its
-// partials stay within job.partial_room. LLAMA_HIP_FLASH_SPLITS = n forces n (1: never split), for tuning and tests.
+// estimated time, with one 64-position walk taking the kernel's measured time (below): unsplit, the longest pair's
+// chunks times the rounds of the CUs its grid takes; split, the longest share's chunks times the rounds, plus the
+// merge; a split must save a tenth. Its partials stay within job.partial_room. LLAMA_HIP_FLASH_SPLITS = n forces n
+// (1: never split), for tuning and tests.
 int flash_splits(const AttentionJob &job, int chunks) {
   const int kv_mul = job.n_heads / job.n_kv_heads;
   const int tile_rows = 128 / kv_mul, tiles = (job.rows + tile_rows - 1) / tile_rows;
@@ -1646,15 +1654,22 @@ int flash_splits(const AttentionJob &job, int chunks) {
   if (splits <= 0) {
     auto walk = [&](int t) { return (job.pos0 + min((t + 1) * tile_rows, job.rows) - 1) / kChunk + 1; };
     auto rounds = [&](long long blocks) { return (double)((blocks + cus - 1) / cus); };
-    const double chunk_us = job.head_dim == 128 ? 10.0 : 6.0;
+    // the BF16-part kernel walks a 64-position span in about 5.7 us at head_dim 128 (3.5 at 64), and its merge grows
+    // with the shares (each share's partials read and rescaled): fitted to forced splits of 128 to 512 rows at 8B, 3B
+    // and 1B heads; the FP32-product kernel's figures are the first ones measured
+    const bool bf3 = attention_flash_bf3();
+    const double chunk_us = bf3 ? (job.head_dim == 128 ? 5.7 : 3.5) : (job.head_dim == 128 ? 10.0 : 6.0);
+    auto merge = [&](int s) {
+      const double per_row = job.rows * job.n_heads / 32.0;
+      return bf3 ? 2.0 + 0.011 * per_row * s * job.head_dim / 128.0 : 2.0 + 0.012 * per_row;
+    };
     const int pairs = (tiles + 1) / 2;
     const double unsplit = chunk_us * (walk(tiles - 1) + (tiles > 1 ? walk(0) : 0)) *
                            rounds((long long)pairs * job.n_kv_heads);
-    const double merge = 2.0 + 0.012 * job.rows * job.n_heads / 32.0;
     double best = 0.9 * unsplit;
     splits = 1;
     for (int s = 2; s <= 16; s *= 2) {
-      const double t = chunk_us * ((chunks + s - 1) / s) * rounds((long long)tiles * job.n_kv_heads * s) + merge;
+      const double t = chunk_us * ((chunks + s - 1) / s) * rounds((long long)tiles * job.n_kv_heads * s) + merge(s);
       if (t < best)
         best = t, splits = s;
     }
@@ -1721,8 +1736,7 @@ bool launch_attention(const AttentionJob &job, float *partial, hipStream_t strea
     p.splits = flash_splits(job, p.chunks);
     const dim3 grid(p.splits ? (unsigned)tiles : (unsigned)((tiles + 1) / 2), (unsigned)job.n_kv_heads,
                     p.splits ? (unsigned)p.splits : 1u);
-    const char *form = getenv("LLAMA_HIP_FLASH_FORM"); // fp32: attn_flash; unset or bf16x3: attn_flash3
-    const bool bf3 = !form || strcmp(form, "fp32") != 0;
+    const bool bf3 = attention_flash_bf3();
     const bool fused_quant = job.qout && bf3 && !p.splits;
     if (fused_quant) {
       p.qout = job.qout;
