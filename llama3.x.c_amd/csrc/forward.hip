@@ -183,38 +183,35 @@ __global__ __launch_bounds__(kThreads) void rope_kv_rows(float *__restrict__ q, 
   }
 }
 
-// rope_kv_rows for head_dim HD = 64 or 128: block (x, row) takes units 256 x .. of one row (no division by a runtime
-// size, so none in 64 bits), each unit the float4 rope_kv_rows gives the thread of the same row and unit; the same
-// products in the same order, so the results are bitwise those of rope_kv_rows.
+// rope_kv_rows for head_dim HD = 64 or 128: thread (row, d4) takes dimensions 4 d4 .. 4 d4 + 3 of every head of its
+// row (q heads, then k, then v), so the row's table values for them are loaded once and all of its loads are in
+// flight together; each element gets the same products in the same order as in rope_kv_rows, so the results are
+// bitwise those of rope_kv_rows.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void rope_kv_rows_hd(float *__restrict__ q, size_t q_stride, float *__restrict__ k,
                                                             const float *__restrict__ v, size_t kv_stride,
                                                             const float *__restrict__ table, size_t table_stride,
-                                                            int n_heads, int n_kv_heads, float *__restrict__ key_cache,
+                                                            int rows, int n_heads, int n_kv_heads,
+                                                            float *__restrict__ key_cache,
                                                             float *__restrict__ value_cache, int pos0,
                                                             size_t pos_stride, size_t head_base) {
-  constexpr int hd4 = HD / 4;
-  const int qu = n_heads * hd4, ku = n_kv_heads * hd4;
-  const int u = blockIdx.x * kThreads + threadIdx.x, r = blockIdx.y;
-  if (u >= qu + 2 * ku)
+  constexpr int hd4 = HD / 4, kRowsPerBlock = kThreads / hd4;
+  const int r = blockIdx.x * kRowsPerBlock + threadIdx.x / hd4, d = 4 * (threadIdx.x % hd4);
+  if (r >= rows)
     return;
-  const float *t = table + (size_t)r * table_stride;
-  if (u < qu) {
-    const int h = u / hd4, d = 4 * (u % hd4);
-    float4 *p = reinterpret_cast<float4 *>(q + (size_t)r * q_stride + (size_t)h * HD + d);
-    *p = rotate4(*p, t, HD, d);
-    return;
+  const Rot4 rot = rot4_of(table + (size_t)r * table_stride, HD, d);
+  float *qr = q + (size_t)r * q_stride + d;
+  for (int h = 0; h < n_heads; h++) {
+    float4 *pq = reinterpret_cast<float4 *>(qr + (size_t)h * HD);
+    *pq = rotate4(*pq, rot);
   }
-  const bool is_k = u < qu + ku;
-  const int w = is_k ? u - qu : u - qu - ku, g = w / hd4, d = 4 * (w % hd4);
-  const size_t at = (size_t)r * kv_stride + (size_t)g * HD + d;
-  const size_t slot = (size_t)(pos0 + r) * pos_stride + (size_t)g * head_base + d;
-  if (is_k) {
-    float4 *p = reinterpret_cast<float4 *>(k + at);
-    const float4 x = rotate4(*p, t, HD, d);
-    *p = x;
+  const size_t slot0 = (size_t)(pos0 + r) * pos_stride + d;
+  for (int g = 0; g < n_kv_heads; g++) {
+    const size_t at = (size_t)r * kv_stride + (size_t)g * HD + d, slot = slot0 + (size_t)g * head_base;
+    float4 *pk = reinterpret_cast<float4 *>(k + at);
+    const float4 x = rotate4(*pk, rot);
+    *pk = x;
     *reinterpret_cast<float4 *>(key_cache + slot) = x;
-  } else {
     *reinterpret_cast<float4 *>(value_cache + slot) = *reinterpret_cast<const float4 *>(v + at);
   }
 }
@@ -1516,14 +1513,15 @@ bool launch_rope_kv_rows(float *q, size_t q_stride, float *k, const float *v, si
                          size_t table_stride, int rows, int n_heads, int n_kv_heads, int head_dim, float *key_cache,
                          float *value_cache, int pos0, size_t pos_stride, size_t head_base, hipStream_t stream) {
   const int per_row = (n_heads + 2 * n_kv_heads) * (head_dim / 4);
-  if ((head_dim == 128 || head_dim == 64) && rows <= 65535) {
-    const dim3 grid((unsigned)((per_row + kThreads - 1) / kThreads), (unsigned)rows);
+  if (head_dim == 128 || head_dim == 64) {
+    const int rows_per_block = kThreads / (head_dim / 4);
+    const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
     if (head_dim == 128)
       hipLaunchKernelGGL(rope_kv_rows_hd<128>, grid, dim3(kThreads), 0, stream, q, q_stride, k, v, kv_stride, table,
-                         table_stride, n_heads, n_kv_heads, key_cache, value_cache, pos0, pos_stride, head_base);
+                         table_stride, rows, n_heads, n_kv_heads, key_cache, value_cache, pos0, pos_stride, head_base);
     else
       hipLaunchKernelGGL(rope_kv_rows_hd<64>, grid, dim3(kThreads), 0, stream, q, q_stride, k, v, kv_stride, table,
-                         table_stride, n_heads, n_kv_heads, key_cache, value_cache, pos0, pos_stride, head_base);
+                         table_stride, rows, n_heads, n_kv_heads, key_cache, value_cache, pos0, pos_stride, head_base);
     return launch_ok("rope_kv_rows_hd");
   }
   const long long threads = (long long)rows * per_row;
